@@ -1,0 +1,197 @@
+/*
+ * rusty_hip.h — C ABI of librusty_hip.so, the MI355X (gfx950) backend for
+ * RustyLLM's decode step.
+ *
+ * Every rusty_hip_* export below "Reference seam" mirrors one rusty_metal_*
+ * declaration of the reference's src/metal.rs FFI block (lines cited), with
+ * the same parameter order, types (usize -> uintptr_t) and return convention:
+ * 1 = the full output was written, 0 = not handled (not initialised, null
+ * pointer, zero or unsupported dimension, buffer too small, device error) and
+ * the caller runs its CPU kernel instead (src/metal.rs:716-720).
+ *
+ * Weights passed by host pointer are uploaded once and cached by (pointer,
+ * length) for the life of the process, as the Metal shim does
+ * (src/metal_backend.m:788-842); row starts are padded to 16 bytes in the
+ * device copy, block bytes are unchanged.  Calls are synchronous.  The per-op
+ * exports share staging buffers and must be serialised by the caller, like
+ * the reference's (src/runtime.rs:3167-3170); the library also holds an
+ * internal mutex.
+ *
+ * Numerics follow the reference's x86 path: Q4_K, Q6_K and Q8_0 (K % 256 ==
+ * 0) multiply against the Q8_K-quantized activation (src/simd.rs:944-959);
+ * Q8_0 with other K and MXFP4 use f32 activations.
+ */
+#ifndef RUSTY_HIP_H
+#define RUSTY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== Reference seam (src/metal.rs:123-340) ============================== */
+
+/* rusty_metal_available, src/metal.rs:127.  Initialises the device context. */
+int rusty_hip_available(void);
+
+/* rusty_metal_q4k_matvec / q6k_matvec, src/metal.rs:129-145. */
+int rusty_hip_q4k_matvec(const uint8_t *weights, uintptr_t weights_len, const float *x, uintptr_t rows,
+                         uintptr_t cols, float *out);
+int rusty_hip_q6k_matvec(const uint8_t *weights, uintptr_t weights_len, const float *x, uintptr_t rows,
+                         uintptr_t cols, float *out);
+
+/* rusty_metal_q6k_matvec2 / 3, src/metal.rs:147-176. */
+int rusty_hip_q6k_matvec2(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                          const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b, const float *x,
+                          uintptr_t cols, float *out_a, float *out_b);
+int rusty_hip_q6k_matvec3(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                          const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b,
+                          const uint8_t *weights_c, uintptr_t weights_c_len, uintptr_t rows_c, const float *x,
+                          uintptr_t cols, float *out_a, float *out_b, float *out_c);
+
+/* rusty_metal_q4k_matvec2 / 3, src/metal.rs:177-206. */
+int rusty_hip_q4k_matvec2(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                          const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b, const float *x,
+                          uintptr_t cols, float *out_a, float *out_b);
+int rusty_hip_q4k_matvec3(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                          const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b,
+                          const uint8_t *weights_c, uintptr_t weights_c_len, uintptr_t rows_c, const float *x,
+                          uintptr_t cols, float *out_a, float *out_b, float *out_c);
+
+/* rusty_metal_q4k_q4k_q6k_matvec3, src/metal.rs:207-222. */
+int rusty_hip_q4k_q4k_q6k_matvec3(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                                  const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b,
+                                  const uint8_t *weights_c, uintptr_t weights_c_len, uintptr_t rows_c,
+                                  const float *x, uintptr_t cols, float *out_a, float *out_b, float *out_c);
+
+/* rusty_metal_q4k_q4k_q6k_ffn, src/metal.rs:224-237: out = down * (silu(gate*x) (.) up*x). */
+int rusty_hip_q4k_q4k_q6k_ffn(const uint8_t *gate_weights, uintptr_t gate_weights_len, const uint8_t *up_weights,
+                              uintptr_t up_weights_len, const uint8_t *down_weights, uintptr_t down_weights_len,
+                              const float *x, uintptr_t input_cols, uintptr_t hidden_rows, uintptr_t down_rows,
+                              uintptr_t down_cols, float *out);
+
+/* rusty_metal_mistral_post_attention_ffn, src/metal.rs:239-257:
+ * x += wo*attn_out; x += down * (silu(gate*n) (.) up*n), n = rmsnorm(x)*ffn_norm. */
+int rusty_hip_mistral_post_attention_ffn(const uint8_t *wo_weights, uintptr_t wo_weights_len,
+                                         const uint8_t *gate_weights, uintptr_t gate_weights_len,
+                                         const uint8_t *up_weights, uintptr_t up_weights_len,
+                                         const uint8_t *down_weights, uintptr_t down_weights_len, float *x,
+                                         uintptr_t dim, const float *attn_out, uintptr_t attn_cols,
+                                         const float *ffn_norm, float rms_eps, uintptr_t hidden_rows,
+                                         uintptr_t down_rows, uintptr_t down_cols);
+
+/* rusty_metal_q8_0_matvec, src/metal.rs:268-275 (int8 Q8_K path when cols % 256
+ * == 0, f32 activations otherwise, as src/simd.rs dot_row). */
+int rusty_hip_q8_0_matvec(const uint8_t *weights, uintptr_t weights_len, const float *x, uintptr_t rows,
+                          uintptr_t cols, float *out);
+
+/* rusty_metal_attention, src/metal.rs:277-299.  *_len are byte lengths;
+ * keys/values are the whole layer cache (slot_count * stride floats). */
+int rusty_hip_attention(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
+                        const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,
+                        float *out, uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim,
+                        uintptr_t value_dim, uintptr_t key_stride, uintptr_t value_stride, uintptr_t slot_count,
+                        uintptr_t start_t, uintptr_t end_t, float scale, int use_sink);
+
+/* ResidentLayerDesc, src/metal.rs:347-360 (#[repr(C)]).  Weight order: wq,
+ * wk, wv, wo, gate(w1), up(w3), down(w2).  w_dt: 0 = Q4_K, 1 = Q6_K as in the
+ * reference; this library also accepts 2 = Q8_0, 3 = MXFP4, or the GGML type
+ * id itself (8, 12, 14, 39). */
+typedef struct {
+    const uint8_t *w[7];
+    uintptr_t w_len[7];
+    uint32_t w_rows[7];
+    uint32_t w_dt[7];
+    const float *attn_norm;
+    const float *ffn_norm;
+    const float *bq;
+    uint32_t bq_len;
+    const float *bk;
+    uint32_t bk_len;
+    const float *bv;
+    uint32_t bv_len;
+} RustyResidentLayerDesc;
+
+/* rusty_metal_resident_configure / set_layer / set_output / decode,
+ * src/metal.rs:302-338.  The KV cache lives in HBM. */
+int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                 uint32_t head_dim, uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab,
+                                 uint32_t storage_len, float eps, uint32_t neox);
+int rusty_hip_resident_set_layer(uint32_t l, const RustyResidentLayerDesc *desc);
+int rusty_hip_resident_set_output(const float *output_norm, const uint8_t *output_w, uintptr_t output_w_len,
+                                  uint32_t output_rows, uint32_t output_dt, const float *inv_freq,
+                                  uint32_t inv_freq_len);
+int rusty_hip_resident_decode(const float *x_embed, uint32_t pos, uint32_t start_t, int want_logits,
+                              float *logits_out);
+
+/* ===== Exports without a Metal counterpart ================================ */
+
+/* MXFP4 has no Metal hook (src/simd.rs:4020-4024); these serve
+ * matvec_mxfp4_into (src/simd.rs:4020) and the expert pair of
+ * ExpertWeight::try_matvec_expert_pair_into (src/model.rs:962-1017). */
+int rusty_hip_mxfp4_matvec(const uint8_t *weights, uintptr_t weights_len, const float *x, uintptr_t rows,
+                           uintptr_t cols, float *out);
+int rusty_hip_mxfp4_matvec2(const uint8_t *weights_a, uintptr_t weights_a_len, uintptr_t rows_a,
+                            const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b, const float *x,
+                            uintptr_t cols, float *out_a, float *out_b);
+
+/* Generic single matvec for any supported GGML type (8, 12, 14, 39): the
+ * Weight::matvec_into dispatch of src/model.rs:218-257. */
+int rusty_hip_matvec(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, const float *x,
+                     uintptr_t rows, uintptr_t cols, float *out);
+
+/* Resident decoder, device-token mode (no reference counterpart; the
+ * Metal decoder takes the embedding from the host).  The embedding table is
+ * held in HBM and the greedy pick (repeat penalty + first finite maximum,
+ * src/sampling.rs:78-83, 321-356) runs on the device, so a whole token is one
+ * graph replay with no host round trip. */
+int rusty_hip_resident_set_embedding(const uint8_t *embd, uintptr_t embd_len, uint32_t ggml_type);
+/* Prefills `prompt` at positions start_pos.., then greedily generates n_gen
+ * tokens into out_tokens (recent-token window of 64, src/runtime.rs:493-521).
+ * logits_out (vocab floats, may be null) receives the logits of the last
+ * forward. */
+int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32_t start_pos, uint32_t n_gen,
+                                float repeat_penalty, int32_t *out_tokens, float *logits_out);
+/* Copies slots [slot0, slot0+n_slots) of layer l's K (which = 0) or V
+ * (which = 1) cache to / from host memory. */
+int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);
+int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in);
+
+/* Frees every cached device weight copy (no reference counterpart: the
+ * Metal cache lives as long as the process because the reference's weights
+ * are mmap'd and never freed).  Call it before freeing host weight memory
+ * whose addresses may be reused; rusty_hip_resident_configure also clears. */
+int rusty_hip_weight_cache_clear(void);
+
+/* Timing on the library's stream (the stream every kernel is launched on). */
+int rusty_hip_sync(void);
+/* Per-kernel-family timing: while enabled, every launch is bracketed by a
+ * HIP event pair on the library stream and graphs are bypassed. */
+int rusty_hip_profile_enable(int on);
+/* Family i: returns 0 past the last one; fills name (<= 63 chars), total
+ * milliseconds and launch count accumulated since enable. */
+int rusty_hip_profile_get(int i, char *name, double *total_ms, int64_t *count);
+/* Times n_tokens decode steps (graph replays in device-token mode) between
+ * two HIP events on the library stream; returns elapsed ms via *ms. */
+int rusty_hip_resident_time_decode(uint32_t n_tokens, float repeat_penalty, double *ms);
+
+/* Test hooks (device results of single stages, for bit-exactness checks). */
+int rusty_hip_debug_quantize_q8k(const float *x, uintptr_t n, int8_t *qs, float *d, int16_t *bsums);
+int rusty_hip_debug_dequant(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, uintptr_t rows,
+                            uintptr_t cols, float *out);
+int rusty_hip_debug_block_ints(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, uintptr_t rows,
+                               uintptr_t cols, const float *x, int32_t *out);
+int rusty_hip_debug_rmsnorm(const float *x, const float *w, float eps, uintptr_t n, float *out);
+int rusty_hip_debug_silu_mul(const float *gate, const float *up, uintptr_t n, float *out);
+int rusty_hip_debug_rope(float *q, float *k, uint32_t pos, uint32_t head_dim, uint32_t n_heads, uint32_t n_kv_heads,
+                         const float *inv_freq, uint32_t neox);
+int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *recent, uint32_t n_recent, float penalty,
+                           int32_t *token);
+int rusty_hip_debug_f16(const uint16_t *h, uintptr_t n, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,339 @@
+"""ctypes bindings for the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the CPU
+baseline that bench.py reports.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py may import this module.  It restates
+SimonWaldherr/RustyLLM's x86-64 numerics (src/simd.rs, src/model.rs); each C
+function cites the reference line it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, Q8_0, Q4_K, Q6_K, MXFP4 = 0, 8, 12, 14, 39
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210), MXFP4: (32, 17), F32: (1, 4)}
+
+
+def build() -> None:
+    """Compile liboracle.so from oracle.c (make, in this directory)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(_LIB_PATH):
+        build()
+    return C.CDLL(_LIB_PATH)
+
+
+lib = _load()
+_p = C.c_void_p
+_i64 = C.c_int64
+_f = C.c_float
+
+
+def _sig(name, res, *args):
+    fn = getattr(lib, name)
+    fn.restype = res
+    fn.argtypes = list(args)
+    return fn
+
+
+_sig("orc_f16_to_f32", _f, C.c_uint16)
+_sig("orc_mxfp4_scale", _f, C.c_uint8)
+_sig("orc_quantize_row_q8k_scalar", None, _p, _i64, _p, _p, _p)
+_sig("orc_quantize_row_q8k_avx2", None, _p, _i64, _p, _p, _p)
+_sig("orc_dequant_row", None, C.c_int, _p, _p, _i64)
+for _n in ("orc_dot_q4_k_q8k_avx2", "orc_dot_q6_k_q8k_avx2", "orc_dot_q8_0_q8k_avx2", "orc_emulate_q4_k_q8k"):
+    _sig(_n, _f, _p, _p, _p, _p, _i64)
+_sig("orc_emulate_q6_k_q8k", _f, _p, _p, _p, _i64)
+_sig("orc_emulate_q8_0_q8k", _f, _p, _p, _p, _i64)
+_sig("orc_dot_q8_0_f32_avx2", _f, _p, _p, _i64)
+_sig("orc_dot_mxfp4_f32_scalar", _f, _p, _p, _i64)
+_sig("orc_dot_f32_avx2", _f, _p, _p, _i64)
+_sig("orc_q4k_block_ints", None, _p, _p, _p, _i64, _p, _p)
+_sig("orc_q6k_block_ints", None, _p, _p, _i64, _p)
+_sig("orc_q8_0_block_ints", None, _p, _p, _i64, _p)
+_sig("orc_row_bytes", _i64, C.c_int, _i64)
+_sig("orc_matvec", None, C.c_int, _p, _p, _i64, _i64, _p, C.c_int)
+_sig("orc_set_threads", None, C.c_int)
+_sig("orc_online_attention", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
+_sig("orc_online_attention_with_sink", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _f, _p)
+_sig("orc_online_attention_grouped", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
+_sig("orc_attention_over_kv_heads", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
+_sig("orc_attention_sink_heads", None, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
+_sig("orc_attention_start_pos", _i64, _i64, _i64)
+_sig("orc_rms_norm", None, _p, _p, _f, _i64, _p)
+_sig("orc_build_rope_inv_freq", None, _f, _i64, _f, _p)
+_sig("orc_rope_qk", None, _p, _p, _i64, _i64, _i64, _i64, _p)
+_sig("orc_rope_qk_neox", None, _p, _p, _i64, _i64, _i64, _i64, _p)
+_sig("orc_silu_mul_avx2", None, _p, _p, _p, _i64)
+_sig("orc_silu_mul_scalar", None, _p, _p, _p, _i64)
+_sig("orc_swiglu_gpt_oss", _f, _f, _f)
+_sig("orc_select_top_logits", None, _p, _i64, _i64, _p, _p)
+_sig("orc_softmax_selected", None, _p, _i64, _p)
+_sig("orc_apply_repeat_penalty", None, _p, _i64, _p, _i64, _f)
+_sig("orc_argmax_finite", C.c_uint32, _p, _i64)
+_sig("orc_greedy", C.c_uint32, _p, _i64, _p, _i64, _f)
+_sig("orc_model_create", _p, _p)
+_sig("orc_model_free", None, _p)
+_sig("orc_model_set_layer", C.c_int, _p, C.c_int32, _p)
+_sig("orc_model_set_output", C.c_int, _p, _p, _p, C.c_uint32, _p, C.c_uint32, _p)
+_sig("orc_model_forward", None, _p, C.c_uint32, _i64, _p, C.c_int)
+_sig("orc_model_kv", C.POINTER(C.c_float), _p, C.c_int32, C.c_int32)
+_sig("orc_model_generate", _i64, _p, _p, _i64, _i64, _i64, _f, _p, _p)
+_sig("orc_make_q4k_weights", None, _i64, _i64, C.c_uint8, _p)
+_sig("orc_make_q4k_weights_dmin", None, _i64, _i64, C.c_uint8, _p)
+_sig("orc_make_q6k_weights", None, _i64, _i64, C.c_uint8, _p)
+_sig("orc_make_q8_0_row_scaled", None, _i64, C.c_uint8, _p)
+_sig("orc_make_mxfp4_test_row", None, _i64, _p)
+_sig("orc_test_activation", None, _i64, _p)
+_sig("orc_mxfp4_test_activation", None, _i64, _p)
+
+
+def ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return int(lib.orc_row_bytes(dtype, cols))
+
+
+# ---- Q8_K ------------------------------------------------------------------
+def quantize_q8k(x: np.ndarray, avx2: bool = True):
+    x = f32(x)
+    n = x.size
+    qs = np.zeros(n, np.int8)
+    d = np.zeros(n // 256, np.float32)
+    bs = np.zeros(n // 32, np.int16)
+    fn = lib.orc_quantize_row_q8k_avx2 if avx2 else lib.orc_quantize_row_q8k_scalar
+    fn(ptr(x), n, ptr(qs), ptr(d), ptr(bs))
+    return qs, d, bs
+
+
+def dequant_row(dtype: int, q: np.ndarray, n: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    out = np.empty(n, np.float32)
+    lib.orc_dequant_row(dtype, ptr(q), ptr(out), n)
+    return out
+
+
+def dequant(dtype: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint8)
+    rb = row_bytes(dtype, cols)
+    out = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        lib.orc_dequant_row(dtype, ptr(w) + r * rb, ptr(out) + r * cols * 4, cols)
+    return out
+
+
+def matvec(dtype: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, threads: int = 0) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.uint8)
+    x = f32(x)
+    out = np.empty(rows, np.float32)
+    lib.orc_matvec(dtype, ptr(w), ptr(x), rows, cols, ptr(out), threads)
+    return out
+
+
+def block_ints(dtype: int, w_row: np.ndarray, qs: np.ndarray, bs: np.ndarray, cols: int):
+    w_row = np.ascontiguousarray(w_row, np.uint8)
+    if dtype == Q4_K:
+        isum = np.zeros(cols // 256, np.int32)
+        imin = np.zeros(cols // 256, np.int32)
+        lib.orc_q4k_block_ints(ptr(w_row), ptr(qs), ptr(bs), cols, ptr(isum), ptr(imin))
+        return isum, imin
+    if dtype == Q6_K:
+        isum = np.zeros(cols // 256, np.int32)
+        lib.orc_q6k_block_ints(ptr(w_row), ptr(qs), cols, ptr(isum))
+        return isum, None
+    if dtype == Q8_0:
+        s = np.zeros(cols // 32, np.int32)
+        lib.orc_q8_0_block_ints(ptr(w_row), ptr(qs), cols, ptr(s))
+        return s, None
+    raise ValueError(dtype)
+
+
+def attention(q, k, v, n_heads, n_kv, hd, vd, key_stride, value_stride, slot_count, start_t, end_t, scale,
+              sinks=None) -> np.ndarray:
+    """Reference attention over all heads: grouped GQA (model.rs:5952) or, with
+    sinks, the gpt-oss per-head sink loop (model.rs:6812-6833)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.zeros(n_heads * vd, np.float32)
+    kv_mul = n_heads // n_kv
+    if sinks is None:
+        lib.orc_attention_over_kv_heads(ptr(q), ptr(k), ptr(v), key_stride, value_stride, slot_count, hd, vd,
+                                        n_kv, kv_mul, start_t, end_t, scale, ptr(out))
+    else:
+        s = f32(sinks)
+        lib.orc_attention_sink_heads(ptr(q), ptr(k), ptr(v), ptr(s), key_stride, value_stride, slot_count, hd, vd,
+                                     n_heads, kv_mul, start_t, end_t, scale, ptr(out))
+    return out
+
+
+def rms_norm(x, w, eps):
+    x, w = f32(x), f32(w)
+    out = np.empty_like(x)
+    lib.orc_rms_norm(ptr(x), ptr(w), eps, x.size, ptr(out))
+    return out
+
+
+def rope_inv_freq(theta: float, head_dim: int, scaling: float = 1.0) -> np.ndarray:
+    inv = np.zeros(head_dim // 2, np.float32)
+    lib.orc_build_rope_inv_freq(theta, head_dim, scaling, ptr(inv))
+    return inv
+
+
+def rope(q, k, pos, hd, nh, nkv, inv_freq, neox=False):
+    q, k, inv = f32(q).copy(), f32(k).copy(), f32(inv_freq)
+    (lib.orc_rope_qk_neox if neox else lib.orc_rope_qk)(ptr(q), ptr(k), pos, hd, nh, nkv, ptr(inv))
+    return q, k
+
+
+def silu_mul(gate, up, avx2=True):
+    g, u = f32(gate), f32(up)
+    out = np.empty_like(g)
+    (lib.orc_silu_mul_avx2 if avx2 else lib.orc_silu_mul_scalar)(ptr(g), ptr(u), ptr(out), g.size)
+    return out
+
+
+def greedy(logits, recent, penalty):
+    lg = f32(logits).copy()
+    r = np.ascontiguousarray(recent, np.uint32)
+    tok = lib.orc_greedy(ptr(lg), lg.size, ptr(r) if r.size else None, r.size, penalty)
+    return int(tok), lg
+
+
+def top_k_router(logits, k):
+    lg = f32(logits)
+    idx = np.zeros(k, np.int32)
+    val = np.zeros(k, np.float32)
+    lib.orc_select_top_logits(ptr(lg), lg.size, k, ptr(idx), ptr(val))
+    probs = np.zeros(k, np.float32)
+    lib.orc_softmax_selected(ptr(val), k, ptr(probs))
+    return idx, val, probs
+
+
+# ---- reference fixtures ------------------------------------------------------
+def make_q4k_weights(rows, cols, seed, dmin=False):
+    out = np.zeros(rows * (cols // 256) * 144, np.uint8)
+    (lib.orc_make_q4k_weights_dmin if dmin else lib.orc_make_q4k_weights)(rows, cols, seed, ptr(out))
+    return out
+
+
+def make_q6k_weights(rows, cols, seed):
+    out = np.zeros(rows * (cols // 256) * 210, np.uint8)
+    lib.orc_make_q6k_weights(rows, cols, seed, ptr(out))
+    return out
+
+
+def make_q8_0_row_scaled(cols, seed):
+    out = np.zeros((cols // 32) * 34, np.uint8)
+    lib.orc_make_q8_0_row_scaled(cols, seed, ptr(out))
+    return out
+
+
+def make_mxfp4_test_row(blocks):
+    out = np.zeros(blocks * 17, np.uint8)
+    lib.orc_make_mxfp4_test_row(blocks, ptr(out))
+    return out
+
+
+def test_activation(cols):
+    out = np.zeros(cols, np.float32)
+    lib.orc_test_activation(cols, ptr(out))
+    return out
+
+
+def mxfp4_test_activation(n):
+    out = np.zeros(n, np.float32)
+    lib.orc_mxfp4_test_activation(n, ptr(out))
+    return out
+
+
+# ---- model -------------------------------------------------------------------
+class OrcConfig(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("dim", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("value_dim", C.c_int32), ("hidden_dim", C.c_int32), ("vocab", C.c_int32),
+                ("storage_len", C.c_int32), ("sliding_window", C.c_int32), ("neox", C.c_int32), ("eps", C.c_float)]
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("w", C.c_void_p * 7), ("w_len", C.c_uint64 * 7), ("w_rows", C.c_uint32 * 7),
+                ("w_type", C.c_uint32 * 7), ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+                ("bq", C.c_void_p), ("bq_len", C.c_uint32), ("bk", C.c_void_p), ("bk_len", C.c_uint32),
+                ("bv", C.c_void_p), ("bv_len", C.c_uint32)]
+
+
+class OracleModel:
+    """Oracle forward_into (model.rs:7177-7358) over a model dict produced by
+    rustyllm_amd.synth (the same bytes the HIP decoder consumes)."""
+
+    def __init__(self, model, storage_len: int, threads: int = 0):
+        cfg = model["config"]
+        self.model = model
+        self.cfg = cfg
+        self.vocab = cfg["vocab"]
+        c = OrcConfig(cfg["n_layers"], cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
+                      cfg["value_dim"], cfg["hidden_dim"], cfg["vocab"], storage_len, cfg.get("sliding_window", 0),
+                      1 if cfg.get("neox") else 0, cfg["eps"])
+        if threads:
+            lib.orc_set_threads(threads)
+        self.h = lib.orc_model_create(C.byref(c))
+        self._keep = []
+        for l, layer in enumerate(model["layers"]):
+            L = OrcLayer()
+            for i, (arr, dt, rows) in enumerate(layer["w"]):
+                L.w[i] = ptr(arr)
+                L.w_len[i] = arr.nbytes
+                L.w_rows[i] = rows
+                L.w_type[i] = dt
+            L.attn_norm = ptr(layer["attn_norm"])
+            L.ffn_norm = ptr(layer["ffn_norm"])
+            for nm in ("bq", "bk", "bv"):
+                b = layer.get(nm)
+                if b is not None:
+                    setattr(L, nm, ptr(b))
+                    setattr(L, nm + "_len", b.size)
+            lib.orc_model_set_layer(self.h, l, C.byref(L))
+        out_w, out_dt = model["output"]
+        emb_w, emb_dt = model["token_embd"]
+        lib.orc_model_set_output(self.h, ptr(model["output_norm"]), ptr(out_w), out_dt, ptr(emb_w), emb_dt,
+                                 ptr(model["inv_freq"]))
+
+    def forward(self, token: int, pos: int, want_logits: bool = True):
+        logits = np.zeros(self.vocab, np.float32)
+        lib.orc_model_forward(self.h, token, pos, ptr(logits), 1 if want_logits else 0)
+        return logits
+
+    def kv(self, layer: int, storage_len: int):
+        cfg = self.cfg
+        kd = cfg["n_kv_heads"] * cfg["head_dim"]
+        vd = cfg["n_kv_heads"] * cfg["value_dim"]
+        kp = lib.orc_model_kv(self.h, layer, 0)
+        vp = lib.orc_model_kv(self.h, layer, 1)
+        k = np.ctypeslib.as_array(kp, shape=(storage_len * kd,))
+        v = np.ctypeslib.as_array(vp, shape=(storage_len * vd,))
+        return k, v
+
+    def generate(self, prompt, n_gen, penalty=1.1, start_pos=0):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(n_gen, 1), np.uint32)
+        logits = np.zeros(self.vocab, np.float32)
+        n = lib.orc_model_generate(self.h, ptr(p), p.size, start_pos, n_gen, penalty, ptr(out), ptr(logits))
+        return out[:n], logits
+
+    def __del__(self):
+        try:
+            lib.orc_model_free(self.h)
+        except Exception:
+            pass

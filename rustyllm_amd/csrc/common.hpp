@@ -1,0 +1,115 @@
+// common.hpp — device helpers shared by the gfx950 kernels.
+//
+// Built with -ffp-contract=off: a*b+c stays two roundings unless a kernel
+// calls fmaf() explicitly, which it does only where the reference uses an FMA
+// intrinsic or where no reference rounding point is being reproduced.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RH_WAVE 64
+
+namespace rh {
+
+// ---- byte-stream loads (block fields are only 1/2/4-byte aligned) --------
+// memcpy keeps these well defined for any alignment; on gfx950 hipcc lowers a
+// 16-byte copy to a single global_load_dwordx4.
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint16_t ld2(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+// IEEE half -> float (exact; v_cvt_f32_f16).
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float ldh(const uint8_t *p) { return h2f(ld2(p)); }
+
+// v_dot4_i32_i8: c + sum_k a.byte[k] * b.byte[k] (signed bytes, exact).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---- DPP / swizzle reductions ---------------------------------------------
+// quad_perm controls: xor-1 = [1,0,3,2] = 0xB1, xor-2 = [2,3,0,1] = 0x4E.
+__device__ __forceinline__ int quad_sum_i32(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
+// ds_swizzle bit mode within 32 lanes: offset = and_mask | or<<5 | xor<<10.
+template <int XOR>
+__device__ __forceinline__ float swz_xor(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (XOR << 10)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Block-wide (256 threads = 4 waves) reductions through LDS; every thread
+// receives the same value, computed in the same order on every block.
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    v = wave_sum(v);
+    int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float r = (red[0] + red[1]) + (red[2] + red[3]);
+    return r;
+}
+__device__ __forceinline__ float block_max_256(float v, float *red) {
+    v = wave_max(v);
+    int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Q8_K activation buffers (device): int8 quants, per-256 f32 scale, per-32
+// and per-16 int16 group sums.  The per-16 sums serve the Q6_K kernel's
+// "-32" offset and are not part of the reference layout.
+struct XQ {
+    int8_t *qs;
+    float *d;
+    int16_t *bsums;
+    int16_t *sums16;
+};
+
+// Decode step state kept on the device so a captured graph can replay every
+// token without host updates.
+struct StepState {
+    int32_t pos;       // position being written / attended to (end_t)
+    int32_t start_t;   // first attended position
+    int32_t token;     // current input token (device-token mode)
+    int32_t n_recent;  // valid entries in recent[]
+    int32_t recent[64];
+};
+
+}  // namespace rh

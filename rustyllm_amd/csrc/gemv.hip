@@ -1,0 +1,652 @@
+// gemv.hip — fused dequant-dot matrix-vector kernels for gfx950 (wave64).
+//
+// Weights stay in raw GGUF block bytes (device copy of the tensor, rows padded
+// to a 16-byte stride).  Activations arrive already quantized to Q8_K (int8 per
+// element, f32 scale per 256, int16 sums per 32 and per 16) for Q4_K, Q6_K and
+// Q8_0 with K % 256 == 0, exactly as the reference's x86 path does
+// (prepare_xq_kquant, src/simd.rs:944-959); Q8_0 with other K and MXFP4 read
+// f32 activations (src/simd.rs:6671-6692, 5886-5902).
+//
+// Work split: a 256-thread workgroup owns a tile of 4*R consecutive rows, R per
+// wave.  Inside a wave, lane l handles "unit" l + 64*i of the row (i <
+// ITERS): a quarter of a 256-block for K-quants (64 weights), one whole
+// 32-block for Q8_0/MXFP4.  Integer partial sums are exact, so their lane
+// order is free; each block's f32 value is then formed with the reference's
+// own rounding sequence and the per-row sum runs serially in block order, so
+// Q4_K, Q6_K and Q8_0 (int) rows reproduce the reference row bit for bit.
+#include "common.hpp"
+
+namespace rh {
+
+enum Fmt : int { F_Q8_0 = 8, F_Q4_K = 12, F_Q6_K = 14, F_MXFP4 = 39 };
+
+// Epilogue of a matrix inside a launch.
+enum Epi : int {
+    EPI_STORE = 0,   // y[r] = v (+ bias)
+    EPI_ADD = 1,     // y[r] += v (+ bias): residual stream update
+    EPI_SWIGLU = 2,  // matrices 0 (gate) and 1 (up): y[r] = silu(g) * u
+};
+
+struct GemvMat {
+    const uint8_t *w;
+    int64_t row_stride;  // bytes between device rows (>= raw row bytes, 16-aligned)
+    int32_t rows;
+    int32_t fmt;
+    float *y;
+    const float *bias;
+    int32_t tile_begin;  // first tile index of this matrix in the launch
+    int32_t pad;
+};
+
+#define GEMV_MAX_MATS 4
+
+struct GemvArgs {
+    GemvMat m[GEMV_MAX_MATS];
+    int32_t n_mats;
+    int32_t n_tiles;
+    int32_t K;
+    int32_t epi;
+    XQ xq;            // Q8_K activation (int paths)
+    const float *x;   // f32 activation (f32 paths)
+};
+
+#define KMAX 16384
+#define NB256_MAX (KMAX / 256)
+#define NB32_MAX (KMAX / 32)
+
+// Cephes-style expf restated from the reference's silu_mul_avx2
+// (src/simd.rs:2406-2464, constants :2410-2421), step for step, so SiLU on the
+// GPU rounds exactly like the AVX2 path.
+__device__ __forceinline__ float exp_cephes(float x) {
+    x = fminf(88.37626f, fmaxf(-88.37626f, x));
+    float fx = fmaf(x, 1.44269504088896340736f, 0.5f);
+    fx = floorf(fx);
+    x = fmaf(-fx, 0.6933594f, x);
+    x = fmaf(-fx, -2.1219444e-4f, x);
+    float y = 1.9875691e-4f;
+    y = fmaf(y, x, 1.3982e-3f);
+    y = fmaf(y, x, 8.333452e-3f);
+    y = fmaf(y, x, 4.1665796e-2f);
+    y = fmaf(y, x, 1.6666665e-1f);
+    y = fmaf(y, x, 0.5f);
+    float x2 = x * x;
+    y = fmaf(y, x2, x) + 1.0f;
+    int n = (int)fx;
+    float p2 = __builtin_bit_cast(float, (n + 0x7f) << 23);
+    return y * p2;
+}
+
+__device__ __forceinline__ float silu_mul_ref(float g, float u) {
+    float e = exp_cephes(0.0f - g);
+    float s = g / (1.0f + e);
+    return s * u;
+}
+
+// get_scale_min_k4 (src/simd.rs:4537-4546) on the 12 scale bytes held in
+// three dwords (s03 = bytes 0..3, s47 = 4..7, s811 = 8..11).
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s03, uint32_t s47, uint32_t s811, int &sc, int &m) {
+    if (j < 4) {
+        sc = (s03 >> (8 * j)) & 63;
+        m = (s47 >> (8 * j)) & 63;
+    } else {
+        int k = j - 4;
+        uint32_t a = (s811 >> (8 * k)) & 0xFF;
+        sc = (a & 0xF) | (((s03 >> (8 * k + 6)) & 3) << 4);
+        m = (a >> 4) | (((s47 >> (8 * k + 6)) & 3) << 4);
+    }
+}
+
+// ---- K-quant units ----------------------------------------------------------
+// Q4_K unit q of block b: 32 qs bytes (offset 16+32q) = 64 weights; low
+// nibbles pair with xq[64q .. 64q+32), high nibbles with xq[64q+32 .. 64q+64).
+struct Q4KLoad {
+    uint4 hdr, a, b;
+};
+__device__ __forceinline__ Q4KLoad q4k_load(const uint8_t *blk, int q) {
+    Q4KLoad L;
+    L.hdr = *(const uint4 *)blk;  // 144-byte blocks of 16-aligned rows are 16-aligned
+    L.a = *(const uint4 *)(blk + 16 + 32 * q);
+    L.b = *(const uint4 *)(blk + 32 + 32 * q);
+    return L;
+}
+
+// Returns the exact partial (isum, imin) of this quarter.
+__device__ __forceinline__ void q4k_unit(const Q4KLoad &L, int q, const int32_t *xq32, const int16_t *bs, int &isum,
+                                         int &imin) {
+    int sc1, m1, sc2, m2;
+    scale_min_k4(2 * q, L.hdr.y, L.hdr.z, L.hdr.w, sc1, m1);
+    scale_min_k4(2 * q + 1, L.hdr.y, L.hdr.z, L.hdr.w, sc2, m2);
+    const uint32_t w[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
+    const int4 *xl = (const int4 *)(xq32 + 16 * q);
+    int4 x0 = xl[0], x1 = xl[1], x2 = xl[2], x3 = xl[3];
+    const int xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                        x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+    int slo = 0, shi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        slo = sdot4(w[k] & 0x0F0F0F0Fu, (uint32_t)xv[k], slo);
+        shi = sdot4((w[k] >> 4) & 0x0F0F0F0Fu, (uint32_t)xv[8 + k], shi);
+    }
+    isum = sc1 * slo + sc2 * shi;
+    imin = m1 * (int)bs[2 * q] + m2 * (int)bs[2 * q + 1];
+}
+
+// Q6_K unit q = (g = q>>1, j = q&1) of block b: positions l in [16j, 16j+16) of
+// half g, i.e. elements 128g + 32k + l for k = 0..3 (64 weights).
+struct Q6KLoad {
+    uint4 ql0, ql1, qh;
+    uint2 sc;
+    uint32_t d;
+};
+__device__ __forceinline__ Q6KLoad q6k_load(const uint8_t *blk, int q) {
+    int g = q >> 1, j = q & 1;
+    Q6KLoad L;
+    L.ql0 = ld16(blk + 64 * g + 16 * j);
+    L.ql1 = ld16(blk + 64 * g + 32 + 16 * j);
+    L.qh = ld16(blk + 128 + 32 * g + 16 * j);
+    L.sc = ld8(blk + 192 + 8 * g);
+    L.d = ld2(blk + 208);
+    return L;
+}
+
+__device__ __forceinline__ int q6k_unit(const Q6KLoad &L, int q, const int32_t *xqb32, const int16_t *s16b) {
+    int g = q >> 1, j = q & 1;
+    const uint32_t l0[4] = {L.ql0.x, L.ql0.y, L.ql0.z, L.ql0.w};
+    const uint32_t l1[4] = {L.ql1.x, L.ql1.y, L.ql1.z, L.ql1.w};
+    const uint32_t h[4] = {L.qh.x, L.qh.y, L.qh.z, L.qh.w};
+    int isum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int e0 = 128 * g + 32 * k + 16 * j;  // first element of this 16-run
+        const int4 *xp = (const int4 *)(xqb32 + e0 / 4);
+        int4 xv = xp[0];
+        const int xa[4] = {xv.x, xv.y, xv.z, xv.w};
+        int dot = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint32_t lo = (k & 1) ? l1[t] : l0[t];
+            uint32_t nib = (k & 2) ? ((lo >> 4) & 0x0F0F0F0Fu) : (lo & 0x0F0F0F0Fu);
+            uint32_t hb = ((h[t] >> (2 * k)) & 0x03030303u) << 4;
+            dot = sdot4(nib | hb, (uint32_t)xa[t], dot);
+        }
+        dot -= 32 * (int)s16b[e0 / 16];
+        int sidx = j + 2 * k;  // scale byte sc[8g + j + 2k]
+        uint32_t sw = sidx < 4 ? L.sc.x : L.sc.y;
+        int sc = (int)(int8_t)((sw >> (8 * (sidx & 3))) & 0xFF);
+        isum += sc * dot;
+    }
+    return isum;
+}
+
+template <int ITERS, int R>
+__global__ __launch_bounds__(256) void gemv_kquant_kernel(GemvArgs A) {
+    __shared__ int32_t s_xq[KMAX / 4];
+    __shared__ float s_dx[NB256_MAX];
+    __shared__ int16_t s_bs[NB32_MAX];
+    __shared__ int16_t s_s16[KMAX / 16];
+    __shared__ float s_v[4 * R][NB256_MAX];
+
+    const int K = A.K, nb = K >> 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        const int4 *src = (const int4 *)A.xq.qs;
+        int4 *dst = (int4 *)s_xq;
+        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
+        for (int i = tid; i < nb; i += 256) s_dx[i] = A.xq.d[i];
+        for (int i = tid; i < K / 32; i += 256) s_bs[i] = A.xq.bsums[i];
+        for (int i = tid; i < K / 16; i += 256) s_s16[i] = A.xq.sums16[i];
+    }
+    __syncthreads();
+
+    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
+        int mi = 0;
+#pragma unroll
+        for (int t = 1; t < GEMV_MAX_MATS; t++)
+            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+        const GemvMat M = A.m[mi];
+        int row0 = (tile - M.tile_begin) * (4 * R);
+        int wrow0 = row0 + wave * R;
+
+        if (M.fmt == F_Q4_K) {
+            Q4KLoad L[R][ITERS];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2;
+                    int row = wrow0 + r;
+                    if (b < nb && row < M.rows) L[r][i] = q4k_load(M.w + (int64_t)row * M.row_stride + b * 144, u & 3);
+                }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
+                    int row = wrow0 + r;
+                    bool ok = b < nb && row < M.rows;
+                    int isum = 0, imin = 0;
+                    if (ok) q4k_unit(L[r][i], q, s_xq + b * 64, s_bs + b * 8, isum, imin);
+                    isum = quad_sum_i32(isum);
+                    imin = quad_sum_i32(imin);
+                    if (ok && q == 0) {
+                        float d = h2f(L[r][i].hdr.x & 0xFFFF), dmin = h2f(L[r][i].hdr.x >> 16);
+                        float t1 = d * (float)isum;
+                        float t2 = dmin * (float)imin;
+                        s_v[wave * R + r][b] = s_dx[b] * (t1 - t2);
+                    }
+                }
+        } else {
+            Q6KLoad L[R][ITERS];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2;
+                    int row = wrow0 + r;
+                    if (b < nb && row < M.rows) L[r][i] = q6k_load(M.w + (int64_t)row * M.row_stride + b * 210, u & 3);
+                }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
+                    int row = wrow0 + r;
+                    bool ok = b < nb && row < M.rows;
+                    int isum = 0;
+                    if (ok) isum = q6k_unit(L[r][i], q, s_xq + b * 64, s_s16 + b * 16);
+                    isum = quad_sum_i32(isum);
+                    if (ok && q == 0) {
+                        float d = h2f(L[r][i].d & 0xFFFF);
+                        s_v[wave * R + r][b] = (s_dx[b] * d) * (float)isum;
+                    }
+                }
+        }
+        __syncthreads();
+        if (tid < 4 * R) {
+            int row = row0 + tid;
+            if (row < M.rows) {
+                float acc = 0.0f;
+                for (int b = 0; b < nb; b++) acc += s_v[tid][b];
+                if (M.bias) acc += M.bias[row];
+                if (A.epi == EPI_ADD)
+                    M.y[row] += acc;
+                else
+                    M.y[row] = acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Gate/up pair with the SwiGLU epilogue (EPI_SWIGLU): m[0] = gate, m[1] = up,
+// same row count.  A tile is 2R rows; waves 0-1 take them from the gate matrix
+// and waves 2-3 the same rows of up, so one thread can finish silu(g) * u.
+template <int ITERS, int R>
+__global__ __launch_bounds__(256) void gemv_kquant_swiglu_kernel(GemvArgs A) {
+    __shared__ int32_t s_xq[KMAX / 4];
+    __shared__ float s_dx[NB256_MAX];
+    __shared__ int16_t s_bs[NB32_MAX];
+    __shared__ int16_t s_s16[KMAX / 16];
+    __shared__ float s_v[4 * R][NB256_MAX];
+
+    const int K = A.K, nb = K >> 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        const int4 *src = (const int4 *)A.xq.qs;
+        int4 *dst = (int4 *)s_xq;
+        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
+        for (int i = tid; i < nb; i += 256) s_dx[i] = A.xq.d[i];
+        for (int i = tid; i < K / 32; i += 256) s_bs[i] = A.xq.bsums[i];
+        for (int i = tid; i < K / 16; i += 256) s_s16[i] = A.xq.sums16[i];
+    }
+    __syncthreads();
+
+    const int half = wave >> 1;  // 0 = gate, 1 = up
+    const GemvMat M = A.m[half];
+    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
+        int row0 = tile * (2 * R);
+        int wrow0 = row0 + (wave & 1) * R;
+        if (M.fmt == F_Q4_K) {
+            Q4KLoad L[R][ITERS];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2;
+                    int row = wrow0 + r;
+                    if (b < nb && row < M.rows) L[r][i] = q4k_load(M.w + (int64_t)row * M.row_stride + b * 144, u & 3);
+                }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
+                    int row = wrow0 + r;
+                    bool ok = b < nb && row < M.rows;
+                    int isum = 0, imin = 0;
+                    if (ok) q4k_unit(L[r][i], q, s_xq + b * 64, s_bs + b * 8, isum, imin);
+                    isum = quad_sum_i32(isum);
+                    imin = quad_sum_i32(imin);
+                    if (ok && q == 0) {
+                        float d = h2f(L[r][i].hdr.x & 0xFFFF), dmin = h2f(L[r][i].hdr.x >> 16);
+                        float t1 = d * (float)isum;
+                        float t2 = dmin * (float)imin;
+                        s_v[wave * R + r][b] = s_dx[b] * (t1 - t2);
+                    }
+                }
+        } else {
+            Q6KLoad L[R][ITERS];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2;
+                    int row = wrow0 + r;
+                    if (b < nb && row < M.rows) L[r][i] = q6k_load(M.w + (int64_t)row * M.row_stride + b * 210, u & 3);
+                }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
+                    int row = wrow0 + r;
+                    bool ok = b < nb && row < M.rows;
+                    int isum = 0;
+                    if (ok) isum = q6k_unit(L[r][i], q, s_xq + b * 64, s_s16 + b * 16);
+                    isum = quad_sum_i32(isum);
+                    if (ok && q == 0) {
+                        float d = h2f(L[r][i].d & 0xFFFF);
+                        s_v[wave * R + r][b] = (s_dx[b] * d) * (float)isum;
+                    }
+                }
+        }
+        __syncthreads();
+        if (tid < 2 * R) {
+            int row = row0 + tid;
+            if (row < A.m[0].rows) {
+                float g = 0.0f, u = 0.0f;
+                for (int b = 0; b < nb; b++) g += s_v[tid][b];
+                for (int b = 0; b < nb; b++) u += s_v[2 * R + tid][b];
+                A.m[0].y[row] = silu_mul_ref(g, u);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---- 32-element-block formats: Q8_0 (int / f32) and MXFP4 --------------------
+#define B32_VMAX 8192  // floats of per-row staging in LDS
+
+__constant__ float kMxfp4Lut[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                    -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+__device__ __forceinline__ float mxfp4_scale(uint32_t e) {
+    // 2^(e-127) as an exact power of two (e = 0 is the subnormal 2^-127).
+    if (e == 0) return __builtin_bit_cast(float, 0x00400000u);
+    return __builtin_bit_cast(float, e << 23);
+}
+
+// Q8_0, K % 256 == 0: reproduces dot_q8_0_q8k_avx2 (src/simd.rs:7184-7210):
+// eight lane accumulators acc_j = fma(dx*d_b, s_{b,j}, acc_j) over blocks in
+// order, s_{b,j} = exact int dot of bytes 4j..4j+3, then the hsum_avx tree.
+template <int ITERS, int R>
+__global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
+    __shared__ int32_t s_xq[KMAX / 4];
+    __shared__ float s_dx[NB256_MAX];
+    extern __shared__ float s_part[];  // [4R][nb32][9]: scale, s_0..s_7
+    const int K = A.K, nb = K >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        const int4 *src = (const int4 *)A.xq.qs;
+        int4 *dst = (int4 *)s_xq;
+        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
+        for (int i = tid; i < (K >> 8); i += 256) s_dx[i] = A.xq.d[i];
+    }
+    __syncthreads();
+    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
+        int mi = 0;
+#pragma unroll
+        for (int t = 1; t < GEMV_MAX_MATS; t++)
+            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+        const GemvMat M = A.m[mi];
+        int row0 = (tile - M.tile_begin) * (4 * R);
+        uint4 wa[R][ITERS], wb[R][ITERS];
+        uint32_t dd[R][ITERS];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < ITERS; i++) {
+                int b = lane + 64 * i, row = row0 + wave * R + r;
+                if (b < nb && row < M.rows) {
+                    const uint8_t *blk = M.w + (int64_t)row * M.row_stride + b * 34;
+                    dd[r][i] = ld2(blk);
+                    wa[r][i] = ld16(blk + 2);
+                    wb[r][i] = ld16(blk + 18);
+                }
+            }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < ITERS; i++) {
+                int b = lane + 64 * i, row = row0 + wave * R + r;
+                if (b < nb && row < M.rows) {
+                    const int4 *xp = (const int4 *)(s_xq + b * 8);
+                    int4 x0 = xp[0], x1 = xp[1];
+                    float *dst = s_part + ((size_t)(wave * R + r) * nb + b) * 9;
+                    dst[0] = s_dx[b >> 3] * h2f(dd[r][i]);
+                    dst[1] = (float)sdot4(wa[r][i].x, x0.x, 0);
+                    dst[2] = (float)sdot4(wa[r][i].y, x0.y, 0);
+                    dst[3] = (float)sdot4(wa[r][i].z, x0.z, 0);
+                    dst[4] = (float)sdot4(wa[r][i].w, x0.w, 0);
+                    dst[5] = (float)sdot4(wb[r][i].x, x1.x, 0);
+                    dst[6] = (float)sdot4(wb[r][i].y, x1.y, 0);
+                    dst[7] = (float)sdot4(wb[r][i].z, x1.z, 0);
+                    dst[8] = (float)sdot4(wb[r][i].w, x1.w, 0);
+                }
+            }
+        __syncthreads();
+        // 8 threads per row run the lane chains; 4R rows need 32R threads.
+        {
+            int rr = tid >> 3, j = tid & 7;
+            float acc = 0.0f;
+            int row = row0 + rr;
+            if (rr < 4 * R && row < M.rows) {
+                const float *p = s_part + (size_t)rr * nb * 9;
+                for (int b = 0; b < nb; b++) acc = fmaf(p[b * 9], p[b * 9 + 1 + j], acc);
+            }
+            // hsum_avx: t_i = a_i + a_{i+4}; ((t0+t1) + (t2+t3))
+            float t = acc + __shfl_xor(acc, 4, 64);
+            float u = t + __shfl_xor(t, 1, 64);
+            float v = u + __shfl_xor(u, 2, 64);
+            if (rr < 4 * R && j == 0 && row < M.rows) {
+                if (M.bias) v += M.bias[row];
+                if (A.epi == EPI_ADD)
+                    M.y[row] += v;
+                else
+                    M.y[row] = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// f32-activation paths: Q8_0 with K % 256 != 0 and MXFP4.  Each lane forms
+// one block's f32 partial; the row sum then runs serially in block order.
+// The reference sums these formats in one serial chain per row
+// (src/simd.rs:6671-6692, 5886-5902), so this path is compared with a
+// tolerance, not bit for bit.
+template <int ITERS, int R>
+__global__ __launch_bounds__(256) void gemv_b32_f32_kernel(GemvArgs A) {
+    extern __shared__ float s_dyn[];
+    float *s_x = s_dyn;            // [K]
+    float *s_v = s_dyn + A.K;      // [4R][nb]
+    const int K = A.K, nb = K >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < K; i += 256) s_x[i] = A.x[i];
+    __syncthreads();
+    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
+        int mi = 0;
+#pragma unroll
+        for (int t = 1; t < GEMV_MAX_MATS; t++)
+            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+        const GemvMat M = A.m[mi];
+        int row0 = (tile - M.tile_begin) * (4 * R);
+        uint4 wa[R][ITERS], wb[R][ITERS];
+        uint32_t dd[R][ITERS];
+        const int bsz = M.fmt == F_Q8_0 ? 34 : 17;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < ITERS; i++) {
+                int b = lane + 64 * i, row = row0 + wave * R + r;
+                if (b < nb && row < M.rows) {
+                    const uint8_t *blk = M.w + (int64_t)row * M.row_stride + b * bsz;
+                    if (M.fmt == F_Q8_0) {
+                        dd[r][i] = ld2(blk);
+                        wa[r][i] = ld16(blk + 2);
+                        wb[r][i] = ld16(blk + 18);
+                    } else {
+                        wa[r][i] = ld16(blk);
+                        dd[r][i] = blk[16];
+                    }
+                }
+            }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < ITERS; i++) {
+                int b = lane + 64 * i, row = row0 + wave * R + r;
+                if (b < nb && row < M.rows) {
+                    const float *xb = s_x + b * 32;
+                    float acc = 0.0f;
+                    if (M.fmt == F_Q8_0) {
+                        float d = h2f(dd[r][i]);
+                        const uint32_t w[8] = {wa[r][i].x, wa[r][i].y, wa[r][i].z, wa[r][i].w,
+                                               wb[r][i].x, wb[r][i].y, wb[r][i].z, wb[r][i].w};
+#pragma unroll
+                        for (int k = 0; k < 8; k++)
+#pragma unroll
+                            for (int t = 0; t < 4; t++) {
+                                float q = (float)(int8_t)((w[k] >> (8 * t)) & 0xFF);
+                                acc = fmaf(d * q, xb[4 * k + t], acc);
+                            }
+                    } else {
+                        float s = mxfp4_scale(dd[r][i]);
+                        const uint32_t w[4] = {wa[r][i].x, wa[r][i].y, wa[r][i].z, wa[r][i].w};
+#pragma unroll
+                        for (int k = 0; k < 4; k++)
+#pragma unroll
+                            for (int t = 0; t < 4; t++) {
+                                uint32_t byte = (w[k] >> (8 * t)) & 0xFF;
+                                float lo = kMxfp4Lut[byte & 0xF] * s;
+                                float hi = kMxfp4Lut[byte >> 4] * s;
+                                acc = acc + lo * xb[8 * k + 2 * t];
+                                acc = acc + hi * xb[8 * k + 2 * t + 1];
+                            }
+                    }
+                    s_v[(wave * R + r) * nb + b] = acc;
+                }
+            }
+        __syncthreads();
+        if (tid < 4 * R) {
+            int row = row0 + tid;
+            if (row < M.rows) {
+                float acc = 0.0f;
+                for (int b = 0; b < nb; b++) acc += s_v[tid * nb + b];
+                if (M.bias) acc += M.bias[row];
+                if (A.epi == EPI_ADD)
+                    M.y[row] += acc;
+                else
+                    M.y[row] = acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---- debug kernels: per-block integer parts (bit-exactness checks) -----------
+// Q4_K: out[row*nb*2 + 2b] = isum, +1 = imin.  Q6_K: out[row*nb + b] = isum.
+// Q8_0: out[row*nb32 + b] = s (int dot of the 32-block).
+__global__ void block_ints_kernel(const uint8_t *w, int64_t row_stride, int rows, int K, int fmt, XQ xq, int *out) {
+    int row = blockIdx.x;
+    if (row >= rows) return;
+    const uint8_t *wr = w + (int64_t)row * row_stride;
+    if (fmt == F_Q8_0) {
+        int nb = K >> 5;
+        for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+            const uint8_t *blk = wr + b * 34;
+            uint4 a = ld16(blk + 2), c = ld16(blk + 18);
+            const int32_t *x = (const int32_t *)(xq.qs + b * 32);
+            int s = 0;
+            s = sdot4(a.x, x[0], s); s = sdot4(a.y, x[1], s); s = sdot4(a.z, x[2], s); s = sdot4(a.w, x[3], s);
+            s = sdot4(c.x, x[4], s); s = sdot4(c.y, x[5], s); s = sdot4(c.z, x[6], s); s = sdot4(c.w, x[7], s);
+            out[(int64_t)row * nb + b] = s;
+        }
+        return;
+    }
+    int nb = K >> 8;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        const int32_t *xq32 = (const int32_t *)(xq.qs + b * 256);
+        if (fmt == F_Q4_K) {
+            int isum = 0, imin = 0;
+            for (int q = 0; q < 4; q++) {
+                Q4KLoad L = q4k_load(wr + b * 144, q);
+                int a, m;
+                q4k_unit(L, q, xq32, xq.bsums + b * 8, a, m);
+                isum += a;
+                imin += m;
+            }
+            out[((int64_t)row * nb + b) * 2] = isum;
+            out[((int64_t)row * nb + b) * 2 + 1] = imin;
+        } else {
+            int isum = 0;
+            for (int q = 0; q < 4; q++) {
+                Q6KLoad L = q6k_load(wr + b * 210, q);
+                isum += q6k_unit(L, q, xq32, xq.sums16 + b * 16);
+            }
+            out[(int64_t)row * nb + b] = isum;
+        }
+    }
+}
+
+// ---- dequantization (bit-exact with src/simd.rs:4044-4294) --------------------
+__global__ void dequant_rows_kernel(const uint8_t *w, int64_t row_stride, int rows, int K, int fmt, float *out) {
+    int row = blockIdx.y;
+    if (row >= rows) return;
+    const uint8_t *wr = w + (int64_t)row * row_stride;
+    float *o = out + (int64_t)row * K;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < K; e += gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (fmt == F_Q8_0) {
+            const uint8_t *blk = wr + (e >> 5) * 34;
+            v = ldh(blk) * (float)(int8_t)blk[2 + (e & 31)];
+        } else if (fmt == F_Q4_K) {
+            const uint8_t *blk = wr + (e >> 8) * 144;
+            int p = e & 255, j = p >> 6, hi = (p >> 5) & 1, l = p & 31;
+            uint32_t s03 = ld4(blk + 4), s47 = ld4(blk + 8), s811 = ld4(blk + 12);
+            int sc, m;
+            scale_min_k4(2 * j + hi, s03, s47, s811, sc, m);
+            float d1 = ldh(blk) * (float)sc, m1 = ldh(blk + 2) * (float)m;
+            uint8_t byte = blk[16 + 32 * j + l];
+            int qv = hi ? (byte >> 4) : (byte & 0xF);
+            v = d1 * (float)qv - m1;
+        } else if (fmt == F_Q6_K) {
+            const uint8_t *blk = wr + (e >> 8) * 210;
+            int p = e & 255, n = p >> 7, pp = p & 127, k = pp >> 5, l = pp & 31;
+            const uint8_t *ql = blk + 64 * n, *qh = blk + 128 + 32 * n;
+            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * n);
+            uint8_t lo = (k & 1) ? ql[l + 32] : ql[l];
+            int nib = (k & 2) ? (lo >> 4) : (lo & 0xF);
+            int q = (nib | (((qh[l] >> (2 * k)) & 3) << 4)) - 32;
+            v = ldh(blk + 208) * (float)sc[l / 16 + 2 * k] * (float)q;
+        } else if (fmt == F_MXFP4) {
+            const uint8_t *blk = wr + (e >> 5) * 17;
+            int p = e & 31;
+            uint8_t byte = blk[p >> 1];
+            v = kMxfp4Lut[(p & 1) ? (byte >> 4) : (byte & 0xF)] * mxfp4_scale(blk[16]);
+        }
+        o[e] = v;
+    }
+}
+
+}  // namespace rh

@@ -1,0 +1,1474 @@
+// rusty_hip.hip — host side of librusty_hip.so: device context, weight cache,
+// kernel launch helpers, the C ABI declared in include/rusty_hip.h and the
+// resident (whole-token-on-device) decoder.
+//
+// One translation unit: the kernel sources are included so launches see the
+// templates directly.
+#include "gemv.hip"
+#include "attention.hip"
+#include "ops.hip"
+
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/rusty_hip.h"
+
+namespace rh {
+
+// ---- errors -------------------------------------------------------------------
+static bool debug_on() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RUSTY_HIP_DEBUG");
+        v = (e && *e && strcmp(e, "0") != 0) ? 1 : 0;
+    }
+    return v == 1;
+}
+#define RH_CHECK(expr)                                                                          \
+    do {                                                                                        \
+        hipError_t _e = (expr);                                                                 \
+        if (_e != hipSuccess) {                                                                 \
+            if (debug_on()) fprintf(stderr, "[rusty_hip] %s failed: %s (%s:%d)\n", #expr,       \
+                                    hipGetErrorString(_e), __FILE__, __LINE__);                 \
+            return 0;                                                                           \
+        }                                                                                       \
+    } while (0)
+#define RH_LAUNCH_OK()                                                                          \
+    do {                                                                                        \
+        hipError_t _e = hipGetLastError();                                                      \
+        if (_e != hipSuccess) {                                                                 \
+            if (debug_on()) fprintf(stderr, "[rusty_hip] launch failed: %s (%s:%d)\n",          \
+                                    hipGetErrorString(_e), __FILE__, __LINE__);                 \
+            return 0;                                                                           \
+        }                                                                                       \
+    } while (0)
+
+// ---- context --------------------------------------------------------------------
+struct DevW {
+    const uint8_t *p = nullptr;
+    int64_t stride = 0;
+    int32_t rows = 0, cols = 0, fmt = 0;
+    uint64_t fp = 0;  // sampled fingerprint of the host bytes it was copied from
+};
+
+struct KeyHash {
+    size_t operator()(const std::pair<const void *, size_t> &k) const {
+        return std::hash<const void *>()(k.first) ^ (std::hash<size_t>()(k.second) * 0x9E3779B97F4A7C15ull);
+    }
+};
+
+struct Profile {
+    std::map<std::string, int> index;
+    std::vector<std::string> names;
+    std::vector<double> total_ms;
+    std::vector<int64_t> count;
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
+    std::vector<hipEvent_t> pool;
+    bool on = false;
+};
+
+struct Ctx {
+    int state = 0;  // 0 = untried, 1 = ok, -1 = failed
+    int dev = 0;
+    int n_cu = 256;
+    hipStream_t s = nullptr;
+    std::mutex mu;
+    std::unordered_map<std::pair<const void *, size_t>, DevW, KeyHash> wcache;
+    // per-op staging
+    float *x = nullptr, *y = nullptr, *y2 = nullptr, *y3 = nullptr, *hid = nullptr, *hid2 = nullptr;
+    size_t x_cap = 0, y_cap = 0, hid_cap = 0;
+    XQ xq{};
+    size_t xq_cap = 0;
+    XQ xq2{};
+    size_t xq2_cap = 0;
+    float *part = nullptr;
+    size_t part_cap = 0;
+    float *kv_k = nullptr, *kv_v = nullptr;
+    size_t kv_cap = 0;
+    int32_t *ibuf = nullptr;
+    size_t ibuf_cap = 0;
+    Profile prof;
+};
+static Ctx g;
+
+static int64_t row_bytes_of(int fmt, int64_t cols) {
+    switch (fmt) {
+    case 0: return cols * 4;
+    case 8: return (cols / 32) * 34;
+    case 12: return (cols / 256) * 144;
+    case 14: return (cols / 256) * 210;
+    case 39: return (cols / 32) * 17;
+    default: return -1;
+    }
+}
+static int block_elems(int fmt) { return (fmt == 12 || fmt == 14) ? 256 : (fmt == 0 ? 1 : 32); }
+
+static int init_locked() {
+    if (g.state != 0) return g.state == 1;
+    g.state = -1;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    RH_CHECK(hipSetDevice(0));
+    hipDeviceProp_t prop;
+    RH_CHECK(hipGetDeviceProperties(&prop, 0));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (debug_on()) fprintf(stderr, "[rusty_hip] device is %s, built for gfx950\n", prop.gcnArchName);
+        return 0;
+    }
+    g.n_cu = prop.multiProcessorCount;
+    RH_CHECK(hipStreamCreateWithFlags(&g.s, hipStreamNonBlocking));
+    g.state = 1;
+    return 1;
+}
+
+template <class T>
+static int ensure(T **p, size_t *cap, size_t n) {
+    if (*cap >= n && *p) return 1;
+    if (*p) RH_CHECK(hipFree(*p));
+    *p = nullptr;
+    size_t want = n < 256 ? 256 : n;
+    RH_CHECK(hipMalloc((void **)p, want * sizeof(T)));
+    *cap = want;
+    return 1;
+}
+
+static int alloc_xq(XQ *xq, size_t n) {
+    size_t nb = (n + 255) / 256;
+    RH_CHECK(hipMalloc((void **)&xq->qs, nb * 256));
+    RH_CHECK(hipMalloc((void **)&xq->d, nb * sizeof(float)));
+    RH_CHECK(hipMalloc((void **)&xq->bsums, nb * 8 * sizeof(int16_t)));
+    RH_CHECK(hipMalloc((void **)&xq->sums16, nb * 16 * sizeof(int16_t)));
+    return 1;
+}
+static void free_xq(XQ *xq) {
+    if (xq->qs) (void)hipFree(xq->qs);
+    if (xq->d) (void)hipFree(xq->d);
+    if (xq->bsums) (void)hipFree(xq->bsums);
+    if (xq->sums16) (void)hipFree(xq->sums16);
+    *xq = XQ{};
+}
+static int ensure_xq(XQ *xq, size_t *cap, size_t n) {
+    if (*cap >= n && xq->qs) return 1;
+    free_xq(xq);
+    if (!alloc_xq(xq, n)) return 0;
+    *cap = (n + 255) / 256 * 256;
+    return 1;
+}
+
+// FNV-1a over 256 16-byte samples spread across the buffer (plus both
+// ends): cheap next to an upload, and it catches a host address that was
+// freed and reused for different bytes.
+static uint64_t fingerprint(const uint8_t *p, size_t len) {
+    uint64_t h = 1469598103934665603ull ^ len;
+    auto mix = [&](size_t off) {
+        size_t n = std::min<size_t>(16, len - off);
+        for (size_t i = 0; i < n; i++) h = (h ^ p[off + i]) * 1099511628211ull;
+    };
+    if (len == 0) return h;
+    for (int k = 0; k < 256; k++) mix((size_t)((unsigned __int128)len * k / 256));
+    mix(len > 16 ? len - 16 : 0);
+    return h;
+}
+
+// Device copy of a host weight, cached by (pointer, length) and checked
+// against a sampled fingerprint of the bytes.  Rows are padded to a 16-byte
+// stride; block bytes are copied unchanged.
+static int get_weight(const uint8_t *host, size_t len, int64_t rows, int64_t cols, int fmt, DevW *out) {
+    if (!host || rows <= 0 || cols <= 0) return 0;
+    int64_t rb = row_bytes_of(fmt, cols);
+    if (rb <= 0 || cols % block_elems(fmt) != 0) return 0;
+    if ((int64_t)len < rows * rb) return 0;
+    auto key = std::make_pair((const void *)host, len);
+    auto it = g.wcache.find(key);
+    uint64_t fp = fingerprint(host, len);
+    if (it != g.wcache.end()) {
+        if (it->second.rows == rows && it->second.cols == cols && it->second.fmt == fmt && it->second.fp == fp) {
+            *out = it->second;
+            return 1;
+        }
+        (void)hipStreamSynchronize(g.s);
+        (void)hipFree((void *)it->second.p);
+        g.wcache.erase(it);
+    }
+    int64_t stride = (rb + 15) / 16 * 16;
+    uint8_t *d = nullptr;
+    RH_CHECK(hipMalloc((void **)&d, (size_t)(rows * stride)));
+    if (stride == rb) {
+        RH_CHECK(hipMemcpy(d, host, (size_t)(rows * rb), hipMemcpyHostToDevice));
+    } else {
+        RH_CHECK(hipMemcpy2D(d, (size_t)stride, host, (size_t)rb, (size_t)rb, (size_t)rows, hipMemcpyHostToDevice));
+    }
+    DevW w;
+    w.p = d;
+    w.stride = stride;
+    w.rows = (int32_t)rows;
+    w.cols = (int32_t)cols;
+    w.fmt = fmt;
+    w.fp = fp;
+    g.wcache[key] = w;
+    *out = w;
+    return 1;
+}
+
+// Frees every cached device copy.  Needed when host weight memory is freed and
+// its addresses may be reused for different bytes (the reference never frees
+// its mmap'd weights, so its cache has no such call).
+static void wcache_clear() {
+    (void)hipStreamSynchronize(g.s);
+    for (auto &kv : g.wcache) (void)hipFree((void *)kv.second.p);
+    g.wcache.clear();
+}
+
+// ---- profiling -------------------------------------------------------------------
+struct ProfScope {
+    int idx = -1;
+    hipEvent_t a = nullptr, b = nullptr;
+    ProfScope(const char *name, hipStream_t s) {
+        if (!g.prof.on) return;
+        auto it = g.prof.index.find(name);
+        if (it == g.prof.index.end()) {
+            idx = (int)g.prof.names.size();
+            g.prof.index[name] = idx;
+            g.prof.names.push_back(name);
+            g.prof.total_ms.push_back(0.0);
+            g.prof.count.push_back(0);
+        } else {
+            idx = it->second;
+        }
+        a = take();
+        b = take();
+        if (a && b) (void)hipEventRecord(a, s);
+        stream = s;
+    }
+    ~ProfScope() {
+        if (idx < 0 || !a || !b) return;
+        (void)hipEventRecord(b, stream);
+        g.prof.pending.push_back({idx, {a, b}});
+    }
+    static hipEvent_t take() {
+        if (!g.prof.pool.empty()) {
+            hipEvent_t e = g.prof.pool.back();
+            g.prof.pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+    hipStream_t stream = nullptr;
+};
+
+static void prof_drain() {
+    if (g.prof.pending.empty()) return;
+    (void)hipStreamSynchronize(g.s);
+    for (auto &p : g.prof.pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.second.first, p.second.second) == hipSuccess) {
+            g.prof.total_ms[p.first] += ms;
+            g.prof.count[p.first] += 1;
+        }
+        g.prof.pool.push_back(p.second.first);
+        g.prof.pool.push_back(p.second.second);
+    }
+    g.prof.pending.clear();
+}
+
+// ---- launch helpers -------------------------------------------------------------
+struct MatSpec {
+    DevW w;
+    float *y;
+    const float *bias;
+};
+
+enum Cat { CAT_KQ = 1, CAT_Q8I = 2, CAT_F32 = 3 };
+static int cat_of(int fmt, int K) {
+    if (fmt == 12 || fmt == 14) return K % 256 == 0 && K <= KMAX ? CAT_KQ : 0;
+    if (fmt == 8) {
+        if (K % 256 == 0 && K <= 8192) return CAT_Q8I;
+        return K % 32 == 0 && K <= 12288 ? CAT_F32 : 0;
+    }
+    if (fmt == 39) return K % 32 == 0 && K <= 12288 ? CAT_F32 : 0;
+    return 0;
+}
+
+static int grid_cap() { return g.n_cu * 8; }
+
+template <int IT, int R>
+static int launch_kq(const GemvArgs &A, hipStream_t s) {
+    int grid = std::min(A.n_tiles, grid_cap());
+    ProfScope ps("gemv_kquant", s);
+    hipLaunchKernelGGL((gemv_kquant_kernel<IT, R>), dim3(grid), dim3(256), 0, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+template <int IT, int R>
+static int launch_kq_swiglu(const GemvArgs &A, hipStream_t s) {
+    int grid = std::min(A.n_tiles, grid_cap());
+    ProfScope ps("gemv_kquant_swiglu", s);
+    hipLaunchKernelGGL((gemv_kquant_swiglu_kernel<IT, R>), dim3(grid), dim3(256), 0, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+template <int IT, int R>
+static int launch_q8i(const GemvArgs &A, hipStream_t s) {
+    int grid = std::min(A.n_tiles, grid_cap());
+    size_t lds = (size_t)4 * R * (A.K / 32) * 9 * sizeof(float);
+    ProfScope ps("gemv_q8_0_int", s);
+    hipLaunchKernelGGL((gemv_q8_0_int_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+template <int IT, int R>
+static int launch_f32(const GemvArgs &A, hipStream_t s) {
+    int grid = std::min(A.n_tiles, grid_cap());
+    size_t lds = ((size_t)A.K + (size_t)4 * R * (A.K / 32)) * sizeof(float);
+    ProfScope ps("gemv_b32_f32", s);
+    hipLaunchKernelGGL((gemv_b32_f32_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// rows per tile for each (category, ITERS)
+static void pick_iters(int cat, int K, int *it, int *r) {
+    int units = (cat == CAT_KQ) ? (K / 256) * 4 : K / 32;
+    int iters = (units + 63) / 64;
+    if (cat == CAT_KQ) {
+        if (iters <= 1) { *it = 1; *r = 4; }
+        else if (iters == 2) { *it = 2; *r = 2; }
+        else if (iters == 3) { *it = 3; *r = 1; }
+        else { *it = 4; *r = 1; }
+    } else {
+        if (iters <= 1) { *it = 1; *r = 4; }
+        else if (iters == 2) { *it = 2; *r = 2; }
+        else if (iters <= 3) { *it = 3; *r = 1; }
+        else if (iters <= 4) { *it = 4; *r = 1; }
+        else if (iters <= 6) { *it = 6; *r = 1; }
+        else { *it = 8; *r = 1; }
+    }
+}
+
+// Launches y_i = W_i x for matrices of one category.
+static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, const float *xf, hipStream_t s) {
+    if (n <= 0 || n > GEMV_MAX_MATS) return 0;
+    int cat = cat_of(ms[0].w.fmt, K);
+    if (!cat) return 0;
+    for (int i = 1; i < n; i++)
+        if (cat_of(ms[i].w.fmt, K) != cat) return 0;
+    int it, r;
+    pick_iters(cat, K, &it, &r);
+    if (cat == CAT_KQ && it > 4) return 0;
+    GemvArgs A;
+    memset(&A, 0, sizeof(A));
+    A.K = K;
+    A.epi = epi;
+    A.xq = xq;
+    A.x = xf;
+    A.n_mats = n;
+    int tiles = 0;
+    int rows_per_tile = (epi == EPI_SWIGLU) ? 2 * r : 4 * r;
+    for (int i = 0; i < n; i++) {
+        GemvMat &m = A.m[i];
+        m.w = ms[i].w.p;
+        m.row_stride = ms[i].w.stride;
+        m.rows = ms[i].w.rows;
+        m.fmt = ms[i].w.fmt;
+        m.y = ms[i].y;
+        m.bias = ms[i].bias;
+        m.tile_begin = (epi == EPI_SWIGLU) ? 0 : tiles;
+        if (epi != EPI_SWIGLU) tiles += (m.rows + rows_per_tile - 1) / rows_per_tile;
+    }
+    if (epi == EPI_SWIGLU) {
+        if (n != 2 || cat != CAT_KQ || A.m[0].rows != A.m[1].rows) return 0;
+        tiles = (A.m[0].rows + rows_per_tile - 1) / rows_per_tile;
+    }
+    A.n_tiles = tiles;
+    if (cat == CAT_KQ) {
+        if (epi == EPI_SWIGLU) {
+            switch (it) {
+            case 1: return launch_kq_swiglu<1, 4>(A, s);
+            case 2: return launch_kq_swiglu<2, 2>(A, s);
+            case 3: return launch_kq_swiglu<3, 1>(A, s);
+            default: return launch_kq_swiglu<4, 1>(A, s);
+            }
+        }
+        switch (it) {
+        case 1: return launch_kq<1, 4>(A, s);
+        case 2: return launch_kq<2, 2>(A, s);
+        case 3: return launch_kq<3, 1>(A, s);
+        default: return launch_kq<4, 1>(A, s);
+        }
+    }
+    if (cat == CAT_Q8I) {
+        switch (it) {
+        case 1: return launch_q8i<1, 4>(A, s);
+        case 2: return launch_q8i<2, 2>(A, s);
+        case 3: return launch_q8i<3, 1>(A, s);
+        case 4: return launch_q8i<4, 1>(A, s);
+        default: return 0;
+        }
+    }
+    switch (it) {
+    case 1: return launch_f32<1, 4>(A, s);
+    case 2: return launch_f32<2, 2>(A, s);
+    case 3: return launch_f32<3, 1>(A, s);
+    case 4: return launch_f32<4, 1>(A, s);
+    case 6: return launch_f32<6, 1>(A, s);
+    default: return launch_f32<8, 1>(A, s);
+    }
+}
+
+// Splits a list of matrices into category groups and launches each.
+static int gemv_multi(const MatSpec *ms, int n, int K, int epi, const XQ &xq, const float *xf, hipStream_t s) {
+    int done[GEMV_MAX_MATS] = {0};
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        int cat = cat_of(ms[i].w.fmt, K);
+        if (!cat) return 0;
+        MatSpec grp[GEMV_MAX_MATS];
+        int ng = 0;
+        for (int j = i; j < n; j++)
+            if (!done[j] && cat_of(ms[j].w.fmt, K) == cat) {
+                grp[ng++] = ms[j];
+                done[j] = 1;
+            }
+        if (!gemv_cat(grp, ng, K, epi, xq, xf, s)) return 0;
+    }
+    return 1;
+}
+
+static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s) {
+    if (n % 256 != 0) return 0;
+    ProfScope ps("quantize_q8k", s);
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(n / 256), dim3(256), 0, s, x, n, xq);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+static int launch_rmsnorm(const float *x, const float *w, float eps, int n, float *xn, const XQ *xq, hipStream_t s) {
+    XQ q = xq ? *xq : XQ{};
+    if (xq && n % 256 != 0) q = XQ{};
+    ProfScope ps("rmsnorm_q8k", s);
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, w, eps, n, xn, q);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+__global__ void silu_mul_kernel(const float *g_, const float *u, int n, float *out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = silu_mul_ref(g_[i], u[i]);
+}
+static int launch_silu(const float *g_, const float *u, int n, float *out, hipStream_t s) {
+    ProfScope ps("silu_mul", s);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g_, u, n, out);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// d = W_gate, W_up -> hidden = silu(gate x) * (up x); K-quant pairs use the
+// fused epilogue, other formats two GEMVs plus the SiLU kernel.
+static int gemv_swiglu(const DevW &gate, const DevW &up, int K, const XQ &xq, const float *xf, float *hidden,
+                       float *tmp_g, float *tmp_u, hipStream_t s) {
+    if (cat_of(gate.fmt, K) == CAT_KQ && cat_of(up.fmt, K) == CAT_KQ && gate.rows == up.rows) {
+        MatSpec ms[2] = {{gate, hidden, nullptr}, {up, hidden, nullptr}};
+        return gemv_cat(ms, 2, K, EPI_SWIGLU, xq, xf, s);
+    }
+    MatSpec ms[2] = {{gate, tmp_g, nullptr}, {up, tmp_u, nullptr}};
+    if (!gemv_multi(ms, 2, K, EPI_STORE, xq, xf, s)) return 0;
+    return launch_silu(tmp_g, tmp_u, gate.rows, hidden, s);
+}
+
+static int attn_launch(const AttnArgs &A, hipStream_t s) {
+    dim3 grid(A.n_chunks, A.n_kv);
+    {
+        ProfScope ps("attn_partial", s);
+#define RH_ATT(HD, KM)                                                                            \
+    if (A.hd == HD && A.vd == HD && A.kv_mul == KM) {                                            \
+        hipLaunchKernelGGL((attn_partial_kernel<HD, HD, KM>), grid, dim3(256), 0, s, A);          \
+        goto launched;                                                                            \
+    }
+        RH_ATT(128, 1) RH_ATT(128, 2) RH_ATT(128, 4) RH_ATT(128, 5) RH_ATT(128, 6) RH_ATT(128, 8)
+        RH_ATT(64, 1) RH_ATT(64, 2) RH_ATT(64, 4) RH_ATT(64, 5) RH_ATT(64, 6) RH_ATT(64, 8)
+#undef RH_ATT
+        return 0;
+    launched:;
+        RH_LAUNCH_OK();
+    }
+    {
+        ProfScope ps("attn_combine", s);
+        int total = A.n_heads * A.vd;
+        hipLaunchKernelGGL(attn_combine_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+    }
+    return 1;
+}
+static bool attn_supported(int hd, int vd, int kv_mul) {
+    return hd == vd && (hd == 64 || hd == 128) &&
+           (kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 5 || kv_mul == 6 || kv_mul == 8);
+}
+static int attn_chunks(int n_kv, int max_ctx) {
+    int want = (2 * g.n_cu + n_kv - 1) / n_kv;
+    int by_ctx = (max_ctx + 15) / 16;
+    int c = std::min(want, by_ctx);
+    return c < 1 ? 1 : c;
+}
+
+// ---- per-op exports ------------------------------------------------------------------
+static int stage_x(const float *x, size_t n) {
+    if (!ensure(&g.x, &g.x_cap, n)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, x, n * sizeof(float), hipMemcpyHostToDevice, g.s));
+    return 1;
+}
+
+// y_i = W_i x for up to 3 matrices sharing x (cols), each of its own type.
+static int matvec_n(int n, const int *fmts, const uint8_t *const *w, const uintptr_t *wl, const uintptr_t *rows,
+                    const float *x, uintptr_t cols, float *const *outs) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !x || cols == 0) return 0;
+    MatSpec ms[3];
+    size_t total = 0;
+    for (int i = 0; i < n; i++) {
+        if (!w[i] || !outs[i] || rows[i] == 0) return 0;
+        if (!cat_of(fmts[i], (int)cols)) return 0;
+        if (!get_weight(w[i], wl[i], (int64_t)rows[i], (int64_t)cols, fmts[i], &ms[i].w)) return 0;
+        total += rows[i];
+    }
+    if (!stage_x(x, cols)) return 0;
+    if (!ensure(&g.y, &g.y_cap, total)) return 0;
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        ms[i].y = g.y + off;
+        ms[i].bias = nullptr;
+        off += rows[i];
+    }
+    bool need_q = false;
+    for (int i = 0; i < n; i++)
+        if (cat_of(fmts[i], (int)cols) != CAT_F32) need_q = true;
+    if (need_q) {
+        if (!ensure_xq(&g.xq, &g.xq_cap, cols)) return 0;
+        if (!launch_quant(g.x, (int)cols, g.xq, g.s)) return 0;
+    }
+    if (!gemv_multi(ms, n, (int)cols, EPI_STORE, g.xq, g.x, g.s)) return 0;
+    off = 0;
+    for (int i = 0; i < n; i++) {
+        RH_CHECK(hipMemcpyAsync(outs[i], g.y + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost, g.s));
+        off += rows[i];
+    }
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+static int ffn_device(const DevW &gate, const DevW &up, const DevW &down, int in_cols, const XQ &xq_in,
+                      const float *x_in, float *y, int epi) {
+    int hidden = gate.rows;
+    if (!ensure(&g.hid, &g.hid_cap, (size_t)hidden * 3)) return 0;
+    float *hbuf = g.hid, *tg = g.hid + hidden, *tu = g.hid + 2 * hidden;
+    if (!gemv_swiglu(gate, up, in_cols, xq_in, x_in, hbuf, tg, tu, g.s)) return 0;
+    bool need_q = cat_of(down.fmt, hidden) != CAT_F32;
+    if (need_q) {
+        if (!ensure_xq(&g.xq2, &g.xq2_cap, hidden)) return 0;
+        if (!launch_quant(hbuf, hidden, g.xq2, g.s)) return 0;
+    }
+    MatSpec md = {down, y, nullptr};
+    return gemv_multi(&md, 1, hidden, epi, g.xq2, hbuf, g.s);
+}
+
+}  // namespace rh
+
+using namespace rh;
+
+extern "C" {
+
+int rusty_hip_available(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    return init_locked();
+}
+
+int rusty_hip_matvec(uint32_t t, const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols,
+                     float *out) {
+    int f[1] = {(int)t};
+    const uint8_t *ws[1] = {w};
+    uintptr_t wls[1] = {wl}, rs[1] = {rows};
+    float *os[1] = {out};
+    return matvec_n(1, f, ws, wls, rs, x, cols, os);
+}
+
+int rusty_hip_q4k_matvec(const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols, float *out) {
+    return rusty_hip_matvec(12, w, wl, x, rows, cols, out);
+}
+int rusty_hip_q6k_matvec(const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols, float *out) {
+    return rusty_hip_matvec(14, w, wl, x, rows, cols, out);
+}
+int rusty_hip_q8_0_matvec(const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols, float *out) {
+    return rusty_hip_matvec(8, w, wl, x, rows, cols, out);
+}
+int rusty_hip_mxfp4_matvec(const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols,
+                           float *out) {
+    return rusty_hip_matvec(39, w, wl, x, rows, cols, out);
+}
+
+static int mv2(int fa, int fb, const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+               uintptr_t rb, const float *x, uintptr_t cols, float *oa, float *ob) {
+    int f[2] = {fa, fb};
+    const uint8_t *ws[2] = {wa, wb};
+    uintptr_t wls[2] = {la, lb}, rs[2] = {ra, rb};
+    float *os[2] = {oa, ob};
+    return matvec_n(2, f, ws, wls, rs, x, cols, os);
+}
+static int mv3(int fa, int fb, int fc, const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb,
+               uintptr_t lb, uintptr_t rb, const uint8_t *wc, uintptr_t lc, uintptr_t rc, const float *x,
+               uintptr_t cols, float *oa, float *ob, float *oc) {
+    int f[3] = {fa, fb, fc};
+    const uint8_t *ws[3] = {wa, wb, wc};
+    uintptr_t wls[3] = {la, lb, lc}, rs[3] = {ra, rb, rc};
+    float *os[3] = {oa, ob, oc};
+    return matvec_n(3, f, ws, wls, rs, x, cols, os);
+}
+
+int rusty_hip_q6k_matvec2(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                          uintptr_t rb, const float *x, uintptr_t cols, float *oa, float *ob) {
+    return mv2(14, 14, wa, la, ra, wb, lb, rb, x, cols, oa, ob);
+}
+int rusty_hip_q6k_matvec3(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                          uintptr_t rb, const uint8_t *wc, uintptr_t lc, uintptr_t rc, const float *x, uintptr_t cols,
+                          float *oa, float *ob, float *oc) {
+    return mv3(14, 14, 14, wa, la, ra, wb, lb, rb, wc, lc, rc, x, cols, oa, ob, oc);
+}
+int rusty_hip_q4k_matvec2(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                          uintptr_t rb, const float *x, uintptr_t cols, float *oa, float *ob) {
+    return mv2(12, 12, wa, la, ra, wb, lb, rb, x, cols, oa, ob);
+}
+int rusty_hip_q4k_matvec3(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                          uintptr_t rb, const uint8_t *wc, uintptr_t lc, uintptr_t rc, const float *x, uintptr_t cols,
+                          float *oa, float *ob, float *oc) {
+    return mv3(12, 12, 12, wa, la, ra, wb, lb, rb, wc, lc, rc, x, cols, oa, ob, oc);
+}
+int rusty_hip_q4k_q4k_q6k_matvec3(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                                  uintptr_t rb, const uint8_t *wc, uintptr_t lc, uintptr_t rc, const float *x,
+                                  uintptr_t cols, float *oa, float *ob, float *oc) {
+    return mv3(12, 12, 14, wa, la, ra, wb, lb, rb, wc, lc, rc, x, cols, oa, ob, oc);
+}
+int rusty_hip_mxfp4_matvec2(const uint8_t *wa, uintptr_t la, uintptr_t ra, const uint8_t *wb, uintptr_t lb,
+                            uintptr_t rb, const float *x, uintptr_t cols, float *oa, float *ob) {
+    return mv2(39, 39, wa, la, ra, wb, lb, rb, x, cols, oa, ob);
+}
+
+int rusty_hip_q4k_q4k_q6k_ffn(const uint8_t *gw, uintptr_t gl, const uint8_t *uw, uintptr_t ul, const uint8_t *dw,
+                              uintptr_t dl, const float *x, uintptr_t in_cols, uintptr_t hidden_rows,
+                              uintptr_t down_rows, uintptr_t down_cols, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !gw || !uw || !dw || !x || !out || in_cols == 0 || hidden_rows == 0 || down_rows == 0 ||
+        down_cols == 0 || hidden_rows != down_cols || in_cols % 256 != 0 || down_cols % 256 != 0)
+        return 0;
+    DevW G, U, D;
+    if (!get_weight(gw, gl, hidden_rows, in_cols, 12, &G) || !get_weight(uw, ul, hidden_rows, in_cols, 12, &U) ||
+        !get_weight(dw, dl, down_rows, down_cols, 14, &D))
+        return 0;
+    if (!stage_x(x, in_cols) || !ensure(&g.y, &g.y_cap, down_rows)) return 0;
+    if (!ensure_xq(&g.xq, &g.xq_cap, in_cols) || !launch_quant(g.x, (int)in_cols, g.xq, g.s)) return 0;
+    if (!ffn_device(G, U, D, (int)in_cols, g.xq, g.x, g.y, EPI_STORE)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.y, down_rows * sizeof(float), hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_mistral_post_attention_ffn(const uint8_t *ow, uintptr_t ol, const uint8_t *gw, uintptr_t gl,
+                                         const uint8_t *uw, uintptr_t ul, const uint8_t *dw, uintptr_t dl, float *x,
+                                         uintptr_t dim, const float *attn_out, uintptr_t attn_cols,
+                                         const float *ffn_norm, float eps, uintptr_t hidden_rows,
+                                         uintptr_t down_rows, uintptr_t down_cols) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !ow || !gw || !uw || !dw || !x || !attn_out || !ffn_norm || dim == 0 || attn_cols == 0 ||
+        hidden_rows == 0 || down_rows == 0 || down_cols == 0 || down_rows != dim || hidden_rows != down_cols ||
+        dim % 256 != 0 || attn_cols % 256 != 0 || down_cols % 256 != 0)
+        return 0;
+    DevW O, G, U, D;
+    if (!get_weight(ow, ol, dim, attn_cols, 12, &O) || !get_weight(gw, gl, hidden_rows, dim, 12, &G) ||
+        !get_weight(uw, ul, hidden_rows, dim, 12, &U) || !get_weight(dw, dl, down_rows, down_cols, 14, &D))
+        return 0;
+    // device layout in g.y: [x (dim) | attn (attn_cols) | norm w (dim) | xn (dim)]
+    if (!ensure(&g.y, &g.y_cap, 3 * dim + attn_cols)) return 0;
+    float *dx = g.y, *da = g.y + dim, *dw_ = da + attn_cols, *dxn = dw_ + dim;
+    RH_CHECK(hipMemcpyAsync(dx, x, dim * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(da, attn_out, attn_cols * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(dw_, ffn_norm, dim * 4, hipMemcpyHostToDevice, g.s));
+    if (!ensure_xq(&g.xq, &g.xq_cap, std::max(dim, attn_cols))) return 0;
+    if (!launch_quant(da, (int)attn_cols, g.xq, g.s)) return 0;
+    MatSpec mo = {O, dx, nullptr};
+    if (!gemv_multi(&mo, 1, (int)attn_cols, EPI_ADD, g.xq, da, g.s)) return 0;
+    if (!launch_rmsnorm(dx, dw_, eps, (int)dim, dxn, &g.xq, g.s)) return 0;
+    if (!ffn_device(G, U, D, (int)dim, g.xq, dxn, dx, EPI_ADD)) return 0;
+    RH_CHECK(hipMemcpyAsync(x, dx, dim * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_attention(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
+                        const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len, float *out,
+                        uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim, uintptr_t value_dim,
+                        uintptr_t key_stride, uintptr_t value_stride, uintptr_t slot_count, uintptr_t start_t,
+                        uintptr_t end_t, float scale, int use_sink) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !query || !keys || !values || !out || heads == 0 || kv_mul == 0 || head_dim == 0 ||
+        value_dim == 0 || slot_count == 0 || head_dim > 256 || value_dim > 256)
+        return 0;
+    if (heads % kv_mul != 0 || !attn_supported((int)head_dim, (int)value_dim, (int)kv_mul)) return 0;
+    if (key_stride % 4 != 0 || value_stride % 4 != 0) return 0;
+    size_t n_kv = heads / kv_mul;
+    if (key_stride < n_kv * head_dim || value_stride < n_kv * value_dim) return 0;
+    if (query_len < heads * head_dim * 4 || keys_len < slot_count * key_stride * 4 ||
+        values_len < slot_count * value_stride * 4 || out_len < heads * value_dim * 4 ||
+        (use_sink && (!sinks || sinks_len < heads * 4)))
+        return 0;
+    if (start_t > end_t) {  // empty range: the reference leaves out untouched
+        return 1;
+    }
+    // Upload only the slots the scan visits.
+    size_t lo, n_slots;
+    if (end_t < slot_count) {
+        lo = start_t;
+        n_slots = end_t - start_t + 1;
+    } else {
+        lo = 0;
+        n_slots = slot_count;
+    }
+    size_t kfl = slot_count * key_stride, vfl = slot_count * value_stride;
+    if (!ensure(&g.kv_k, &g.kv_cap, kfl + vfl)) return 0;
+    g.kv_v = g.kv_k + kfl;
+    RH_CHECK(hipMemcpyAsync(g.kv_k + lo * key_stride, keys + lo * key_stride, n_slots * key_stride * 4,
+                            hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(g.kv_v + lo * value_stride, values + lo * value_stride, n_slots * value_stride * 4,
+                            hipMemcpyHostToDevice, g.s));
+    size_t qn = heads * head_dim, on = heads * value_dim;
+    if (!ensure(&g.x, &g.x_cap, qn + heads) || !ensure(&g.y, &g.y_cap, on)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, query, qn * 4, hipMemcpyHostToDevice, g.s));
+    if (use_sink) RH_CHECK(hipMemcpyAsync(g.x + qn, sinks, heads * 4, hipMemcpyHostToDevice, g.s));
+    AttnArgs A;
+    memset(&A, 0, sizeof(A));
+    A.q = g.x;
+    A.k = g.kv_k;
+    A.v = g.kv_v;
+    A.sinks = use_sink ? g.x + qn : nullptr;
+    A.out = g.y;
+    A.n_heads = (int)heads;
+    A.n_kv = (int)n_kv;
+    A.kv_mul = (int)kv_mul;
+    A.hd = (int)head_dim;
+    A.vd = (int)value_dim;
+    A.key_stride = (int64_t)key_stride;
+    A.value_stride = (int64_t)value_stride;
+    A.slot_count = (int)slot_count;
+    A.start_t = (int)start_t;
+    A.end_t = (int)end_t;
+    A.n_chunks = attn_chunks((int)n_kv, (int)(end_t - start_t + 1));
+    A.scale = scale;
+    if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * (value_dim + 2))) return 0;
+    A.part = g.part;
+    if (!attn_launch(A, g.s)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.y, on * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_weight_cache_clear(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    wcache_clear();
+    return 1;
+}
+
+int rusty_hip_sync(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_profile_enable(int on) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    prof_drain();
+    g.prof.on = on != 0;
+    if (on) {
+        for (auto &t : g.prof.total_ms) t = 0.0;
+        for (auto &c : g.prof.count) c = 0;
+    }
+    return 1;
+}
+
+int rusty_hip_profile_get(int i, char *name, double *total_ms, int64_t *count) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    prof_drain();
+    if (i < 0 || i >= (int)g.prof.names.size()) return 0;
+    if (name) {
+        strncpy(name, g.prof.names[i].c_str(), 63);
+        name[63] = 0;
+    }
+    if (total_ms) *total_ms = g.prof.total_ms[i];
+    if (count) *count = g.prof.count[i];
+    return 1;
+}
+
+// ---- debug hooks ----------------------------------------------------------------------
+int rusty_hip_debug_quantize_q8k(const float *x, uintptr_t n, int8_t *qs, float *d, int16_t *bsums) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !x || n == 0 || n % 256 != 0) return 0;
+    if (!stage_x(x, n) || !ensure_xq(&g.xq, &g.xq_cap, n) || !launch_quant(g.x, (int)n, g.xq, g.s)) return 0;
+    RH_CHECK(hipMemcpyAsync(qs, g.xq.qs, n, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipMemcpyAsync(d, g.xq.d, n / 256 * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipMemcpyAsync(bsums, g.xq.bsums, n / 32 * 2, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+int rusty_hip_debug_dequant(uint32_t t, const uint8_t *w, uintptr_t wl, uintptr_t rows, uintptr_t cols, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !w || !out) return 0;
+    DevW W;
+    if (!get_weight(w, wl, rows, cols, (int)t, &W)) return 0;
+    if (!ensure(&g.y, &g.y_cap, rows * cols)) return 0;
+    dim3 grid((unsigned)std::min<uintptr_t>((cols + 255) / 256, 64), (unsigned)rows);
+    hipLaunchKernelGGL(dequant_rows_kernel, grid, dim3(256), 0, g.s, W.p, W.stride, (int)rows, (int)cols, (int)t, g.y);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(out, g.y, rows * cols * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+int rusty_hip_debug_block_ints(uint32_t t, const uint8_t *w, uintptr_t wl, uintptr_t rows, uintptr_t cols,
+                               const float *x, int32_t *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !w || !x || !out || cols % 256 != 0) return 0;
+    if (t != 8 && t != 12 && t != 14) return 0;
+    DevW W;
+    if (!get_weight(w, wl, rows, cols, (int)t, &W)) return 0;
+    if (!stage_x(x, cols) || !ensure_xq(&g.xq, &g.xq_cap, cols) || !launch_quant(g.x, (int)cols, g.xq, g.s)) return 0;
+    size_t n = (t == 8) ? rows * (cols / 32) : (t == 12 ? rows * (cols / 256) * 2 : rows * (cols / 256));
+    if (!ensure(&g.ibuf, &g.ibuf_cap, n)) return 0;
+    hipLaunchKernelGGL(block_ints_kernel, dim3((unsigned)rows), dim3(64), 0, g.s, W.p, W.stride, (int)rows, (int)cols,
+                       (int)t, g.xq, g.ibuf);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(out, g.ibuf, n * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+int rusty_hip_debug_rmsnorm(const float *x, const float *w, float eps, uintptr_t n, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !x || !w || !out || n == 0) return 0;
+    if (!ensure(&g.x, &g.x_cap, 2 * n) || !ensure(&g.y, &g.y_cap, n)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, x, n * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(g.x + n, w, n * 4, hipMemcpyHostToDevice, g.s));
+    if (!launch_rmsnorm(g.x, g.x + n, eps, (int)n, g.y, nullptr, g.s)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+int rusty_hip_debug_silu_mul(const float *gt, const float *up, uintptr_t n, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !gt || !up || !out || n == 0) return 0;
+    if (!ensure(&g.x, &g.x_cap, 2 * n) || !ensure(&g.y, &g.y_cap, n)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, gt, n * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(g.x + n, up, n * 4, hipMemcpyHostToDevice, g.s));
+    if (!launch_silu(g.x, g.x + n, (int)n, g.y, g.s)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+__global__ void f16_kernel(const uint16_t *h, int n, float *out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = h2f(h[i]);
+}
+int rusty_hip_debug_f16(const uint16_t *h, uintptr_t n, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !h || !out || n == 0) return 0;
+    if (!ensure(&g.x, &g.x_cap, n) || !ensure(&g.y, &g.y_cap, n)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, h, n * 2, hipMemcpyHostToDevice, g.s));
+    hipLaunchKernelGGL(f16_kernel, dim3(256), dim3(256), 0, g.s, (const uint16_t *)g.x, (int)n, g.y);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+int rusty_hip_debug_rope(float *q, float *k, uint32_t pos, uint32_t hd, uint32_t nh, uint32_t nkv,
+                         const float *inv_freq, uint32_t neox) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !q || !k || !inv_freq || hd == 0 || hd % 2 != 0) return 0;
+    size_t half = hd / 2, nq = (size_t)nh * hd, nk = (size_t)nkv * hd;
+    std::vector<float> ct(half), stb(half);
+    for (size_t i = 0; i < half; i++) {
+        float ang = (float)pos * inv_freq[i];
+        stb[i] = sinf(ang);
+        ct[i] = cosf(ang);
+    }
+    // device: [q | k | cache_k (nk) | cache_v (1 float) | cos | sin]
+    if (!ensure(&g.x, &g.x_cap, nq + 2 * nk + 2 * half + 4)) return 0;
+    float *dq = g.x, *dk = dq + nq, *ck = dk + nk, *dcos = ck + nk, *dsin = dcos + half;
+    RH_CHECK(hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(dk, k, nk * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(dcos, ct.data(), half * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(dsin, stb.data(), half * 4, hipMemcpyHostToDevice, g.s));
+    RopeArgs A;
+    memset(&A, 0, sizeof(A));
+    A.q = dq;
+    A.k = dk;
+    A.v = dk;
+    A.kcache = ck;
+    A.vcache = ck;  // value copy writes are disabled by n_kv*vd = 0 below
+    A.cos_t = dcos;
+    A.sin_t = dsin;
+    A.pos = 0;
+    A.max_pos = 1;
+    A.n_heads = (int)nh;
+    A.n_kv = (int)nkv;
+    A.hd = (int)hd;
+    A.vd = 0;
+    A.slots = 1;
+    A.ring = 0;
+    A.neox = (int)neox;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(64), dim3(256), 0, g.s, A);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(q, dq, nq * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipMemcpyAsync(k, ck, nk * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+}  // extern "C"
+
+// ===== resident decoder ====================================================================
+namespace rh {
+
+struct RLayer {
+    DevW w[7];
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    float *bias[3] = {nullptr, nullptr, nullptr};
+    float *k = nullptr, *v = nullptr;
+};
+
+struct Resident {
+    bool configured = false, ready = false;
+    uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, vd = 0, hidden = 0, vocab = 0, storage = 0;
+    uint32_t neox = 0;
+    float eps = 1e-5f;
+    std::vector<RLayer> L;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float *hid = nullptr, *tg = nullptr, *tu = nullptr, *logits = nullptr;
+    XQ xq_dim{}, xq_attn{}, xq_hid{};
+    DevW out_w;
+    float *out_norm = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    DevW embd;
+    bool has_embd = false;
+    StepState *st = nullptr;
+    StepState *st_host = nullptr;  // pinned staging
+    float *part = nullptr;
+    int n_chunks = 1;
+    float *am_v = nullptr;
+    int32_t *am_i = nullptr;
+    uint32_t *ticket = nullptr;
+    int32_t *tokens = nullptr;   // device prompt / output tokens
+    int32_t *out_idx = nullptr;
+    uint32_t tok_cap = 0;
+    int am_blocks = 256;
+    std::map<int, hipGraphExec_t> graphs;
+    std::vector<void *> allocs;
+};
+static Resident R;
+
+enum { MODE_DEVTOK = 1, MODE_LOGITS = 2, MODE_GREEDY = 4 };
+
+static int r_alloc(void **p, size_t bytes) {
+    RH_CHECK(hipMalloc(p, bytes));
+    R.allocs.push_back(*p);
+    return 1;
+}
+
+static void r_reset() {
+    if (g.s) (void)hipStreamSynchronize(g.s);
+    for (auto &kv : R.graphs) (void)hipGraphExecDestroy(kv.second);
+    R.graphs.clear();
+    for (void *p : R.allocs) (void)hipFree(p);
+    R.allocs.clear();
+    if (R.st_host) (void)hipHostFree(R.st_host);
+    R.st_host = nullptr;
+    R.L.clear();
+    R.configured = R.ready = false;
+    R.has_embd = false;
+    R.tok_cap = 0;
+}
+
+static void r_invalidate_graphs() {
+    if (!R.graphs.empty()) (void)hipStreamSynchronize(g.s);  // no exec may still be in flight
+    for (auto &kv : R.graphs) (void)hipGraphExecDestroy(kv.second);
+    R.graphs.clear();
+}
+
+static int dt_to_fmt(uint32_t dt) {
+    switch (dt) {
+    case 0: return 12;
+    case 1: return 14;
+    case 2: return 8;
+    case 3: return 39;
+    case 8: case 12: case 14: case 39: return (int)dt;
+    default: return -1;
+    }
+}
+
+// One token through the layer stack (and head / greedy by mode) on stream s.
+static int r_enqueue(int mode, float penalty, hipStream_t s) {
+    const int dim = R.dim, qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd;
+    const int attn_cols = R.n_heads * R.vd;
+    if (mode & MODE_DEVTOK) {
+        ProfScope ps("embed", s);
+        hipLaunchKernelGGL(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, R.embd.p, R.embd.stride,
+                           R.embd.fmt, dim, R.st, 0, R.x);
+        RH_LAUNCH_OK();
+    }
+    for (uint32_t l = 0; l < R.n_layers; l++) {
+        RLayer &Ly = R.L[l];
+        if (!launch_rmsnorm(R.x, Ly.attn_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
+        MatSpec qkv[3] = {{Ly.w[0], R.q, Ly.bias[0]}, {Ly.w[1], R.k, Ly.bias[1]}, {Ly.w[2], R.v, Ly.bias[2]}};
+        if (!gemv_multi(qkv, 3, dim, EPI_STORE, R.xq_dim, R.xn, s)) return 0;
+        {
+            RopeArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.q;
+            A.k = R.k;
+            A.v = R.v;
+            A.kcache = Ly.k;
+            A.vcache = Ly.v;
+            A.cos_t = R.cos_t;
+            A.sin_t = R.sin_t;
+            A.st = R.st;
+            A.max_pos = R.storage;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.slots = R.storage;
+            A.ring = 0;
+            A.neox = R.neox;
+            int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+            ProfScope ps("rope_kv", s);
+            hipLaunchKernelGGL(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
+            RH_LAUNCH_OK();
+        }
+        {
+            AttnArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.q;
+            A.k = Ly.k;
+            A.v = Ly.v;
+            A.sinks = nullptr;
+            A.part = R.part;
+            A.out = R.attn;
+            A.xq = (attn_cols % 256 == 0) ? R.xq_attn : XQ{};
+            A.st = R.st;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.kv_mul = R.n_heads / R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.key_stride = kd;
+            A.value_stride = vdim;
+            A.slot_count = R.storage;
+            A.window = 0;
+            A.n_chunks = R.n_chunks;
+            A.scale = 1.0f / sqrtf((float)R.hd);
+            if (!attn_launch(A, s)) return 0;
+        }
+        MatSpec mo = {Ly.w[3], R.x, nullptr};
+        if (!gemv_multi(&mo, 1, attn_cols, EPI_ADD, R.xq_attn, R.attn, s)) return 0;
+        if (!launch_rmsnorm(R.x, Ly.ffn_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
+        if (!gemv_swiglu(Ly.w[4], Ly.w[5], dim, R.xq_dim, R.xn, R.hid, R.tg, R.tu, s)) return 0;
+        if (cat_of(Ly.w[6].fmt, R.hidden) != CAT_F32)
+            if (!launch_quant(R.hid, R.hidden, R.xq_hid, s)) return 0;
+        MatSpec md = {Ly.w[6], R.x, nullptr};
+        if (!gemv_multi(&md, 1, R.hidden, EPI_ADD, R.xq_hid, R.hid, s)) return 0;
+    }
+    (void)qd;
+    if (mode & (MODE_LOGITS | MODE_GREEDY)) {
+        if (!launch_rmsnorm(R.x, R.out_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
+        MatSpec mh = {R.out_w, R.logits, nullptr};
+        if (!gemv_multi(&mh, 1, dim, EPI_STORE, R.xq_dim, R.xn, s)) return 0;
+    }
+    if (mode & MODE_GREEDY) {
+        ArgmaxArgs A;
+        memset(&A, 0, sizeof(A));
+        A.logits = R.logits;
+        A.n = R.vocab;
+        A.penalty = penalty;
+        A.st = R.st;
+        A.part_v = R.am_v;
+        A.part_i = R.am_i;
+        A.ticket = R.ticket;
+        A.out_tokens = R.tokens;
+        A.out_index = R.out_idx;
+        A.advance = 1;
+        ProfScope ps("argmax_greedy", s);
+        hipLaunchKernelGGL(argmax_greedy_kernel, dim3(R.am_blocks), dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+    }
+    return 1;
+}
+
+static bool use_graphs() {
+    if (g.prof.on) return false;
+    const char *e = getenv("RUSTY_HIP_GRAPH");
+    return !(e && strcmp(e, "0") == 0);
+}
+
+// Runs one token in `mode`, via a cached graph when allowed.  The penalty is
+// baked into the greedy graph, so graphs are keyed by (mode, penalty bits).
+static int r_run(int mode, float penalty) {
+    if (!use_graphs()) return r_enqueue(mode, penalty, g.s);
+    uint32_t pb;
+    memcpy(&pb, &penalty, 4);
+    int key = mode ^ (int)(pb * 2654435761u & 0x7ffffff8u);
+    auto it = R.graphs.find(key);
+    if (it == R.graphs.end()) {
+        hipGraph_t graph;
+        RH_CHECK(hipStreamBeginCapture(g.s, hipStreamCaptureModeThreadLocal));
+        int ok = r_enqueue(mode, penalty, g.s);
+        hipError_t e = hipStreamEndCapture(g.s, &graph);
+        if (!ok || e != hipSuccess) {
+            if (e == hipSuccess) (void)hipGraphDestroy(graph);
+            return 0;
+        }
+        hipGraphExec_t exec;
+        hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        RH_CHECK(ie);
+        it = R.graphs.emplace(key, exec).first;
+    }
+    RH_CHECK(hipGraphLaunch(it->second, g.s));
+    return 1;
+}
+
+static int r_set_state(int pos, int start_t, int token, bool reset_recent) {
+    StepState *h = R.st_host;
+    RH_CHECK(hipStreamSynchronize(g.s));  // staging buffer reuse
+    RH_CHECK(hipMemcpy(h, R.st, sizeof(StepState), hipMemcpyDeviceToHost));
+    h->pos = pos;
+    h->start_t = start_t;
+    h->token = token;
+    if (reset_recent) h->n_recent = 0;
+    RH_CHECK(hipMemcpyAsync(R.st, h, sizeof(StepState), hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    return 1;
+}
+
+}  // namespace rh
+
+extern "C" {
+
+int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                 uint32_t head_dim, uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab,
+                                 uint32_t storage_len, float eps, uint32_t neox) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    if (n_layers == 0 || n_layers > 512 || n_kv_heads == 0 || n_heads % n_kv_heads != 0) return 0;
+    if (head_dim == 0 || head_dim > 256 || value_dim == 0 || value_dim > 256) return 0;
+    if (dim % 256 != 0 || hidden_dim % 256 != 0 || storage_len == 0 || vocab == 0) return 0;
+    if (!attn_supported((int)head_dim, (int)value_dim, (int)(n_heads / n_kv_heads))) return 0;
+    r_reset();
+    wcache_clear();  // a new model: cached copies keyed by old host addresses are stale
+    R.n_layers = n_layers;
+    R.dim = dim;
+    R.n_heads = n_heads;
+    R.n_kv = n_kv_heads;
+    R.hd = head_dim;
+    R.vd = value_dim;
+    R.hidden = hidden_dim;
+    R.vocab = vocab;
+    R.storage = storage_len;
+    R.eps = eps;
+    R.neox = neox;
+    R.L.resize(n_layers);
+    size_t qd = (size_t)n_heads * head_dim, kd = (size_t)n_kv_heads * head_dim, vdim = (size_t)n_kv_heads * value_dim;
+    size_t attn_cols = (size_t)n_heads * value_dim;
+    if (!r_alloc((void **)&R.x, dim * 4) || !r_alloc((void **)&R.xn, dim * 4) || !r_alloc((void **)&R.q, qd * 4) ||
+        !r_alloc((void **)&R.k, kd * 4) || !r_alloc((void **)&R.v, vdim * 4) ||
+        !r_alloc((void **)&R.attn, attn_cols * 4) || !r_alloc((void **)&R.hid, hidden_dim * 4) ||
+        !r_alloc((void **)&R.tg, hidden_dim * 4) || !r_alloc((void **)&R.tu, hidden_dim * 4) ||
+        !r_alloc((void **)&R.logits, (size_t)vocab * 4))
+        return 0;
+    XQ *xqs[3] = {&R.xq_dim, &R.xq_attn, &R.xq_hid};
+    size_t ns[3] = {dim, attn_cols, hidden_dim};
+    for (int i = 0; i < 3; i++) {
+        size_t nb = (ns[i] + 255) / 256;
+        if (!r_alloc((void **)&xqs[i]->qs, nb * 256) || !r_alloc((void **)&xqs[i]->d, nb * 4) ||
+            !r_alloc((void **)&xqs[i]->bsums, nb * 16) || !r_alloc((void **)&xqs[i]->sums16, nb * 32))
+            return 0;
+    }
+    R.n_chunks = attn_chunks((int)n_kv_heads, (int)storage_len);
+    if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * (value_dim + 2) * 4))
+        return 0;
+    R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
+    if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
+        !r_alloc((void **)&R.ticket, 64) || !r_alloc((void **)&R.st, sizeof(StepState)) ||
+        !r_alloc((void **)&R.out_idx, 64))
+        return 0;
+    RH_CHECK(hipMemset(R.ticket, 0, 64));
+    RH_CHECK(hipMemset(R.st, 0, sizeof(StepState)));
+    RH_CHECK(hipMemset(R.out_idx, 0, 64));
+    RH_CHECK(hipHostMalloc((void **)&R.st_host, sizeof(StepState), hipHostMallocDefault));
+    R.configured = true;
+    return 1;
+}
+
+int rusty_hip_resident_set_layer(uint32_t l, const RustyResidentLayerDesc *d) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || !d || l >= R.n_layers) return 0;
+    RLayer &Ly = R.L[l];
+    uint32_t cols[7] = {R.dim, R.dim, R.dim, R.n_heads * R.vd, R.dim, R.dim, R.hidden};
+    uint32_t want_rows[7] = {R.n_heads * R.hd, R.n_kv * R.hd, R.n_kv * R.vd, R.dim, R.hidden, R.hidden, R.dim};
+    for (int i = 0; i < 7; i++) {
+        int fmt = dt_to_fmt(d->w_dt[i]);
+        if (!d->w[i] || fmt < 0 || d->w_rows[i] != want_rows[i] || !cat_of(fmt, (int)cols[i])) return 0;
+        if (!get_weight(d->w[i], d->w_len[i], d->w_rows[i], cols[i], fmt, &Ly.w[i])) return 0;
+    }
+    if (!d->attn_norm || !d->ffn_norm) return 0;
+    if (!r_alloc((void **)&Ly.attn_norm, R.dim * 4) || !r_alloc((void **)&Ly.ffn_norm, R.dim * 4)) return 0;
+    RH_CHECK(hipMemcpy(Ly.attn_norm, d->attn_norm, R.dim * 4, hipMemcpyHostToDevice));
+    RH_CHECK(hipMemcpy(Ly.ffn_norm, d->ffn_norm, R.dim * 4, hipMemcpyHostToDevice));
+    const float *bs[3] = {d->bq, d->bk, d->bv};
+    uint32_t bl[3] = {d->bq_len, d->bk_len, d->bv_len};
+    for (int i = 0; i < 3; i++) {
+        Ly.bias[i] = nullptr;
+        if (bs[i] && bl[i]) {
+            if (bl[i] != want_rows[i]) return 0;
+            if (!r_alloc((void **)&Ly.bias[i], bl[i] * 4)) return 0;
+            RH_CHECK(hipMemcpy(Ly.bias[i], bs[i], bl[i] * 4, hipMemcpyHostToDevice));
+        }
+    }
+    size_t kd = (size_t)R.n_kv * R.hd, vdim = (size_t)R.n_kv * R.vd;
+    if (!r_alloc((void **)&Ly.k, (size_t)R.storage * kd * 4) || !r_alloc((void **)&Ly.v, (size_t)R.storage * vdim * 4))
+        return 0;
+    RH_CHECK(hipMemset(Ly.k, 0, (size_t)R.storage * kd * 4));
+    RH_CHECK(hipMemset(Ly.v, 0, (size_t)R.storage * vdim * 4));
+    r_invalidate_graphs();
+    return 1;
+}
+
+int rusty_hip_resident_set_output(const float *output_norm, const uint8_t *output_w, uintptr_t output_w_len,
+                                  uint32_t output_rows, uint32_t output_dt, const float *inv_freq,
+                                  uint32_t inv_freq_len) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || !output_norm || !output_w || !inv_freq || output_rows != R.vocab) return 0;
+    if (inv_freq_len < R.hd / 2) return 0;
+    int fmt = dt_to_fmt(output_dt);
+    if (fmt < 0 || !cat_of(fmt, (int)R.dim)) return 0;
+    if (!get_weight(output_w, output_w_len, output_rows, R.dim, fmt, &R.out_w)) return 0;
+    if (!r_alloc((void **)&R.out_norm, R.dim * 4)) return 0;
+    RH_CHECK(hipMemcpy(R.out_norm, output_norm, R.dim * 4, hipMemcpyHostToDevice));
+    // RoPE table: the reference's angle (float)pos * inv_freq[i] and libm
+    // sinf/cosf (apply_rope_qk, src/model.rs:5574-5575).
+    size_t half = R.hd / 2;
+    std::vector<float> ct((size_t)R.storage * half), stb((size_t)R.storage * half);
+    for (size_t p = 0; p < R.storage; p++)
+        for (size_t i = 0; i < half; i++) {
+            float ang = (float)p * inv_freq[i];
+            stb[p * half + i] = sinf(ang);
+            ct[p * half + i] = cosf(ang);
+        }
+    if (!r_alloc((void **)&R.cos_t, ct.size() * 4) || !r_alloc((void **)&R.sin_t, stb.size() * 4)) return 0;
+    RH_CHECK(hipMemcpy(R.cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));
+    RH_CHECK(hipMemcpy(R.sin_t, stb.data(), stb.size() * 4, hipMemcpyHostToDevice));
+    for (uint32_t l = 0; l < R.n_layers; l++)
+        if (!R.L[l].k) return 0;
+    r_invalidate_graphs();
+    R.ready = true;
+    return 1;
+}
+
+int rusty_hip_resident_set_embedding(const uint8_t *embd, uintptr_t embd_len, uint32_t t) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || !embd) return 0;
+    int fmt = (int)t;
+    if (row_bytes_of(fmt, R.dim) <= 0) return 0;
+    if (!get_weight(embd, embd_len, R.vocab, R.dim, fmt, &R.embd)) return 0;
+    R.has_embd = true;
+    r_invalidate_graphs();
+    return 1;
+}
+
+int rusty_hip_resident_decode(const float *x_embed, uint32_t pos, uint32_t start_t, int want_logits,
+                              float *logits_out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.ready || !x_embed || pos >= R.storage) return 0;
+    if (want_logits && !logits_out) return 0;
+    if (!r_set_state((int)pos, (int)start_t, 0, false)) return 0;
+    RH_CHECK(hipMemcpyAsync(R.x, x_embed, R.dim * 4, hipMemcpyHostToDevice, g.s));
+    if (!r_run(want_logits ? MODE_LOGITS : 0, 1.0f)) return 0;
+    if (want_logits) RH_CHECK(hipMemcpyAsync(logits_out, R.logits, (size_t)R.vocab * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32_t start_pos, uint32_t n_gen,
+                                float penalty, int32_t *out_tokens, float *logits_out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.ready || !R.has_embd || !prompt || n_prompt == 0 || (n_gen > 0 && !out_tokens)) return 0;
+    if ((uint64_t)start_pos + n_prompt + n_gen > (uint64_t)R.storage + 1) return 0;
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || (uint32_t)prompt[i] >= R.vocab) return 0;
+    uint32_t need = std::max(n_prompt, n_gen) + 1;
+    if (R.tok_cap < need) {
+        need = std::max<uint32_t>(need, std::min<uint32_t>(R.storage + 1, 8192));
+        if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
+        R.tok_cap = need;
+        r_invalidate_graphs();  // greedy graph records the token pointer
+    }
+    RH_CHECK(hipMemcpy(R.tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    if (!r_set_state((int)start_pos, 0, prompt[0], true)) return 0;
+    // recent window = last <= 64 prompt tokens (recent_token_tail, src/runtime.rs:508-512)
+    uint32_t tail = n_prompt > 64 ? n_prompt - 64 : 0;
+    for (uint32_t i = 0; i < n_prompt; i++) {
+        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(64), 0, g.s, R.st, R.tokens, (int)i, (int)(start_pos + i),
+                           i >= tail ? 1 : 0);
+        RH_LAUNCH_OK();
+        if (i + 1 < n_prompt) {
+            if (!r_run(MODE_DEVTOK, 1.0f)) return 0;
+        }
+    }
+    RH_CHECK(hipMemsetAsync(R.out_idx, 0, 4, g.s));
+    if (n_gen == 0) {
+        if (!r_run(MODE_DEVTOK | MODE_LOGITS, 1.0f)) return 0;
+    } else {
+        // The prompt copy in R.tokens is consumed; generated tokens overwrite it.
+        for (uint32_t i = 0; i < n_gen; i++)
+            if (!r_run(MODE_DEVTOK | MODE_GREEDY, penalty)) return 0;
+        RH_CHECK(hipMemcpyAsync(out_tokens, R.tokens, (size_t)n_gen * 4, hipMemcpyDeviceToHost, g.s));
+    }
+    if (logits_out) RH_CHECK(hipMemcpyAsync(logits_out, R.logits, (size_t)R.vocab * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_resident_time_decode(uint32_t n_tokens, float penalty, double *ms) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.ready || !R.has_embd || !ms) return 0;
+    if (R.tok_cap < n_tokens + 1) {
+        uint32_t need = std::max<uint32_t>(n_tokens + 1, std::min<uint32_t>(R.storage + 1, 8192));
+        if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
+        R.tok_cap = need;
+        r_invalidate_graphs();
+    }
+    RH_CHECK(hipStreamSynchronize(g.s));
+    RH_CHECK(hipMemcpy(R.st_host, R.st, sizeof(StepState), hipMemcpyDeviceToHost));
+    if ((uint64_t)R.st_host->pos + n_tokens > R.storage) return 0;
+    RH_CHECK(hipMemsetAsync(R.out_idx, 0, 4, g.s));
+    // make sure the graph exists before timing
+    if (use_graphs()) {
+        uint32_t pb;
+        memcpy(&pb, &penalty, 4);
+        int key = (MODE_DEVTOK | MODE_GREEDY) ^ (int)(pb * 2654435761u & 0x7ffffff8u);
+        if (R.graphs.find(key) == R.graphs.end()) {
+            // capture only (no launch): replay below is timed
+            hipGraph_t graph;
+            RH_CHECK(hipStreamBeginCapture(g.s, hipStreamCaptureModeThreadLocal));
+            int ok = r_enqueue(MODE_DEVTOK | MODE_GREEDY, penalty, g.s);
+            hipError_t e = hipStreamEndCapture(g.s, &graph);
+            if (!ok || e != hipSuccess) return 0;
+            hipGraphExec_t exec;
+            hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            RH_CHECK(ie);
+            R.graphs.emplace(key, exec);
+        }
+    }
+    hipEvent_t a, b;
+    RH_CHECK(hipEventCreate(&a));
+    RH_CHECK(hipEventCreate(&b));
+    RH_CHECK(hipEventRecord(a, g.s));
+    for (uint32_t i = 0; i < n_tokens; i++)
+        if (!r_run(MODE_DEVTOK | MODE_GREEDY, penalty)) return 0;
+    RH_CHECK(hipEventRecord(b, g.s));
+    RH_CHECK(hipEventSynchronize(b));
+    float t = 0.0f;
+    RH_CHECK(hipEventElapsedTime(&t, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *ms = t;
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || l >= R.n_layers || !host_out || (uint64_t)slot0 + n_slots > R.storage) return 0;
+    size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd;
+    float *src = which ? R.L[l].v : R.L[l].k;
+    if (!src) return 0;
+    RH_CHECK(hipStreamSynchronize(g.s));
+    RH_CHECK(hipMemcpy(host_out, src + (size_t)slot0 * w, (size_t)n_slots * w * 4, hipMemcpyDeviceToHost));
+    return 1;
+}
+
+int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || l >= R.n_layers || !host_in || (uint64_t)slot0 + n_slots > R.storage) return 0;
+    size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd;
+    float *dst = which ? R.L[l].v : R.L[l].k;
+    if (!dst) return 0;
+    RH_CHECK(hipStreamSynchronize(g.s));
+    RH_CHECK(hipMemcpy(dst + (size_t)slot0 * w, host_in, (size_t)n_slots * w * 4, hipMemcpyHostToDevice));
+    return 1;
+}
+
+int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *recent, uint32_t n_recent, float penalty,
+                           int32_t *token) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !logits || n == 0 || !token || n_recent > 64) return 0;
+    // scratch: logits | partials | state
+    size_t blocks = std::min<size_t>(256, (n + 255) / 256);
+    size_t need = n + 2 * blocks + sizeof(StepState) / 4 + 64;
+    if (!ensure(&g.y, &g.y_cap, need)) return 0;
+    float *dl = g.y;
+    float *pv = dl + n;
+    int32_t *pi = (int32_t *)(pv + blocks);
+    StepState *st = (StepState *)(pi + blocks);
+    uint32_t *ticket = (uint32_t *)(st + 1);
+    StepState hs;
+    memset(&hs, 0, sizeof(hs));
+    hs.n_recent = (int)n_recent;
+    for (uint32_t i = 0; i < n_recent; i++) hs.recent[i] = recent[i];
+    RH_CHECK(hipMemcpyAsync(dl, logits, n * 4, hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemcpyAsync(st, &hs, sizeof(hs), hipMemcpyHostToDevice, g.s));
+    RH_CHECK(hipMemsetAsync(ticket, 0, 4, g.s));
+    ArgmaxArgs A;
+    memset(&A, 0, sizeof(A));
+    A.logits = dl;
+    A.n = (int)n;
+    A.penalty = penalty;
+    A.st = st;
+    A.part_v = pv;
+    A.part_i = pi;
+    A.ticket = ticket;
+    A.advance = 1;
+    hipLaunchKernelGGL(argmax_greedy_kernel, dim3((unsigned)blocks), dim3(256), 0, g.s, A);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(&hs, st, sizeof(hs), hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    *token = hs.token;
+    return 1;
+}
+
+}  // extern "C"
