@@ -159,6 +159,13 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);
 int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in);
 
+/* Attention order for every later call (no reference counterpart).
+ * 0 (default): the reference's serial online-softmax order with glibc's expf,
+ * bit for bit (src/model.rs:5739-6198); 1: split-K flash decode, within
+ * 1e-4 x row norm but not bit-exact.  RUSTY_HIP_ATTN=fast picks 1 at start.
+ * Returns the previous mode; other values only query. */
+int rusty_hip_attention_mode(int mode);
+
 /* Frees every cached device weight copy (no reference counterpart: the
  * Metal cache lives as long as the process because the reference's weights
  * are mmap'd and never freed).  Call it before freeing host weight memory
@@ -190,6 +197,7 @@ int rusty_hip_debug_rope(float *q, float *k, uint32_t pos, uint32_t head_dim, ui
 int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *recent, uint32_t n_recent, float penalty,
                            int32_t *token);
 int rusty_hip_debug_f16(const uint16_t *h, uintptr_t n, float *out);
+int rusty_hip_debug_expf(const float *x, uintptr_t n, float *out);
 
 #ifdef __cplusplus
 }

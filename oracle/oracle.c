@@ -1272,3 +1272,8 @@ void orc_mxfp4_test_activation(int64_t n, float *out) {
     /* simd.rs:7847-7849 */
     for (int64_t i = 0; i < n; i++) out[i] = sinf((float)i * 0.071f) * 0.9f + (float)(i % 13) * 0.02f;
 }
+
+/* libm expf over an array: exp_attn (model.rs:5720-5726) is f32::exp. */
+void orc_expf_array(const float *x, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; i++) out[i] = expf(x[i]);
+}

@@ -103,6 +103,7 @@ void orc_select_top_logits(const float *logits, int64_t n, int64_t k, int32_t *i
 void orc_softmax_selected(const float *val, int64_t k, float *out);
 void orc_apply_repeat_penalty(float *logits, int64_t n, const uint32_t *recent, int64_t nrecent, float penalty);
 uint32_t orc_argmax_finite(const float *logits, int64_t n);
+void orc_expf_array(const float *x, int64_t n, float *out);
 uint32_t orc_greedy(float *logits, int64_t n, const uint32_t *recent, int64_t nrecent, float penalty);
 
 /* ---- standard (llama / qwen2) decode model ------------------------------- */

@@ -81,6 +81,7 @@ _sig("orc_softmax_selected", None, _p, _i64, _p)
 _sig("orc_apply_repeat_penalty", None, _p, _i64, _p, _i64, _f)
 _sig("orc_argmax_finite", C.c_uint32, _p, _i64)
 _sig("orc_greedy", C.c_uint32, _p, _i64, _p, _i64, _f)
+_sig("orc_expf_array", None, _p, _i64, _p)
 _sig("orc_model_create", _p, _p)
 _sig("orc_model_free", None, _p)
 _sig("orc_model_set_layer", C.c_int, _p, C.c_int32, _p)
@@ -211,6 +212,13 @@ def greedy(logits, recent, penalty):
     r = np.ascontiguousarray(recent, np.uint32)
     tok = lib.orc_greedy(ptr(lg), lg.size, ptr(r) if r.size else None, r.size, penalty)
     return int(tok), lg
+
+
+def expf(x):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib.orc_expf_array(ptr(x), x.size, ptr(out))
+    return out
 
 
 def top_k_router(logits, k):

@@ -31,20 +31,61 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *x, int n
     q8k_block_store(v, blockIdx.x, e, xq, red);
 }
 
+// sum(x*x) in the exact order of dot_f32_avx2(x, x) (src/simd.rs:6547-6586):
+// 32 lanes = four 8-wide FMA accumulators over 32-element chunks, combined as
+// (acc0+acc1)+(acc2+acc3), then the 8-element tail chunks, the hsum_avx tree
+// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)), then the scalar tail.  Every
+// workgroup that calls it computes the same value.  red needs 33 floats.
+__device__ float sumsq_avx2_order(const float *x, int n, float *red) {
+    const int main32 = n / 32;
+    if (threadIdx.x < 32) {
+        const int L = threadIdx.x;
+        float acc = 0.0f;
+        int c = 0;
+        for (; c + 8 <= main32; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = x[32 * (c + j) + L];
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc = fmaf(v[j], v[j], acc);
+        }
+        for (; c < main32; c++) {
+            float v = x[32 * c + L];
+            acc = fmaf(v, v, acc);
+        }
+        red[L] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) t[l] = (red[l] + red[8 + l]) + (red[16 + l] + red[24 + l]);
+        const int ts = main32 * 32, tail8 = (n - ts) / 8;
+        for (int i = 0; i < tail8; i++)
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                float v = x[ts + 8 * i + l];
+                t[l] = fmaf(v, v, t[l]);
+            }
+        float sum = ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
+        for (int i = ts + tail8 * 8; i < n; i++) sum += x[i] * x[i];
+        red[32] = sum;
+    }
+    __syncthreads();
+    float r = red[32];
+    __syncthreads();
+    return r;
+}
+
 // RMSNorm (rms_norm_into, src/model.rs:5429-5437): ss = sum(x^2)/n,
-// scale = 1/sqrt(ss + eps), out = (x*scale)*w.  Every block recomputes the
-// sum with the same thread mapping and reduction tree, so all blocks agree on
-// scale; each block then writes its 256 outputs and, when xq.qs != null and
+// scale = 1/sqrt(ss + eps), out = (x*scale)*w, with the sum in the
+// reference's order (so scale, and everything after it, matches bit for
+// bit).  Each block then writes its 256 outputs and, when xq.qs != null and
 // n % 256 == 0, their Q8_K quantization.
 __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *x, const float *w, float eps, int n,
                                                           float *xn, XQ xq) {
-    __shared__ float red[4];
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        float v = x[i];
-        ss = fmaf(v, v, ss);
-    }
-    ss = block_sum_256(ss, red);
+    __shared__ float red[40];
+    float ss = sumsq_avx2_order(x, n, red);
     float scale = 1.0f / sqrtf(ss / (float)n + eps);
     int e = blockIdx.x * 256 + threadIdx.x;
     float o = 0.0f;

@@ -6,6 +6,7 @@
 // templates directly.
 #include "gemv.hip"
 #include "attention.hip"
+#include "attention_exact.hip"
 #include "ops.hip"
 
 #include <atomic>
@@ -95,6 +96,9 @@ struct Ctx {
     size_t kv_cap = 0;
     int32_t *ibuf = nullptr;
     size_t ibuf_cap = 0;
+    float *ex = nullptr;  // exact-attention scratch: scores | coef | masks
+    size_t ex_cap = 0;
+    int attn_fast = -1;   // -1: read RUSTY_HIP_ATTN once; 0 exact, 1 split-K
     Profile prof;
 };
 static Ctx g;
@@ -520,6 +524,46 @@ static int attn_chunks(int n_kv, int max_ctx) {
     return c < 1 ? 1 : c;
 }
 
+// Attention order: 0 = the reference's serial online-softmax order, bit for
+// bit (default); 1 = split-K flash decode (within the 1e-4 tolerance, not
+// bit-exact).  RUSTY_HIP_ATTN=fast selects 1 before the first call.
+static int attn_fast_mode() {
+    if (g.attn_fast < 0) {
+        const char *e = getenv("RUSTY_HIP_ATTN");
+        g.attn_fast = (e && strcmp(e, "fast") == 0) ? 1 : 0;
+    }
+    return g.attn_fast;
+}
+
+static size_t exact_scratch_floats(int n_heads, int cap) {
+    return (size_t)n_heads * cap * 3 + (size_t)n_heads * (cap / 32);
+}
+
+// Launches the exact attention kernels; cap = positions reserved per head
+// (multiple of 64, >= the longest range this launch may see).
+static int attn_exact_launch(AttnExactArgs A, float *scratch, int grid_tiles, hipStream_t s) {
+    A.scores = scratch;
+    A.coef = (float2 *)(scratch + (size_t)A.n_heads * A.cap);
+    A.newmask = (uint32_t *)(scratch + (size_t)A.n_heads * A.cap * 3);
+    {
+        ProfScope ps("attn_exact_scores", s);
+        size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1)) * sizeof(float);
+        hipLaunchKernelGGL(attn_exact_scores_kernel, dim3(grid_tiles, A.n_kv), dim3(256), lds, s, A);
+        RH_LAUNCH_OK();
+    }
+    {
+        ProfScope ps("attn_exact_coef", s);
+        hipLaunchKernelGGL(attn_exact_coef_kernel, dim3(A.n_heads), dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+    }
+    {
+        ProfScope ps("attn_exact_chain", s);
+        hipLaunchKernelGGL(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
+        RH_LAUNCH_OK();
+    }
+    return 1;
+}
+
 // ---- per-op exports ------------------------------------------------------------------
 static int stage_x(const float *x, size_t n) {
     if (!ensure(&g.x, &g.x_cap, n)) return 0;
@@ -584,6 +628,10 @@ static int ffn_device(const DevW &gate, const DevW &up, const DevW &down, int in
 }  // namespace rh
 
 using namespace rh;
+
+namespace rh {
+void r_invalidate_graphs_extern();
+}
 
 extern "C" {
 
@@ -772,12 +820,64 @@ int rusty_hip_attention(const float *query, uintptr_t query_len, const float *ke
     A.end_t = (int)end_t;
     A.n_chunks = attn_chunks((int)n_kv, (int)(end_t - start_t + 1));
     A.scale = scale;
-    if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * (value_dim + 2))) return 0;
-    A.part = g.part;
-    if (!attn_launch(A, g.s)) return 0;
+    if (attn_fast_mode()) {
+        if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * (value_dim + 2))) return 0;
+        A.part = g.part;
+        if (!attn_launch(A, g.s)) return 0;
+    } else {
+        AttnExactArgs E;
+        memset(&E, 0, sizeof(E));
+        E.q = A.q;
+        E.k = A.k;
+        E.v = A.v;
+        E.sinks = A.sinks;
+        E.out = A.out;
+        E.n_heads = A.n_heads;
+        E.n_kv = A.n_kv;
+        E.kv_mul = A.kv_mul;
+        E.hd = A.hd;
+        E.vd = A.vd;
+        E.key_stride = A.key_stride;
+        E.value_stride = A.value_stride;
+        E.slot_count = A.slot_count;
+        E.start_t = A.start_t;
+        E.end_t = A.end_t;
+        E.scale = scale;
+        int ctx = (int)(end_t - start_t + 1);
+        E.cap = (ctx + 63) / 64 * 64;
+        if (!ensure(&g.ex, &g.ex_cap, exact_scratch_floats(E.n_heads, E.cap))) return 0;
+        if (!attn_exact_launch(E, g.ex, E.cap / EX_TILE, g.s)) return 0;
+    }
     RH_CHECK(hipMemcpyAsync(out, g.y, on * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
+    return 1;
+}
+
+int rusty_hip_attention_mode(int mode) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    int prev = attn_fast_mode();
+    if (mode == 0 || mode == 1) {
+        if (mode != prev) {
+            g.attn_fast = mode;
+            r_invalidate_graphs_extern();
+        }
+    }
+    return prev;
+}
+
+__global__ void expf_kernel(const float *x, int n, float *out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = expf_glibc(x[i]);
+}
+int rusty_hip_debug_expf(const float *x, uintptr_t n, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !x || !out || n == 0) return 0;
+    if (!ensure(&g.x, &g.x_cap, n) || !ensure(&g.y, &g.y_cap, n)) return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, x, n * 4, hipMemcpyHostToDevice, g.s));
+    hipLaunchKernelGGL(expf_kernel, dim3(1024), dim3(256), 0, g.s, g.x, (int)n, g.y);
+    RH_LAUNCH_OK();
+    RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
     return 1;
 }
 
@@ -977,6 +1077,8 @@ struct Resident {
     StepState *st_host = nullptr;  // pinned staging
     float *part = nullptr;
     int n_chunks = 1;
+    float *ex = nullptr;  // exact-attention scratch
+    int ex_cap = 0;
     float *am_v = nullptr;
     int32_t *am_i = nullptr;
     uint32_t *ticket = nullptr;
@@ -1016,6 +1118,7 @@ static void r_invalidate_graphs() {
     for (auto &kv : R.graphs) (void)hipGraphExecDestroy(kv.second);
     R.graphs.clear();
 }
+void r_invalidate_graphs_extern() { r_invalidate_graphs(); }
 
 static int dt_to_fmt(uint32_t dt) {
     switch (dt) {
@@ -1067,7 +1170,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             hipLaunchKernelGGL(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
             RH_LAUNCH_OK();
         }
-        {
+        if (attn_fast_mode()) {
             AttnArgs A;
             memset(&A, 0, sizeof(A));
             A.q = R.q;
@@ -1090,6 +1193,27 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.n_chunks = R.n_chunks;
             A.scale = 1.0f / sqrtf((float)R.hd);
             if (!attn_launch(A, s)) return 0;
+        } else {
+            AttnExactArgs E;
+            memset(&E, 0, sizeof(E));
+            E.q = R.q;
+            E.k = Ly.k;
+            E.v = Ly.v;
+            E.out = R.attn;
+            E.st = R.st;
+            E.n_heads = R.n_heads;
+            E.n_kv = R.n_kv;
+            E.kv_mul = R.n_heads / R.n_kv;
+            E.hd = R.hd;
+            E.vd = R.vd;
+            E.key_stride = kd;
+            E.value_stride = vdim;
+            E.slot_count = R.storage;
+            E.window = 0;
+            E.cap = R.ex_cap;
+            E.scale = 1.0f / sqrtf((float)R.hd);
+            if (!attn_exact_launch(E, R.ex, R.ex_cap / EX_TILE, s)) return 0;
+            if (attn_cols % 256 == 0 && !launch_quant(R.attn, attn_cols, R.xq_attn, s)) return 0;
         }
         MatSpec mo = {Ly.w[3], R.x, nullptr};
         if (!gemv_multi(&mo, 1, attn_cols, EPI_ADD, R.xq_attn, R.attn, s)) return 0;
@@ -1218,6 +1342,8 @@ int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_hea
     R.n_chunks = attn_chunks((int)n_kv_heads, (int)storage_len);
     if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * (value_dim + 2) * 4))
         return 0;
+    R.ex_cap = (int)((storage_len + 63) / 64 * 64);
+    if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_heads, R.ex_cap) * 4)) return 0;
     R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
     if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
         !r_alloc((void **)&R.ticket, 64) || !r_alloc((void **)&R.st, sizeof(StepState)) ||

@@ -30,7 +30,7 @@ SYMBOLS = [
     "rusty_hip_profile_enable", "rusty_hip_profile_get", "rusty_hip_resident_time_decode",
     "rusty_hip_debug_quantize_q8k", "rusty_hip_debug_dequant", "rusty_hip_debug_block_ints",
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
-    "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear",
+    "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
 ]
 
 
@@ -72,6 +72,8 @@ _sig("rusty_hip_resident_kv_read", _i, _u32, _u32, _u32, _u32, _p)
 _sig("rusty_hip_resident_kv_write", _i, _u32, _u32, _u32, _u32, _p)
 _sig("rusty_hip_sync", _i)
 _sig("rusty_hip_weight_cache_clear", _i)
+_sig("rusty_hip_attention_mode", _i, _i)
+_sig("rusty_hip_debug_expf", _i, _p, _u, _p)
 _sig("rusty_hip_profile_enable", _i, _i)
 _sig("rusty_hip_profile_get", _i, _i, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64))
 _sig("rusty_hip_resident_time_decode", _i, _u32, _f, C.POINTER(C.c_double))
@@ -321,6 +323,20 @@ def profile_results():
 
 def sync() -> None:
     lib.rusty_hip_sync()
+
+
+def attention_mode(mode: str | None = None) -> str:
+    """'exact' (reference order, bit for bit; default) or 'fast' (split-K).
+    Returns the mode in force before the call."""
+    code = {"exact": 0, "fast": 1, None: -1}[mode]
+    return "fast" if lib.rusty_hip_attention_mode(code) == 1 else "exact"
+
+
+def debug_expf(x):
+    x = _f32(x)
+    out = np.zeros_like(x)
+    assert lib.rusty_hip_debug_expf(_ptr(x), x.size, _ptr(out)) == 1
+    return out
 
 
 def weight_cache_clear() -> None:

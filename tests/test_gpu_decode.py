@@ -3,7 +3,12 @@ forward_into (src/model.rs:7177-7358) and decode loop (greedy + repeat
 penalty, src/runtime.rs:3266-3342, src/sampling.rs:78-83).
 
 Bars: logits within 1e-2 absolute, greedy token
-streams identical for the first 64 tokens.
+streams identical for the first 64 tokens.  With attention in the reference's
+order (the default) every stage is bit-exact, so logits and KV are asserted
+bit-identical; split-K attention ("fast") is held to the logit bar on short
+runs only, because the int8 (Q8_K) activation path turns its last-bit
+attention differences into growing logit drift (a one-quantum rounding flip
+changes a projection by ~|w|*amax/127).
 """
 import os
 
@@ -22,39 +27,68 @@ def _pair(name, storage, seed=11):
     return model, hip.Resident(model, storage), O.OracleModel(model, storage, threads=16)
 
 
+@pytest.fixture
+def exact(hip):
+    prev = hip.attention_mode("exact")
+    yield
+    hip.attention_mode(prev)
+
+
+@pytest.fixture
+def fast(hip):
+    prev = hip.attention_mode("fast")
+    yield
+    hip.attention_mode(prev)
+
+
 @pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8", "tiny-qwen"])
-def test_host_embedding_decode_logits(hip, name):
+def test_host_embedding_decode_bit_exact(hip, exact, name):
     """rusty_hip_resident_decode with the embedding row from the host, as the
     reference's resident path calls it (src/model.rs:7193-7199)."""
     model, res, orc = _pair(name, 64)
     emb, emb_t = model["token_embd"]
     dim = model["config"]["dim"]
-    toks = synth.token_ids(3, 20, model["config"]["vocab"])
+    toks = synth.token_ids(3, 40, model["config"]["vocab"])
     for pos, t in enumerate(toks):
         x = O.dequant_row(emb_t, emb[int(t) * O.row_bytes(emb_t, dim):], dim)
         g = res.decode(x, pos, 0, True)
         r = orc.forward(int(t), pos)
-        assert np.max(np.abs(g - r)) < 1e-2, (pos, np.max(np.abs(g - r)))
-    # KV cache after 20 positions
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (pos, np.max(np.abs(g - r)))
     for layer in range(model["config"]["n_layers"]):
         for which in (0, 1):
-            gk = res.kv_read(layer, which, 0, 20)
+            gk = res.kv_read(layer, which, 0, 40)
             ok, ov = orc.kv(layer, 64)
-            ref = (ov if which else ok)[: gk.size]
-            assert np.max(np.abs(gk - ref)) <= 1e-4 * np.abs(ref).max()
+            assert np.array_equal(gk, (ov if which else ok)[: gk.size])
+
+
+@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8", "tiny-qwen"])
+def test_fast_attention_decode_logits(hip, fast, name):
+    """Split-K attention stays within 1e-4 x row norm per call (kernel tests),
+    but through the Q8_K activations its last-bit differences grow: logits
+    drift past the 1e-2 bar within ~10 positions on these models.  This mode
+    is therefore not the default; the check here bounds the drift at 5e-2."""
+    model, res, orc = _pair(name, 64)
+    emb, emb_t = model["token_embd"]
+    dim = model["config"]["dim"]
+    toks = synth.token_ids(3, 12, model["config"]["vocab"])
+    for pos, t in enumerate(toks):
+        x = O.dequant_row(emb_t, emb[int(t) * O.row_bytes(emb_t, dim):], dim)
+        g = res.decode(x, pos, 0, True)
+        r = orc.forward(int(t), pos)
+        assert np.max(np.abs(g - r)) < 5e-2, (pos, np.max(np.abs(g - r)))
 
 
 @pytest.mark.parametrize("name,penalty", [("tiny-q4km", 1.1), ("tiny-q8", 1.1), ("tiny-qwen", 1.0)])
-def test_greedy_stream_64_tokens(hip, name, penalty):
+def test_greedy_stream_64_tokens(hip, exact, name, penalty):
     model, res, orc = _pair(name, 160)
     prompt = synth.token_ids(21, 32, model["config"]["vocab"])
     g_toks, g_logits = res.generate(prompt, 64, penalty=penalty)
     o_toks, o_logits = orc.generate(prompt, 64, penalty=penalty)
     assert list(g_toks) == list(o_toks)
-    assert np.max(np.abs(g_logits - o_logits)) < 1e-2
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))
 
 
-def test_graph_replay_matches_eager(hip, monkeypatch):
+def test_graph_replay_matches_eager(hip, exact, monkeypatch):
     model, res, _ = _pair("tiny-q4km", 128, seed=5)
     prompt = synth.token_ids(8, 16, model["config"]["vocab"])
     a, la = res.generate(prompt, 24, penalty=1.1)
@@ -67,7 +101,7 @@ def test_graph_replay_matches_eager(hip, monkeypatch):
 
 
 @pytest.mark.skipif(os.environ.get("RUSTY_HIP_SKIP_LARGE") == "1", reason="large config disabled")
-def test_tinyllama_config1_stream(hip):
+def test_tinyllama_config1_stream(hip, exact):
     """TinyLlama-1.1B shape, Q8_0, 32-token random prompt,
     greedy decode (64 tokens checked against the oracle)."""
     model, res, orc = _pair("tinyllama-1.1b-q8_0", 160, seed=1)
@@ -75,4 +109,4 @@ def test_tinyllama_config1_stream(hip):
     g_toks, g_logits = res.generate(prompt, 64, penalty=1.1)
     o_toks, o_logits = orc.generate(prompt, 64, penalty=1.1)
     assert list(g_toks) == list(o_toks)
-    assert np.max(np.abs(g_logits - o_logits)) < 1e-2
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))

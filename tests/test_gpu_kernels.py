@@ -205,8 +205,15 @@ ATTN = [  # (n_heads, n_kv, head_dim, ctx)
 ]
 
 
+@pytest.fixture(params=["exact", "fast"])
+def attn_mode(request, hip):
+    prev = hip.attention_mode(request.param)
+    yield request.param
+    hip.attention_mode(prev)
+
+
 @pytest.mark.parametrize("nh,nkv,hd,ctx", ATTN)
-def test_attention_vs_oracle(hip, nh, nkv, hd, ctx):
+def test_attention_vs_oracle(hip, attn_mode, nh, nkv, hd, ctx):
     rng = np.random.default_rng(ctx + nh)
     slots = ctx + 5
     q = rng.standard_normal(nh * hd).astype(np.float32)
@@ -216,6 +223,9 @@ def test_attention_vs_oracle(hip, nh, nkv, hd, ctx):
     out = np.zeros(nh * hd, np.float32)
     assert hip.attention_into(q, K, V, out, nh, nh // nkv, hd, hd, nkv * hd, nkv * hd, slots, 0, ctx - 1, scale)
     ref = O.attention(q, K, V, nh, nkv, hd, hd, nkv * hd, nkv * hd, slots, 0, ctx - 1, scale)
+    if attn_mode == "exact":
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        return
     o = out.reshape(nh, hd)
     r = ref.reshape(nh, hd)
     err = np.abs(o - r).max(axis=1)
@@ -223,7 +233,7 @@ def test_attention_vs_oracle(hip, nh, nkv, hd, ctx):
 
 
 @pytest.mark.parametrize("window,pos,slots", [(128, 300, 128), (128, 50, 128), (16, 40, 16)])
-def test_attention_sink_window_ring(hip, window, pos, slots):
+def test_attention_sink_window_ring(hip, attn_mode, window, pos, slots):
     rng = np.random.default_rng(pos)
     nh, nkv, hd = 64, 8, 64
     q = rng.standard_normal(nh * hd).astype(np.float32)
@@ -236,19 +246,41 @@ def test_attention_sink_window_ring(hip, window, pos, slots):
         assert hip.attention_with_sink_into(q, K, V, sinks, out, nh, nh // nkv, hd, hd, nkv * hd, nkv * hd, slots,
                                             start, pos, scale)
         ref = O.attention(q, K, V, nh, nkv, hd, hd, nkv * hd, nkv * hd, slots, start, pos, scale, sinks=sinks)
+        if attn_mode == "exact":
+            assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+            continue
         r = ref.reshape(nh, hd)
         err = np.abs(out.reshape(nh, hd) - r).max(axis=1)
         assert np.all(err <= 1e-4 * np.linalg.norm(r, axis=1) + 1e-7)
 
 
-def test_rmsnorm_close(hip):
+def test_rmsnorm_bit_exact(hip):
+    """The sum of squares follows dot_f32_avx2's lane and tree order, so the
+    normalised vector matches rms_norm_into bit for bit (incl. tails)."""
     rng = np.random.default_rng(3)
-    for n in (2048, 4096, 5120, 2880):
-        x = rng.standard_normal(n).astype(np.float32)
+    for n in (2048, 4096, 5120, 2880, 256, 300, 77):
+        x = (rng.standard_normal(n) * rng.uniform(0.01, 30)).astype(np.float32)
         w = rng.uniform(0.5, 1.5, n).astype(np.float32)
         got = hip.debug_rmsnorm(x, w, 1e-5)
         ref = O.rms_norm(x, w, 1e-5)
-        assert np.max(np.abs(got - ref) / np.abs(ref).max()) < 2e-7
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), n
+
+
+def test_expf_bit_exact(hip):
+    """Device expf (restated glibc algorithm) equals the host's libm expf."""
+    rng = np.random.default_rng(12)
+    x = np.concatenate([
+        rng.uniform(-110, 90, 1 << 23).astype(np.float32),
+        -np.abs(rng.standard_normal(1 << 22)).astype(np.float32) * 20,
+        np.array([0.0, -0.0, 88.0, 88.72283, 88.72284, -103.97, -103.28, -87.3, 1e-30, -1e-30,
+                  np.inf, -np.inf, np.nan], np.float32),
+        (np.arange(1 << 21, dtype=np.uint32) * 2047).view(np.float32),
+    ])
+    got = hip.debug_expf(x)
+    ref = O.expf(x)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
 
 
 def test_silu_mul_bit_exact(hip):
