@@ -178,116 +178,82 @@ __device__ __forceinline__ int q6k_unit(const Q6KLoad &L, int q, const int32_t *
     return isum;
 }
 
-template <int ITERS, int R>
-__global__ __launch_bounds__(256) void gemv_kquant_kernel(GemvArgs A) {
-    __shared__ int32_t s_xq[KMAX / 4];
-    __shared__ float s_dx[NB256_MAX];
-    __shared__ int16_t s_bs[NB32_MAX];
-    __shared__ int16_t s_s16[KMAX / 16];
-    __shared__ float s_v[4 * R][NB256_MAX];
+// One unit's raw bytes, either format: Q4_K uses a = header (d, dmin, 12
+// scale bytes), b/c = its 32 qs bytes; Q6_K uses a/b = ql bytes, c = qh bytes,
+// sc = its 8 scale bytes, dd = d.
+struct UnitLoad {
+    uint4 a, b, c;
+    uint2 sc;
+    uint32_t dd;
+};
 
-    const int K = A.K, nb = K >> 8;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    {
-        const int4 *src = (const int4 *)A.xq.qs;
-        int4 *dst = (int4 *)s_xq;
-        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
-        for (int i = tid; i < nb; i += 256) s_dx[i] = A.xq.d[i];
-        for (int i = tid; i < K / 32; i += 256) s_bs[i] = A.xq.bsums[i];
-        for (int i = tid; i < K / 16; i += 256) s_s16[i] = A.xq.sums16[i];
+__device__ __forceinline__ UnitLoad unit_load(const uint8_t *blk, int fmt, int q) {
+    UnitLoad L;
+    if (fmt == F_Q4_K) {
+        L.a = *(const uint4 *)blk;  // 144-byte blocks of 16-aligned rows are 16-aligned
+        L.b = *(const uint4 *)(blk + 16 + 32 * q);
+        L.c = *(const uint4 *)(blk + 32 + 32 * q);
+    } else {
+        int g = q >> 1, j = q & 1;
+        L.a = ld16(blk + 64 * g + 16 * j);
+        L.b = ld16(blk + 64 * g + 32 + 16 * j);
+        L.c = ld16(blk + 128 + 32 * g + 16 * j);
+        L.sc = ld8(blk + 192 + 8 * g);
+        L.dd = ld2(blk + 208);
     }
-    __syncthreads();
-
-    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
-        int mi = 0;
-#pragma unroll
-        for (int t = 1; t < GEMV_MAX_MATS; t++)
-            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        const GemvMat M = A.m[mi];
-        int row0 = (tile - M.tile_begin) * (4 * R);
-        int wrow0 = row0 + wave * R;
-
-        if (M.fmt == F_Q4_K) {
-            Q4KLoad L[R][ITERS];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2;
-                    int row = wrow0 + r;
-                    if (b < nb && row < M.rows) L[r][i] = q4k_load(M.w + (int64_t)row * M.row_stride + b * 144, u & 3);
-                }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
-                    int row = wrow0 + r;
-                    bool ok = b < nb && row < M.rows;
-                    int isum = 0, imin = 0;
-                    if (ok) q4k_unit(L[r][i], q, s_xq + b * 64, s_bs + b * 8, isum, imin);
-                    isum = quad_sum_i32(isum);
-                    imin = quad_sum_i32(imin);
-                    if (ok && q == 0) {
-                        float d = h2f(L[r][i].hdr.x & 0xFFFF), dmin = h2f(L[r][i].hdr.x >> 16);
-                        float t1 = d * (float)isum;
-                        float t2 = dmin * (float)imin;
-                        s_v[wave * R + r][b] = s_dx[b] * (t1 - t2);
-                    }
-                }
-        } else {
-            Q6KLoad L[R][ITERS];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2;
-                    int row = wrow0 + r;
-                    if (b < nb && row < M.rows) L[r][i] = q6k_load(M.w + (int64_t)row * M.row_stride + b * 210, u & 3);
-                }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
-                    int row = wrow0 + r;
-                    bool ok = b < nb && row < M.rows;
-                    int isum = 0;
-                    if (ok) isum = q6k_unit(L[r][i], q, s_xq + b * 64, s_s16 + b * 16);
-                    isum = quad_sum_i32(isum);
-                    if (ok && q == 0) {
-                        float d = h2f(L[r][i].d & 0xFFFF);
-                        s_v[wave * R + r][b] = (s_dx[b] * d) * (float)isum;
-                    }
-                }
-        }
-        __syncthreads();
-        if (tid < 4 * R) {
-            int row = row0 + tid;
-            if (row < M.rows) {
-                float acc = 0.0f;
-                for (int b = 0; b < nb; b++) acc += s_v[tid][b];
-                if (M.bias) acc += M.bias[row];
-                if (A.epi == EPI_ADD)
-                    M.y[row] += acc;
-                else
-                    M.y[row] = acc;
-            }
-        }
-        __syncthreads();
-    }
+    return L;
 }
 
-// Gate/up pair with the SwiGLU epilogue (EPI_SWIGLU): m[0] = gate, m[1] = up,
-// same row count.  A tile is 2R rows; waves 0-1 take them from the gate matrix
-// and waves 2-3 the same rows of up, so one thread can finish silu(g) * u.
-template <int ITERS, int R>
-__global__ __launch_bounds__(256) void gemv_kquant_swiglu_kernel(GemvArgs A) {
+// f32 value of one 256-block, summed over the block's four units (quad).  The
+// integer parts are exact; the f32 combine is the reference's own sequence
+// (dot_q4_k_q8k_avx2: dx*(d*isum - dmin*imin); dot_q6_k_q8k_avx2:
+// (dx*d)*isum).  Valid in lane q == 0 of each quad.
+__device__ __forceinline__ float unit_block_value(const UnitLoad &L, int fmt, int q, bool ok, const int32_t *xq32,
+                                                  const int16_t *bs, const int16_t *s16, float dx) {
+    if (fmt == F_Q4_K) {
+        int isum = 0, imin = 0;
+        if (ok) {
+            Q4KLoad Q;
+            Q.hdr = L.a;
+            Q.a = L.b;
+            Q.b = L.c;
+            q4k_unit(Q, q, xq32, bs, isum, imin);
+        }
+        isum = quad_sum_i32(isum);
+        imin = quad_sum_i32(imin);
+        float d = h2f(L.a.x & 0xFFFF), dmin = h2f(L.a.x >> 16);
+        float t1 = d * (float)isum;
+        float t2 = dmin * (float)imin;
+        return dx * (t1 - t2);
+    }
+    int isum = 0;
+    if (ok) {
+        Q6KLoad Q;
+        Q.ql0 = L.a;
+        Q.ql1 = L.b;
+        Q.qh = L.c;
+        Q.sc = L.sc;
+        Q.d = L.dd;
+        isum = q6k_unit(Q, q, xq32, s16);
+    }
+    isum = quad_sum_i32(isum);
+    return (dx * h2f(L.dd & 0xFFFF)) * (float)isum;
+}
+
+// K-quant GEMV.  Workgroups are persistent: the Q8_K activation is staged in
+// LDS once, then every wave takes tiles of R rows (SWIGLU: R gate rows and the
+// same R up rows) in a grid-stride loop.  Unit u = lane + 64*i of a row is
+// quarter u&3 of block u>>2; each block's value goes to a wave-private LDS row
+// and lane r sums row r in block order, so there is no workgroup barrier in
+// the loop.
+template <int ITERS, int R, bool SWIGLU>
+__global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
+    constexpr int NM = SWIGLU ? 2 : 1;
     __shared__ int32_t s_xq[KMAX / 4];
     __shared__ float s_dx[NB256_MAX];
     __shared__ int16_t s_bs[NB32_MAX];
     __shared__ int16_t s_s16[KMAX / 16];
-    __shared__ float s_v[4 * R][NB256_MAX];
+    __shared__ float s_v[4][NM * R][NB256_MAX];
 
     const int K = A.K, nb = K >> 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -301,76 +267,68 @@ __global__ __launch_bounds__(256) void gemv_kquant_swiglu_kernel(GemvArgs A) {
     }
     __syncthreads();
 
-    const int half = wave >> 1;  // 0 = gate, 1 = up
-    const GemvMat M = A.m[half];
-    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
-        int row0 = tile * (2 * R);
-        int wrow0 = row0 + (wave & 1) * R;
-        if (M.fmt == F_Q4_K) {
-            Q4KLoad L[R][ITERS];
+    const int nwaves = gridDim.x * 4;
+    for (int tile = blockIdx.x * 4 + wave; tile < A.n_tiles; tile += nwaves) {
+        int mi = 0;
+        if (!SWIGLU) {
+#pragma unroll
+            for (int t = 1; t < GEMV_MAX_MATS; t++)
+                if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+        }
+        const int row0 = (tile - A.m[mi].tile_begin) * R;
+        UnitLoad L[NM][R][ITERS];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const GemvMat &M = A.m[SWIGLU ? m : mi];
+            const int bsz = M.fmt == F_Q4_K ? 144 : 210;
 #pragma unroll
             for (int r = 0; r < R; r++)
 #pragma unroll
                 for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2;
-                    int row = wrow0 + r;
-                    if (b < nb && row < M.rows) L[r][i] = q4k_load(M.w + (int64_t)row * M.row_stride + b * 144, u & 3);
-                }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
-                    int row = wrow0 + r;
-                    bool ok = b < nb && row < M.rows;
-                    int isum = 0, imin = 0;
-                    if (ok) q4k_unit(L[r][i], q, s_xq + b * 64, s_bs + b * 8, isum, imin);
-                    isum = quad_sum_i32(isum);
-                    imin = quad_sum_i32(imin);
-                    if (ok && q == 0) {
-                        float d = h2f(L[r][i].hdr.x & 0xFFFF), dmin = h2f(L[r][i].hdr.x >> 16);
-                        float t1 = d * (float)isum;
-                        float t2 = dmin * (float)imin;
-                        s_v[wave * R + r][b] = s_dx[b] * (t1 - t2);
-                    }
-                }
-        } else {
-            Q6KLoad L[R][ITERS];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2;
-                    int row = wrow0 + r;
-                    if (b < nb && row < M.rows) L[r][i] = q6k_load(M.w + (int64_t)row * M.row_stride + b * 210, u & 3);
-                }
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, q = u & 3;
-                    int row = wrow0 + r;
-                    bool ok = b < nb && row < M.rows;
-                    int isum = 0;
-                    if (ok) isum = q6k_unit(L[r][i], q, s_xq + b * 64, s_s16 + b * 16);
-                    isum = quad_sum_i32(isum);
-                    if (ok && q == 0) {
-                        float d = h2f(L[r][i].d & 0xFFFF);
-                        s_v[wave * R + r][b] = (s_dx[b] * d) * (float)isum;
-                    }
+                    int u = lane + 64 * i, b = u >> 2, row = row0 + r;
+                    if (b < nb && row < M.rows) L[m][r][i] = unit_load(M.w + (int64_t)row * M.row_stride + b * bsz, M.fmt, u & 3);
                 }
         }
-        __syncthreads();
-        if (tid < 2 * R) {
-            int row = row0 + tid;
-            if (row < A.m[0].rows) {
-                float g = 0.0f, u = 0.0f;
-                for (int b = 0; b < nb; b++) g += s_v[tid][b];
-                for (int b = 0; b < nb; b++) u += s_v[2 * R + tid][b];
-                A.m[0].y[row] = silu_mul_ref(g, u);
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const GemvMat &M = A.m[SWIGLU ? m : mi];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int i = 0; i < ITERS; i++) {
+                    int u = lane + 64 * i, b = u >> 2, q = u & 3, row = row0 + r;
+                    bool ok = b < nb && row < M.rows;
+                    int bb = b < nb ? b : 0;
+                    float v = unit_block_value(L[m][r][i], M.fmt, q, ok, s_xq + bb * 64, s_bs + bb * 8, s_s16 + bb * 16,
+                                               s_dx[bb]);
+                    if (ok && q == 0) s_v[wave][m * R + r][b] = v;
+                }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < R) {
+            const int row = row0 + lane;
+            const GemvMat &M = A.m[mi];
+            if (row < M.rows) {
+                float acc = 0.0f;
+                for (int b = 0; b < nb; b++) acc += s_v[wave][lane][b];
+                if (SWIGLU) {
+                    float u = 0.0f;
+                    for (int b = 0; b < nb; b++) u += s_v[wave][R + lane][b];
+                    A.m[0].y[row] = silu_mul_ref(acc, u);
+                } else {
+                    if (M.bias) acc += M.bias[row];
+                    if (A.epi == EPI_ADD)
+                        M.y[row] += acc;
+                    else
+                        M.y[row] = acc;
+                }
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 

@@ -293,6 +293,9 @@ struct MatSpec {
 };
 
 enum Cat { CAT_KQ = 1, CAT_Q8I = 2, CAT_F32 = 3 };
+#ifndef KQ_R1
+#define KQ_R1 2  // rows per wave tile for K-quant rows of <= 16 blocks
+#endif
 static int cat_of(int fmt, int K) {
     if (fmt == 12 || fmt == 14) return K % 256 == 0 && K <= KMAX ? CAT_KQ : 0;
     if (fmt == 8) {
@@ -305,19 +308,32 @@ static int cat_of(int fmt, int K) {
 
 static int grid_cap() { return g.n_cu * 8; }
 
-template <int IT, int R>
-static int launch_kq(const GemvArgs &A, hipStream_t s) {
-    int grid = std::min(A.n_tiles, grid_cap());
-    ProfScope ps("gemv_kquant", s);
-    hipLaunchKernelGGL((gemv_kquant_kernel<IT, R>), dim3(grid), dim3(256), 0, s, A);
-    RH_LAUNCH_OK();
-    return 1;
+// Persistent grid: as many workgroups as fit on the device at once (queried
+// once per kernel instantiation), never more than the tiles need.
+template <class Kern>
+static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
+    static std::map<const void *, int> occ;
+    auto it = occ.find((const void *)kernel);
+    int per_cu;
+    if (it == occ.end()) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, 256, 0) != hipSuccess || nb <= 0) nb = 2;
+        occ[(const void *)kernel] = nb;
+        per_cu = nb;
+    } else {
+        per_cu = it->second;
+    }
+    int need = (n_tiles + waves_per_wg - 1) / waves_per_wg;
+    int grid = std::min(need, per_cu * g.n_cu);
+    return grid < 1 ? 1 : grid;
 }
-template <int IT, int R>
-static int launch_kq_swiglu(const GemvArgs &A, hipStream_t s) {
-    int grid = std::min(A.n_tiles, grid_cap());
-    ProfScope ps("gemv_kquant_swiglu", s);
-    hipLaunchKernelGGL((gemv_kquant_swiglu_kernel<IT, R>), dim3(grid), dim3(256), 0, s, A);
+
+template <int IT, int R, bool SW>
+static int launch_kq(const GemvArgs &A, hipStream_t s) {
+    auto kern = gemv_kq_kernel<IT, R, SW>;
+    int grid = persistent_grid(kern, A.n_tiles, 4);
+    ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -345,8 +361,8 @@ static void pick_iters(int cat, int K, int *it, int *r) {
     int units = (cat == CAT_KQ) ? (K / 256) * 4 : K / 32;
     int iters = (units + 63) / 64;
     if (cat == CAT_KQ) {
-        if (iters <= 1) { *it = 1; *r = 4; }
-        else if (iters == 2) { *it = 2; *r = 2; }
+        if (iters <= 1) { *it = 1; *r = KQ_R1; }
+        else if (iters == 2) { *it = 2; *r = 1; }
         else if (iters == 3) { *it = 3; *r = 1; }
         else { *it = 4; *r = 1; }
     } else {
@@ -377,7 +393,7 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, cons
     A.x = xf;
     A.n_mats = n;
     int tiles = 0;
-    int rows_per_tile = (epi == EPI_SWIGLU) ? 2 * r : 4 * r;
+    int rows_per_tile = (cat == CAT_KQ) ? r : 4 * r;
     for (int i = 0; i < n; i++) {
         GemvMat &m = A.m[i];
         m.w = ms[i].w.p;
@@ -397,17 +413,17 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, cons
     if (cat == CAT_KQ) {
         if (epi == EPI_SWIGLU) {
             switch (it) {
-            case 1: return launch_kq_swiglu<1, 4>(A, s);
-            case 2: return launch_kq_swiglu<2, 2>(A, s);
-            case 3: return launch_kq_swiglu<3, 1>(A, s);
-            default: return launch_kq_swiglu<4, 1>(A, s);
+            case 1: return launch_kq<1, KQ_R1, true>(A, s);
+            case 2: return launch_kq<2, 1, true>(A, s);
+            case 3: return launch_kq<3, 1, true>(A, s);
+            default: return launch_kq<4, 1, true>(A, s);
             }
         }
         switch (it) {
-        case 1: return launch_kq<1, 4>(A, s);
-        case 2: return launch_kq<2, 2>(A, s);
-        case 3: return launch_kq<3, 1>(A, s);
-        default: return launch_kq<4, 1>(A, s);
+        case 1: return launch_kq<1, KQ_R1, false>(A, s);
+        case 2: return launch_kq<2, 1, false>(A, s);
+        case 3: return launch_kq<3, 1, false>(A, s);
+        default: return launch_kq<4, 1, false>(A, s);
         }
     }
     if (cat == CAT_Q8I) {
