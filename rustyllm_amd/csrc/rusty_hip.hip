@@ -6,8 +6,8 @@
 // templates directly.
 #include "gemv.hip"
 #include "attention.hip"
-#include "attention_exact.hip"
 #include "ops.hip"
+#include "attention_exact.hip"
 
 #include <atomic>
 #include <cmath>
@@ -551,30 +551,57 @@ static int attn_fast_mode() {
     return g.attn_fast;
 }
 
-static size_t exact_scratch_floats(int n_heads, int cap) {
-    return (size_t)n_heads * cap * 3 + (size_t)n_heads * (cap / 32);
+static size_t exact_e_floats(int n_kv, int kv_mul, int cap) {
+    return (size_t)n_kv * ((kv_mul + 3) / 4) * cap * 4;
+}
+static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
+    size_t n = (size_t)n_kv * kv_mul;
+    return n * cap + exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
 }
 
 // Launches the exact attention kernels; cap = positions reserved per head
-// (multiple of 64, >= the longest range this launch may see).
-static int attn_exact_launch(AttnExactArgs A, float *scratch, int grid_tiles, hipStream_t s) {
+// (multiple of 64, >= the longest range this launch may see).  The output is
+// normalised in place and, when xq.qs is set, quantized to Q8_K
+// (n_heads * vd must then be a multiple of 256).
+static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s) {
+    const size_t nh = (size_t)A.n_heads, cap = (size_t)A.cap;
+    const int ntl = A.cap / EX_TILE;
     A.scores = scratch;
-    A.coef = (float2 *)(scratch + (size_t)A.n_heads * A.cap);
-    A.newmask = (uint32_t *)(scratch + (size_t)A.n_heads * A.cap * 3);
+    A.e = scratch + nh * cap;
+    A.tmax = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
+    A.newmask = (uint32_t *)(A.tmax + nh * (cap / 64));
+    A.den = (float *)(A.newmask + nh * (cap / 32));
+    A.kvec = (A.key_stride % 4 == 0 && A.hd % 4 == 0 && ((uintptr_t)A.k & 15) == 0) ? 1 : 0;
+    const int n_out = A.n_heads * A.vd;
+    if (xq.qs && n_out % 256 != 0) return 0;
     {
         ProfScope ps("attn_exact_scores", s);
-        size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1)) * sizeof(float);
-        hipLaunchKernelGGL(attn_exact_scores_kernel, dim3(grid_tiles, A.n_kv), dim3(256), lds, s, A);
+        size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1) + (size_t)A.kv_mul * EX_TILE) *
+                     sizeof(float);
+        hipLaunchKernelGGL(attn_exact_scores_kernel, dim3(ntl, A.n_kv), dim3(256), lds, s, A);
         RH_LAUNCH_OK();
     }
     {
         ProfScope ps("attn_exact_coef", s);
-        hipLaunchKernelGGL(attn_exact_coef_kernel, dim3(A.n_heads), dim3(256), 0, s, A);
+        hipLaunchKernelGGL(attn_exact_coef_kernel, dim3(ntl, A.n_heads), dim3(64), 0, s, A);
         RH_LAUNCH_OK();
     }
     {
         ProfScope ps("attn_exact_chain", s);
-        hipLaunchKernelGGL(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
+        const bool dma = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
+                         A.slot_count >= 64 && (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
+        if (dma) {
+            int blocks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
+            hipLaunchKernelGGL(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64), 0, s, A);
+        } else {
+            hipLaunchKernelGGL(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
+        }
+        RH_LAUNCH_OK();
+    }
+    {
+        ProfScope ps("attn_exact_finish", s);
+        hipLaunchKernelGGL(attn_exact_finish_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, A.out, A.den, A.vd,
+                           n_out, xq);
         RH_LAUNCH_OK();
     }
     return 1;
@@ -861,8 +888,8 @@ int rusty_hip_attention(const float *query, uintptr_t query_len, const float *ke
         E.scale = scale;
         int ctx = (int)(end_t - start_t + 1);
         E.cap = (ctx + 63) / 64 * 64;
-        if (!ensure(&g.ex, &g.ex_cap, exact_scratch_floats(E.n_heads, E.cap))) return 0;
-        if (!attn_exact_launch(E, g.ex, E.cap / EX_TILE, g.s)) return 0;
+        if (!ensure(&g.ex, &g.ex_cap, exact_scratch_floats(E.n_kv, E.kv_mul, E.cap))) return 0;
+        if (!attn_exact_launch(E, g.ex, XQ{}, g.s)) return 0;
     }
     RH_CHECK(hipMemcpyAsync(out, g.y, on * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
@@ -1228,8 +1255,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.window = 0;
             E.cap = R.ex_cap;
             E.scale = 1.0f / sqrtf((float)R.hd);
-            if (!attn_exact_launch(E, R.ex, R.ex_cap / EX_TILE, s)) return 0;
-            if (attn_cols % 256 == 0 && !launch_quant(R.attn, attn_cols, R.xq_attn, s)) return 0;
+            if (!attn_exact_launch(E, R.ex, attn_cols % 256 == 0 ? R.xq_attn : XQ{}, s)) return 0;
         }
         MatSpec mo = {Ly.w[3], R.x, nullptr};
         if (!gemv_multi(&mo, 1, attn_cols, EPI_ADD, R.xq_attn, R.attn, s)) return 0;
@@ -1359,7 +1385,7 @@ int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_hea
     if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * (value_dim + 2) * 4))
         return 0;
     R.ex_cap = (int)((storage_len + 63) / 64 * 64);
-    if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_heads, R.ex_cap) * 4)) return 0;
+    if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_kv_heads, (int)(n_heads / n_kv_heads), R.ex_cap) * 4)) return 0;
     R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
     if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
         !r_alloc((void **)&R.ticket, 64) || !r_alloc((void **)&R.st, sizeof(StepState)) ||
