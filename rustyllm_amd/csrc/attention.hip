@@ -61,7 +61,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs A) {
     __shared__ float s_run[KVMUL][3];  // running max, running denominator, rescale
 
     const int c = blockIdx.x, h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
     int start_t, end_t;
     attn_range(A, start_t, end_t);
     const int ctx = end_t - start_t + 1;

@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A)
     const int ctx = e0 - s0 + 1;
     const int t_base = blockIdx.x * EX_TILE;
     if (ctx <= 0 || t_base >= ctx) return;
-    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nt = min(EX_TILE, ctx - t_base);
     for (int i = tid; i < kvm * hd; i += 256) s_q[i] = A.q[(size_t)h * kvm * hd + i];
     const float *kh = A.k + (size_t)h * hd;

@@ -40,15 +40,40 @@ struct GemvMat {
 
 #define GEMV_MAX_MATS 4
 
+// The Q8_K activation a launch consumes is always prepared by a standalone
+// kernel (host ActSpec); building it inside every GEMV workgroup was measured
+// slower (each workgroup repeats the work ahead of its first tile).
 struct GemvArgs {
     GemvMat m[GEMV_MAX_MATS];
     int32_t n_mats;
     int32_t n_tiles;
     int32_t K;
     int32_t epi;
-    XQ xq;            // Q8_K activation (int paths)
-    const float *x;   // f32 activation (f32 paths)
+    int32_t tile_rows;  // K-quant kernel: rows per wave tile (per matrix for SWIGLU)
+    XQ xq;              // Q8_K activation (int paths)
+    const float *x;     // f32 activation (f32 paths)
 };
+
+// Matrix mi of a launch with mi wave-uniform.  The byval kernel argument
+// must not be indexed with a run-time value (the compiler then copies it to
+// scratch and reads it back with vector loads followed by vmcnt(0) waits,
+// which drain every weight load in flight).  The descriptor is read instead
+// through the kernarg segment pointer: GemvArgs is each kernel's first
+// argument, at offset 0, so these are scalar loads at a uniform offset.
+typedef const __attribute__((address_space(4))) GemvArgs KGemvArgs;
+__device__ __forceinline__ GemvMat mat_sel(const GemvArgs &, int mi) {
+    KGemvArgs *ka = (KGemvArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    GemvMat r;
+    r.w = ka->m[mi].w;
+    r.row_stride = ka->m[mi].row_stride;
+    r.rows = ka->m[mi].rows;
+    r.fmt = ka->m[mi].fmt;
+    r.y = ka->m[mi].y;
+    r.bias = ka->m[mi].bias;
+    r.tile_begin = ka->m[mi].tile_begin;
+    r.pad = 0;
+    return r;
+}
 
 #define KMAX 16384
 #define NB256_MAX (KMAX / 256)
@@ -178,18 +203,18 @@ __device__ __forceinline__ int q6k_unit(const Q6KLoad &L, int q, const int32_t *
     return isum;
 }
 
-// One unit's raw bytes, either format: Q4_K uses a = header (d, dmin, 12
-// scale bytes), b/c = its 32 qs bytes; Q6_K uses a/b = ql bytes, c = qh bytes,
-// sc = its 8 scale bytes, dd = d.
+// One unit's raw bytes: Q4_K uses a = header (d, dmin, 12 scale bytes),
+// b/c = its 32 qs bytes; Q6_K uses a/b = ql bytes, c = qh bytes, sc = its 8
+// scale bytes, dd = d.
 struct UnitLoad {
     uint4 a, b, c;
     uint2 sc;
     uint32_t dd;
 };
 
-__device__ __forceinline__ UnitLoad unit_load(const uint8_t *blk, int fmt, int q) {
-    UnitLoad L;
-    if (fmt == F_Q4_K) {
+template <int FMT>
+__device__ __forceinline__ void unit_load(const uint8_t *blk, int q, UnitLoad &L) {
+    if (FMT == F_Q4_K) {
         L.a = *(const uint4 *)blk;  // 144-byte blocks of 16-aligned rows are 16-aligned
         L.b = *(const uint4 *)(blk + 16 + 32 * q);
         L.c = *(const uint4 *)(blk + 32 + 32 * q);
@@ -201,16 +226,16 @@ __device__ __forceinline__ UnitLoad unit_load(const uint8_t *blk, int fmt, int q
         L.sc = ld8(blk + 192 + 8 * g);
         L.dd = ld2(blk + 208);
     }
-    return L;
 }
 
-// f32 value of one 256-block, summed over the block's four units (quad).  The
-// integer parts are exact; the f32 combine is the reference's own sequence
-// (dot_q4_k_q8k_avx2: dx*(d*isum - dmin*imin); dot_q6_k_q8k_avx2:
-// (dx*d)*isum).  Valid in lane q == 0 of each quad.
-__device__ __forceinline__ float unit_block_value(const UnitLoad &L, int fmt, int q, bool ok, const int32_t *xq32,
+// f32 value of one 256-block from its four units (one per lane of a quad).
+// The integer parts are exact; the f32 combine is the reference's own
+// sequence (dot_q4_k_q8k_avx2: dx*(d*isum - dmin*imin); dot_q6_k_q8k_avx2:
+// (dx*d)*isum).  Every lane of the quad returns the value.
+template <int FMT>
+__device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, bool ok, const int32_t *xq32,
                                                   const int16_t *bs, const int16_t *s16, float dx) {
-    if (fmt == F_Q4_K) {
+    if (FMT == F_Q4_K) {
         int isum = 0, imin = 0;
         if (ok) {
             Q4KLoad Q;
@@ -240,95 +265,184 @@ __device__ __forceinline__ float unit_block_value(const UnitLoad &L, int fmt, in
     return (dx * h2f(L.dd & 0xFFFF)) * (float)isum;
 }
 
-// K-quant GEMV.  Workgroups are persistent: the Q8_K activation is staged in
-// LDS once, then every wave takes tiles of R rows (SWIGLU: R gate rows and the
-// same R up rows) in a grid-stride loop.  Unit u = lane + 64*i of a row is
-// quarter u&3 of block u>>2; each block's value goes to a wave-private LDS row
-// and lane r sums row r in block order, so there is no workgroup barrier in
-// the loop.
-template <int ITERS, int R, bool SWIGLU>
+// K-quant GEMV.  A wave tile is TR rows x all nb blocks, 4*TR*nb <= 256
+// quarter-block units, so every lane owns at most KQ_U = 4 units (unit u =
+// lane + 64*i is quarter u&3 of block (u>>2)%nb of tile row (u>>2)/nb).  Each
+// block's f32 value goes to a wave-private LDS row; lane r then sums row r
+// serially in block order (the reference's accumulation order).  Waves are
+// persistent over tiles and load the next tile's weights before computing the
+// current one; the Q8_K activation is staged in LDS once per workgroup while
+// the first tile's weights are in flight.  SWIGLU tiles hold TR gate rows
+// followed by the same TR up rows.  FM: 1 = Q4_K only, 2 = Q6_K only, 3 = a
+// launch mixing both (the format is uniform per tile).
+#define KQ_U_MAX 4
+#define KQ_XQ_IT (KMAX / 16 / 256)
+
+struct KqTile {
+    GemvMat M;  // the tile's matrix (SWIGLU: the gate matrix)
+    int row0, valid;
+};
+
+template <int FMT, bool SWIGLU, int KQ_U>
+__device__ __forceinline__ void kq_load_tile(const GemvArgs &A, const KqTile &T, int tr, int nb, int lane,
+                                             UnitLoad (&L)[KQ_U]) {
+    // Every lane issues the same loads on every path (units past the tile or
+    // the matrix read row 0, block 0 and are discarded), so the compiler's
+    // vmcnt bookkeeping stays exact and the next tile's loads stay in flight
+    // while this tile computes.
+    const int units = (SWIGLU ? 2 : 1) * tr * nb * 4;
+#pragma unroll
+    for (int i = 0; i < KQ_U; i++) {
+        const int u = lane + 64 * i;
+        const int rt = (u >> 2) / nb, b = (u >> 2) - rt * nb;
+        const bool up = SWIGLU && rt >= tr;
+        const int row = T.row0 + (up ? rt - tr : rt);
+        const uint8_t *w = up ? A.m[1].w : T.M.w;
+        const int64_t stride = up ? A.m[1].row_stride : T.M.row_stride;
+        const int rows = up ? A.m[1].rows : T.M.rows;
+        const bool ok = T.valid && u < units && row < rows;
+        const int64_t off = ok ? (int64_t)row * stride + b * (FMT == F_Q4_K ? 144 : 210) : 0;
+        unit_load<FMT>(w + off, u & 3, L[i]);
+    }
+}
+
+// Epilogue operands of a tile (lane r: row row0 + r), loaded before the next
+// tile's weights so that waiting for them does not wait for those.  The loads
+// are unconditional (clamped row, y standing in for a null bias).
+struct KqEpi {
+    float bias, y;
+};
+template <bool SWIGLU>
+__device__ __forceinline__ KqEpi kq_epi_load(const KqTile &T, int lane) {
+    KqEpi E = {0.0f, 0.0f};
+    if (!SWIGLU) {
+        const int row = min(T.row0 + lane, T.M.rows - 1);
+        const float *bp = T.M.bias ? T.M.bias : T.M.y;
+        E.bias = bp[row];
+        E.y = T.M.y[row];
+    }
+    return E;
+}
+
+template <int FMT, bool SWIGLU, int KQ_U>
+__device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile &T, const KqEpi &E, int tr, int nb,
+                                                int lane, const UnitLoad (&L)[KQ_U], const int32_t *s_xq,
+                                                const float *s_dx, const int16_t *s_bs, const int16_t *s_s16,
+                                                float *s_v) {
+    const int units = (SWIGLU ? 2 : 1) * tr * nb * 4;
+#pragma unroll
+    for (int i = 0; i < KQ_U; i++) {
+        const int u = lane + 64 * i;
+        const int rt = (u >> 2) / nb, b = (u >> 2) - rt * nb;
+        const bool up = SWIGLU && rt >= tr;
+        const int row = T.row0 + (up ? rt - tr : rt);
+        const bool ok = u < units && row < (up ? A.m[1].rows : T.M.rows);
+        const int bb = ok ? b : 0;
+        float v = unit_block_value<FMT>(L[i], u & 3, ok, s_xq + bb * 64, s_bs + bb * 8, s_s16 + bb * 16, s_dx[bb]);
+        if (ok && (u & 3) == 0) s_v[rt * nb + b] = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < tr) {
+        const GemvMat &M = T.M;
+        const int row = T.row0 + lane;
+        if (row < M.rows) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) acc += s_v[lane * nb + b];
+            if (SWIGLU) {
+                float up = 0.0f;
+                for (int b = 0; b < nb; b++) up += s_v[(tr + lane) * nb + b];
+                M.y[row] = silu_mul_ref(acc, up);
+            } else {
+                if (M.bias) acc += E.bias;
+                if (A.epi == EPI_ADD)
+                    M.y[row] = E.y + acc;
+                else
+                    M.y[row] = acc;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool SWIGLU>
+__device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int tr) {
+    KqTile T;
+    T.valid = tile < A.n_tiles;
+    int mi = 0;
+    if (!SWIGLU) {
+#pragma unroll
+        for (int t = 1; t < GEMV_MAX_MATS; t++)
+            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+    }
+    T.M = mat_sel(A, mi);
+    T.row0 = (tile - T.M.tile_begin) * tr;
+    return T;
+}
+
+// FMT: every matrix of the launch has this format (Q4_K or Q6_K).  KQ_U:
+// units per lane (a wave tile is 64*KQ_U quarter-block units).
+template <int FMT, bool SWIGLU, int KQ_U>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
-    constexpr int NM = SWIGLU ? 2 : 1;
     __shared__ int32_t s_xq[KMAX / 4];
     __shared__ float s_dx[NB256_MAX];
     __shared__ int16_t s_bs[NB32_MAX];
     __shared__ int16_t s_s16[KMAX / 16];
-    __shared__ float s_v[4][NM * R][NB256_MAX];
+    __shared__ float s_v[4][64];
 
     const int K = A.K, nb = K >> 8;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tr = A.tile_rows;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
+    const int step = gridDim.x * 4;
+    int tile = blockIdx.x * 4 + wave;
+
+    // First tile's weights, then the activation: both are in flight together,
+    // and the LDS writes wait only for the activation loads issued last... in
+    // order: the weights are older, so they are complete by then as well.
+    UnitLoad L0[KQ_U], L1[KQ_U];
+    KqTile T0 = kq_tile_info<SWIGLU>(A, tile, tr);
+    kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, tr, nb, lane, L0);
+
     {
+        static_assert(KQ_XQ_IT == 4, "staging below is written for K <= 16384");
+        const int n16 = K >> 4;
+        const int nbs = K >> 8;   // int4 chunks of bsums (8 per 256)
+        const int ns16 = K >> 7;  // int4 chunks of sums16 (16 per 256)
         const int4 *src = (const int4 *)A.xq.qs;
+        const int4 x0 = src[min(tid, n16 - 1)];
+        const int4 x1 = src[min(tid + 256, n16 - 1)];
+        const int4 x2 = src[min(tid + 512, n16 - 1)];
+        const int4 x3 = src[min(tid + 768, n16 - 1)];
+        const int4 bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
+        const int4 s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
+        const float dxr = A.xq.d[min(tid, nb - 1)];
         int4 *dst = (int4 *)s_xq;
-        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
-        for (int i = tid; i < nb; i += 256) s_dx[i] = A.xq.d[i];
-        for (int i = tid; i < K / 32; i += 256) s_bs[i] = A.xq.bsums[i];
-        for (int i = tid; i < K / 16; i += 256) s_s16[i] = A.xq.sums16[i];
+        if (tid < n16) dst[tid] = x0;
+        if (tid + 256 < n16) dst[tid + 256] = x1;
+        if (tid + 512 < n16) dst[tid + 512] = x2;
+        if (tid + 768 < n16) dst[tid + 768] = x3;
+        if (tid < nbs) ((int4 *)s_bs)[tid] = bsr;
+        if (tid < ns16) ((int4 *)s_s16)[tid] = s16r;
+        if (tid < nb) s_dx[tid] = dxr;
     }
     __syncthreads();
 
-    const int nwaves = gridDim.x * 4;
-    for (int tile = blockIdx.x * 4 + wave; tile < A.n_tiles; tile += nwaves) {
-        int mi = 0;
-        if (!SWIGLU) {
-#pragma unroll
-            for (int t = 1; t < GEMV_MAX_MATS; t++)
-                if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        }
-        const int row0 = (tile - A.m[mi].tile_begin) * R;
-        UnitLoad L[NM][R][ITERS];
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            const GemvMat &M = A.m[SWIGLU ? m : mi];
-            const int bsz = M.fmt == F_Q4_K ? 144 : 210;
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, row = row0 + r;
-                    if (b < nb && row < M.rows) L[m][r][i] = unit_load(M.w + (int64_t)row * M.row_stride + b * bsz, M.fmt, u & 3);
-                }
-        }
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            const GemvMat &M = A.m[SWIGLU ? m : mi];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int i = 0; i < ITERS; i++) {
-                    int u = lane + 64 * i, b = u >> 2, q = u & 3, row = row0 + r;
-                    bool ok = b < nb && row < M.rows;
-                    int bb = b < nb ? b : 0;
-                    float v = unit_block_value(L[m][r][i], M.fmt, q, ok, s_xq + bb * 64, s_bs + bb * 8, s_s16 + bb * 16,
-                                               s_dx[bb]);
-                    if (ok && q == 0) s_v[wave][m * R + r][b] = v;
-                }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < R) {
-            const int row = row0 + lane;
-            const GemvMat &M = A.m[mi];
-            if (row < M.rows) {
-                float acc = 0.0f;
-                for (int b = 0; b < nb; b++) acc += s_v[wave][lane][b];
-                if (SWIGLU) {
-                    float u = 0.0f;
-                    for (int b = 0; b < nb; b++) u += s_v[wave][R + lane][b];
-                    A.m[0].y[row] = silu_mul_ref(acc, u);
-                } else {
-                    if (M.bias) acc += M.bias[row];
-                    if (A.epi == EPI_ADD)
-                        M.y[row] += acc;
-                    else
-                        M.y[row] = acc;
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    while (T0.valid) {
+        const KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
+        KqTile T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, tr, nb, lane, L1);
+        kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T0, E0, tr, nb, lane, L0, s_xq, s_dx, s_bs, s_s16, s_v[wave]);
+        tile += step;
+        if (!T1.valid) break;
+        const KqEpi E1 = kq_epi_load<SWIGLU>(T1, lane);
+        T0 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, tr, nb, lane, L0);
+        kq_compute_tile<FMT, SWIGLU>(A, T1, E1, tr, nb, lane, L1, s_xq, s_dx, s_bs, s_s16, s_v[wave]);
+        tile += step;
     }
 }
 
@@ -353,7 +467,8 @@ __global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
     __shared__ float s_dx[NB256_MAX];
     extern __shared__ float s_part[];  // [4R][nb32][9]: scale, s_0..s_7
     const int K = A.K, nb = K >> 5;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
     {
         const int4 *src = (const int4 *)A.xq.qs;
         int4 *dst = (int4 *)s_xq;
@@ -366,7 +481,7 @@ __global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
 #pragma unroll
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        const GemvMat M = A.m[mi];
+        const GemvMat M = mat_sel(A, mi);
         int row0 = (tile - M.tile_begin) * (4 * R);
         uint4 wa[R][ITERS], wb[R][ITERS];
         uint32_t dd[R][ITERS];
@@ -439,7 +554,8 @@ __global__ __launch_bounds__(256) void gemv_b32_f32_kernel(GemvArgs A) {
     float *s_x = s_dyn;            // [K]
     float *s_v = s_dyn + A.K;      // [4R][nb]
     const int K = A.K, nb = K >> 5;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
     for (int i = tid; i < K; i += 256) s_x[i] = A.x[i];
     __syncthreads();
     for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
@@ -447,7 +563,7 @@ __global__ __launch_bounds__(256) void gemv_b32_f32_kernel(GemvArgs A) {
 #pragma unroll
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        const GemvMat M = A.m[mi];
+        const GemvMat M = mat_sel(A, mi);
         int row0 = (tile - M.tile_begin) * (4 * R);
         uint4 wa[R][ITERS], wb[R][ITERS];
         uint32_t dd[R][ITERS];

@@ -34,9 +34,10 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *x, int n
 // sum(x*x) in the exact order of dot_f32_avx2(x, x) (src/simd.rs:6547-6586):
 // 32 lanes = four 8-wide FMA accumulators over 32-element chunks, combined as
 // (acc0+acc1)+(acc2+acc3), then the 8-element tail chunks, the hsum_avx tree
-// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)), then the scalar tail.  Every
-// workgroup that calls it computes the same value.  red needs 33 floats.
-__device__ float sumsq_avx2_order(const float *x, int n, float *red) {
+// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)), then the scalar tail.  x is read
+// from LDS (s_x, already staged); every workgroup computes the same value.
+// red needs 33 floats.
+__device__ float sumsq_avx2_order(const float *s_x, int n, float *red) {
     const int main32 = n / 32;
     if (threadIdx.x < 32) {
         const int L = threadIdx.x;
@@ -45,12 +46,12 @@ __device__ float sumsq_avx2_order(const float *x, int n, float *red) {
         for (; c + 8 <= main32; c += 8) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = x[32 * (c + j) + L];
+            for (int j = 0; j < 8; j++) v[j] = s_x[32 * (c + j) + L];
 #pragma unroll
             for (int j = 0; j < 8; j++) acc = fmaf(v[j], v[j], acc);
         }
         for (; c < main32; c++) {
-            float v = x[32 * c + L];
+            float v = s_x[32 * c + L];
             acc = fmaf(v, v, acc);
         }
         red[L] = acc;
@@ -64,11 +65,11 @@ __device__ float sumsq_avx2_order(const float *x, int n, float *red) {
         for (int i = 0; i < tail8; i++)
 #pragma unroll
             for (int l = 0; l < 8; l++) {
-                float v = x[ts + 8 * i + l];
+                float v = s_x[ts + 8 * i + l];
                 t[l] = fmaf(v, v, t[l]);
             }
         float sum = ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
-        for (int i = ts + tail8 * 8; i < n; i++) sum += x[i] * x[i];
+        for (int i = ts + tail8 * 8; i < n; i++) sum += s_x[i] * s_x[i];
         red[32] = sum;
     }
     __syncthreads();
@@ -80,17 +81,32 @@ __device__ float sumsq_avx2_order(const float *x, int n, float *red) {
 // RMSNorm (rms_norm_into, src/model.rs:5429-5437): ss = sum(x^2)/n,
 // scale = 1/sqrt(ss + eps), out = (x*scale)*w, with the sum in the
 // reference's order (so scale, and everything after it, matches bit for
-// bit).  Each block then writes its 256 outputs and, when xq.qs != null and
-// n % 256 == 0, their Q8_K quantization.
+// bit).  x is first staged in LDS by all threads at once (dynamic LDS of n
+// floats).  Each block then writes its 256 outputs and, when xq.qs != null
+// and n % 256 == 0, their Q8_K quantization.
 __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *x, const float *w, float eps, int n,
                                                           float *xn, XQ xq) {
+    extern __shared__ float s_x[];
     __shared__ float red[40];
-    float ss = sumsq_avx2_order(x, n, red);
+    {
+        // all loads first (n <= 16384: at most 16 float4 per thread)
+        const int n4 = n >> 2, tid = threadIdx.x;
+        float4 t[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (tid + 256 * k < n4) t[k] = ((const float4 *)x)[tid + 256 * k];
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            if (tid + 256 * k < n4) ((float4 *)s_x)[tid + 256 * k] = t[k];
+        for (int i = 4 * n4 + tid; i < n; i += 256) s_x[i] = x[i];
+    }
+    __syncthreads();
+    float ss = sumsq_avx2_order(s_x, n, red);
     float scale = 1.0f / sqrtf(ss / (float)n + eps);
     int e = blockIdx.x * 256 + threadIdx.x;
     float o = 0.0f;
     if (e < n) {
-        o = x[e] * scale * w[e];
+        o = s_x[e] * scale * w[e];
         if (xn) xn[e] = o;
     }
     if (xq.qs) q8k_block_store(o, blockIdx.x, e, xq, red);

@@ -292,10 +292,31 @@ struct MatSpec {
     const float *bias;
 };
 
+// The activation a GEMV call consumes.  ACT_XQ: xq holds the Q8_K vector and
+// x the f32 one.  The other modes name the op that produces it from x
+// (quantize, RMSNorm then quantize, attention normalisation then quantize);
+// the GEMV call runs that op's kernel into xq (and xn) first.
+enum ActMode : int { ACT_XQ = 0, ACT_QUANT = 1, ACT_RMSNORM = 2, ACT_DEN = 3 };
+struct ActSpec {
+    int mode;
+    float *x;
+    const float *norm_w;
+    float eps;
+    const float *den;
+    int group;
+    XQ xq;
+    float *xn;
+};
+static ActSpec act_xq(const XQ &xq, const float *x) {
+    ActSpec a;
+    memset(&a, 0, sizeof(a));
+    a.mode = ACT_XQ;
+    a.xq = xq;
+    a.x = (float *)x;
+    return a;
+}
+
 enum Cat { CAT_KQ = 1, CAT_Q8I = 2, CAT_F32 = 3 };
-#ifndef KQ_R1
-#define KQ_R1 2  // rows per wave tile for K-quant rows of <= 16 blocks
-#endif
 static int cat_of(int fmt, int K) {
     if (fmt == 12 || fmt == 14) return K % 256 == 0 && K <= KMAX ? CAT_KQ : 0;
     if (fmt == 8) {
@@ -328,9 +349,9 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
     return grid < 1 ? 1 : grid;
 }
 
-template <int IT, int R, bool SW>
+template <int FMT, bool SW, int U>
 static int launch_kq(const GemvArgs &A, hipStream_t s) {
-    auto kern = gemv_kq_kernel<IT, R, SW>;
+    auto kern = gemv_kq_kernel<FMT, SW, U>;
     int grid = persistent_grid(kern, A.n_tiles, 4);
     ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, A);
@@ -356,15 +377,43 @@ static int launch_f32(const GemvArgs &A, hipStream_t s) {
     return 1;
 }
 
+// K-quant tiles: it = units per lane (a wave tile is 64*it quarter-block
+// units of r whole rows; SWIGLU tiles hold r gate + r up rows).  Small
+// launches use fewer units per lane so more waves share the latency; large
+// ones use more so each wave keeps more bytes in flight.  RUSTY_HIP_KQ_U
+// forces a preferred value.
+static int kq_units_per_lane(int K, int rows, bool swiglu) {
+    const int nb = K / 256;
+    const int need = ((swiglu ? 2 : 1) * nb * 4 + 63) / 64;  // one row (pair) must fit
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("RUSTY_HIP_KQ_U");
+        forced = e ? atoi(e) : 0;
+    }
+    int pref;
+    if (forced > 0) {
+        pref = forced;
+    } else {
+        const double units = (double)rows * nb * 4;      // all quarter-block units of the launch
+        const double lanes = (double)g.n_cu * 4 * 4 * 64; // about four waves per SIMD
+        pref = units <= lanes ? 1 : units <= 2 * lanes ? 2 : 4;
+    }
+    int u = std::max(pref, need);
+    return u > 4 ? 0 : u;
+}
+static int kq_tile_rows(int K, int units_per_lane, bool swiglu) {
+    const int nb = K / 256;
+    return std::max(1, 16 * units_per_lane / nb / (swiglu ? 2 : 1));
+}
+
 // rows per tile for each (category, ITERS)
 static void pick_iters(int cat, int K, int *it, int *r) {
     int units = (cat == CAT_KQ) ? (K / 256) * 4 : K / 32;
     int iters = (units + 63) / 64;
     if (cat == CAT_KQ) {
-        if (iters <= 1) { *it = 1; *r = KQ_R1; }
-        else if (iters == 2) { *it = 2; *r = 1; }
-        else if (iters == 3) { *it = 3; *r = 1; }
-        else { *it = 4; *r = 1; }
+        // wave tile = r rows x all blocks in 64*it units (it = units per lane)
+        *it = 1;
+        *r = 1;
     } else {
         if (iters <= 1) { *it = 1; *r = 4; }
         else if (iters == 2) { *it = 2; *r = 2; }
@@ -376,7 +425,7 @@ static void pick_iters(int cat, int K, int *it, int *r) {
 }
 
 // Launches y_i = W_i x for matrices of one category.
-static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, const float *xf, hipStream_t s) {
+static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
     if (n <= 0 || n > GEMV_MAX_MATS) return 0;
     int cat = cat_of(ms[0].w.fmt, K);
     if (!cat) return 0;
@@ -384,13 +433,19 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, cons
         if (cat_of(ms[i].w.fmt, K) != cat) return 0;
     int it, r;
     pick_iters(cat, K, &it, &r);
-    if (cat == CAT_KQ && it > 4) return 0;
+    if (cat == CAT_KQ) {
+        int rows = 0;
+        for (int i = 0; i < n; i++) rows += ms[i].w.rows;
+        it = kq_units_per_lane(K, rows, epi == EPI_SWIGLU);
+        r = kq_tile_rows(K, it, epi == EPI_SWIGLU);
+    }
+    if (act.mode != ACT_XQ) return 0;
     GemvArgs A;
     memset(&A, 0, sizeof(A));
     A.K = K;
     A.epi = epi;
-    A.xq = xq;
-    A.x = xf;
+    A.xq = act.xq;
+    A.x = act.x;
     A.n_mats = n;
     int tiles = 0;
     int rows_per_tile = (cat == CAT_KQ) ? r : 4 * r;
@@ -410,21 +465,19 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, cons
         tiles = (A.m[0].rows + rows_per_tile - 1) / rows_per_tile;
     }
     A.n_tiles = tiles;
+    A.tile_rows = r;
     if (cat == CAT_KQ) {
-        if (epi == EPI_SWIGLU) {
-            switch (it) {
-            case 1: return launch_kq<1, KQ_R1, true>(A, s);
-            case 2: return launch_kq<2, 1, true>(A, s);
-            case 3: return launch_kq<3, 1, true>(A, s);
-            default: return launch_kq<4, 1, true>(A, s);
-            }
-        }
-        switch (it) {
-        case 1: return launch_kq<1, KQ_R1, false>(A, s);
-        case 2: return launch_kq<2, 1, false>(A, s);
-        case 3: return launch_kq<3, 1, false>(A, s);
-        default: return launch_kq<4, 1, false>(A, s);
-        }
+        for (int i = 1; i < n; i++)
+            if (A.m[i].fmt != A.m[0].fmt) return 0;  // gemv_multi groups by format
+        const bool q4 = A.m[0].fmt == 12;
+#define RH_KQ_U(U)                                                                                     \
+    if (it == U) {                                                                                     \
+        if (epi == EPI_SWIGLU) return q4 ? launch_kq<F_Q4_K, true, U>(A, s) : launch_kq<F_Q6_K, true, U>(A, s); \
+        return q4 ? launch_kq<F_Q4_K, false, U>(A, s) : launch_kq<F_Q6_K, false, U>(A, s);             \
+    }
+        RH_KQ_U(1) RH_KQ_U(2) RH_KQ_U(3) RH_KQ_U(4)
+#undef RH_KQ_U
+        return 0;
     }
     if (cat == CAT_Q8I) {
         switch (it) {
@@ -445,8 +498,42 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const XQ &xq, cons
     }
 }
 
-// Splits a list of matrices into category groups and launches each.
-static int gemv_multi(const MatSpec *ms, int n, int K, int epi, const XQ &xq, const float *xf, hipStream_t s) {
+static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s);
+static int launch_rmsnorm(const float *x, const float *w, float eps, int n, float *xn, const XQ *xq, hipStream_t s);
+
+// Runs the standalone kernel that produces an ActSpec's Q8_K (and f32)
+// vector, for launches that cannot build it in their prologue.
+static int act_materialize(const ActSpec &a, int K, ActSpec *out, hipStream_t s) {
+    switch (a.mode) {
+    case ACT_XQ:
+        *out = a;
+        return 1;
+    case ACT_QUANT:
+        if (K % 256 == 0 && !launch_quant(a.x, K, a.xq, s)) return 0;
+        *out = act_xq(K % 256 == 0 ? a.xq : XQ{}, a.x);
+        return 1;
+    case ACT_RMSNORM:
+        if (!a.xn) return 0;
+        if (!launch_rmsnorm(a.x, a.norm_w, a.eps, K, a.xn, K % 256 == 0 ? &a.xq : nullptr, s)) return 0;
+        *out = act_xq(K % 256 == 0 ? a.xq : XQ{}, a.xn);
+        return 1;
+    case ACT_DEN: {
+        ProfScope ps("attn_exact_finish", s);
+        XQ q = K % 256 == 0 ? a.xq : XQ{};
+        hipLaunchKernelGGL(attn_exact_finish_kernel, dim3((K + 255) / 256), dim3(256), 0, s, a.x, a.den, a.group, K, q);
+        RH_LAUNCH_OK();
+        *out = act_xq(q, a.x);
+        return 1;
+    }
+    }
+    return 0;
+}
+
+// Splits a list of matrices into launch groups (one per category; K-quant
+// groups also share one format) and launches each.
+static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
+    ActSpec use;
+    if (!act_materialize(act, K, &use, s)) return 0;
     int done[GEMV_MAX_MATS] = {0};
     for (int i = 0; i < n; i++) {
         if (done[i]) continue;
@@ -455,13 +542,17 @@ static int gemv_multi(const MatSpec *ms, int n, int K, int epi, const XQ &xq, co
         MatSpec grp[GEMV_MAX_MATS];
         int ng = 0;
         for (int j = i; j < n; j++)
-            if (!done[j] && cat_of(ms[j].w.fmt, K) == cat) {
+            if (!done[j] && cat_of(ms[j].w.fmt, K) == cat && (cat != CAT_KQ || ms[j].w.fmt == ms[i].w.fmt)) {
                 grp[ng++] = ms[j];
                 done[j] = 1;
             }
-        if (!gemv_cat(grp, ng, K, epi, xq, xf, s)) return 0;
+        if (!gemv_cat(grp, ng, K, epi, use, s)) return 0;
     }
     return 1;
+}
+
+static int gemv_multi(const MatSpec *ms, int n, int K, int epi, const XQ &xq, const float *xf, hipStream_t s) {
+    return gemv_multi_act(ms, n, K, epi, act_xq(xq, xf), s);
 }
 
 static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s) {
@@ -473,10 +564,12 @@ static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s) {
 }
 
 static int launch_rmsnorm(const float *x, const float *w, float eps, int n, float *xn, const XQ *xq, hipStream_t s) {
+    if (n > 16384 || ((uintptr_t)x & 15)) return 0;
     XQ q = xq ? *xq : XQ{};
     if (xq && n % 256 != 0) q = XQ{};
     ProfScope ps("rmsnorm_q8k", s);
-    hipLaunchKernelGGL(rmsnorm_q8k_kernel, dim3((n + 255) / 256), dim3(256), 0, s, x, w, eps, n, xn, q);
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel, dim3((n + 255) / 256), dim3(256), (size_t)n * sizeof(float), s, x, w, eps,
+                       n, xn, q);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -494,15 +587,21 @@ static int launch_silu(const float *g_, const float *u, int n, float *out, hipSt
 
 // d = W_gate, W_up -> hidden = silu(gate x) * (up x); K-quant pairs use the
 // fused epilogue, other formats two GEMVs plus the SiLU kernel.
-static int gemv_swiglu(const DevW &gate, const DevW &up, int K, const XQ &xq, const float *xf, float *hidden,
-                       float *tmp_g, float *tmp_u, hipStream_t s) {
-    if (cat_of(gate.fmt, K) == CAT_KQ && cat_of(up.fmt, K) == CAT_KQ && gate.rows == up.rows) {
+static int gemv_swiglu_act(const DevW &gate, const DevW &up, int K, const ActSpec &act, float *hidden,
+                           float *tmp_g, float *tmp_u, hipStream_t s) {
+    if (cat_of(gate.fmt, K) == CAT_KQ && gate.fmt == up.fmt && gate.rows == up.rows && K / 256 <= 32) {
         MatSpec ms[2] = {{gate, hidden, nullptr}, {up, hidden, nullptr}};
-        return gemv_cat(ms, 2, K, EPI_SWIGLU, xq, xf, s);
+        ActSpec use;
+        if (!act_materialize(act, K, &use, s)) return 0;
+        return gemv_cat(ms, 2, K, EPI_SWIGLU, use, s);
     }
     MatSpec ms[2] = {{gate, tmp_g, nullptr}, {up, tmp_u, nullptr}};
-    if (!gemv_multi(ms, 2, K, EPI_STORE, xq, xf, s)) return 0;
+    if (!gemv_multi_act(ms, 2, K, EPI_STORE, act, s)) return 0;
     return launch_silu(tmp_g, tmp_u, gate.rows, hidden, s);
+}
+static int gemv_swiglu(const DevW &gate, const DevW &up, int K, const XQ &xq, const float *xf, float *hidden,
+                       float *tmp_g, float *tmp_u, hipStream_t s) {
+    return gemv_swiglu_act(gate, up, K, act_xq(xq, xf), hidden, tmp_g, tmp_u, s);
 }
 
 static int attn_launch(const AttnArgs &A, hipStream_t s) {
@@ -563,7 +662,8 @@ static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
 // (multiple of 64, >= the longest range this launch may see).  The output is
 // normalised in place and, when xq.qs is set, quantized to Q8_K
 // (n_heads * vd must then be a multiple of 256).
-static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s) {
+static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s, bool finish = true,
+                             const float **den_out = nullptr) {
     const size_t nh = (size_t)A.n_heads, cap = (size_t)A.cap;
     const int ntl = A.cap / EX_TILE;
     A.scores = scratch;
@@ -598,7 +698,8 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         }
         RH_LAUNCH_OK();
     }
-    {
+    if (den_out) *den_out = A.den;
+    if (finish) {
         ProfScope ps("attn_exact_finish", s);
         hipLaunchKernelGGL(attn_exact_finish_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, A.out, A.den, A.vd,
                            n_out, xq);
@@ -1174,6 +1275,19 @@ static int dt_to_fmt(uint32_t dt) {
     }
 }
 
+// RMSNorm of the residual stream as a GEMV activation.
+static ActSpec r_act_norm(const float *norm_w) {
+    ActSpec a;
+    memset(&a, 0, sizeof(a));
+    a.mode = ACT_RMSNORM;
+    a.x = R.x;
+    a.norm_w = norm_w;
+    a.eps = R.eps;
+    a.xq = R.xq_dim;
+    a.xn = R.xn;
+    return a;
+}
+
 // One token through the layer stack (and head / greedy by mode) on stream s.
 static int r_enqueue(int mode, float penalty, hipStream_t s) {
     const int dim = R.dim, qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd;
@@ -1186,9 +1300,8 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
     }
     for (uint32_t l = 0; l < R.n_layers; l++) {
         RLayer &Ly = R.L[l];
-        if (!launch_rmsnorm(R.x, Ly.attn_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
         MatSpec qkv[3] = {{Ly.w[0], R.q, Ly.bias[0]}, {Ly.w[1], R.k, Ly.bias[1]}, {Ly.w[2], R.v, Ly.bias[2]}};
-        if (!gemv_multi(qkv, 3, dim, EPI_STORE, R.xq_dim, R.xn, s)) return 0;
+        if (!gemv_multi_act(qkv, 3, dim, EPI_STORE, r_act_norm(Ly.attn_norm), s)) return 0;
         {
             RopeArgs A;
             memset(&A, 0, sizeof(A));
@@ -1213,6 +1326,8 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             hipLaunchKernelGGL(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
             RH_LAUNCH_OK();
         }
+        ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
+        act_o.xq = attn_cols % 256 == 0 ? R.xq_attn : XQ{};
         if (attn_fast_mode()) {
             AttnArgs A;
             memset(&A, 0, sizeof(A));
@@ -1255,22 +1370,27 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.window = 0;
             E.cap = R.ex_cap;
             E.scale = 1.0f / sqrtf((float)R.hd);
-            if (!attn_exact_launch(E, R.ex, attn_cols % 256 == 0 ? R.xq_attn : XQ{}, s)) return 0;
+            const float *den = nullptr;
+            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
+            act_o.mode = ACT_DEN;
+            act_o.den = den;
+            act_o.group = R.vd;
         }
         MatSpec mo = {Ly.w[3], R.x, nullptr};
-        if (!gemv_multi(&mo, 1, attn_cols, EPI_ADD, R.xq_attn, R.attn, s)) return 0;
-        if (!launch_rmsnorm(R.x, Ly.ffn_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
-        if (!gemv_swiglu(Ly.w[4], Ly.w[5], dim, R.xq_dim, R.xn, R.hid, R.tg, R.tu, s)) return 0;
-        if (cat_of(Ly.w[6].fmt, R.hidden) != CAT_F32)
-            if (!launch_quant(R.hid, R.hidden, R.xq_hid, s)) return 0;
+        if (!gemv_multi_act(&mo, 1, attn_cols, EPI_ADD, act_o, s)) return 0;
+        if (!gemv_swiglu_act(Ly.w[4], Ly.w[5], dim, r_act_norm(Ly.ffn_norm), R.hid, R.tg, R.tu, s)) return 0;
+        ActSpec act_h;
+        memset(&act_h, 0, sizeof(act_h));
+        act_h.mode = ACT_QUANT;
+        act_h.x = R.hid;
+        act_h.xq = R.xq_hid;
         MatSpec md = {Ly.w[6], R.x, nullptr};
-        if (!gemv_multi(&md, 1, R.hidden, EPI_ADD, R.xq_hid, R.hid, s)) return 0;
+        if (!gemv_multi_act(&md, 1, R.hidden, EPI_ADD, act_h, s)) return 0;
     }
     (void)qd;
     if (mode & (MODE_LOGITS | MODE_GREEDY)) {
-        if (!launch_rmsnorm(R.x, R.out_norm, R.eps, dim, R.xn, &R.xq_dim, s)) return 0;
         MatSpec mh = {R.out_w, R.logits, nullptr};
-        if (!gemv_multi(&mh, 1, dim, EPI_STORE, R.xq_dim, R.xn, s)) return 0;
+        if (!gemv_multi_act(&mh, 1, dim, EPI_STORE, r_act_norm(R.out_norm), s)) return 0;
     }
     if (mode & MODE_GREEDY) {
         ArgmaxArgs A;
