@@ -79,8 +79,7 @@ struct AttnExactArgs {
     const float *v;
     const float *sinks;  // [n_heads] or null
     float *scores;       // [n_heads][cap]   q.k * scale per position
-    float *e;            // [n_kv][ceil(kv_mul/4)][cap][4]  the step's expf value
-                         // (see below), four heads of a kv group interleaved
+    float *e;            // [n_heads][cap]   the step's expf value (see below)
     float *tmax;         // [n_heads][cap/64] max score of each 64-position tile
     uint32_t *newmask;   // [n_heads][cap/32] bit t%32 set when step t sets a new max
     float *den;          // [n_heads]         final denominators
@@ -111,11 +110,9 @@ __device__ __forceinline__ bool is_x4(const AttnExactArgs &A, int g) {
 
 #define EX_TILE 64
 
-// e of (kv head h, head g of its group, position t): groups of four heads are
-// interleaved per position so one 64-position tile of a group is 1 KB.
+// e of (kv head h, head g of its group, position t).
 __device__ __forceinline__ size_t e_index(const AttnExactArgs &A, int h, int g, int t) {
-    const int hgroups = (A.kv_mul + 3) / 4;
-    return ((size_t)(h * hgroups + g / 4) * A.cap + t) * 4 + (g & 3);
+    return (size_t)(h * A.kv_mul + g) * A.cap + t;
 }
 
 // A: one workgroup per (tile of EX_TILE positions, kv head).  Writes the
@@ -267,24 +264,30 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A) {
 //   new max: out = affine_add: fma(v, 1, out*e) | scale_add: fma(out, e, v)
 //            den = den*e + 1 (two roundings)
 //   else:    out = fma(e, v, out);  den = den + e
-// in the reference's step order.  One wave covers up to four query heads of a
-// kv group (lane = head slot * 16 + dim) for 16 value dims, so every V element
-// is read from HBM once per layer.  An extra "slice" per group runs the
-// denominator as the same recurrence with v = 1 (fma(e, 1, d) = d + e and
-// fma(1, 1, d*e) = d*e + 1 round exactly like the reference's scalar ops).
+// in the reference's step order.  A wave's own instruction stream is the
+// limit here (one dependent FMA per step and lane, ~3 ns per instruction for
+// a wave alone on its SIMD), so each recurrence wave gets a SIMD to itself and
+// everything else is kept out of its stream.
 //
-// V, e and the new-max words reach LDS through direct global->LDS loads
-// (global_load_lds_dwordx4 / _dword) into a ring of CH_NT 64-position tiles,
-// CH_P tiles ahead of the recurrence; the wave waits on its own vmcnt, so no
-// barrier is involved.  LDS is read only with 32-bit reads (ds_read_b32 /
-// ds_read2_b32): the compiler drains vmcnt to zero before any wider LDS read
-// while direct loads are in flight, which would empty the pipeline.
-#ifndef CH_NT
-#define CH_NT 16
-#endif
-#ifndef CH_P
-#define CH_P 11
-#endif
+// Chain workgroups, one per (query head, 64 value dims), one wave per SIMD:
+//   wave 0     the consumer, lane = value dim; e is wave-uniform and read four
+//              positions per broadcast ds_read_b128 (the consumer never has
+//              direct loads in flight, so the compiler's drain before wide
+//              LDS reads costs nothing).  LDS return bandwidth (256 B per wave
+//              read) is what a second consumer on the CU would compete for;
+//   waves 1-2  producers: direct global->LDS loads (global_load_lds) of V
+//              [64 positions][64 dims], e and the new-max words into a ring
+//              of CH_NT tiles, CH_P tiles ahead, waiting on their own vmcnt.
+// The query heads of a kv head sit on the same XCD (block % n_kv), so their
+// repeated V reads hit its L2.  Denominator workgroups, one per kv head:
+// wave 0 runs the heads' denominators (lane = head) as the same recurrence
+// with v = 1 (fma(e, 1, d) = d + e and fma(1, 1, d*e) = d*e + 1 round exactly
+// like the scalar ops); wave 1 loads e and the words.  One s_barrier per
+// tile publishes it and releases the slot read two tiles earlier.
+#define CH_NT 8
+#define CH_P 6
+#define CH_MAXG 8    // query heads per kv head handled by this kernel
+#define CH_WAVES 3
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
@@ -297,16 +300,22 @@ __device__ __forceinline__ void dma4(const void *src, void *lds) {
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
 #define RH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
+// lgkmcnt(0) only
+#define RH_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14))
+
+// Workgroup barrier without the memory-model waits of __syncthreads (which
+// would drain the producers' loads); the asm statements keep the compiler
+// from moving memory operations across it.
+__device__ __forceinline__ void tile_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 template <int IPT>
 __device__ __forceinline__ void wait_tiles_after(int n_after) {
-    // n_after: tiles issued after the one about to be read (0..CH_P-1)
+    // n_after: this producer's tiles issued after the one to be published
     switch (n_after) {
-        case 10: RH_WAIT_VM(10 * IPT); break;
-        case 9: RH_WAIT_VM(9 * IPT); break;
-        case 8: RH_WAIT_VM(8 * IPT); break;
-        case 7: RH_WAIT_VM(7 * IPT); break;
-        case 6: RH_WAIT_VM(6 * IPT); break;
         case 5: RH_WAIT_VM(5 * IPT); break;
         case 4: RH_WAIT_VM(4 * IPT); break;
         case 3: RH_WAIT_VM(3 * IPT); break;
@@ -315,158 +324,305 @@ __device__ __forceinline__ void wait_tiles_after(int n_after) {
         default: RH_WAIT_VM(0); break;
     }
 }
-static_assert(CH_P - 1 <= 10, "wait_tiles_after covers at most 10 tiles");
-static_assert(6 * (CH_P - 1) <= 63, "vmcnt is 6 bits");
+static_assert(CH_P - 1 <= 5, "wait_tiles_after covers at most 5 tiles");
+static_assert(9 * CH_P <= 63, "vmcnt is 6 bits");
 
 struct ChainLds {
-    float v[CH_NT][EX_TILE * 16];   // [slot][position][16 dims]
-    float e[CH_NT][EX_TILE * 4];    // [slot][position][head slot]
-    uint32_t m[CH_NT][8];           // [slot][head slot][2 words]
+    float v[CH_NT][EX_TILE * 64];       // [slot][position][64 dims]
+    float e[CH_NT][CH_MAXG * EX_TILE];  // [slot][head row][position]
+    uint32_t m[CH_NT][2 * CH_MAXG];     // [slot][head row][2 words]
 };
 
-// 16 steps of e (position-major, stride 4 floats) and v (stride 16 floats)
-template <bool DEN>
-__device__ __forceinline__ void chain_load16(const float *et, const float *vt, int k, float *e, float *v) {
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        e[j] = et[(k * 16 + j) * 4];
-        if (!DEN) v[j] = vt[(k * 16 + j) * 16];
-    }
-}
-// 16 recurrence steps; bits = this lane's new-max flags for them.  The
-// branch is wave-uniform: plain FMAs unless some head has a new max here.
-template <bool DEN, bool X4>
-__device__ __forceinline__ void chain_steps16(const float *e, const float *v, float &o, uint32_t bits) {
-    if (!__any(bits != 0u)) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) o = fmaf(e[j], DEN ? 1.0f : v[j], o);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const float vj = DEN ? 1.0f : v[j];
-            const float on = fmaf(e[j], vj, o);
-            const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * e[j]) : fmaf(o, e[j], vj);
-            o = ((bits >> j) & 1u) ? ox : on;
+// Barrier j publishes tiles 2j and 2j+1 (CH_PER tiles per barrier); the slots
+// refilled after it held tiles 2j-2 and 2j-1, read before it.
+#define CH_PER 2
+template <int IPT, class Issue>
+__device__ __forceinline__ void chain_producer_loop(int ntiles, Issue &issue) {
+    const int ngroups = (ntiles + CH_PER - 1) / CH_PER;
+    for (int i = 0; i < min(CH_P, ntiles); i++) issue(i);
+    for (int j = 0; j < ngroups; j++) {
+        const int last = min(CH_PER * j + CH_PER - 1, ntiles - 1);   // newest tile to publish
+        const int issued = min(CH_P + CH_PER * j, ntiles);           // tiles issued so far
+        wait_tiles_after<IPT>(issued - 1 - last);
+        tile_barrier();
+        for (int t = 0; t < CH_PER; t++) {
+            const int i = CH_P + CH_PER * j + t;
+            if (i < ntiles) issue(i);
         }
     }
 }
+static_assert(CH_NT >= CH_P + CH_PER, "ring too small");
 
-template <bool DEN, bool X4>
-__device__ void chain_run(const AttnExactArgs &A, ChainLds &L, int s0, int ctx, int h, int hg, int slice) {
-    const int lane = threadIdx.x, gs = lane >> 4, c = lane & 15;
-    const int kvm = A.kv_mul;
-    const int head_g = hg * 4 + gs;
-    const bool hvalid = head_g < kvm;
+// Chain workgroup producer P: V rows k = 8P..8P+7 of every tile (4 positions
+// each); P = 0 also loads the head's e, P = 1 its two new-max words.
+template <int P>
+__device__ void chain_producer(const AttnExactArgs &A, ChainLds &L, int s0, int ctx, int h, int g, int slice) {
+    constexpr int IPT = 9;
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
-    constexpr int IPT = DEN ? 2 : 6;
-    // DMA sources: wave-uniform bases plus 32-bit per-lane byte offsets.  V
-    // row offsets advance 64 positions per tile and wrap at slot_count
-    // (>= 64, so one conditional subtraction keeps them in range).
-    const char *e_base = (const char *)(A.e + e_index(A, h, hg * 4, 0)) + lane * 16;
-    const int m_gs = (lane >> 1) & 3;
-    const int m_head = h * kvm + ((hg * 4 + m_gs < kvm) ? hg * 4 + m_gs : hg * 4);
-    const char *m_base = (const char *)(A.newmask + (size_t)m_head * (A.cap / 32)) + (lane & 1) * 4;
-    const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 16) + (lane & 3) * 16;
+    const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 64) + (lane & 15) * 16;
     const uint32_t row_bytes = (uint32_t)A.value_stride * 4u;
     const uint32_t wrap = (uint32_t)A.slot_count * row_bytes;
     const uint32_t step = 64u * row_bytes;
-    uint32_t roff[4];
+    uint32_t roff[8];
 #pragma unroll
-    for (int k = 0; k < 4; k++) roff[k] = (uint32_t)((s0 + k * 16 + (lane >> 2)) % A.slot_count) * row_bytes;
+    for (int kk = 0; kk < 8; kk++) {
+        const int tt = 4 * (8 * P + kk) + (lane >> 4);
+        roff[kk] = (uint32_t)((s0 + tt) % A.slot_count) * row_bytes;
+    }
+    const char *e_base = (const char *)(A.e + e_index(A, h, g, 0)) + lane * 4;
+    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + g) * (A.cap / 32)) + (lane & 1) * 4;
 
     auto issue = [&](int i) {
         const int sl = i & (CH_NT - 1);
-        if (!DEN) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                dma16(v_base + roff[k], &L.v[sl][k * 256]);
-                roff[k] += step;
-                if (roff[k] >= wrap) roff[k] -= wrap;
-            }
+        for (int kk = 0; kk < 8; kk++) {
+            dma16(v_base + roff[kk], &L.v[sl][(8 * P + kk) * 256]);
+            roff[kk] += step;
+            if (roff[kk] >= wrap) roff[kk] -= wrap;
         }
-        dma16(e_base + (uint32_t)i * 1024u, &L.e[sl][0]);
-        if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
+        if (P == 0) dma4(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
+        if (P == 1)
+            if (lane < 2) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
     };
 
-    float o = (DEN && A.sinks) ? 1.0f : 0.0f;
-    auto process = [&](int i) {
+    chain_producer_loop<IPT>(ntiles, issue);
+}
+
+// Denominator workgroup producer: e rows of all kv_mul heads (two 4-head
+// loads) and their new-max words.
+__device__ void den_producer(const AttnExactArgs &A, ChainLds &L, int ctx, int h) {
+    constexpr int IPT = 3;
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int eg0 = min(lane >> 4, kvm - 1), eg1 = min(4 + (lane >> 4), kvm - 1);
+    const char *e0 = (const char *)(A.e + e_index(A, h, eg0, 0)) + (lane & 15) * 16;
+    const char *e1 = (const char *)(A.e + e_index(A, h, eg1, 0)) + (lane & 15) * 16;
+    const int mg = min((lane >> 1) & 7, kvm - 1);
+    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + mg) * (A.cap / 32)) + (lane & 1) * 4;
+    auto issue = [&](int i) {
         const int sl = i & (CH_NT - 1);
-        const int ntok = min(EX_TILE, ctx - i * EX_TILE);
-        const float *vt = &L.v[sl][c];
-        const float *et = &L.e[sl][gs];
-        const uint32_t mw0 = hvalid ? L.m[sl][gs * 2] : 0u;
-        const uint32_t mw1 = hvalid ? L.m[sl][gs * 2 + 1] : 0u;
-        if (ntok == EX_TILE) {
-            // 64 steps in 16-step chunks; LDS reads run two chunks ahead of
-            // the arithmetic
-            float e0[16], v0[16], e1[16], v1[16], e2[16], v2[16];
-            chain_load16<DEN>(et, vt, 0, e0, v0);
-            chain_load16<DEN>(et, vt, 1, e1, v1);
-            chain_load16<DEN>(et, vt, 2, e2, v2);
-            __builtin_amdgcn_sched_barrier(0);
-            chain_steps16<DEN, X4>(e0, v0, o, mw0 & 0xFFFFu);
-            __builtin_amdgcn_sched_barrier(0);
-            chain_load16<DEN>(et, vt, 3, e0, v0);
-            __builtin_amdgcn_sched_barrier(0);
-            chain_steps16<DEN, X4>(e1, v1, o, mw0 >> 16);
-            __builtin_amdgcn_sched_barrier(0);
-            chain_steps16<DEN, X4>(e2, v2, o, mw1 & 0xFFFFu);
-            __builtin_amdgcn_sched_barrier(0);
-            chain_steps16<DEN, X4>(e0, v0, o, mw1 >> 16);
-        } else {
-            for (int t = 0; t < ntok; t++) {
-                const uint32_t mw = t < 32 ? mw0 : mw1;
-                const float e = et[t * 4];
-                const float v = DEN ? 1.0f : vt[t * 16];
-                const float on = fmaf(e, v, o);
-                const float ox = (DEN || X4) ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
-                o = ((mw >> (t & 31)) & 1u) ? ox : on;
-            }
-        }
+        dma16(e0 + (uint32_t)i * 256u, &L.e[sl][0]);
+        dma16(e1 + (uint32_t)i * 256u, &L.e[sl][256]);
+        if (lane < 16) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
     };
+    chain_producer_loop<IPT>(ntiles, issue);
+}
 
-    const int pro = min(CH_P - 1, ntiles);
-    for (int i = 0; i < pro; i++) issue(i);
-    int i = 0;
-    for (; i + CH_P - 1 < ntiles; i++) {  // steady state: CH_P - 1 tiles behind this one
-        issue(i + CH_P - 1);
-        RH_WAIT_VM((CH_P - 1) * IPT);
-        process(i);
-    }
-    for (; i < ntiles; i++) {  // drain
-        wait_tiles_after<IPT>(ntiles - 1 - i);
-        process(i);
-    }
-    if (hvalid) {
-        const int head = h * kvm + head_g;
-        if (DEN) {
-            if (c == 0) A.den[head] = o;
-        } else {
-            A.out[(size_t)head * A.vd + slice * 16 + c] = o;
-        }
+// Denominator wave: 16 steps of its own head's e (four b128 reads).
+__device__ __forceinline__ void den_load16(const float *et, int k, float *e) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float4 q = *(const float4 *)(et + k * 16 + 4 * j);
+        e[4 * j] = q.x;
+        e[4 * j + 1] = q.y;
+        e[4 * j + 2] = q.z;
+        e[4 * j + 3] = q.w;
     }
 }
 
-// grid: n_kv * ceil(kv_mul/4) * (vd/16 + 1) workgroups of one wave; block b
-// serves kv head b % n_kv, so consecutive blocks spread over the XCDs.
-__global__ __launch_bounds__(64) void attn_exact_chain_dma_kernel(AttnExactArgs A) {
+// Consumer: 16 steps.  e16 holds e of step (lane & 15) in every 16-lane row
+// (one ds_read_b32); v[j] = v of step j for this lane's dim.
+__device__ __forceinline__ void cons_load16(const float *et, const float *vt, int k, int lane, float &e16, float *v) {
+    e16 = et[k * 16 + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = vt[(k * 16 + j) * 64];
+}
+
+// e of step J broadcast from lane J of each row.
+template <int J>
+__device__ __forceinline__ float bcast16(float e16) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, e16), 0x150 + J, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void bcast16_all(float e16, float *e) {
+    e[0] = bcast16<0>(e16);   e[1] = bcast16<1>(e16);   e[2] = bcast16<2>(e16);   e[3] = bcast16<3>(e16);
+    e[4] = bcast16<4>(e16);   e[5] = bcast16<5>(e16);   e[6] = bcast16<6>(e16);   e[7] = bcast16<7>(e16);
+    e[8] = bcast16<8>(e16);   e[9] = bcast16<9>(e16);   e[10] = bcast16<10>(e16); e[11] = bcast16<11>(e16);
+    e[12] = bcast16<12>(e16); e[13] = bcast16<13>(e16); e[14] = bcast16<14>(e16); e[15] = bcast16<15>(e16);
+}
+
+// 16 plain steps o = fma(e_j, v_j, o) with e_j taken straight from lane j of
+// the row by the FMA's DPP operand (row_newbcast), so e costs no instruction
+// of its own.  s_nop 1 gives the two wait states a DPP source needs after a
+// VALU write.
+__device__ __forceinline__ void cons_fma16_dpp(float e16, const float *v, float &o) {
+    asm("s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+        : "+v"(o)
+        : "v"(e16), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]),
+          "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
+}
+
+// 16 recurrence steps with per-step new-max flags `bits`: the update forms
+// selected per step (rare: only chunks holding a new maximum come here).
+template <bool DEN, bool X4>
+__device__ __forceinline__ void chain_steps16_flags(const float *e, const float *v, float &o, uint32_t bits) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float vj = DEN ? 1.0f : v[j];
+        const float on = fmaf(e[j], vj, o);
+        const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * e[j]) : fmaf(o, e[j], vj);
+        o = ((bits >> j) & 1u) ? ox : on;
+    }
+}
+
+// Consumer chunk: plain steps through the DPP FMAs unless a flag is set.
+template <bool X4>
+__device__ __forceinline__ void cons_steps16(float e16, const float *v, float &o, uint32_t bits) {
+    if (__builtin_amdgcn_readfirstlane(bits) == 0u) {
+        cons_fma16_dpp(e16, v, o);
+    } else {
+        float e[16];
+        bcast16_all(e16, e);
+        chain_steps16_flags<false, X4>(e, v, o, __builtin_amdgcn_readfirstlane(bits));
+    }
+}
+
+// Denominator chunk (per-lane flags).
+__device__ __forceinline__ void den_steps16(const float *e, float &o, uint32_t bits) {
+    if (!__any(bits != 0u)) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) o = fmaf(e[j], 1.0f, o);
+    } else {
+        chain_steps16_flags<true, true>(e, nullptr, o, bits);
+    }
+}
+
+// Consumer (DEN = false: e/flag row `row`, lane = value dim; the row's flags
+// are wave-uniform) or denominator wave (DEN = true: lane = head = row).
+// active = false only keeps the wave in step with the barriers.
+template <bool DEN, bool X4>
+__device__ void chain_consumer(const AttnExactArgs &A, ChainLds &L, int ctx, int row, bool active, float *dst) {
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int ngroups = (ntiles + CH_PER - 1) / CH_PER;
+    const int r = DEN ? min(lane, kvm - 1) : row;
+    float o = (DEN && A.sinks) ? 1.0f : 0.0f;
+    for (int j = 0; j < ngroups; j++) {
+        tile_barrier();
+        if (!active) continue;
+        const int i0 = CH_PER * j;
+        const bool full = i0 + CH_PER <= ntiles && ctx >= (i0 + CH_PER) * EX_TILE;
+        if (!DEN && full) {
+            // 8 chunks of 16 steps over the group's two tiles.  A chunk is 9
+            // LDS reads and lgkmcnt holds at most 15, so one chunk is in
+            // flight: each chunk's reads are issued after the previous chunk
+            // has landed and before that chunk's FMAs, which cover them.
+            const int sa = i0 & (CH_NT - 1), sb = (i0 + 1) & (CH_NT - 1);
+            const float *va = &L.v[sa][lane], *vb = &L.v[sb][lane];
+            const float *ea = &L.e[sa][r * EX_TILE], *eb = &L.e[sb][r * EX_TILE];
+            const uint32_t m0 = L.m[sa][2 * r], m1 = L.m[sa][2 * r + 1];
+            const uint32_t m2 = L.m[sb][2 * r], m3 = L.m[sb][2 * r + 1];
+            float a0, a1, v0[16], v1[16];
+            cons_load16(ea, va, 0, lane, a0, v0);
+            __builtin_amdgcn_sched_barrier(0);
+#define CH_STEP(ET, VT, K, NA, NV, CA, CV, BITS)       \
+    RH_WAIT_LGKM0();                                   \
+    cons_load16(ET, VT, K, lane, NA, NV);              \
+    __builtin_amdgcn_sched_barrier(0);                 \
+    cons_steps16<X4>(CA, CV, o, BITS);                 \
+    __builtin_amdgcn_sched_barrier(0);
+            CH_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu)
+            CH_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16)
+            CH_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu)
+            CH_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16)
+            CH_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu)
+            CH_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16)
+            CH_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu)
+#undef CH_STEP
+            RH_WAIT_LGKM0();
+            cons_steps16<X4>(a1, v1, o, m3 >> 16);
+        } else {
+            for (int i = i0; i < min(i0 + CH_PER, ntiles); i++) {
+                const int sl = i & (CH_NT - 1);
+                const int ntok = min(EX_TILE, ctx - i * EX_TILE);
+                const float *vt = &L.v[sl][lane];
+                const float *et = &L.e[sl][r * EX_TILE];
+                uint32_t mw0 = L.m[sl][2 * r], mw1 = L.m[sl][2 * r + 1];
+                if (DEN && lane >= kvm) mw0 = mw1 = 0u;
+                if (DEN && ntok == EX_TILE) {
+                    float e0[16], e1[16], e2[16];
+                    den_load16(et, 0, e0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_load16(et, 1, e1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_load16(et, 2, e2);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_steps16(e0, o, mw0 & 0xFFFFu);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_load16(et, 3, e0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_steps16(e1, o, mw0 >> 16);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_steps16(e2, o, mw1 & 0xFFFFu);
+                    __builtin_amdgcn_sched_barrier(0);
+                    den_steps16(e0, o, mw1 >> 16);
+                } else {
+                    for (int t = 0; t < ntok; t++) {
+                        const uint32_t mw = t < 32 ? mw0 : mw1;
+                        const float e = et[t];
+                        const float v = DEN ? 1.0f : vt[t * 64];
+                        const float on = fmaf(e, v, o);
+                        const float ox = (DEN || X4) ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
+                        o = ((mw >> (t & 31)) & 1u) ? ox : on;
+                    }
+                }
+            }
+        }
+        RH_WAIT_LGKM0();  // the group's LDS reads are done before its slots are reused
+    }
+    if (active && dst) *dst = o;
+}
+
+// grid: n_heads * (vd/64) chain workgroups, then n_kv denominator
+// workgroups, CH_WAVES waves each; block b serves kv head b % n_kv, so the
+// heads of a kv head share an XCD.
+__global__ __launch_bounds__(64 * CH_WAVES) void attn_exact_chain_dma_kernel(AttnExactArgs A) {
     __shared__ ChainLds L;
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
     if (ctx <= 0) return;
-    const int nsl = A.vd / 16;
-    const int h = blockIdx.x % A.n_kv;
-    const int r = blockIdx.x / A.n_kv;
-    const int hg = r / (nsl + 1), slice = r % (nsl + 1);
-    if (slice == nsl) {
-        chain_run<true, true>(A, L, s0, ctx, h, hg, 0);
+    const int kvm = A.kv_mul, nsl = A.vd / 64;
+    const int h = blockIdx.x % A.n_kv, r = blockIdx.x / A.n_kv;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r < kvm * nsl) {
+        const int g = r / nsl, slice = r % nsl;
+        if (wave == 1) {
+            chain_producer<0>(A, L, s0, ctx, h, g, slice);
+        } else if (wave == 2) {
+            chain_producer<1>(A, L, s0, ctx, h, g, slice);
+        } else {
+            float *dst = A.out + (size_t)(h * kvm + g) * A.vd + slice * 64 + lane;
+            const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4;
+            if (x4)
+                chain_consumer<false, true>(A, L, ctx, 0, true, dst);
+            else
+                chain_consumer<false, false>(A, L, ctx, 0, true, dst);
+        }
     } else {
-        const bool x4 = A.sinks == nullptr && (A.kv_mul == 4 || A.kv_mul == 6) && hg == 0;
-        if (x4)
-            chain_run<false, true>(A, L, s0, ctx, h, hg, slice);
-        else
-            chain_run<false, false>(A, L, s0, ctx, h, hg, slice);
+        if (wave == 1) {
+            den_producer(A, L, ctx, h);
+        } else {
+            float *dst = lane < kvm ? A.den + h * kvm + lane : nullptr;
+            chain_consumer<true, true>(A, L, ctx, 0, wave == 0, dst);
+        }
     }
 }
 
@@ -496,7 +652,7 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A) {
             int t = t0 + j < ctx ? t0 + j : ctx - 1;
             int slot = (s0 + t) % A.slot_count;
             vb[j] = vbase[(size_t)slot * A.value_stride];
-            eb[j] = ef[(size_t)t * 4];
+            eb[j] = ef[t];
         }
         const uint32_t bits = mk[t0 >> 5];
         if (bits == 0 && n == 32) {

@@ -650,9 +650,7 @@ static int attn_fast_mode() {
     return g.attn_fast;
 }
 
-static size_t exact_e_floats(int n_kv, int kv_mul, int cap) {
-    return (size_t)n_kv * ((kv_mul + 3) / 4) * cap * 4;
-}
+static size_t exact_e_floats(int n_kv, int kv_mul, int cap) { return (size_t)n_kv * kv_mul * cap; }
 static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
     size_t n = (size_t)n_kv * kv_mul;
     return n * cap + exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
@@ -688,11 +686,12 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     {
         ProfScope ps("attn_exact_chain", s);
-        const bool dma = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
-                         A.slot_count >= 64 && (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
+        const bool dma = A.vd % 64 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
+                         A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
+                         (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
         if (dma) {
-            int blocks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
-            hipLaunchKernelGGL(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64), 0, s, A);
+            int blocks = A.n_kv * (A.kv_mul * (A.vd / 64) + 1);
+            hipLaunchKernelGGL(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64 * CH_WAVES), 0, s, A);
         } else {
             hipLaunchKernelGGL(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
         }
