@@ -59,12 +59,19 @@ def main():
     ap.add_argument("--kv-fill", choices=["prefill", "random"], default="prefill",
                     help="prefill: run the ctx random-id prompt through the decoder; random: write N(0,1) K/V "
                          "directly (same per-token decode work, far fewer dispatches, for profiler runs)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run only a plain device copy (y = x * 1) over this many MiB, 5 launches, and exit: the "
+                         "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
 
     import numpy as np
     from rustyllm_amd import hip, synth
@@ -123,6 +130,8 @@ def main():
     token_bytes = synth.weight_bytes(model) + kv_per_tok * pos_mid
     eff_gbs = token_bytes * tok_s / 1e9
 
+    traffic = recorded_traffic(args)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(model, res, storage, args, log)
@@ -153,7 +162,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": swiglu_bytes,
             "avg_launch_us": round(avg_ms * 1e3, 3),
             "launches": cnt,
@@ -166,6 +175,31 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_kquant_swiglu_llama3-8b-q4km_traffic.json")
+
+
+def recorded_traffic(args):
+    """HBM bytes per launch of the roofline kernel, from the two rocprofv3
+    --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded for this workload, each
+    scaled by the same counter's reading on a copy kernel of known size."""
+    if args.config != "llama3-8b-q4km" or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        rec = json.load(f)
+    return rec.get("traffic_bytes_per_launch")
+
+
+def copy_probe(mib):
+    import torch
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    log(f"copy probe: 5 x {mib} MiB read + {mib} MiB written")
 
 
 def cpu_baseline(model, res, storage, args, log):

@@ -9,6 +9,8 @@
 #include "ops.hip"
 #include "attention_exact.hip"
 
+#include <hip/hip_ext.h>
+
 #include <atomic>
 #include <cmath>
 #include <cstdio>
@@ -74,6 +76,7 @@ struct Profile {
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> pending;
     std::vector<hipEvent_t> pool;
     bool on = false;
+    struct ProfScope *cur = nullptr;  // scope whose launches rh_launch times
 };
 
 struct Ctx {
@@ -232,9 +235,15 @@ static void wcache_clear() {
 }
 
 // ---- profiling -------------------------------------------------------------------
+// A scope names one launch family.  Its kernel is timed by the dispatch
+// itself (hipExtLaunchKernel's start/stop events are stamped from the AQL
+// packet's own begin/end), which is the interval a kernel trace reports; a
+// scope that issues several launches stops at the end of its last one.
 struct ProfScope {
     int idx = -1;
+    int launches = 0;
     hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t stream = nullptr;
     ProfScope(const char *name, hipStream_t s) {
         if (!g.prof.on) return;
         auto it = g.prof.index.find(name);
@@ -249,12 +258,22 @@ struct ProfScope {
         }
         a = take();
         b = take();
-        if (a && b) (void)hipEventRecord(a, s);
+        if (!a || !b) {
+            idx = -1;
+            return;
+        }
         stream = s;
+        g.prof.cur = this;
     }
     ~ProfScope() {
-        if (idx < 0 || !a || !b) return;
-        (void)hipEventRecord(b, stream);
+        if (idx < 0) return;
+        if (g.prof.cur == this) g.prof.cur = nullptr;
+        if (launches == 0) {
+            g.prof.pool.push_back(a);
+            g.prof.pool.push_back(b);
+            return;
+        }
+        if (launches > 1) (void)hipEventRecord(b, stream);
         g.prof.pending.push_back({idx, {a, b}});
     }
     static hipEvent_t take() {
@@ -267,8 +286,18 @@ struct ProfScope {
         if (hipEventCreate(&e) != hipSuccess) return nullptr;
         return e;
     }
-    hipStream_t stream = nullptr;
 };
+
+// Every library launch goes through here: inside an active profiling scope
+// the first launch carries the scope's events.
+template <class F, class... Args>
+static void rh_launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+    ProfScope *ps = g.prof.cur;
+    if (ps && ps->stream == s && ps->launches++ == 0)
+        hipExtLaunchKernelGGL(kernel, grid, block, shm, s, ps->a, ps->b, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+}
 
 static void prof_drain() {
     if (g.prof.pending.empty()) return;
@@ -354,7 +383,7 @@ static int launch_kq(const GemvArgs &A, hipStream_t s) {
     auto kern = gemv_kq_kernel<FMT, SW, U>;
     int grid = persistent_grid(kern, A.n_tiles, 4);
     ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, A);
+    rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -363,7 +392,7 @@ static int launch_q8i(const GemvArgs &A, hipStream_t s) {
     int grid = std::min(A.n_tiles, grid_cap());
     size_t lds = (size_t)4 * R * (A.K / 32) * 9 * sizeof(float);
     ProfScope ps("gemv_q8_0_int", s);
-    hipLaunchKernelGGL((gemv_q8_0_int_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+    rh_launch((gemv_q8_0_int_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -372,7 +401,7 @@ static int launch_f32(const GemvArgs &A, hipStream_t s) {
     int grid = std::min(A.n_tiles, grid_cap());
     size_t lds = ((size_t)A.K + (size_t)4 * R * (A.K / 32)) * sizeof(float);
     ProfScope ps("gemv_b32_f32", s);
-    hipLaunchKernelGGL((gemv_b32_f32_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+    rh_launch((gemv_b32_f32_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -520,7 +549,7 @@ static int act_materialize(const ActSpec &a, int K, ActSpec *out, hipStream_t s)
     case ACT_DEN: {
         ProfScope ps("attn_exact_finish", s);
         XQ q = K % 256 == 0 ? a.xq : XQ{};
-        hipLaunchKernelGGL(attn_exact_finish_kernel, dim3((K + 255) / 256), dim3(256), 0, s, a.x, a.den, a.group, K, q);
+        rh_launch(attn_exact_finish_kernel, dim3((K + 255) / 256), dim3(256), 0, s, a.x, a.den, a.group, K, q);
         RH_LAUNCH_OK();
         *out = act_xq(q, a.x);
         return 1;
@@ -558,7 +587,7 @@ static int gemv_multi(const MatSpec *ms, int n, int K, int epi, const XQ &xq, co
 static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s) {
     if (n % 256 != 0) return 0;
     ProfScope ps("quantize_q8k", s);
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(n / 256), dim3(256), 0, s, x, n, xq);
+    rh_launch(quantize_q8k_kernel, dim3(n / 256), dim3(256), 0, s, x, n, xq);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -568,7 +597,7 @@ static int launch_rmsnorm(const float *x, const float *w, float eps, int n, floa
     XQ q = xq ? *xq : XQ{};
     if (xq && n % 256 != 0) q = XQ{};
     ProfScope ps("rmsnorm_q8k", s);
-    hipLaunchKernelGGL(rmsnorm_q8k_kernel, dim3((n + 255) / 256), dim3(256), (size_t)n * sizeof(float), s, x, w, eps,
+    rh_launch(rmsnorm_q8k_kernel, dim3((n + 255) / 256), dim3(256), (size_t)n * sizeof(float), s, x, w, eps,
                        n, xn, q);
     RH_LAUNCH_OK();
     return 1;
@@ -580,7 +609,7 @@ __global__ void silu_mul_kernel(const float *g_, const float *u, int n, float *o
 }
 static int launch_silu(const float *g_, const float *u, int n, float *out, hipStream_t s) {
     ProfScope ps("silu_mul", s);
-    hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g_, u, n, out);
+    rh_launch(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g_, u, n, out);
     RH_LAUNCH_OK();
     return 1;
 }
@@ -610,7 +639,7 @@ static int attn_launch(const AttnArgs &A, hipStream_t s) {
         ProfScope ps("attn_partial", s);
 #define RH_ATT(HD, KM)                                                                            \
     if (A.hd == HD && A.vd == HD && A.kv_mul == KM) {                                            \
-        hipLaunchKernelGGL((attn_partial_kernel<HD, HD, KM>), grid, dim3(256), 0, s, A);          \
+        rh_launch((attn_partial_kernel<HD, HD, KM>), grid, dim3(256), 0, s, A);          \
         goto launched;                                                                            \
     }
         RH_ATT(128, 1) RH_ATT(128, 2) RH_ATT(128, 4) RH_ATT(128, 5) RH_ATT(128, 6) RH_ATT(128, 8)
@@ -623,7 +652,7 @@ static int attn_launch(const AttnArgs &A, hipStream_t s) {
     {
         ProfScope ps("attn_combine", s);
         int total = A.n_heads * A.vd;
-        hipLaunchKernelGGL(attn_combine_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A);
+        rh_launch(attn_combine_kernel, dim3((total + 255) / 256), dim3(256), 0, s, A);
         RH_LAUNCH_OK();
     }
     return 1;
@@ -676,12 +705,12 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         ProfScope ps("attn_exact_scores", s);
         size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1) + (size_t)A.kv_mul * EX_TILE) *
                      sizeof(float);
-        hipLaunchKernelGGL(attn_exact_scores_kernel, dim3(ntl, A.n_kv), dim3(256), lds, s, A);
+        rh_launch(attn_exact_scores_kernel, dim3(ntl, A.n_kv), dim3(256), lds, s, A);
         RH_LAUNCH_OK();
     }
     {
         ProfScope ps("attn_exact_coef", s);
-        hipLaunchKernelGGL(attn_exact_coef_kernel, dim3(ntl, A.n_heads), dim3(64), 0, s, A);
+        rh_launch(attn_exact_coef_kernel, dim3(ntl, A.n_heads), dim3(64), 0, s, A);
         RH_LAUNCH_OK();
     }
     {
@@ -691,16 +720,16 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
                          (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
         if (dma) {
             int blocks = A.n_kv * (A.kv_mul * (A.vd / 64) + 1);
-            hipLaunchKernelGGL(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64 * CH_WAVES), 0, s, A);
+            rh_launch(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64 * CH_WAVES), 0, s, A);
         } else {
-            hipLaunchKernelGGL(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
+            rh_launch(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
         }
         RH_LAUNCH_OK();
     }
     if (den_out) *den_out = A.den;
     if (finish) {
         ProfScope ps("attn_exact_finish", s);
-        hipLaunchKernelGGL(attn_exact_finish_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, A.out, A.den, A.vd,
+        rh_launch(attn_exact_finish_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, A.out, A.den, A.vd,
                            n_out, xq);
         RH_LAUNCH_OK();
     }
@@ -1017,7 +1046,7 @@ int rusty_hip_debug_expf(const float *x, uintptr_t n, float *out) {
     if (!init_locked() || !x || !out || n == 0) return 0;
     if (!ensure(&g.x, &g.x_cap, n) || !ensure(&g.y, &g.y_cap, n)) return 0;
     RH_CHECK(hipMemcpyAsync(g.x, x, n * 4, hipMemcpyHostToDevice, g.s));
-    hipLaunchKernelGGL(expf_kernel, dim3(1024), dim3(256), 0, g.s, g.x, (int)n, g.y);
+    rh_launch(expf_kernel, dim3(1024), dim3(256), 0, g.s, g.x, (int)n, g.y);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
@@ -1083,7 +1112,7 @@ int rusty_hip_debug_dequant(uint32_t t, const uint8_t *w, uintptr_t wl, uintptr_
     if (!get_weight(w, wl, rows, cols, (int)t, &W)) return 0;
     if (!ensure(&g.y, &g.y_cap, rows * cols)) return 0;
     dim3 grid((unsigned)std::min<uintptr_t>((cols + 255) / 256, 64), (unsigned)rows);
-    hipLaunchKernelGGL(dequant_rows_kernel, grid, dim3(256), 0, g.s, W.p, W.stride, (int)rows, (int)cols, (int)t, g.y);
+    rh_launch(dequant_rows_kernel, grid, dim3(256), 0, g.s, W.p, W.stride, (int)rows, (int)cols, (int)t, g.y);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(out, g.y, rows * cols * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
@@ -1100,7 +1129,7 @@ int rusty_hip_debug_block_ints(uint32_t t, const uint8_t *w, uintptr_t wl, uintp
     if (!stage_x(x, cols) || !ensure_xq(&g.xq, &g.xq_cap, cols) || !launch_quant(g.x, (int)cols, g.xq, g.s)) return 0;
     size_t n = (t == 8) ? rows * (cols / 32) : (t == 12 ? rows * (cols / 256) * 2 : rows * (cols / 256));
     if (!ensure(&g.ibuf, &g.ibuf_cap, n)) return 0;
-    hipLaunchKernelGGL(block_ints_kernel, dim3((unsigned)rows), dim3(64), 0, g.s, W.p, W.stride, (int)rows, (int)cols,
+    rh_launch(block_ints_kernel, dim3((unsigned)rows), dim3(64), 0, g.s, W.p, W.stride, (int)rows, (int)cols,
                        (int)t, g.xq, g.ibuf);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(out, g.ibuf, n * 4, hipMemcpyDeviceToHost, g.s));
@@ -1140,7 +1169,7 @@ int rusty_hip_debug_f16(const uint16_t *h, uintptr_t n, float *out) {
     if (!init_locked() || !h || !out || n == 0) return 0;
     if (!ensure(&g.x, &g.x_cap, n) || !ensure(&g.y, &g.y_cap, n)) return 0;
     RH_CHECK(hipMemcpyAsync(g.x, h, n * 2, hipMemcpyHostToDevice, g.s));
-    hipLaunchKernelGGL(f16_kernel, dim3(256), dim3(256), 0, g.s, (const uint16_t *)g.x, (int)n, g.y);
+    rh_launch(f16_kernel, dim3(256), dim3(256), 0, g.s, (const uint16_t *)g.x, (int)n, g.y);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(out, g.y, n * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
@@ -1183,7 +1212,7 @@ int rusty_hip_debug_rope(float *q, float *k, uint32_t pos, uint32_t hd, uint32_t
     A.slots = 1;
     A.ring = 0;
     A.neox = (int)neox;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(64), dim3(256), 0, g.s, A);
+    rh_launch(rope_kv_kernel, dim3(64), dim3(256), 0, g.s, A);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(q, dq, nq * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipMemcpyAsync(k, ck, nk * 4, hipMemcpyDeviceToHost, g.s));
@@ -1293,7 +1322,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
     const int attn_cols = R.n_heads * R.vd;
     if (mode & MODE_DEVTOK) {
         ProfScope ps("embed", s);
-        hipLaunchKernelGGL(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, R.embd.p, R.embd.stride,
+        rh_launch(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, R.embd.p, R.embd.stride,
                            R.embd.fmt, dim, R.st, 0, R.x);
         RH_LAUNCH_OK();
     }
@@ -1322,7 +1351,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.neox = R.neox;
             int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
             ProfScope ps("rope_kv", s);
-            hipLaunchKernelGGL(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
+            rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
             RH_LAUNCH_OK();
         }
         ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
@@ -1405,7 +1434,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
         A.out_index = R.out_idx;
         A.advance = 1;
         ProfScope ps("argmax_greedy", s);
-        hipLaunchKernelGGL(argmax_greedy_kernel, dim3(R.am_blocks), dim3(256), 0, s, A);
+        rh_launch(argmax_greedy_kernel, dim3(R.am_blocks), dim3(256), 0, s, A);
         RH_LAUNCH_OK();
     }
     return 1;
@@ -1627,7 +1656,7 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
     // recent window = last <= 64 prompt tokens (recent_token_tail, src/runtime.rs:508-512)
     uint32_t tail = n_prompt > 64 ? n_prompt - 64 : 0;
     for (uint32_t i = 0; i < n_prompt; i++) {
-        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(64), 0, g.s, R.st, R.tokens, (int)i, (int)(start_pos + i),
+        rh_launch(set_step_kernel, dim3(1), dim3(64), 0, g.s, R.st, R.tokens, (int)i, (int)(start_pos + i),
                            i >= tail ? 1 : 0);
         RH_LAUNCH_OK();
         if (i + 1 < n_prompt) {
@@ -1750,7 +1779,7 @@ int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *rece
     A.part_i = pi;
     A.ticket = ticket;
     A.advance = 1;
-    hipLaunchKernelGGL(argmax_greedy_kernel, dim3((unsigned)blocks), dim3(256), 0, g.s, A);
+    rh_launch(argmax_greedy_kernel, dim3((unsigned)blocks), dim3(256), 0, g.s, A);
     RH_LAUNCH_OK();
     RH_CHECK(hipMemcpyAsync(&hs, st, sizeof(hs), hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
