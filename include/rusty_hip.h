@@ -174,8 +174,9 @@ int rusty_hip_weight_cache_clear(void);
 
 /* Timing on the library's stream (the stream every kernel is launched on). */
 int rusty_hip_sync(void);
-/* Per-kernel-family timing: while enabled, every launch is bracketed by a
- * HIP event pair on the library stream and graphs are bypassed. */
+/* Per-kernel-family timing: while enabled, graphs are bypassed and each
+ * family's launch is timed by a HIP event pair that the dispatch itself
+ * stamps (hipExtLaunchKernel start/stop events) on the library stream. */
 int rusty_hip_profile_enable(int on);
 /* Family i: returns 0 past the last one; fills name (<= 63 chars), total
  * milliseconds and launch count accumulated since enable. */

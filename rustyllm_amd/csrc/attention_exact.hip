@@ -270,11 +270,14 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A) {
 // everything else is kept out of its stream.
 //
 // Chain workgroups, one per (query head, 64 value dims), one wave per SIMD:
-//   wave 0     the consumer, lane = value dim; e is wave-uniform and read four
-//              positions per broadcast ds_read_b128 (the consumer never has
-//              direct loads in flight, so the compiler's drain before wide
-//              LDS reads costs nothing).  LDS return bandwidth (256 B per wave
-//              read) is what a second consumer on the CU would compete for;
+//   wave 0     the consumer, lane = value dim.  Per 16 positions it issues
+//              one ds_read_b32 of e (lane j of each 16-lane row holds
+//              position j; the FMAs take it through their DPP row_newbcast
+//              operand, so e costs no instruction of its own) and eight
+//              ds_read2st64_b32 of V position pairs.  It never has direct
+//              loads in flight, so nothing drains before its LDS reads.  A
+//              single consumer per CU: a second one would compete for LDS
+//              return bandwidth (256 B per wave read) and its SIMD's issue;
 //   waves 1-2  producers: direct global->LDS loads (global_load_lds) of V
 //              [64 positions][64 dims], e and the new-max words into a ring
 //              of CH_NT tiles, CH_P tiles ahead, waiting on their own vmcnt.
@@ -282,8 +285,8 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A) {
 // repeated V reads hit its L2.  Denominator workgroups, one per kv head:
 // wave 0 runs the heads' denominators (lane = head) as the same recurrence
 // with v = 1 (fma(e, 1, d) = d + e and fma(1, 1, d*e) = d*e + 1 round exactly
-// like the scalar ops); wave 1 loads e and the words.  One s_barrier per
-// tile publishes it and releases the slot read two tiles earlier.
+// like the scalar ops); wave 1 loads e and the words.  One s_barrier per two
+// tiles publishes them and releases the slots of the pair read before it.
 #define CH_NT 8
 #define CH_P 6
 #define CH_MAXG 8    // query heads per kv head handled by this kernel

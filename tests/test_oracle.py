@@ -419,6 +419,26 @@ def test_router_topk_matches_full_softmax():
         assert np.allclose(probs, sel, atol=1e-6)
 
 
+# ---- gpt-oss SwiGLU (model.rs:6596-6600) ----------------------------------------------------------
+def _swiglu_f64(g, u):
+    g = min(float(g), 7.0) if not np.isnan(g) else 7.0   # f32::min ignores a NaN operand
+    u = float(np.clip(u, -7.0, 7.0))                       # clamp keeps NaN
+    return g / (1.0 + np.exp(1.702 * -g)) * (u + 1.0)
+
+
+def test_swiglu_gpt_oss_closed_form_and_clamps():
+    f = O.lib.orc_swiglu_gpt_oss
+    rng = np.random.default_rng(3)
+    for g, u in zip(rng.normal(0, 4, 2000).astype(np.float32), rng.normal(0, 4, 2000).astype(np.float32)):
+        ref = _swiglu_f64(g, u)
+        assert abs(f(g, u) - ref) <= 4e-7 * max(1.0, abs(ref)), (g, u)
+    assert f(0.0, 3.0) == 0.0 and f(2.5, -1.0) == 0.0           # a zero factor
+    assert f(100.0, 2.0) == f(7.0, 2.0) and f(1.5, 50.0) == f(1.5, 7.0) and f(1.5, -50.0) == f(1.5, -7.0)
+    assert f(float("nan"), 1.0) == f(7.0, 1.0)                    # min(NaN, 7) = 7
+    assert np.isnan(f(1.0, float("nan")))
+    assert f(-30.0, 0.0) < 0.0 and abs(f(-30.0, 0.0)) < 1e-20     # g * sigmoid(1.702 g) -> -0
+
+
 # ---- greedy sampling (sampling.rs tests) -------------------------------------------------------------
 def test_repeat_penalty_pushes_seen_logits_toward_zero():
     lg = np.array([4.0, -4.0, 2.0], np.float32)
