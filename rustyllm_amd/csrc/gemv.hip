@@ -135,25 +135,62 @@ __device__ __forceinline__ Q4KLoad q4k_load(const uint8_t *blk, int q) {
     return L;
 }
 
+// Scale/min fields of quarter q (sub-blocks 2q and 2q+1) in get_scale_min_k4
+// (src/simd.rs:4537-4546): sub-block j < 4 is 6 bits of byte j of words 0
+// (scale) and 1 (min); j >= 4 is 4 bits of byte j-4 of word 2 with the top 2
+// bits of byte j-4 of word 0 / 1 above them.  q is fixed per lane, so both
+// forms become one bit-field extract of a selected word plus a second
+// extract (zero width for j < 4) shifted in at bit 4, with no branch.
+struct Q4KScaleSel {
+    bool hi;  // q >= 2
+    uint32_t sh_sc[2], sh_m[2], sh_hb[2], w_lo, w_hb;
+};
+__device__ __forceinline__ Q4KScaleSel q4k_scale_sel(int q) {
+    Q4KScaleSel S;
+    S.hi = q >= 2;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int j = 2 * q + t, k = j - 4;
+        S.sh_sc[t] = S.hi ? 8 * k : 8 * j;
+        S.sh_m[t] = S.hi ? 8 * k + 4 : 8 * j;
+        S.sh_hb[t] = S.hi ? 8 * k + 6 : 0;
+    }
+    S.w_lo = S.hi ? 4 : 6;
+    S.w_hb = S.hi ? 2 : 0;
+    return S;
+}
+__device__ __forceinline__ void q4k_scale_min(const Q4KScaleSel &S, int t, uint32_t s03, uint32_t s47, uint32_t s811,
+                                              int &sc, int &m) {
+    const uint32_t a_sc = S.hi ? s811 : s03, a_m = S.hi ? s811 : s47;
+    sc = (int)(__builtin_amdgcn_ubfe(a_sc, S.sh_sc[t], S.w_lo) | (__builtin_amdgcn_ubfe(s03, S.sh_hb[t], S.w_hb) << 4));
+    m = (int)(__builtin_amdgcn_ubfe(a_m, S.sh_m[t], S.w_lo) | (__builtin_amdgcn_ubfe(s47, S.sh_hb[t], S.w_hb) << 4));
+}
+
 // Returns the exact partial (isum, imin) of this quarter.
-__device__ __forceinline__ void q4k_unit(const Q4KLoad &L, int q, const int32_t *xq32, const int16_t *bs, int &isum,
-                                         int &imin) {
+__device__ __forceinline__ void q4k_unit(const Q4KLoad &L, int q, const Q4KScaleSel &S, const int32_t *xq32,
+                                         const int16_t *bs, int &isum, int &imin) {
     int sc1, m1, sc2, m2;
-    scale_min_k4(2 * q, L.hdr.y, L.hdr.z, L.hdr.w, sc1, m1);
-    scale_min_k4(2 * q + 1, L.hdr.y, L.hdr.z, L.hdr.w, sc2, m2);
+    q4k_scale_min(S, 0, L.hdr.y, L.hdr.z, L.hdr.w, sc1, m1);
+    q4k_scale_min(S, 1, L.hdr.y, L.hdr.z, L.hdr.w, sc2, m2);
     const uint32_t w[8] = {L.a.x, L.a.y, L.a.z, L.a.w, L.b.x, L.b.y, L.b.z, L.b.w};
     const int4 *xl = (const int4 *)(xq32 + 16 * q);
     int4 x0 = xl[0], x1 = xl[1], x2 = xl[2], x3 = xl[3];
     const int xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
                         x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-    int slo = 0, shi = 0;
+    int slo0 = 0, slo1 = 0, shi0 = 0, shi1 = 0;  // four short chains instead of two long ones
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        slo = sdot4(w[k] & 0x0F0F0F0Fu, (uint32_t)xv[k], slo);
-        shi = sdot4((w[k] >> 4) & 0x0F0F0F0Fu, (uint32_t)xv[8 + k], shi);
+    for (int k = 0; k < 8; k += 2) {
+        slo0 = sdot4(w[k] & 0x0F0F0F0Fu, (uint32_t)xv[k], slo0);
+        shi0 = sdot4((w[k] >> 4) & 0x0F0F0F0Fu, (uint32_t)xv[8 + k], shi0);
+        slo1 = sdot4(w[k + 1] & 0x0F0F0F0Fu, (uint32_t)xv[k + 1], slo1);
+        shi1 = sdot4((w[k + 1] >> 4) & 0x0F0F0F0Fu, (uint32_t)xv[9 + k], shi1);
     }
-    isum = sc1 * slo + sc2 * shi;
-    imin = m1 * (int)bs[2 * q] + m2 * (int)bs[2 * q + 1];
+    const int slo = slo0 + slo1, shi = shi0 + shi1;
+    const int bsw = *(const int *)(bs + 2 * q);  // bsums of sub-blocks 2q, 2q+1
+    // 24-bit products are exact here (|slo|, |shi| <= 32*15*128, scales and
+    // mins < 64, |bsums| <= 32*128) and issue at full rate.
+    isum = __mul24(sc2, shi) + __mul24(sc1, slo);
+    imin = __mul24(m2, bsw >> 16) + __mul24(m1, (int)(int16_t)(bsw & 0xFFFF));
 }
 
 // Q6_K unit q = (g = q>>1, j = q&1) of block b: positions l in [16j, 16j+16) of
@@ -198,7 +235,7 @@ __device__ __forceinline__ int q6k_unit(const Q6KLoad &L, int q, const int32_t *
         int sidx = j + 2 * k;  // scale byte sc[8g + j + 2k]
         uint32_t sw = sidx < 4 ? L.sc.x : L.sc.y;
         int sc = (int)(int8_t)((sw >> (8 * (sidx & 3))) & 0xFF);
-        isum += sc * dot;
+        isum += __mul24(sc, dot);  // |dot| <= 16*64*128: exact in 24 bits
     }
     return isum;
 }
@@ -233,35 +270,34 @@ __device__ __forceinline__ void unit_load(const uint8_t *blk, int q, UnitLoad &L
 // sequence (dot_q4_k_q8k_avx2: dx*(d*isum - dmin*imin); dot_q6_k_q8k_avx2:
 // (dx*d)*isum).  Every lane of the quad returns the value.
 template <int FMT>
-__device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, bool ok, const int32_t *xq32,
-                                                  const int16_t *bs, const int16_t *s16, float dx) {
+__device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, const Q4KScaleSel &S, bool ok,
+                                                  const int32_t *xq32, const int16_t *bs, const int16_t *s16,
+                                                  float dx) {
+    // Computed unconditionally (a unit outside the tile holds clamped,
+    // in-bounds bytes and is zeroed here), so no branch separates the units
+    // and the scheduler can interleave their dot-product chains.
     if (FMT == F_Q4_K) {
-        int isum = 0, imin = 0;
-        if (ok) {
-            Q4KLoad Q;
-            Q.hdr = L.a;
-            Q.a = L.b;
-            Q.b = L.c;
-            q4k_unit(Q, q, xq32, bs, isum, imin);
-        }
-        isum = quad_sum_i32(isum);
-        imin = quad_sum_i32(imin);
+        int isum, imin;
+        Q4KLoad Q;
+        Q.hdr = L.a;
+        Q.a = L.b;
+        Q.b = L.c;
+        q4k_unit(Q, q, S, xq32, bs, isum, imin);
+        isum = quad_sum_i32(ok ? isum : 0);
+        imin = quad_sum_i32(ok ? imin : 0);
         float d = h2f(L.a.x & 0xFFFF), dmin = h2f(L.a.x >> 16);
         float t1 = d * (float)isum;
         float t2 = dmin * (float)imin;
         return dx * (t1 - t2);
     }
-    int isum = 0;
-    if (ok) {
-        Q6KLoad Q;
-        Q.ql0 = L.a;
-        Q.ql1 = L.b;
-        Q.qh = L.c;
-        Q.sc = L.sc;
-        Q.d = L.dd;
-        isum = q6k_unit(Q, q, xq32, s16);
-    }
-    isum = quad_sum_i32(isum);
+    Q6KLoad Q;
+    Q.ql0 = L.a;
+    Q.ql1 = L.b;
+    Q.qh = L.c;
+    Q.sc = L.sc;
+    Q.d = L.dd;
+    int isum = q6k_unit(Q, q, xq32, s16);
+    isum = quad_sum_i32(ok ? isum : 0);
     return (dx * h2f(L.dd & 0xFFFF)) * (float)isum;
 }
 
@@ -277,32 +313,66 @@ __device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, bool
 // launch mixing both (the format is uniform per tile).
 #define KQ_U_MAX 4
 #define KQ_XQ_IT (KMAX / 16 / 256)
+// The Q8_K activation is staged in LDS with each 256-element block padded to
+// 272 bytes: the four quads a ds_read_b128 pass serves read four different
+// blocks at the same in-block offset, which would otherwise share banks.
+#define KQ_XQ_STRIDE 68
 
 struct KqTile {
     GemvMat M;  // the tile's matrix (SWIGLU: the gate matrix)
     int row0, valid;
 };
 
+// Where lane's units sit in every tile of a launch: unit u = lane + 64*i is
+// quarter u&3 of block (u>>2) % nb of tile row (u>>2) / nb.  The layout is
+// the same for all tiles, so it is worked out once per wave.
+template <int KQ_U>
+struct KqGeo {
+    int rrow[KQ_U];      // row offset from the tile's first row (SWIGLU up rows: from the up matrix's)
+    int64_t roff[KQ_U];  // byte offset of the unit's block from the tile's first row
+    int blk[KQ_U];   // block index
+    int vidx[KQ_U];  // slot of the block value in the wave's LDS row buffer
+    bool up[KQ_U];   // SWIGLU: the unit reads the up matrix
+    bool in[KQ_U];   // the unit index is inside the tile
+};
 template <int FMT, bool SWIGLU, int KQ_U>
-__device__ __forceinline__ void kq_load_tile(const GemvArgs &A, const KqTile &T, int tr, int nb, int lane,
-                                             UnitLoad (&L)[KQ_U]) {
-    // Every lane issues the same loads on every path (units past the tile or
-    // the matrix read row 0, block 0 and are discarded), so the compiler's
-    // vmcnt bookkeeping stays exact and the next tile's loads stay in flight
-    // while this tile computes.
+__device__ __forceinline__ KqGeo<KQ_U> kq_geo(int tr, int nb, int nbp, int64_t stride, int lane) {
+    KqGeo<KQ_U> G;
     const int units = (SWIGLU ? 2 : 1) * tr * nb * 4;
 #pragma unroll
     for (int i = 0; i < KQ_U; i++) {
         const int u = lane + 64 * i;
         const int rt = (u >> 2) / nb, b = (u >> 2) - rt * nb;
-        const bool up = SWIGLU && rt >= tr;
-        const int row = T.row0 + (up ? rt - tr : rt);
+        G.up[i] = SWIGLU && rt >= tr;
+        G.rrow[i] = G.up[i] ? rt - tr : rt;
+        G.blk[i] = b;
+        G.roff[i] = (int64_t)G.rrow[i] * stride + b * (FMT == F_Q4_K ? 144 : 210);
+        G.vidx[i] = rt * nbp + b;
+        G.in[i] = u < units;
+    }
+    return G;
+}
+
+template <int FMT, bool SWIGLU, int KQ_U>
+__device__ __forceinline__ void kq_load_tile(const GemvArgs &A, const KqTile &T, const KqGeo<KQ_U> &G,
+                                             UnitLoad (&L)[KQ_U]) {
+    // Every lane issues the same loads on every path (units past the tile or
+    // the matrix read offset 0 and are discarded), so the compiler's vmcnt
+    // bookkeeping stays exact and the next tile's loads stay in flight while
+    // this tile computes.
+    // All matrices of a K-quant launch share one row stride (same format and
+    // K), so a unit's address is the tile's (scalar) row base plus its
+    // precomputed per-lane offset.
+    const int64_t base = (int64_t)T.row0 * A.m[0].row_stride;
+#pragma unroll
+    for (int i = 0; i < KQ_U; i++) {
+        const int row = T.row0 + G.rrow[i];
+        const bool up = G.up[i];
         const uint8_t *w = up ? A.m[1].w : T.M.w;
-        const int64_t stride = up ? A.m[1].row_stride : T.M.row_stride;
         const int rows = up ? A.m[1].rows : T.M.rows;
-        const bool ok = T.valid && u < units && row < rows;
-        const int64_t off = ok ? (int64_t)row * stride + b * (FMT == F_Q4_K ? 144 : 210) : 0;
-        unit_load<FMT>(w + off, u & 3, L[i]);
+        const bool ok = T.valid && G.in[i] && row < rows;
+        const int64_t off = ok ? base + G.roff[i] : 0;
+        unit_load<FMT>(w + off, threadIdx.x & 3, L[i]);
     }
 }
 
@@ -324,22 +394,45 @@ __device__ __forceinline__ KqEpi kq_epi_load(const KqTile &T, int lane) {
     return E;
 }
 
+// Serial sum of n block values in block order (the reference's per-row
+// accumulation), four per LDS read; p is 16-byte aligned.
+__device__ __forceinline__ float kq_row_sum(const float *p, int n) {
+    float acc = 0.0f;
+    int b = 0;
+    for (; b + 16 <= n; b += 16) {
+        const float4 v0 = *(const float4 *)(p + b), v1 = *(const float4 *)(p + b + 4);
+        const float4 v2 = *(const float4 *)(p + b + 8), v3 = *(const float4 *)(p + b + 12);
+        acc += v0.x; acc += v0.y; acc += v0.z; acc += v0.w;
+        acc += v1.x; acc += v1.y; acc += v1.z; acc += v1.w;
+        acc += v2.x; acc += v2.y; acc += v2.z; acc += v2.w;
+        acc += v3.x; acc += v3.y; acc += v3.z; acc += v3.w;
+    }
+    for (; b + 4 <= n; b += 4) {
+        const float4 v = *(const float4 *)(p + b);
+        acc += v.x;
+        acc += v.y;
+        acc += v.z;
+        acc += v.w;
+    }
+    for (; b < n; b++) acc += p[b];
+    return acc;
+}
+
 template <int FMT, bool SWIGLU, int KQ_U>
-__device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile &T, const KqEpi &E, int tr, int nb,
+__device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile &T, const KqEpi &E,
+                                                const KqGeo<KQ_U> &G, const Q4KScaleSel &S, int tr, int nb, int nbp,
                                                 int lane, const UnitLoad (&L)[KQ_U], const int32_t *s_xq,
                                                 const float *s_dx, const int16_t *s_bs, const int16_t *s_s16,
                                                 float *s_v) {
-    const int units = (SWIGLU ? 2 : 1) * tr * nb * 4;
+    const int q = lane & 3;
 #pragma unroll
     for (int i = 0; i < KQ_U; i++) {
-        const int u = lane + 64 * i;
-        const int rt = (u >> 2) / nb, b = (u >> 2) - rt * nb;
-        const bool up = SWIGLU && rt >= tr;
-        const int row = T.row0 + (up ? rt - tr : rt);
-        const bool ok = u < units && row < (up ? A.m[1].rows : T.M.rows);
-        const int bb = ok ? b : 0;
-        float v = unit_block_value<FMT>(L[i], u & 3, ok, s_xq + bb * 64, s_bs + bb * 8, s_s16 + bb * 16, s_dx[bb]);
-        if (ok && (u & 3) == 0) s_v[rt * nb + b] = v;
+        const int row = T.row0 + G.rrow[i];
+        const bool ok = G.in[i] && row < (G.up[i] ? A.m[1].rows : T.M.rows);
+        const int bb = ok ? G.blk[i] : 0;
+        float v = unit_block_value<FMT>(L[i], q, S, ok, s_xq + bb * KQ_XQ_STRIDE, s_bs + bb * 8, s_s16 + bb * 16,
+                                        s_dx[bb]);
+        if (ok && q == 0) s_v[G.vidx[i]] = v;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -348,11 +441,9 @@ __device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile 
         const GemvMat &M = T.M;
         const int row = T.row0 + lane;
         if (row < M.rows) {
-            float acc = 0.0f;
-            for (int b = 0; b < nb; b++) acc += s_v[lane * nb + b];
+            float acc = kq_row_sum(s_v + lane * nbp, nb);
             if (SWIGLU) {
-                float up = 0.0f;
-                for (int b = 0; b < nb; b++) up += s_v[(tr + lane) * nb + b];
+                const float up = kq_row_sum(s_v + (tr + lane) * nbp, nb);
                 M.y[row] = silu_mul_ref(acc, up);
             } else {
                 if (M.bias) acc += E.bias;
@@ -387,44 +478,54 @@ __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int 
 // units per lane (a wave tile is 64*KQ_U quarter-block units).
 template <int FMT, bool SWIGLU, int KQ_U>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
-    __shared__ int32_t s_xq[KMAX / 4];
+    __shared__ int32_t s_xq[NB256_MAX * KQ_XQ_STRIDE];
     __shared__ float s_dx[NB256_MAX];
     __shared__ int16_t s_bs[NB32_MAX];
     __shared__ int16_t s_s16[KMAX / 16];
-    __shared__ float s_v[4][64];
+    __shared__ __align__(16) float s_v[4][64];
 
-    const int K = A.K, nb = K >> 8;
+    const int K = A.K, nb = K >> 8, nbp = (nb + 3) & ~3;
     const int tr = A.tile_rows;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
     const int step = gridDim.x * 4;
     int tile = blockIdx.x * 4 + wave;
+    const KqGeo<KQ_U> G = kq_geo<FMT, SWIGLU, KQ_U>(tr, nb, nbp, A.m[0].row_stride, lane);
+    const Q4KScaleSel S = q4k_scale_sel(lane & 3);
 
-    // First tile's weights, then the activation: both are in flight together,
-    // and the LDS writes wait only for the activation loads issued last... in
-    // order: the weights are older, so they are complete by then as well.
+    // Prologue: the activation's loads first, then the first two tiles'
+    // weights and epilogue operands, so that staging the activation in LDS
+    // waits only for its own loads and both tiles are in flight from the
+    // start.  Each tile's epilogue loads follow its weights: computing a tile
+    // then waits for exactly the loads issued before the next tile's.
+    static_assert(KQ_XQ_IT == 4, "staging below is written for K <= 16384");
+    const int n16 = K >> 4;
+    const int nbs = K >> 8;   // int4 chunks of bsums (8 per 256)
+    const int ns16 = K >> 7;  // int4 chunks of sums16 (16 per 256)
+    const int4 *src = (const int4 *)A.xq.qs;
+    const int4 x0 = src[min(tid, n16 - 1)];
+    const int4 x1 = src[min(tid + 256, n16 - 1)];
+    const int4 x2 = src[min(tid + 512, n16 - 1)];
+    const int4 x3 = src[min(tid + 768, n16 - 1)];
+    const int4 bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
+    const int4 s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
+    const float dxr = A.xq.d[min(tid, nb - 1)];
+
     UnitLoad L0[KQ_U], L1[KQ_U];
     KqTile T0 = kq_tile_info<SWIGLU>(A, tile, tr);
-    kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, tr, nb, lane, L0);
-
+    kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
+    KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
+    KqTile T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+    kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
+    KqEpi E1 = kq_epi_load<SWIGLU>(T1, lane);
     {
-        static_assert(KQ_XQ_IT == 4, "staging below is written for K <= 16384");
-        const int n16 = K >> 4;
-        const int nbs = K >> 8;   // int4 chunks of bsums (8 per 256)
-        const int ns16 = K >> 7;  // int4 chunks of sums16 (16 per 256)
-        const int4 *src = (const int4 *)A.xq.qs;
-        const int4 x0 = src[min(tid, n16 - 1)];
-        const int4 x1 = src[min(tid + 256, n16 - 1)];
-        const int4 x2 = src[min(tid + 512, n16 - 1)];
-        const int4 x3 = src[min(tid + 768, n16 - 1)];
-        const int4 bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
-        const int4 s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
-        const float dxr = A.xq.d[min(tid, nb - 1)];
+        // 16-byte chunk c of the activation goes to block c/16, padded stride
         int4 *dst = (int4 *)s_xq;
-        if (tid < n16) dst[tid] = x0;
-        if (tid + 256 < n16) dst[tid + 256] = x1;
-        if (tid + 512 < n16) dst[tid + 512] = x2;
-        if (tid + 768 < n16) dst[tid + 768] = x3;
+        const int d0 = (tid >> 4) * (KQ_XQ_STRIDE / 4) + (tid & 15);
+        if (tid < n16) dst[d0] = x0;
+        if (tid + 256 < n16) dst[d0 + 16 * (KQ_XQ_STRIDE / 4)] = x1;
+        if (tid + 512 < n16) dst[d0 + 32 * (KQ_XQ_STRIDE / 4)] = x2;
+        if (tid + 768 < n16) dst[d0 + 48 * (KQ_XQ_STRIDE / 4)] = x3;
         if (tid < nbs) ((int4 *)s_bs)[tid] = bsr;
         if (tid < ns16) ((int4 *)s_s16)[tid] = s16r;
         if (tid < nb) s_dx[tid] = dxr;
@@ -432,17 +533,20 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
     __syncthreads();
 
     while (T0.valid) {
-        const KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
-        KqTile T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
-        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, tr, nb, lane, L1);
-        kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T0, E0, tr, nb, lane, L0, s_xq, s_dx, s_bs, s_s16, s_v[wave]);
+        kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T0, E0, G, S, tr, nb, nbp, lane, L0, s_xq, s_dx, s_bs, s_s16,
+                                           s_v[wave]);
         tile += step;
         if (!T1.valid) break;
-        const KqEpi E1 = kq_epi_load<SWIGLU>(T1, lane);
         T0 = kq_tile_info<SWIGLU>(A, tile + step, tr);
-        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, tr, nb, lane, L0);
-        kq_compute_tile<FMT, SWIGLU>(A, T1, E1, tr, nb, lane, L1, s_xq, s_dx, s_bs, s_s16, s_v[wave]);
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
+        E0 = kq_epi_load<SWIGLU>(T0, lane);
+        kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T1, E1, G, S, tr, nb, nbp, lane, L1, s_xq, s_dx, s_bs, s_s16,
+                                           s_v[wave]);
         tile += step;
+        if (!T0.valid) break;
+        T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
+        E1 = kq_epi_load<SWIGLU>(T1, lane);
     }
 }
 
@@ -666,7 +770,7 @@ __global__ void block_ints_kernel(const uint8_t *w, int64_t row_stride, int rows
             for (int q = 0; q < 4; q++) {
                 Q4KLoad L = q4k_load(wr + b * 144, q);
                 int a, m;
-                q4k_unit(L, q, xq32, xq.bsums + b * 8, a, m);
+                q4k_unit(L, q, q4k_scale_sel(q), xq32, xq.bsums + b * 8, a, m);
                 isum += a;
                 imin += m;
             }

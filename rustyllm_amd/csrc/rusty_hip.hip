@@ -430,9 +430,12 @@ static int kq_units_per_lane(int K, int rows, bool swiglu) {
     int u = std::max(pref, need);
     return u > 4 ? 0 : u;
 }
+// Rows per wave tile: all units fit the wave (4*rows*nb <= 64*U quarter
+// blocks) and the block values fit its LDS row buffer (rows padded to a
+// multiple of 4 blocks, 64 slots).
 static int kq_tile_rows(int K, int units_per_lane, bool swiglu) {
-    const int nb = K / 256;
-    return std::max(1, 16 * units_per_lane / nb / (swiglu ? 2 : 1));
+    const int nb = K / 256, nbp = (nb + 3) & ~3, m = swiglu ? 2 : 1;
+    return std::max(1, std::min(16 * units_per_lane / nb, 64 / nbp) / m);
 }
 
 // rows per tile for each (category, ITERS)
@@ -496,8 +499,8 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     A.n_tiles = tiles;
     A.tile_rows = r;
     if (cat == CAT_KQ) {
-        for (int i = 1; i < n; i++)
-            if (A.m[i].fmt != A.m[0].fmt) return 0;  // gemv_multi groups by format
+        for (int i = 1; i < n; i++)  // gemv_multi groups by format; the kernel assumes one row stride
+            if (A.m[i].fmt != A.m[0].fmt || A.m[i].row_stride != A.m[0].row_stride) return 0;
         const bool q4 = A.m[0].fmt == 12;
 #define RH_KQ_U(U)                                                                                     \
     if (it == U) {                                                                                     \
