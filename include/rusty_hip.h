@@ -137,6 +137,27 @@ int rusty_hip_mxfp4_matvec2(const uint8_t *weights_a, uintptr_t weights_a_len, u
                             const uint8_t *weights_b, uintptr_t weights_b_len, uintptr_t rows_b, const float *x,
                             uintptr_t cols, float *out_a, float *out_b);
 
+/* Routed MoE feed-forward block of gpt-oss decode (forward_gpt_oss_into,
+ * src/model.rs:6846-6898; the reference has no GPU hook for it): router
+ * logits = router_w x (+ router_bias), the top_k experts in f32 total order
+ * (ties: lower index, select_top_logits_into :6659-6716), softmax over them
+ * (softmax_selected_into :6639-6656), per expert h = swiglu_gpt_oss(gate x +
+ * gate_bias, up x + up_bias), y = down h + down_bias, out = sum over the
+ * selected experts in order of y * p.  x is the normalized input (xn2);
+ * out (dim floats) receives the block's output before the residual add.
+ * Expert tensors are expert-major [n_experts][rows] of GGML blocks
+ * (ExpertWeight, src/model.rs:922-955) with f32 activations (MXFP4 = 39, or
+ * Q8_0 = 8 when dim / hidden % 256 != 0); biases [n_experts][rows] f32, may be
+ * null.  router_dt / expert_dt are GGML type ids.  selected / probs (top_k
+ * entries each, may be null) receive the chosen experts and their weights.
+ * n_experts <= 64, top_k <= 8.  Bit-identical to the reference. */
+int rusty_hip_moe_ffn(const float *x, uintptr_t dim, const uint8_t *router_w, uintptr_t router_w_len,
+                      uint32_t router_dt, const float *router_bias, uint32_t n_experts, uint32_t top_k,
+                      const uint8_t *gate_w, uintptr_t gate_w_len, const uint8_t *up_w, uintptr_t up_w_len,
+                      const uint8_t *down_w, uintptr_t down_w_len, uint32_t expert_dt, uintptr_t hidden,
+                      const float *gate_bias, const float *up_bias, const float *down_bias, float *out,
+                      int32_t *selected, float *probs);
+
 /* Generic single matvec for any supported GGML type (8, 12, 14, 39): the
  * Weight::matvec_into dispatch of src/model.rs:218-257. */
 int rusty_hip_matvec(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, const float *x,

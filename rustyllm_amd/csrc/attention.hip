@@ -12,6 +12,7 @@
 // from HBM once per token (GQA reuse), and writes (m, l, o) per head.
 // Pass 2 (attn_combine): log-sum-exp merge of the chunks (+ sink), written as
 // f32 and, optionally, as the Q8_K activation the next projection consumes.
+#pragma once
 #include "common.hpp"
 
 namespace rh {

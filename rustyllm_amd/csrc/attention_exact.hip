@@ -26,6 +26,7 @@
 // (fma(v, alpha, out*mul)) for heads 0..3 of kv_mul 4/6 groups, scale_add /
 // axpy (fma(out, old, v) / fma(w, v, out)) otherwise; with sinks every head
 // uses the per-head sink scan (online_attention_with_sink).
+#pragma once
 #include "common.hpp"
 
 namespace rh {

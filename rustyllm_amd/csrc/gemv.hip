@@ -35,10 +35,13 @@ struct GemvMat {
     float *y;
     const float *bias;
     int32_t tile_begin;  // first tile index of this matrix in the launch
-    int32_t pad;
+    int32_t sel_b;       // with sel: floats between the experts' bias rows
+    const float *x;      // f32-activation kernels: this matrix's activation (null: the launch's)
+    const int32_t *sel;  // expert chosen on the device: w += *sel * sel_w, bias += *sel * sel_b
+    int64_t sel_w;       // with sel: bytes between the experts' matrices
 };
 
-#define GEMV_MAX_MATS 4
+#define GEMV_MAX_MATS 8
 
 // The Q8_K activation a launch consumes is always prepared by a standalone
 // kernel (host ActSpec); building it inside every GEMV workgroup was measured
@@ -71,7 +74,10 @@ __device__ __forceinline__ GemvMat mat_sel(const GemvArgs &, int mi) {
     r.y = ka->m[mi].y;
     r.bias = ka->m[mi].bias;
     r.tile_begin = ka->m[mi].tile_begin;
-    r.pad = 0;
+    r.sel_b = ka->m[mi].sel_b;
+    r.x = ka->m[mi].x;
+    r.sel = ka->m[mi].sel;
+    r.sel_w = ka->m[mi].sel_w;
     return r;
 }
 
@@ -647,98 +653,98 @@ __global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
     }
 }
 
-// f32-activation paths: Q8_0 with K % 256 != 0 and MXFP4.  Each lane forms
-// one block's f32 partial; the row sum then runs serially in block order.
-// The reference sums these formats in one serial chain per row
-// (src/simd.rs:6671-6692, 5886-5902), so this path is compared with a
-// tolerance, not bit for bit.
-template <int ITERS, int R>
-__global__ __launch_bounds__(256) void gemv_b32_f32_kernel(GemvArgs A) {
-    extern __shared__ float s_dyn[];
-    float *s_x = s_dyn;            // [K]
-    float *s_v = s_dyn + A.K;      // [4R][nb]
-    const int K = A.K, nb = K >> 5;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
-    for (int i = tid; i < K; i += 256) s_x[i] = A.x[i];
-    __syncthreads();
+// f32-activation GEMVs, bit-identical to the reference rows:
+//   Q8_0  (dot_q8_0_f32_avx2, src/simd.rs:6671-6692): eight accumulators per
+//         row, acc_j = fma(d*q, x, acc_j) over elements 32b + 8i + j (block b
+//         outer, group i inner), then hsum_avx ((a0+a4)+(a1+a5)) +
+//         ((a2+a6)+(a3+a7)); eight lanes per row, eight rows per wave;
+//   MXFP4 (dot_mxfp4_f32_scalar, src/simd.rs:5886-5902): one running sum per
+//         row, sum += (lut*scale)*x element by element; one lane per row.
+// A workgroup is one wave over tiles of 8 (Q8_0) or 64 (MXFP4) rows; the
+// activation (the matrix's own, else the launch's) is staged in LDS.
+template <int FMT>
+__global__ __launch_bounds__(64) void gemv_f32x_kernel(GemvArgs A) {
+    extern __shared__ float s_x[];  // [K]
+    __shared__ float s_lut[16];
+    const int K = A.K, nb = K >> 5, lane = threadIdx.x;
+    if (FMT == F_MXFP4 && lane < 16) s_lut[lane] = kMxfp4Lut[lane];
+    const float *staged = nullptr;
     for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
         int mi = 0;
 #pragma unroll
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
         const GemvMat M = mat_sel(A, mi);
-        int row0 = (tile - M.tile_begin) * (4 * R);
-        uint4 wa[R][ITERS], wb[R][ITERS];
-        uint32_t dd[R][ITERS];
-        const int bsz = M.fmt == F_Q8_0 ? 34 : 17;
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int i = 0; i < ITERS; i++) {
-                int b = lane + 64 * i, row = row0 + wave * R + r;
-                if (b < nb && row < M.rows) {
-                    const uint8_t *blk = M.w + (int64_t)row * M.row_stride + b * bsz;
-                    if (M.fmt == F_Q8_0) {
-                        dd[r][i] = ld2(blk);
-                        wa[r][i] = ld16(blk + 2);
-                        wb[r][i] = ld16(blk + 18);
-                    } else {
-                        wa[r][i] = ld16(blk);
-                        dd[r][i] = blk[16];
-                    }
-                }
-            }
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int i = 0; i < ITERS; i++) {
-                int b = lane + 64 * i, row = row0 + wave * R + r;
-                if (b < nb && row < M.rows) {
-                    const float *xb = s_x + b * 32;
-                    float acc = 0.0f;
-                    if (M.fmt == F_Q8_0) {
-                        float d = h2f(dd[r][i]);
-                        const uint32_t w[8] = {wa[r][i].x, wa[r][i].y, wa[r][i].z, wa[r][i].w,
-                                               wb[r][i].x, wb[r][i].y, wb[r][i].z, wb[r][i].w};
-#pragma unroll
-                        for (int k = 0; k < 8; k++)
-#pragma unroll
-                            for (int t = 0; t < 4; t++) {
-                                float q = (float)(int8_t)((w[k] >> (8 * t)) & 0xFF);
-                                acc = fmaf(d * q, xb[4 * k + t], acc);
-                            }
-                    } else {
-                        float s = mxfp4_scale(dd[r][i]);
-                        const uint32_t w[4] = {wa[r][i].x, wa[r][i].y, wa[r][i].z, wa[r][i].w};
-#pragma unroll
-                        for (int k = 0; k < 4; k++)
-#pragma unroll
-                            for (int t = 0; t < 4; t++) {
-                                uint32_t byte = (w[k] >> (8 * t)) & 0xFF;
-                                float lo = kMxfp4Lut[byte & 0xF] * s;
-                                float hi = kMxfp4Lut[byte >> 4] * s;
-                                acc = acc + lo * xb[8 * k + 2 * t];
-                                acc = acc + hi * xb[8 * k + 2 * t + 1];
-                            }
-                    }
-                    s_v[(wave * R + r) * nb + b] = acc;
-                }
-            }
-        __syncthreads();
-        if (tid < 4 * R) {
-            int row = row0 + tid;
-            if (row < M.rows) {
-                float acc = 0.0f;
-                for (int b = 0; b < nb; b++) acc += s_v[tid * nb + b];
-                if (M.bias) acc += M.bias[row];
-                if (A.epi == EPI_ADD)
-                    M.y[row] += acc;
-                else
-                    M.y[row] = acc;
-            }
+        const float *xs = M.x ? M.x : A.x;
+        if (xs != staged) {
+            __syncthreads();
+            for (int i = 4 * lane; i < K; i += 256) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
+            __syncthreads();
+            staged = xs;
         }
-        __syncthreads();
+        const uint8_t *w = M.w;
+        const float *bias = M.bias;
+        if (M.sel) {
+            const int64_t e = *M.sel;
+            w += e * M.sel_w;
+            if (bias) bias += e * M.sel_b;
+        }
+        float out;
+        int row;
+        bool store;
+        if (FMT == F_MXFP4) {
+            row = (tile - M.tile_begin) * 64 + lane;
+            store = row < M.rows;
+            const uint8_t *rp = w + (int64_t)(store ? row : 0) * M.row_stride;
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint4 q = ld16(rp + b * 17);
+                const float sc = mxfp4_scale(rp[b * 17 + 16]);
+                const float *xb = s_x + b * 32;
+                const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const uint32_t byte = (wd[k] >> (8 * t)) & 0xFFu;
+                        sum += s_lut[byte & 0xFu] * sc * xb[8 * k + 2 * t];
+                        sum += s_lut[byte >> 4] * sc * xb[8 * k + 2 * t + 1];
+                    }
+            }
+            out = sum;
+        } else {
+            const int j = lane & 7;
+            row = (tile - M.tile_begin) * 8 + (lane >> 3);
+            const bool ok = row < M.rows;
+            const uint8_t *rp = w + (int64_t)(ok ? row : 0) * M.row_stride;
+            const uint32_t sh = 8u * (uint32_t)(j & 3);
+            const bool hi = j >= 4;
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *blk = rp + b * 34;
+                const float d = ldh(blk);
+                const uint4 q0 = ld16(blk + 2), q1 = ld16(blk + 18);
+                // byte 8i + j of the 32 quants: dword 2i + j/4, bits 8*(j%4)
+                const uint32_t dw[4] = {hi ? q0.y : q0.x, hi ? q0.w : q0.z, hi ? q1.y : q1.x, hi ? q1.w : q1.z};
+                const float *xb = s_x + b * 32 + j;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float q = (float)(int)__builtin_amdgcn_sbfe((int)dw[i], sh, 8u);
+                    acc = fmaf(d * q, xb[8 * i], acc);
+                }
+            }
+            const float t = acc + __shfl_xor(acc, 4, 64);
+            const float u = t + __shfl_xor(t, 1, 64);
+            out = u + __shfl_xor(u, 2, 64);
+            store = ok && j == 0;
+        }
+        if (store) {
+            if (bias) out += bias[row];
+            if (A.epi == EPI_ADD)
+                M.y[row] += out;
+            else
+                M.y[row] = out;
+        }
     }
 }
 

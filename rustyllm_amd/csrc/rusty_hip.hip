@@ -8,6 +8,7 @@
 #include "attention.hip"
 #include "ops.hip"
 #include "attention_exact.hip"
+#include "moe.hip"
 
 #include <hip/hip_ext.h>
 
@@ -95,6 +96,8 @@ struct Ctx {
     size_t xq2_cap = 0;
     float *part = nullptr;
     size_t part_cap = 0;
+    float *moe = nullptr;  // MoE block scratch: logits, probs, gate, up, proj (+ int32 selection)
+    size_t moe_cap = 0;
     float *kv_k = nullptr, *kv_v = nullptr;
     size_t kv_cap = 0;
     int32_t *ibuf = nullptr;
@@ -396,16 +399,15 @@ static int launch_q8i(const GemvArgs &A, hipStream_t s) {
     RH_LAUNCH_OK();
     return 1;
 }
-template <int IT, int R>
-static int launch_f32(const GemvArgs &A, hipStream_t s) {
-    int grid = std::min(A.n_tiles, grid_cap());
-    size_t lds = ((size_t)A.K + (size_t)4 * R * (A.K / 32)) * sizeof(float);
-    ProfScope ps("gemv_b32_f32", s);
-    rh_launch((gemv_b32_f32_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+template <int FMT>
+static int launch_f32x(const GemvArgs &A, hipStream_t s) {
+    auto kern = gemv_f32x_kernel<FMT>;
+    int grid = std::min(A.n_tiles, g.n_cu * 8);
+    ProfScope ps("gemv_f32x", s);
+    rh_launch(kern, dim3(grid), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
     RH_LAUNCH_OK();
     return 1;
 }
-
 // K-quant tiles: it = units per lane (a wave tile is 64*it quarter-block
 // units of r whole rows; SWIGLU tiles hold r gate + r up rows).  Small
 // launches use fewer units per lane so more waves share the latency; large
@@ -480,7 +482,10 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     A.x = act.x;
     A.n_mats = n;
     int tiles = 0;
-    int rows_per_tile = (cat == CAT_KQ) ? r : 4 * r;
+    int rows_per_tile = (cat == CAT_KQ) ? r : (cat == CAT_F32) ? (ms[0].w.fmt == 8 ? 8 : 64) : 4 * r;
+    if (cat == CAT_F32)
+        for (int i = 1; i < n; i++)
+            if (ms[i].w.fmt != ms[0].w.fmt) return 0;  // one format per launch
     for (int i = 0; i < n; i++) {
         GemvMat &m = A.m[i];
         m.w = ms[i].w.p;
@@ -520,14 +525,7 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
         default: return 0;
         }
     }
-    switch (it) {
-    case 1: return launch_f32<1, 4>(A, s);
-    case 2: return launch_f32<2, 2>(A, s);
-    case 3: return launch_f32<3, 1>(A, s);
-    case 4: return launch_f32<4, 1>(A, s);
-    case 6: return launch_f32<6, 1>(A, s);
-    default: return launch_f32<8, 1>(A, s);
-    }
+    return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
 }
 
 static int launch_quant(const float *x, int n, const XQ &xq, hipStream_t s);
@@ -574,7 +572,7 @@ static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpe
         MatSpec grp[GEMV_MAX_MATS];
         int ng = 0;
         for (int j = i; j < n; j++)
-            if (!done[j] && cat_of(ms[j].w.fmt, K) == cat && (cat != CAT_KQ || ms[j].w.fmt == ms[i].w.fmt)) {
+            if (!done[j] && cat_of(ms[j].w.fmt, K) == cat && (cat == CAT_Q8I || ms[j].w.fmt == ms[i].w.fmt)) {
                 grp[ng++] = ms[j];
                 done[j] = 1;
             }
@@ -798,6 +796,116 @@ static int ffn_device(const DevW &gate, const DevW &up, const DevW &down, int in
     }
     MatSpec md = {down, y, nullptr};
     return gemv_multi(&md, 1, hidden, epi, g.xq2, hbuf, g.s);
+}
+
+// Routed MoE block (forward_gpt_oss_into, src/model.rs:6846-6898) on the
+// device: router GEMV (+ bias), top-k + softmax, the k experts' gate and up
+// rows in one launch (expert read on the device), SwiGLU with biases, the k
+// down products in one launch (each with its own activation), then the
+// combine.  Experts: rows of all experts stacked expert-major; f32-activation
+// formats (MXFP4, Q8_0 with K % 256 != 0).  Scratch lives in `buf`
+// (moe_scratch_floats); sel/prob are int32/f32 slots [k] inside it.
+static size_t moe_scratch_floats(int n_exp, int k, int dim, int hidden) {
+    return (size_t)64 + n_exp + 2 * 8 + (size_t)2 * k * hidden + (size_t)k * dim;
+}
+struct MoeDev {
+    DevW router, gate, up, down;
+    const float *router_bias, *gb, *ub, *db;  // device, may be null (router_bias: per expert; others [n_exp][rows])
+    int gb_stride, ub_stride, db_stride;      // floats between expert bias rows
+    int n_exp, k, dim, hidden;
+};
+static int moe_ffn_enqueue(const MoeDev &M, const float *xn, float *moe_out, float *x_add, float *buf, hipStream_t s,
+                           int32_t **sel_out = nullptr, float **prob_out = nullptr) {
+    const int k = M.k, dim = M.dim, hidden = M.hidden;
+    if (k < 1 || k > 8 || M.n_exp > 64 || k > M.n_exp) return 0;
+    if (cat_of(M.gate.fmt, dim) != CAT_F32 || M.up.fmt != M.gate.fmt || cat_of(M.down.fmt, hidden) != CAT_F32)
+        return 0;
+    float *logits = buf;                        // [64]
+    int32_t *sel = (int32_t *)(buf + 64);       // [8]
+    float *prob = buf + 72;                     // [8]
+    float *gate = buf + 80 + M.n_exp;           // [k][hidden]
+    float *up = gate + (size_t)k * hidden;      // [k][hidden]
+    float *proj = up + (size_t)k * hidden;      // [k][dim]
+    gate = (float *)(((uintptr_t)gate + 15) & ~(uintptr_t)15);
+    up = gate + (size_t)k * hidden;
+    proj = up + (size_t)k * hidden;
+    {
+        MatSpec mr = {M.router, logits, M.router_bias};
+        ActSpec a;
+        memset(&a, 0, sizeof(a));
+        a.mode = dim % 256 == 0 ? ACT_QUANT : ACT_XQ;
+        a.x = (float *)xn;
+        a.xq = g.xq;
+        if (a.mode == ACT_QUANT && !ensure_xq(&g.xq, &g.xq_cap, dim)) return 0;
+        a.xq = g.xq;
+        if (!gemv_multi_act(&mr, 1, dim, EPI_STORE, a, s)) return 0;
+    }
+    {
+        ProfScope ps("moe_topk", s);
+        rh_launch(moe_topk_kernel, dim3(1), dim3(64), 0, s, (const float *)logits, M.n_exp, k, sel, prob);
+        RH_LAUNCH_OK();
+    }
+    auto expert_mat = [&](const DevW &W, int rows, int r, float *y, const float *x) {
+        GemvMat m;
+        memset(&m, 0, sizeof(m));
+        m.w = W.p;
+        m.row_stride = W.stride;
+        m.rows = rows;
+        m.fmt = W.fmt;
+        m.y = y;
+        m.x = x;
+        m.sel = sel + r;
+        m.sel_w = (int64_t)rows * W.stride;
+        return m;
+    };
+    auto launch = [&](GemvArgs &A, int rows_per_tile) {
+        int tiles = 0;
+        for (int i = 0; i < A.n_mats; i++) {
+            A.m[i].tile_begin = tiles;
+            tiles += (A.m[i].rows + rows_per_tile - 1) / rows_per_tile;
+        }
+        A.n_tiles = tiles;
+        return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
+    };
+    const int rpt_in = M.gate.fmt == 8 ? 8 : 64, rpt_down = M.down.fmt == 8 ? 8 : 64;
+    {
+        GemvArgs A;
+        memset(&A, 0, sizeof(A));
+        A.K = dim;
+        A.epi = EPI_STORE;
+        A.x = xn;
+        A.n_mats = 2 * k;
+        for (int r = 0; r < k; r++) {
+            A.m[r] = expert_mat(M.gate, hidden, r, gate + (size_t)r * hidden, nullptr);
+            A.m[k + r] = expert_mat(M.up, hidden, r, up + (size_t)r * hidden, nullptr);
+        }
+        if (!launch(A, rpt_in)) return 0;
+    }
+    {
+        ProfScope ps("moe_swiglu", s);
+        rh_launch(moe_swiglu_kernel, dim3((hidden + 255) / 256, k), dim3(256), 0, s, gate, (const float *)up, hidden, k,
+                  (const int32_t *)sel, M.gb, M.gb_stride, M.ub, M.ub_stride);
+        RH_LAUNCH_OK();
+    }
+    {
+        GemvArgs A;
+        memset(&A, 0, sizeof(A));
+        A.K = hidden;
+        A.epi = EPI_STORE;
+        A.n_mats = k;
+        for (int r = 0; r < k; r++)
+            A.m[r] = expert_mat(M.down, dim, r, proj + (size_t)r * dim, gate + (size_t)r * hidden);
+        if (!launch(A, rpt_down)) return 0;
+    }
+    {
+        ProfScope ps("moe_combine", s);
+        rh_launch(moe_combine_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, (const float *)proj, dim, k,
+                  (const int32_t *)sel, (const float *)prob, M.db, M.db_stride, moe_out, x_add);
+        RH_LAUNCH_OK();
+    }
+    if (sel_out) *sel_out = sel;
+    if (prob_out) *prob_out = prob;
+    return 1;
 }
 
 }  // namespace rh
@@ -1039,6 +1147,65 @@ int rusty_hip_attention_mode(int mode) {
         }
     }
     return prev;
+}
+
+int rusty_hip_moe_ffn(const float *x, uintptr_t dim, const uint8_t *router_w, uintptr_t router_w_len,
+                      uint32_t router_dt, const float *router_bias, uint32_t n_experts, uint32_t top_k,
+                      const uint8_t *gate_w, uintptr_t gate_w_len, const uint8_t *up_w, uintptr_t up_w_len,
+                      const uint8_t *down_w, uintptr_t down_w_len, uint32_t expert_dt, uintptr_t hidden,
+                      const float *gate_bias, const float *up_bias, const float *down_bias, float *out,
+                      int32_t *selected, float *probs) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !x || !router_w || !gate_w || !up_w || !down_w || !out || dim == 0 || hidden == 0 ||
+        n_experts == 0 || n_experts > 64 || top_k == 0 || top_k > 8 || top_k > n_experts)
+        return 0;
+    MoeDev M;
+    memset(&M, 0, sizeof(M));
+    M.n_exp = (int)n_experts;
+    M.k = (int)top_k;
+    M.dim = (int)dim;
+    M.hidden = (int)hidden;
+    auto ggml_type = [](uint32_t t) { return (t == 8 || t == 12 || t == 14 || t == 39) ? (int)t : -1; };
+    const int rdt = ggml_type(router_dt), edt = ggml_type(expert_dt);
+    if (rdt < 0 || edt < 0) return 0;
+    if (!get_weight(router_w, router_w_len, n_experts, dim, rdt, &M.router) ||
+        !get_weight(gate_w, gate_w_len, (int64_t)n_experts * hidden, dim, edt, &M.gate) ||
+        !get_weight(up_w, up_w_len, (int64_t)n_experts * hidden, dim, edt, &M.up) ||
+        !get_weight(down_w, down_w_len, (int64_t)n_experts * dim, hidden, edt, &M.down))
+        return 0;
+    DevW rb, gb, ub, db;
+    if (router_bias) {
+        if (!get_weight((const uint8_t *)router_bias, n_experts * 4, 1, n_experts, 0, &rb)) return 0;
+        M.router_bias = (const float *)rb.p;
+    }
+    if (gate_bias) {
+        if (!get_weight((const uint8_t *)gate_bias, n_experts * hidden * 4, n_experts, hidden, 0, &gb)) return 0;
+        M.gb = (const float *)gb.p;
+        M.gb_stride = (int)(gb.stride / 4);
+    }
+    if (up_bias) {
+        if (!get_weight((const uint8_t *)up_bias, n_experts * hidden * 4, n_experts, hidden, 0, &ub)) return 0;
+        M.ub = (const float *)ub.p;
+        M.ub_stride = (int)(ub.stride / 4);
+    }
+    if (down_bias) {
+        if (!get_weight((const uint8_t *)down_bias, n_experts * dim * 4, n_experts, dim, 0, &db)) return 0;
+        M.db = (const float *)db.p;
+        M.db_stride = (int)(db.stride / 4);
+    }
+    if (!ensure(&g.x, &g.x_cap, dim) || !ensure(&g.y, &g.y_cap, dim) ||
+        !ensure(&g.moe, &g.moe_cap, moe_scratch_floats(M.n_exp, M.k, M.dim, M.hidden) + 8))
+        return 0;
+    RH_CHECK(hipMemcpyAsync(g.x, x, dim * 4, hipMemcpyHostToDevice, g.s));
+    int32_t *sel = nullptr;
+    float *prob = nullptr;
+    if (!moe_ffn_enqueue(M, g.x, g.y, nullptr, g.moe, g.s, &sel, &prob)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.y, dim * 4, hipMemcpyDeviceToHost, g.s));
+    if (selected) RH_CHECK(hipMemcpyAsync(selected, sel, top_k * 4, hipMemcpyDeviceToHost, g.s));
+    if (probs) RH_CHECK(hipMemcpyAsync(probs, prob, top_k * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
 }
 
 __global__ void expf_kernel(const float *x, int n, float *out) {

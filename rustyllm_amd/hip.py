@@ -85,6 +85,8 @@ _sig("rusty_hip_debug_silu_mul", _i, _p, _p, _u, _p)
 _sig("rusty_hip_debug_rope", _i, _p, _p, _u32, _u32, _u32, _u32, _p, _u32)
 _sig("rusty_hip_debug_greedy", _i, _p, _u, _p, _u32, _f, _p)
 _sig("rusty_hip_debug_f16", _i, _p, _u, _p)
+_sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
+     _p, _p)
 
 Q8_0, Q4_K, Q6_K, MXFP4 = 8, 12, 14, 39
 
@@ -217,6 +219,33 @@ def attention_with_sink_into(query, keys, values, sinks, out, heads, kv_mul, hea
 
 
 # ---- resident decoder (src/metal.rs:302-360) --------------------------------------------
+def moe_ffn(x, router, router_dt, router_bias, experts, expert_dt, hidden, biases, top_k):
+    """Routed MoE block of gpt-oss decode on the device (rusty_hip_moe_ffn).
+    router: bytes [n_experts][dim]; experts = (gate, up, down) expert-major
+    block bytes; biases = (gate_b, up_b, down_b) f32 [n_experts][rows] or
+    None.  Returns (out, selected experts, weights), or None if unhandled."""
+    x = _f32(x)
+    dim = x.size
+    router = _u8(router)
+    n_exp = router.nbytes // (O_ROW_BYTES[router_dt](dim))
+    gate, up, down = (_u8(e) for e in experts)
+    rb = None if router_bias is None else _f32(router_bias)
+    gb, ub, db = (None if b is None else _f32(b) for b in (biases or (None, None, None)))
+    out = np.zeros(dim, np.float32)
+    sel = np.zeros(top_k, np.int32)
+    prob = np.zeros(top_k, np.float32)
+    ok = lib.rusty_hip_moe_ffn(_ptr(x), dim, _ptr(router), router.nbytes, router_dt,
+                               None if rb is None else _ptr(rb), n_exp, top_k, _ptr(gate), gate.nbytes, _ptr(up),
+                               up.nbytes, _ptr(down), down.nbytes, expert_dt, hidden,
+                               None if gb is None else _ptr(gb), None if ub is None else _ptr(ub),
+                               None if db is None else _ptr(db), _ptr(out), _ptr(sel), _ptr(prob))
+    return (out, sel, prob) if ok == 1 else None
+
+
+O_ROW_BYTES = {8: lambda c: c // 32 * 34, 39: lambda c: c // 32 * 17, 12: lambda c: c // 256 * 144,
+               14: lambda c: c // 256 * 210}
+
+
 class ResidentLayerDesc(C.Structure):
     _fields_ = [("w", C.c_void_p * 7), ("w_len", C.c_size_t * 7), ("w_rows", C.c_uint32 * 7),
                 ("w_dt", C.c_uint32 * 7), ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
