@@ -31,6 +31,7 @@ SYMBOLS = [
     "rusty_hip_debug_quantize_q8k", "rusty_hip_debug_dequant", "rusty_hip_debug_block_ints",
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
+    "rusty_hip_moe_ffn",
 ]
 
 
