@@ -180,6 +180,38 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);
 int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in);
 
+/* gpt-oss mode of the resident decoder: the whole forward_gpt_oss_into step
+ * (src/model.rs:6733-6908) on the device, one graph per token.  The reference
+ * runs this model on the CPU with per-op GPU hooks; this path has no Metal
+ * counterpart.  Per layer: RMSNorm, Q/K/V (+ biases), RoPE with the YaRN
+ * concentration, KV store, attention with per-head sinks (sliding window on
+ * even layers), wo (+ bo) into the residual, RMSNorm, the routed MoE block
+ * (as rusty_hip_moe_ffn) into the residual.  Configure with this call, then
+ * set every layer with rusty_hip_resident_set_moe_layer, then
+ * rusty_hip_resident_set_output / _set_embedding; decode, generate, kv_read
+ * and time_decode work as for the standard decoder.  value_dim = head_dim. */
+typedef struct {
+    const uint8_t *w[4];       /* wq, wk, wv, wo */
+    uintptr_t w_len[4];
+    uint32_t w_dt[4];          /* GGML type ids */
+    const float *bq, *bk, *bv, *bo;
+    const float *sinks;        /* n_heads */
+    const float *attn_norm, *post_attn_norm;
+    const uint8_t *router;     /* [n_experts][dim] */
+    uintptr_t router_len;
+    uint32_t router_dt;
+    const float *router_bias;  /* n_experts */
+    const uint8_t *exps[3];    /* gate, up [n_experts*hidden][dim]; down [n_experts*dim][hidden] */
+    uintptr_t exps_len[3];
+    uint32_t exps_dt;
+    const float *exps_bias[3]; /* [n_experts][hidden] x 2, [n_experts][dim] */
+} RustyMoeLayerDesc;
+int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                     uint32_t head_dim, uint32_t hidden_dim, uint32_t n_experts, uint32_t top_k,
+                                     uint32_t vocab, uint32_t storage_len, uint32_t sliding_window, float eps,
+                                     float rope_concentration);
+int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *desc);
+
 /* Attention order for every later call (no reference counterpart).
  * 0 (default): the reference's serial online-softmax order with glibc's expf,
  * bit for bit (src/model.rs:5739-6198); 1: split-K flash decode, within

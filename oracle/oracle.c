@@ -889,6 +889,28 @@ void orc_rope_qk(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_
     }
 }
 
+/* apply_rope_gpt_oss, model.rs:6603-6636: adjacent pairs, with cos and sin
+ * scaled by the YaRN concentration before the rotation. */
+void orc_rope_gpt_oss(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, float concentration,
+                      const float *inv_freq) {
+    for (int64_t i = 0; i < hd; i += 2) {
+        float angle = (float)pos * inv_freq[i / 2];
+        float s = sinf(angle) * concentration, c = cosf(angle) * concentration;
+        for (int64_t h = 0; h < nh; h++) {
+            float *p = q + h * hd + i;
+            float v0 = p[0], v1 = p[1];
+            p[0] = v0 * c - v1 * s;
+            p[1] = v0 * s + v1 * c;
+        }
+        for (int64_t h = 0; h < nkv; h++) {
+            float *p = k + h * hd + i;
+            float v0 = p[0], v1 = p[1];
+            p[0] = v0 * c - v1 * s;
+            p[1] = v0 * s + v1 * c;
+        }
+    }
+}
+
 /* apply_rope_qk_neox, model.rs:5606-5647 (rotate-half pairs) */
 void orc_rope_qk_neox(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq) {
     int64_t half = hd / 2;

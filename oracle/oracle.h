@@ -96,6 +96,8 @@ void orc_rms_norm(const float *x, const float *w, float eps, int64_t n, float *o
 void orc_build_rope_inv_freq(float theta, int64_t head_dim, float scaling, float *inv);
 void orc_rope_qk(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq);
 void orc_rope_qk_neox(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq);
+void orc_rope_gpt_oss(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, float concentration,
+                      const float *inv_freq);
 void orc_silu_mul_avx2(const float *gate, const float *up, float *out, int64_t n);
 void orc_silu_mul_scalar(const float *gate, const float *up, float *out, int64_t n);
 float orc_swiglu_gpt_oss(float g, float u);

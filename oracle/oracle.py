@@ -73,6 +73,7 @@ _sig("orc_rms_norm", None, _p, _p, _f, _i64, _p)
 _sig("orc_build_rope_inv_freq", None, _f, _i64, _f, _p)
 _sig("orc_rope_qk", None, _p, _p, _i64, _i64, _i64, _i64, _p)
 _sig("orc_rope_qk_neox", None, _p, _p, _i64, _i64, _i64, _i64, _p)
+_sig("orc_rope_gpt_oss", None, _p, _p, _i64, _i64, _i64, _i64, _f, _p)
 _sig("orc_silu_mul_avx2", None, _p, _p, _p, _i64)
 _sig("orc_silu_mul_scalar", None, _p, _p, _p, _i64)
 _sig("orc_swiglu_gpt_oss", _f, _f, _f)
@@ -229,6 +230,111 @@ def top_k_router(logits, k):
     probs = np.zeros(k, np.float32)
     lib.orc_softmax_selected(ptr(val), k, ptr(probs))
     return idx, val, probs
+
+
+def rope_gpt_oss(q, k, pos, hd, nh, nkv, concentration, inv_freq):
+    q, k, inv = f32(q).copy(), f32(k).copy(), f32(inv_freq)
+    lib.orc_rope_gpt_oss(ptr(q), ptr(k), pos, hd, nh, nkv, concentration, ptr(inv))
+    return q, k
+
+
+def swiglu_gpt_oss(g, u):
+    return np.array([lib.orc_swiglu_gpt_oss(float(a), float(b)) for a, b in zip(g, u)], np.float32)
+
+
+def moe_block(x, router, router_t, router_bias, experts, experts_t, hidden, biases, top_k):
+    """Routed MoE block of forward_gpt_oss_into (model.rs:6846-6898): router
+    matvec + bias, top-k in total order (select_top_logits_into), softmax over
+    the chosen (softmax_selected_into), per expert swiglu_gpt_oss of gate/up
+    (+ biases), down (+ bias), weighted sum in slot order.  Returns (moe,
+    selected experts, weights)."""
+    x = f32(x)
+    dim = x.size
+    n_exp = router.nbytes // row_bytes(router_t, dim)
+    logits = matvec(router_t, router, x, n_exp, dim)
+    if router_bias is not None:
+        logits = (logits + router_bias).astype(np.float32)
+    idx, _, probs = top_k_router(logits, top_k)
+    gate, up, down = experts
+    gb, ub, db = biases if biases is not None else (None, None, None)
+    rg, rd = row_bytes(experts_t, dim) * hidden, row_bytes(experts_t, hidden) * dim
+    moe = np.zeros(dim, np.float32)
+    for s, e in enumerate(idx):
+        g = matvec(experts_t, gate[e * rg:(e + 1) * rg], x, hidden, dim)
+        u = matvec(experts_t, up[e * rg:(e + 1) * rg], x, hidden, dim)
+        if gb is not None:
+            g = (g + gb[e]).astype(np.float32)
+        if ub is not None:
+            u = (u + ub[e]).astype(np.float32)
+        d = matvec(experts_t, down[e * rd:(e + 1) * rd], swiglu_gpt_oss(g, u), dim, hidden)
+        if db is not None:
+            d = (d + db[e]).astype(np.float32)
+        moe = (moe + d * probs[s]).astype(np.float32)
+    return moe, idx, probs
+
+
+class OracleGptOss:
+    """forward_gpt_oss_into (model.rs:6733-6908) composed from the C
+    restatements, with the KV cache on the host (linear slots).  Test
+    infrastructure only."""
+
+    def __init__(self, model, storage_len: int):
+        self.m = model
+        c = self.c = model["config"]
+        self.storage = storage_len
+        self.kd = c["n_kv_heads"] * c["head_dim"]
+        self.vdim = c["n_kv_heads"] * c["value_dim"]
+        self.kc = [np.zeros(storage_len * self.kd, np.float32) for _ in model["layers"]]
+        self.vc = [np.zeros(storage_len * self.vdim, np.float32) for _ in model["layers"]]
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        m, c = self.m, self.c
+        dim, nh, nkv, hd, vd = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["value_dim"]
+        emb, emb_t = m["token_embd"]
+        x = dequant_row(emb_t, emb[token * row_bytes(emb_t, dim):], dim)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+        for l, L in enumerate(m["layers"]):
+            xn = rms_norm(x, L["attn_norm"], c["eps"])
+            q = (matvec(L["wq"][1], L["wq"][0], xn, nh * hd, dim) + L["bq"]).astype(np.float32)
+            k = (matvec(L["wk"][1], L["wk"][0], xn, nkv * hd, dim) + L["bk"]).astype(np.float32)
+            v = (matvec(L["wv"][1], L["wv"][0], xn, nkv * vd, dim) + L["bv"]).astype(np.float32)
+            q, k = rope_gpt_oss(q, k, pos, hd, nh, nkv, m["concentration"], m["inv_freq"])
+            self.kc[l][pos * self.kd:(pos + 1) * self.kd] = k
+            self.vc[l][pos * self.vdim:(pos + 1) * self.vdim] = v
+            start = int(lib.orc_attention_start_pos(pos, c["window"])) if l % 2 == 0 else 0
+            attn = attention(q, self.kc[l], self.vc[l], nh, nkv, hd, vd, self.kd, self.vdim, self.storage, start,
+                             pos, scale, sinks=L["sinks"])
+            proj = matvec(L["wo"][1], L["wo"][0], attn, dim, nh * vd)
+            x = (x + (proj + L["bo"]).astype(np.float32)).astype(np.float32)
+            xn2 = rms_norm(x, L["post_attn_norm"], c["eps"])
+            moe, _, _ = moe_block(xn2, L["router"], Q8_0, L["router_bias"],
+                                  (L["gate_exps"], L["up_exps"], L["down_exps"]), MXFP4, c["hidden_dim"],
+                                  (L["gate_exps_bias"], L["up_exps_bias"], L["down_exps_bias"]), c["top_k"])
+            x = (x + moe).astype(np.float32)
+        xn = rms_norm(x, m["output_norm"], c["eps"])
+        out, out_t = m["output"]
+        return matvec(out_t, out, xn, c["vocab"], dim)
+
+    def generate(self, prompt, n_gen, penalty=1.1, start_pos=0):
+        """The decode loop of the reference runtime (greedy + repeat penalty
+        over the last <= 64 tokens, runtime.rs:493-521), as orc_model_generate."""
+        recent = [int(t) for t in prompt[-64:]]
+        pos = start_pos
+        logits = None
+        for i, t in enumerate(prompt):
+            logits = self.forward(int(t), pos)
+            pos += 1
+        toks = []
+        for g in range(n_gen):
+            last = logits
+            tok, _ = greedy(logits, recent, penalty)
+            toks.append(tok)
+            recent = (recent + [tok])[-64:]
+            if g + 1 == n_gen:
+                break
+            logits = self.forward(tok, pos)
+            pos += 1
+        return np.array(toks, np.uint32), last
 
 
 # ---- reference fixtures ------------------------------------------------------

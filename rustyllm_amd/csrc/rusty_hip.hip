@@ -1397,9 +1397,12 @@ namespace rh {
 
 struct RLayer {
     DevW w[7];
-    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    float *attn_norm = nullptr, *ffn_norm = nullptr;  // gpt-oss: ffn_norm is post_attn_norm
     float *bias[3] = {nullptr, nullptr, nullptr};
     float *k = nullptr, *v = nullptr;
+    // gpt-oss
+    float *bo = nullptr, *sinks = nullptr;
+    MoeDev moe{};
 };
 
 struct Resident {
@@ -1428,6 +1431,11 @@ struct Resident {
     int32_t *out_idx = nullptr;
     uint32_t tok_cap = 0;
     int am_blocks = 256;
+    // gpt-oss mode
+    bool moe = false;
+    uint32_t n_exp = 0, top_k = 0, window = 0;
+    float rope_conc = 1.0f;
+    float *moebuf = nullptr;
     std::map<int, hipGraphExec_t> graphs;
     std::vector<void *> allocs;
 };
@@ -1453,6 +1461,10 @@ static void r_reset() {
     R.configured = R.ready = false;
     R.has_embd = false;
     R.tok_cap = 0;
+    R.moe = false;
+    R.n_exp = R.top_k = R.window = 0;
+    R.rope_conc = 1.0f;
+    R.moebuf = nullptr;
 }
 
 static void r_invalidate_graphs() {
@@ -1487,7 +1499,9 @@ static ActSpec r_act_norm(const float *norm_w) {
 }
 
 // One token through the layer stack (and head / greedy by mode) on stream s.
+static int r_enqueue_moe(int mode, float penalty, hipStream_t s);
 static int r_enqueue(int mode, float penalty, hipStream_t s) {
+    if (R.moe) return r_enqueue_moe(mode, penalty, s);
     const int dim = R.dim, qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd;
     const int attn_cols = R.n_heads * R.vd;
     if (mode & MODE_DEVTOK) {
@@ -1610,6 +1624,128 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
     return 1;
 }
 
+// One gpt-oss token (forward_gpt_oss_into, src/model.rs:6733-6908).
+static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
+    const int dim = R.dim, vdim = R.n_kv * R.vd, kd = R.n_kv * R.hd;
+    const int attn_cols = R.n_heads * R.vd;
+    if (mode & MODE_DEVTOK) {
+        ProfScope ps("embed", s);
+        rh_launch(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, R.embd.p, R.embd.stride, R.embd.fmt, dim,
+                  R.st, 0, R.x);
+        RH_LAUNCH_OK();
+    }
+    for (uint32_t l = 0; l < R.n_layers; l++) {
+        RLayer &Ly = R.L[l];
+        MatSpec qkv[3] = {{Ly.w[0], R.q, Ly.bias[0]}, {Ly.w[1], R.k, Ly.bias[1]}, {Ly.w[2], R.v, Ly.bias[2]}};
+        if (!gemv_multi_act(qkv, 3, dim, EPI_STORE, r_act_norm(Ly.attn_norm), s)) return 0;
+        {
+            RopeArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.q;
+            A.k = R.k;
+            A.v = R.v;
+            A.kcache = Ly.k;
+            A.vcache = Ly.v;
+            A.cos_t = R.cos_t;
+            A.sin_t = R.sin_t;
+            A.st = R.st;
+            A.max_pos = R.storage;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.slots = R.storage;
+            A.neox = 0;
+            int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+            ProfScope ps("rope_kv", s);
+            rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
+            RH_LAUNCH_OK();
+        }
+        // attention with sinks; even layers see the sliding window only
+        // (attention_start_pos, src/model.rs:6788-6792)
+        const int window = (l % 2 == 0) ? (int)R.window : 0;
+        ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
+        if (attn_fast_mode()) {
+            AttnArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.q;
+            A.k = Ly.k;
+            A.v = Ly.v;
+            A.sinks = Ly.sinks;
+            A.part = R.part;
+            A.out = R.attn;
+            A.xq = (attn_cols % 256 == 0) ? R.xq_attn : XQ{};
+            A.st = R.st;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.kv_mul = R.n_heads / R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.key_stride = kd;
+            A.value_stride = vdim;
+            A.slot_count = R.storage;
+            A.window = window;
+            A.n_chunks = R.n_chunks;
+            A.scale = 1.0f / sqrtf((float)R.hd);
+            if (!attn_launch(A, s)) return 0;
+        } else {
+            AttnExactArgs E;
+            memset(&E, 0, sizeof(E));
+            E.q = R.q;
+            E.k = Ly.k;
+            E.v = Ly.v;
+            E.sinks = Ly.sinks;
+            E.out = R.attn;
+            E.st = R.st;
+            E.n_heads = R.n_heads;
+            E.n_kv = R.n_kv;
+            E.kv_mul = R.n_heads / R.n_kv;
+            E.hd = R.hd;
+            E.vd = R.vd;
+            E.key_stride = kd;
+            E.value_stride = vdim;
+            E.slot_count = R.storage;
+            E.window = window;
+            E.cap = R.ex_cap;
+            E.scale = 1.0f / sqrtf((float)R.hd);
+            const float *den = nullptr;
+            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
+            act_o.mode = ACT_DEN;
+            act_o.den = den;
+            act_o.group = R.vd;
+        }
+        // x += wo attn + bo (src/model.rs:6837-6840)
+        MatSpec mo = {Ly.w[3], R.x, Ly.bo};
+        if (!gemv_multi_act(&mo, 1, attn_cols, EPI_ADD, act_o, s)) return 0;
+        // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2)
+        ActSpec use;
+        if (!act_materialize(r_act_norm(Ly.ffn_norm), dim, &use, s)) return 0;
+        if (!moe_ffn_enqueue(Ly.moe, R.xn, nullptr, R.x, R.moebuf, s)) return 0;
+    }
+    if (mode & (MODE_LOGITS | MODE_GREEDY)) {
+        MatSpec mh = {R.out_w, R.logits, nullptr};
+        if (!gemv_multi_act(&mh, 1, dim, EPI_STORE, r_act_norm(R.out_norm), s)) return 0;
+    }
+    if (mode & MODE_GREEDY) {
+        ArgmaxArgs A;
+        memset(&A, 0, sizeof(A));
+        A.logits = R.logits;
+        A.n = R.vocab;
+        A.penalty = penalty;
+        A.st = R.st;
+        A.part_v = R.am_v;
+        A.part_i = R.am_i;
+        A.ticket = R.ticket;
+        A.out_tokens = R.tokens;
+        A.out_index = R.out_idx;
+        A.advance = 1;
+        ProfScope ps("argmax_greedy", s);
+        rh_launch(argmax_greedy_kernel, dim3(R.am_blocks), dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+    }
+    return 1;
+}
+
 static bool use_graphs() {
     if (g.prof.on) return false;
     const char *e = getenv("RUSTY_HIP_GRAPH");
@@ -1660,15 +1796,12 @@ static int r_set_state(int pos, int start_t, int token, bool reset_recent) {
 
 extern "C" {
 
-int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
-                                 uint32_t head_dim, uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab,
-                                 uint32_t storage_len, float eps, uint32_t neox) {
-    std::lock_guard<std::mutex> lk(g.mu);
-    if (!init_locked()) return 0;
-    if (n_layers == 0 || n_layers > 512 || n_kv_heads == 0 || n_heads % n_kv_heads != 0) return 0;
-    if (head_dim == 0 || head_dim > 256 || value_dim == 0 || value_dim > 256) return 0;
-    if (dim % 256 != 0 || hidden_dim % 256 != 0 || storage_len == 0 || vocab == 0) return 0;
-    if (!attn_supported((int)head_dim, (int)value_dim, (int)(n_heads / n_kv_heads))) return 0;
+}  // extern "C"
+
+// Resident buffers for a model shape (shared by both configure calls).
+static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                   uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab, uint32_t storage_len, float eps,
+                   uint32_t neox) {
     r_reset();
     wcache_clear();  // a new model: cached copies keyed by old host addresses are stale
     R.n_layers = n_layers;
@@ -1714,6 +1847,102 @@ int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_hea
     RH_CHECK(hipMemset(R.out_idx, 0, 64));
     RH_CHECK(hipHostMalloc((void **)&R.st_host, sizeof(StepState), hipHostMallocDefault));
     R.configured = true;
+    return 1;
+}
+
+extern "C" {
+
+int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                 uint32_t head_dim, uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab,
+                                 uint32_t storage_len, float eps, uint32_t neox) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    if (n_layers == 0 || n_layers > 512 || n_kv_heads == 0 || n_heads % n_kv_heads != 0) return 0;
+    if (head_dim == 0 || head_dim > 256 || value_dim == 0 || value_dim > 256) return 0;
+    if (dim % 256 != 0 || hidden_dim % 256 != 0 || storage_len == 0 || vocab == 0) return 0;
+    if (!attn_supported((int)head_dim, (int)value_dim, (int)(n_heads / n_kv_heads))) return 0;
+    return r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, value_dim, hidden_dim, vocab, storage_len, eps,
+                   neox);
+}
+
+int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
+                                     uint32_t head_dim, uint32_t hidden_dim, uint32_t n_experts, uint32_t top_k,
+                                     uint32_t vocab, uint32_t storage_len, uint32_t sliding_window, float eps,
+                                     float rope_concentration) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked()) return 0;
+    if (n_layers == 0 || n_layers > 512 || n_kv_heads == 0 || n_heads % n_kv_heads != 0) return 0;
+    if (head_dim == 0 || head_dim > 256 || head_dim % 2 != 0) return 0;
+    // f32-activation paths: dims in whole 32-blocks, within the LDS staging
+    if (dim % 32 != 0 || hidden_dim % 32 != 0 || dim > 12288 || hidden_dim > 12288) return 0;
+    if (storage_len == 0 || vocab == 0 || n_experts == 0 || n_experts > 64 || top_k == 0 || top_k > 8 ||
+        top_k > n_experts)
+        return 0;
+    if (!attn_supported((int)head_dim, (int)head_dim, (int)(n_heads / n_kv_heads))) return 0;
+    if (!r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, head_dim, hidden_dim, vocab, storage_len, eps, 0))
+        return 0;
+    R.moe = true;
+    R.n_exp = n_experts;
+    R.top_k = top_k;
+    R.window = sliding_window;
+    R.rope_conc = rope_concentration;
+    if (!r_alloc((void **)&R.moebuf, (moe_scratch_floats((int)n_experts, (int)top_k, (int)dim, (int)hidden_dim) + 8) * 4))
+        return 0;
+    return 1;
+}
+
+int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *d) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || !R.moe || !d || l >= R.n_layers) return 0;
+    RLayer &Ly = R.L[l];
+    const uint32_t qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd, ac = R.n_heads * R.vd;
+    const uint32_t rows[4] = {qd, kd, vdim, R.dim}, cols[4] = {R.dim, R.dim, R.dim, ac};
+    for (int i = 0; i < 4; i++) {
+        const int fmt = dt_to_fmt(d->w_dt[i]);
+        if (!d->w[i] || fmt < 0 || !cat_of(fmt, (int)cols[i])) return 0;
+        if (!get_weight(d->w[i], d->w_len[i], rows[i], cols[i], fmt, &Ly.w[i])) return 0;
+    }
+    auto upload = [&](const float *h, size_t n, float **dst) {
+        if (!h) return 0;
+        if (!r_alloc((void **)dst, n * 4)) return 0;
+        RH_CHECK(hipMemcpy(*dst, h, n * 4, hipMemcpyHostToDevice));
+        return 1;
+    };
+    if (!upload(d->bq, qd, &Ly.bias[0]) || !upload(d->bk, kd, &Ly.bias[1]) || !upload(d->bv, vdim, &Ly.bias[2]) ||
+        !upload(d->bo, R.dim, &Ly.bo) || !upload(d->sinks, R.n_heads, &Ly.sinks) ||
+        !upload(d->attn_norm, R.dim, &Ly.attn_norm) || !upload(d->post_attn_norm, R.dim, &Ly.ffn_norm))
+        return 0;
+    MoeDev &M = Ly.moe;
+    memset(&M, 0, sizeof(M));
+    M.n_exp = (int)R.n_exp;
+    M.k = (int)R.top_k;
+    M.dim = (int)R.dim;
+    M.hidden = (int)R.hidden;
+    const int rfmt = dt_to_fmt(d->router_dt), efmt = dt_to_fmt(d->exps_dt);
+    if (rfmt < 0 || efmt < 0 || !d->router) return 0;
+    if (!get_weight(d->router, d->router_len, R.n_exp, R.dim, rfmt, &M.router)) return 0;
+    const uint32_t erows[3] = {R.n_exp * R.hidden, R.n_exp * R.hidden, R.n_exp * R.dim};
+    const uint32_t ecols[3] = {R.dim, R.dim, R.hidden};
+    DevW *ew[3] = {&M.gate, &M.up, &M.down};
+    for (int i = 0; i < 3; i++)
+        if (!d->exps[i] || !get_weight(d->exps[i], d->exps_len[i], erows[i], ecols[i], efmt, ew[i])) return 0;
+    float *rb = nullptr, *gb = nullptr, *ub = nullptr, *db = nullptr;
+    if (d->router_bias && !upload(d->router_bias, R.n_exp, &rb)) return 0;
+    if (d->exps_bias[0] && !upload(d->exps_bias[0], (size_t)R.n_exp * R.hidden, &gb)) return 0;
+    if (d->exps_bias[1] && !upload(d->exps_bias[1], (size_t)R.n_exp * R.hidden, &ub)) return 0;
+    if (d->exps_bias[2] && !upload(d->exps_bias[2], (size_t)R.n_exp * R.dim, &db)) return 0;
+    M.router_bias = rb;
+    M.gb = gb;
+    M.ub = ub;
+    M.db = db;
+    M.gb_stride = M.ub_stride = (int)R.hidden;
+    M.db_stride = (int)R.dim;
+    size_t kdim = (size_t)R.n_kv * R.hd;
+    if (!r_alloc((void **)&Ly.k, (size_t)R.storage * kdim * 4) || !r_alloc((void **)&Ly.v, (size_t)R.storage * vdim * 4))
+        return 0;
+    RH_CHECK(hipMemset(Ly.k, 0, (size_t)R.storage * kdim * 4));
+    RH_CHECK(hipMemset(Ly.v, 0, (size_t)R.storage * vdim * 4));
+    r_invalidate_graphs();
     return 1;
 }
 
@@ -1769,8 +1998,10 @@ int rusty_hip_resident_set_output(const float *output_norm, const uint8_t *outpu
     for (size_t p = 0; p < R.storage; p++)
         for (size_t i = 0; i < half; i++) {
             float ang = (float)p * inv_freq[i];
-            stb[p * half + i] = sinf(ang);
-            ct[p * half + i] = cosf(ang);
+            // gpt-oss scales both by the YaRN concentration (apply_rope_gpt_oss,
+            // src/model.rs:6617-6619); 1.0 leaves them unchanged
+            stb[p * half + i] = R.moe ? sinf(ang) * R.rope_conc : sinf(ang);
+            ct[p * half + i] = R.moe ? cosf(ang) * R.rope_conc : cosf(ang);
         }
     if (!r_alloc((void **)&R.cos_t, ct.size() * 4) || !r_alloc((void **)&R.sin_t, stb.size() * 4)) return 0;
     RH_CHECK(hipMemcpy(R.cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));

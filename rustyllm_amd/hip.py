@@ -31,7 +31,7 @@ SYMBOLS = [
     "rusty_hip_debug_quantize_q8k", "rusty_hip_debug_dequant", "rusty_hip_debug_block_ints",
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
-    "rusty_hip_moe_ffn",
+    "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
 ]
 
 
@@ -86,6 +86,9 @@ _sig("rusty_hip_debug_silu_mul", _i, _p, _p, _u, _p)
 _sig("rusty_hip_debug_rope", _i, _p, _p, _u32, _u32, _u32, _u32, _p, _u32)
 _sig("rusty_hip_debug_greedy", _i, _p, _u, _p, _u32, _f, _p)
 _sig("rusty_hip_debug_f16", _i, _p, _u, _p)
+_sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f,
+     _f)
+_sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
 _sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
      _p, _p)
 
@@ -332,6 +335,56 @@ class Resident:
         if lib.rusty_hip_resident_time_decode(n_tokens, penalty, C.byref(ms)) != 1:
             raise RuntimeError("rusty_hip_resident_time_decode failed")
         return ms.value
+
+
+class MoeLayerDesc(C.Structure):
+    _fields_ = [("w", C.c_void_p * 4), ("w_len", C.c_size_t * 4), ("w_dt", C.c_uint32 * 4),
+                ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p), ("bo", C.c_void_p),
+                ("sinks", C.c_void_p), ("attn_norm", C.c_void_p), ("post_attn_norm", C.c_void_p),
+                ("router", C.c_void_p), ("router_len", C.c_size_t), ("router_dt", C.c_uint32),
+                ("router_bias", C.c_void_p), ("exps", C.c_void_p * 3), ("exps_len", C.c_size_t * 3),
+                ("exps_dt", C.c_uint32), ("exps_bias", C.c_void_p * 3)]
+
+
+class ResidentGptOss(Resident):
+    """The resident decoder in gpt-oss mode over a model from
+    rustyllm_amd.synth.make_gptoss (rusty_hip_resident_configure_moe)."""
+
+    def __init__(self, model, storage_len: int):
+        cfg = self.cfg = model["config"]
+        self.storage_len = storage_len
+        self._keep = []
+        ok = lib.rusty_hip_resident_configure_moe(cfg["n_layers"], cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"],
+                                                  cfg["head_dim"], cfg["hidden_dim"], cfg["n_experts"],
+                                                  cfg["top_k"], cfg["vocab"], storage_len, cfg["window"],
+                                                  cfg["eps"], model["concentration"])
+        if ok != 1:
+            raise RuntimeError("rusty_hip_resident_configure_moe failed")
+        for l, L in enumerate(model["layers"]):
+            d = MoeLayerDesc()
+            for i, nm in enumerate(("wq", "wk", "wv", "wo")):
+                arr, t = L[nm]
+                d.w[i], d.w_len[i], d.w_dt[i] = _ptr(arr), arr.nbytes, t
+            for nm in ("bq", "bk", "bv", "bo", "sinks", "attn_norm", "post_attn_norm", "router_bias"):
+                setattr(d, nm, _ptr(_f32(L[nm])))
+            d.router, d.router_len, d.router_dt = _ptr(L["router"]), L["router"].nbytes, Q8_0
+            for i, nm in enumerate(("gate_exps", "up_exps", "down_exps")):
+                d.exps[i], d.exps_len[i] = _ptr(L[nm]), L[nm].nbytes
+                b = np.ascontiguousarray(L[nm + "_bias"], np.float32)
+                self._keep.append(b)
+                d.exps_bias[i] = _ptr(b)
+            d.exps_dt = MXFP4
+            if lib.rusty_hip_resident_set_moe_layer(l, C.byref(d)) != 1:
+                raise RuntimeError(f"rusty_hip_resident_set_moe_layer({l}) failed")
+        out_w, out_dt = model["output"]
+        inv = _f32(model["inv_freq"])
+        if lib.rusty_hip_resident_set_output(_ptr(model["output_norm"]), _ptr(out_w), out_w.nbytes, cfg["vocab"],
+                                             out_dt, _ptr(inv), inv.size) != 1:
+            raise RuntimeError("rusty_hip_resident_set_output failed")
+        emb, emb_dt = model["token_embd"]
+        if lib.rusty_hip_resident_set_embedding(_ptr(emb), emb.nbytes, emb_dt) != 1:
+            raise RuntimeError("rusty_hip_resident_set_embedding failed")
+        self.vocab = cfg["vocab"]
 
 
 # ---- profiling -------------------------------------------------------------------------

@@ -168,6 +168,92 @@ def make_model(name_or_cfg, seed: int = 1234) -> dict:
     return model
 
 
+# gpt-oss family: Q8_0 attention, router and output,
+# MXFP4 experts, learned sinks, sliding window on even layers, YaRN RoPE.
+GPTOSS_CONFIGS = {
+    # parity shape: f32-activation paths (dim % 256 != 0), a Q8_K wo (n_heads*head_dim = 256)
+    "tiny-gptoss": dict(n_layers=3, dim=160, n_heads=4, n_kv_heads=2, head_dim=64, hidden_dim=96, n_experts=6,
+                        top_k=2, vocab=500, window=8, theta=150000.0, rope_scaling=32.0, rope_orig_ctx=4096,
+                        eps=1e-5),
+    "gpt-oss-20b": dict(n_layers=24, dim=2880, n_heads=64, n_kv_heads=8, head_dim=64, hidden_dim=2880,
+                        n_experts=32, top_k=4, vocab=201088, window=128, theta=150000.0, rope_scaling=32.0,
+                        rope_orig_ctx=4096, eps=1e-5),
+}
+
+
+def rope_gpt_oss(theta: float, head_dim: int, scaling: float, orig_ctx: int):
+    """build_rope_inv_freq_gpt_oss (src/model.rs:3059-3098): YaRN frequencies
+    and the concentration 0.1 ln(scaling) + 1, in f32 arithmetic."""
+    f = np.float32
+    d_half = f(head_dim) / f(2.0)
+    low = high = f(0.0)
+    if scaling > 1.0:
+        two_pi = f(2.0) * f(np.pi)
+        low = d_half * (np.log(f(orig_ctx) / (f(32.0) * two_pi)) / np.log(f(theta)))
+        high = d_half * (np.log(f(orig_ctx) / (f(1.0) * two_pi)) / np.log(f(theta)))
+    conc = f(0.1) * np.log(f(scaling)) + f(1.0) if scaling > 1.0 else f(1.0)
+    inv = np.zeros(head_dim // 2, np.float32)
+    for pair in range(head_dim // 2):
+        base = np.power(f(theta), f(pair * 2) / f(head_dim))
+        if scaling > 1.0:
+            ramp = np.clip((f(pair) - low) / (high - low), f(0.0), f(1.0))
+            mask = f(1.0) - ramp
+            interp = f(1.0) / (f(scaling) * base)
+            extrap = f(1.0) / base
+            inv[pair] = interp * (f(1.0) - mask) + extrap * mask
+        else:
+            inv[pair] = f(1.0) / base
+    return inv, float(conc)
+
+
+def make_gptoss(name_or_cfg, seed: int = 1234) -> dict:
+    """A gpt-oss model: per layer wq/wk/wv/wo (Q8_0) with biases, sinks,
+    attn/post-attention norms, router (Q8_0) + bias, expert-major MXFP4
+    gate/up/down with f32 biases; Q8_0 embedding and output."""
+    cfg = dict(GPTOSS_CONFIGS[name_or_cfg]) if isinstance(name_or_cfg, str) else dict(name_or_cfg)
+    cfg.setdefault("value_dim", cfg["head_dim"])
+    cfg["arch"] = "gpt-oss"
+    dim, hd, vd = cfg["dim"], cfg["head_dim"], cfg["value_dim"]
+    nh, nkv, hid, ne, vocab = cfg["n_heads"], cfg["n_kv_heads"], cfg["hidden_dim"], cfg["n_experts"], cfg["vocab"]
+    seed_box = [seed * 1000003 + 17]
+
+    def ns():
+        seed_box[0] += 7919
+        return seed_box[0]
+
+    def vec(n, std):
+        return normal_f32(ns(), 1, n, std).reshape(-1)
+
+    layers = []
+    for _ in range(cfg["n_layers"]):
+        L = {
+            "wq": (normal_quantized(Q8_0, ns(), nh * hd, dim, 0.02), Q8_0),
+            "wk": (normal_quantized(Q8_0, ns(), nkv * hd, dim, 0.02), Q8_0),
+            "wv": (normal_quantized(Q8_0, ns(), nkv * vd, dim, 0.02), Q8_0),
+            "wo": (normal_quantized(Q8_0, ns(), dim, nh * vd, 0.02), Q8_0),
+            "bq": vec(nh * hd, 0.02), "bk": vec(nkv * hd, 0.02), "bv": vec(nkv * vd, 0.02), "bo": vec(dim, 0.02),
+            "sinks": vec(nh, 1.0),
+            "attn_norm": np.ones(dim, np.float32), "post_attn_norm": np.ones(dim, np.float32),
+            "router": normal_quantized(Q8_0, ns(), ne, dim, 0.02), "router_bias": vec(ne, 0.02),
+            "gate_exps": normal_quantized(MXFP4, ns(), ne * hid, dim, 0.02),
+            "up_exps": normal_quantized(MXFP4, ns(), ne * hid, dim, 0.02),
+            "down_exps": normal_quantized(MXFP4, ns(), ne * dim, hid, 0.02),
+            "gate_exps_bias": normal_f32(ns(), ne, hid, 0.02), "up_exps_bias": normal_f32(ns(), ne, hid, 0.02),
+            "down_exps_bias": normal_f32(ns(), ne, dim, 0.02),
+        }
+        layers.append(L)
+    inv, conc = rope_gpt_oss(cfg["theta"], hd, cfg["rope_scaling"], cfg["rope_orig_ctx"])
+    return {
+        "config": cfg,
+        "layers": layers,
+        "token_embd": (normal_quantized(Q8_0, ns(), vocab, dim, 0.02), Q8_0),
+        "output": (normal_quantized(Q8_0, ns(), vocab, dim, 0.02), Q8_0),
+        "output_norm": np.ones(dim, np.float32),
+        "inv_freq": inv,
+        "concentration": conc,
+    }
+
+
 def weight_bytes(model: dict, include_embedding: bool = False) -> int:
     """Bytes of every weight read per decode token (the embedding row is one row)."""
     total = 0

@@ -389,6 +389,27 @@ def test_rope_vs_rotation(neox):
         assert np.max(np.abs(got.reshape(n, hd) - ref)) < 1e-5
 
 
+def test_rope_gpt_oss_reduces_to_interleaved_and_scales():
+    """apply_rope_gpt_oss (model.rs:6603-6636) is apply_rope_qk's adjacent-pair
+    rotation with cos and sin scaled by the concentration: at 1.0 it equals
+    apply_rope_qk bit for bit, otherwise it is that rotation times c."""
+    rng = np.random.default_rng(4)
+    hd, nh, nkv = 64, 3, 1
+    inv = O.rope_inv_freq(150000.0, hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    a_q, a_k = O.rope_gpt_oss(q, k, 37, hd, nh, nkv, 1.0, inv)
+    b_q, b_k = O.rope(q, k, 37, hd, nh, nkv, inv)
+    assert np.array_equal(a_q, b_q) and np.array_equal(a_k, b_k)
+    c = 1.3465736
+    s_q, _ = O.rope_gpt_oss(q, k, 37, hd, nh, nkv, c, inv)
+    ang = 37.0 * inv.astype(np.float64)
+    q2 = q.astype(np.float64).reshape(nh, hd // 2, 2)
+    ref = np.stack([q2[..., 0] * np.cos(ang) - q2[..., 1] * np.sin(ang),
+                    q2[..., 0] * np.sin(ang) + q2[..., 1] * np.cos(ang)], -1).reshape(-1) * c
+    assert np.allclose(s_q, ref, rtol=1e-5, atol=1e-5)
+
+
 def test_silu_mul_simd_matches_scalar():
     """silu_mul_simd_matches_scalar (simd.rs:9019-9040), incl. the clamp region."""
     n = 1003
