@@ -163,6 +163,16 @@ int rusty_hip_moe_ffn(const float *x, uintptr_t dim, const uint8_t *router_w, ui
 int rusty_hip_matvec(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, const float *x,
                      uintptr_t rows, uintptr_t cols, float *out);
 
+/* matvec_kquant_batch_into (src/simd.rs:3417-3435; the reference keeps the
+ * batch on the CPU): one Q4_K / Q6_K matrix (kind 0/1 or GGML 12/14) against
+ * a row-major batch of T = inputs_len / (4 cols) activation rows; out is
+ * row-major [T][rows] (out_len >= 4 T rows bytes).  cols % 256 == 0, as the
+ * reference gates.  Runs on the matrix cores; every out[t][r] is
+ * bit-identical to the single-token matvec of row r with input row t. */
+int rusty_hip_kquant_matvec_batch(uint32_t kind, const uint8_t *weights, uintptr_t weights_len, uintptr_t rows,
+                                  uintptr_t cols, const float *inputs, uintptr_t inputs_len, float *out,
+                                  uintptr_t out_len);
+
 /* Resident decoder, device-token mode (no reference counterpart; the
  * Metal decoder takes the embedding from the host).  The embedding table is
  * held in HBM and the greedy pick (repeat penalty + first finite maximum,

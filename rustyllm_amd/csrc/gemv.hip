@@ -14,6 +14,7 @@
 // order is free; each block's f32 value is then formed with the reference's
 // own rounding sequence and the per-row sum runs serially in block order, so
 // Q4_K, Q6_K and Q8_0 (int) rows reproduce the reference row bit for bit.
+#pragma once
 #include "common.hpp"
 
 namespace rh {

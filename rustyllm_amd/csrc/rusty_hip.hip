@@ -9,6 +9,7 @@
 #include "ops.hip"
 #include "attention_exact.hip"
 #include "moe.hip"
+#include "gemm_mfma.hip"
 
 #include <hip/hip_ext.h>
 
@@ -104,6 +105,10 @@ struct Ctx {
     size_t ibuf_cap = 0;
     float *ex = nullptr;  // exact-attention scratch: scores | coef | masks
     size_t ex_cap = 0;
+    int8_t *bq = nullptr;  // batched Q8_K activations: quants [T][K] | scales [K/256][ldx]
+    size_t bq_cap = 0;
+    float *bx = nullptr, *by = nullptr;  // batched inputs / outputs of the per-op batch export
+    size_t bx_cap = 0, by_cap = 0;
     int attn_fast = -1;   // -1: read RUSTY_HIP_ATTN once; 0 exact, 1 split-K
     Profile prof;
 };
@@ -2185,6 +2190,93 @@ int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *rece
     RH_CHECK(hipMemcpyAsync(&hs, st, sizeof(hs), hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
     *token = hs.token;
+    return 1;
+}
+
+// ---- batched K-quant products (prefill) ------------------------------------------
+// Q8_K activations of T tokens in one buffer: quants [T][K], then the scales
+// token-minor [K/256][ldx] with ldx = T rounded up to the 64-token tile, so the
+// product kernel reads four tokens' scales per 16-byte load without a bound.
+struct BatchXq {
+    int8_t *qs;
+    float *dx;
+    int ldx;
+};
+static int64_t batch_ldx(int T) { return ((int64_t)T + 63) / 64 * 64; }
+static size_t batch_xq_bytes(int T, int K) { return (size_t)T * K + (size_t)(K / 256) * batch_ldx(T) * 4 + 256; }
+static BatchXq batch_xq_at(int8_t *buf, int T, int K) {
+    BatchXq b;
+    b.qs = buf;
+    b.dx = (float *)(buf + ((size_t)T * K + 255) / 256 * 256);
+    b.ldx = (int)batch_ldx(T);
+    return b;
+}
+
+static int quantize_batch_enqueue(const float *x, int ldxf, int T, int K, const BatchXq &b, hipStream_t s) {
+    if (K % 256 != 0 || T <= 0) return 0;
+    ProfScope ps("quantize_q8k_batch", s);
+    rh_launch(quantize_q8k_batch_kernel, dim3((unsigned)(K / 256), (unsigned)T), dim3(256), 0, s, x, K, ldxf, b.qs,
+              b.dx, b.ldx);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// y[t * ldy + r] (=, or += with epi EPI_ADD) row r of W times token t, plus
+// bias[r] when given; rows of one wave tile are 32 weight rows, a workgroup
+// holds 4 tiles and covers 64 tokens.
+static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int ldy, int epi, const float *bias,
+                           hipStream_t s) {
+    if ((W.fmt != 12 && W.fmt != 14) || W.cols % 256 != 0 || W.stride % 16 != 0 || T <= 0 || ldy < W.rows)
+        return 0;
+    GemmArgs A;
+    memset(&A, 0, sizeof(A));
+    A.w = W.p;
+    A.row_stride = W.stride;
+    A.rows = W.rows;
+    A.K = W.cols;
+    A.T = T;
+    A.epi = epi;
+    A.xq = b.qs;
+    A.dx = b.dx;
+    A.ldx = b.ldx;
+    A.ldy = ldy;
+    A.y = y;
+    A.bias = bias;
+    const dim3 grid((unsigned)((W.rows + 127) / 128), (unsigned)((T + 32 * GEMM_NT - 1) / (32 * GEMM_NT)));
+    ProfScope ps(W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma", s);
+    if (W.fmt == 12)
+        rh_launch(gemm_kq_mfma_kernel<F_Q4_K>, grid, dim3(256), 0, s, A);
+    else
+        rh_launch(gemm_kq_mfma_kernel<F_Q6_K>, grid, dim3(256), 0, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// matvec_kquant_batch_into (src/simd.rs:3417-3435): one K-quant matrix
+// against a row-major batch of activations, out row-major [T][rows].  Byte
+// lengths as the other exports; inputs must hold a whole number of
+// cols-wide rows and cols must be a multiple of 256, as the reference gates.
+int rusty_hip_kquant_matvec_batch(uint32_t kind, const uint8_t *w, uintptr_t w_len, uintptr_t rows, uintptr_t cols,
+                                  const float *inputs, uintptr_t inputs_len, float *out, uintptr_t out_len) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !w || !inputs || !out || rows == 0 || cols == 0 || cols % 256 != 0) return 0;
+    const int fmt = dt_to_fmt(kind);
+    if (fmt != 12 && fmt != 14) return 0;
+    if (inputs_len == 0 || inputs_len % (cols * 4) != 0) return 0;
+    const size_t T = inputs_len / (cols * 4);
+    if (T > (1u << 20) || out_len < T * rows * 4) return 0;
+    DevW W;
+    if (!get_weight(w, w_len, (int64_t)rows, (int64_t)cols, fmt, &W)) return 0;
+    if (!ensure(&g.bx, &g.bx_cap, T * cols) || !ensure(&g.by, &g.by_cap, T * rows) ||
+        !ensure(&g.bq, &g.bq_cap, batch_xq_bytes((int)T, (int)cols)))
+        return 0;
+    const BatchXq b = batch_xq_at(g.bq, (int)T, (int)cols);
+    RH_CHECK(hipMemcpyAsync(g.bx, inputs, T * cols * 4, hipMemcpyHostToDevice, g.s));
+    if (!quantize_batch_enqueue(g.bx, (int)cols, (int)T, (int)cols, b, g.s)) return 0;
+    if (!gemm_kq_enqueue(W, b, (int)T, g.by, (int)rows, EPI_STORE, nullptr, g.s)) return 0;
+    RH_CHECK(hipMemcpyAsync(out, g.by, T * rows * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
     return 1;
 }
 

@@ -32,6 +32,7 @@ SYMBOLS = [
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
+    "rusty_hip_kquant_matvec_batch",
 ]
 
 
@@ -89,6 +90,7 @@ _sig("rusty_hip_debug_f16", _i, _p, _u, _p)
 _sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f,
      _f)
 _sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
+_sig("rusty_hip_kquant_matvec_batch", _i, _u32, _p, _u, _u, _u, _p, _u, _p, _u)
 _sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
      _p, _p)
 
@@ -124,6 +126,18 @@ def matvec_into(ggml_type: int, weights: np.ndarray, x: np.ndarray, rows: int, c
     w, xx = _u8(weights), _f32(x)
     assert out.dtype == np.float32 and out.flags.c_contiguous and out.size >= rows
     return lib.rusty_hip_matvec(ggml_type, _ptr(w), w.nbytes, _ptr(xx), rows, cols, _ptr(out)) == 1
+
+
+def kquant_matvec_batch_into(kind: int, weights: np.ndarray, rows: int, cols: int, inputs: np.ndarray,
+                             out: np.ndarray) -> bool:
+    """matvec_kquant_batch_into (simd.rs:3417-3435): inputs [T][cols] row-major,
+    out [T][rows] row-major; kind is Q4_K / Q6_K (GGML id or 0/1)."""
+    if not enabled():
+        return False
+    w, xx = _u8(weights), _f32(inputs)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    return lib.rusty_hip_kquant_matvec_batch(kind, _ptr(w), w.nbytes, rows, cols, _ptr(xx), xx.nbytes, _ptr(out),
+                                             out.nbytes) == 1
 
 
 def q4k_matvec_into(weights, x, rows, cols, out) -> bool:
