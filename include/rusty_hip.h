@@ -182,9 +182,23 @@ int rusty_hip_resident_set_embedding(const uint8_t *embd, uintptr_t embd_len, ui
 /* Prefills `prompt` at positions start_pos.., then greedily generates n_gen
  * tokens into out_tokens (recent-token window of 64, src/runtime.rs:493-521).
  * logits_out (vocab floats, may be null) receives the logits of the last
- * forward. */
+ * forward.  As prefill_prompt_tokens (src/runtime.rs:3368-3420), a prompt of
+ * more than two tokens on a batchable model has all but its last token
+ * prefilled in batched chunks (rusty_hip_resident_prefill); environment
+ * RUSTY_HIP_PREFILL=0 runs them one decode step at a time instead.  Both give
+ * the same bits. */
 int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32_t start_pos, uint32_t n_gen,
                                 float repeat_penalty, int32_t *out_tokens, float *logits_out);
+/* forward_prefill_batch (src/model.rs:9917-10090): advances the KV cache over
+ * tokens[0..n_tokens) at positions start_pos.. without computing logits, in
+ * chunks of up to 256 tokens that run each weight matrix once per chunk on
+ * the matrix cores.  Needs the device embedding (set_embedding) and a model
+ * that standard_prefill_batchable (:9869-9887) accepts: every projection
+ * Q4_K or Q6_K, widths multiples of 256, no MoE; returns 0 otherwise (the
+ * caller then decodes token by token).  start_pos + n_tokens <= storage_len.
+ * Every cached K/V value is bit-identical to decoding the tokens in turn
+ * with the reference-order attention. */
+int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos);
 /* Copies slots [slot0, slot0+n_slots) of layer l's K (which = 0) or V
  * (which = 1) cache to / from host memory. */
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);

@@ -91,7 +91,33 @@ struct AttnExactArgs {
     int32_t slot_count, start_t, end_t, window, cap;
     int32_t kvec;        // 1: K rows are 16-byte aligned (float4 loads)
     float scale;
+    // Several query tokens in one launch (prefill), token z = blockIdx.z at
+    // position pos0 + z: its query at q + z*q_tok, its output at out +
+    // z*o_tok, its own scratch block tok_scratch floats further per token.
+    // n_tok = 0: one token, ranges from st or start_t/end_t.
+    int32_t n_tok, pos0;
+    int64_t q_tok, o_tok, tok_scratch;
 };
+
+// The single-token view of token blockIdx.z of a multi-token launch: its
+// range is start_t (or the window's start) ..= pos0 + z.
+__device__ __forceinline__ AttnExactArgs tok_view(const AttnExactArgs &A0) {
+    if (A0.n_tok == 0) return A0;
+    AttnExactArgs A = A0;
+    const int z = blockIdx.z;
+    const int64_t sc = (int64_t)z * A0.tok_scratch;
+    A.q += (int64_t)z * A0.q_tok;
+    A.out += (int64_t)z * A0.o_tok;
+    A.scores += sc;
+    A.e += sc;
+    A.tmax += sc;
+    A.newmask += sc;
+    A.den += sc;
+    A.st = nullptr;
+    A.end_t = A0.pos0 + z;
+    A.start_t = A0.window > 0 ? max(0, A.end_t + 1 - A0.window) : A0.start_t;
+    return A;
+}
 
 __device__ __forceinline__ void exact_range(const AttnExactArgs &A, int &s, int &e) {
     if (A.st) {
@@ -118,7 +144,8 @@ __device__ __forceinline__ size_t e_index(const AttnExactArgs &A, int h, int g, 
 
 // A: one workgroup per (tile of EX_TILE positions, kv head).  Writes the
 // scores of every query head of the group and each head's tile maximum.
-__global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A) {
+__global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
     extern __shared__ float s_dyn[];
     const int hd = A.hd, kvm = A.kv_mul;
     const int ldk = hd + 1;  // padded row: no bank conflicts on column reads
@@ -226,7 +253,8 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A)
 // scan.  e[t] = isfinite(run) ? expf(run - s) : 0 on a new max (the factor the
 // old output and denominator are scaled by), expf(s - run) otherwise; the
 // new-max steps are marked in newmask.
-__global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A) {
+__global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
@@ -596,7 +624,8 @@ __device__ void chain_consumer(const AttnExactArgs &A, ChainLds &L, int ctx, int
 // grid: n_heads * (vd/64) chain workgroups, then n_kv denominator
 // workgroups, CH_WAVES waves each; block b serves kv head b % n_kv, so the
 // heads of a kv head share an XCD.
-__global__ __launch_bounds__(64 * CH_WAVES) void attn_exact_chain_dma_kernel(AttnExactArgs A) {
+__global__ __launch_bounds__(64 * CH_WAVES) void attn_exact_chain_dma_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
     __shared__ ChainLds L;
     int s0, e0;
     exact_range(A, s0, e0);
@@ -633,7 +662,8 @@ __global__ __launch_bounds__(64 * CH_WAVES) void attn_exact_chain_dma_kernel(Att
 // C (any layout): one wave per (query head, 64 value dims), grid (n_heads,
 // ceil(vd/64)); V read straight from the cache, 32 steps per batch.  The
 // denominator runs in every lane beside the output; slice 0 stores it.
-__global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A) {
+__global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;

@@ -181,19 +181,4 @@ __global__ __launch_bounds__(256) void gemm_kq_mfma_kernel(GemmArgs A) {
         }
 }
 
-// Q8_K of T tokens (quantize_row_q8k per token): qs [T][K], scales token-minor
-// [K/256][ldx].  Same arithmetic as quantize_q8k_kernel.  grid (K/256, T).
-__global__ __launch_bounds__(256) void quantize_q8k_batch_kernel(const float *x, int K, int ldxf, int8_t *qs,
-                                                                 float *dx, int ldx) {
-    __shared__ float red[4];
-    const int b = blockIdx.x, t = blockIdx.y, e = b * 256 + threadIdx.x;
-    const float v = x[(int64_t)t * ldxf + e];
-    const float amax = block_max_256(fabsf(v), red);
-    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-    int q = (int)__builtin_rintf(v * id);
-    q = max(-128, min(127, q));
-    qs[(int64_t)t * K + e] = (int8_t)q;
-    if (threadIdx.x == 0) dx[(int64_t)b * ldx + t] = amax * (1.0f / 127.0f);
-}
-
 }  // namespace rh

@@ -1,4 +1,5 @@
 // ops.hip — the small per-token ops fused around the GEMVs and attention.
+#pragma once
 #include "common.hpp"
 
 namespace rh {
@@ -129,10 +130,15 @@ struct RopeArgs {
     int32_t pos;
     int32_t max_pos;      // rows of the cos/sin table
     int32_t n_heads, n_kv, hd, vd, slots, ring, neox;
+    int32_t q_tok, k_tok, v_tok;  // per-token row strides of q/k/v (prefill: token blockIdx.y at pos + y)
 };
 
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
-    const int pos = A.st ? A.st->pos : A.pos;
+    const int z = blockIdx.y;
+    const int pos = (A.st ? A.st->pos : A.pos) + z;
+    A.q += (int64_t)z * A.q_tok;
+    A.k += (int64_t)z * A.k_tok;
+    A.v += (int64_t)z * A.v_tok;
     if (pos < 0 || pos >= A.max_pos) return;
     const int half = A.hd / 2;
     const int slot = A.ring ? pos % A.slots : pos;

@@ -10,6 +10,7 @@
 #include "attention_exact.hip"
 #include "moe.hip"
 #include "gemm_mfma.hip"
+#include "prefill.hip"
 
 #include <hip/hip_ext.h>
 
@@ -695,10 +696,18 @@ static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
 // (multiple of 64, >= the longest range this launch may see).  The output is
 // normalised in place and, when xq.qs is set, quantized to Q8_K
 // (n_heads * vd must then be a multiple of 256).
+// With A.n_tok > 0 the launch covers that many query tokens (grid z), each
+// with its own scratch block of exact_scratch_floats; finish must then be
+// false (the caller normalises the rows).
 static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s, bool finish = true,
                              const float **den_out = nullptr) {
     const size_t nh = (size_t)A.n_heads, cap = (size_t)A.cap;
     const int ntl = A.cap / EX_TILE;
+    const unsigned nz = A.n_tok > 0 ? (unsigned)A.n_tok : 1u;
+    if (A.n_tok > 0) {
+        if (finish) return 0;
+        A.tok_scratch = (int64_t)exact_scratch_floats(A.n_kv, A.kv_mul, A.cap);
+    }
     A.scores = scratch;
     A.e = scratch + nh * cap;
     A.tmax = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
@@ -711,12 +720,12 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         ProfScope ps("attn_exact_scores", s);
         size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1) + (size_t)A.kv_mul * EX_TILE) *
                      sizeof(float);
-        rh_launch(attn_exact_scores_kernel, dim3(ntl, A.n_kv), dim3(256), lds, s, A);
+        rh_launch(attn_exact_scores_kernel, dim3(ntl, A.n_kv, nz), dim3(256), lds, s, A);
         RH_LAUNCH_OK();
     }
     {
         ProfScope ps("attn_exact_coef", s);
-        rh_launch(attn_exact_coef_kernel, dim3(ntl, A.n_heads), dim3(64), 0, s, A);
+        rh_launch(attn_exact_coef_kernel, dim3(ntl, A.n_heads, nz), dim3(64), 0, s, A);
         RH_LAUNCH_OK();
     }
     {
@@ -726,9 +735,9 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
                          (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
         if (dma) {
             int blocks = A.n_kv * (A.kv_mul * (A.vd / 64) + 1);
-            rh_launch(attn_exact_chain_dma_kernel, dim3(blocks), dim3(64 * CH_WAVES), 0, s, A);
+            rh_launch(attn_exact_chain_dma_kernel, dim3(blocks, 1, nz), dim3(64 * CH_WAVES), 0, s, A);
         } else {
-            rh_launch(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64), dim3(64), 0, s, A);
+            rh_launch(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64, nz), dim3(64), 0, s, A);
         }
         RH_LAUNCH_OK();
     }
@@ -739,6 +748,65 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
                            n_out, xq);
         RH_LAUNCH_OK();
     }
+    return 1;
+}
+
+// ---- batched K-quant products (prefill) ------------------------------------------
+// Q8_K activations of T tokens in one buffer: quants [T][K], then the scales
+// token-minor [K/256][ldx] with ldx = T rounded up to the 64-token tile, so the
+// product kernel reads four tokens' scales per 16-byte load without a bound.
+struct BatchXq {
+    int8_t *qs;
+    float *dx;
+    int ldx;
+};
+static int64_t batch_ldx(int T) { return ((int64_t)T + 63) / 64 * 64; }
+static size_t batch_xq_bytes(int T, int K) { return (size_t)T * K + (size_t)(K / 256) * batch_ldx(T) * 4 + 256; }
+static BatchXq batch_xq_at(int8_t *buf, int T, int K) {
+    BatchXq b;
+    b.qs = buf;
+    b.dx = (float *)(buf + ((size_t)T * K + 255) / 256 * 256);
+    b.ldx = (int)batch_ldx(T);
+    return b;
+}
+
+static int quantize_batch_enqueue(const float *x, int ldxf, int T, int K, const BatchXq &b, hipStream_t s) {
+    if (K % 256 != 0 || T <= 0) return 0;
+    ProfScope ps("quantize_q8k_batch", s);
+    rh_launch(quantize_q8k_batch_kernel, dim3((unsigned)(K / 256), (unsigned)T), dim3(256), 0, s, x, K, ldxf, b.qs,
+              b.dx, b.ldx);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// y[t * ldy + r] (=, or += with epi EPI_ADD) row r of W times token t, plus
+// bias[r] when given; rows of one wave tile are 32 weight rows, a workgroup
+// holds 4 tiles and covers 64 tokens.
+static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int ldy, int epi, const float *bias,
+                           hipStream_t s) {
+    if ((W.fmt != 12 && W.fmt != 14) || W.cols % 256 != 0 || W.stride % 16 != 0 || T <= 0 || ldy < W.rows)
+        return 0;
+    GemmArgs A;
+    memset(&A, 0, sizeof(A));
+    A.w = W.p;
+    A.row_stride = W.stride;
+    A.rows = W.rows;
+    A.K = W.cols;
+    A.T = T;
+    A.epi = epi;
+    A.xq = b.qs;
+    A.dx = b.dx;
+    A.ldx = b.ldx;
+    A.ldy = ldy;
+    A.y = y;
+    A.bias = bias;
+    const dim3 grid((unsigned)((W.rows + 127) / 128), (unsigned)((T + 32 * GEMM_NT - 1) / (32 * GEMM_NT)));
+    ProfScope ps(W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma", s);
+    if (W.fmt == 12)
+        rh_launch(gemm_kq_mfma_kernel<F_Q4_K>, grid, dim3(256), 0, s, A);
+    else
+        rh_launch(gemm_kq_mfma_kernel<F_Q6_K>, grid, dim3(256), 0, s, A);
+    RH_LAUNCH_OK();
     return 1;
 }
 
@@ -1441,6 +1509,11 @@ struct Resident {
     uint32_t n_exp = 0, top_k = 0, window = 0;
     float rope_conc = 1.0f;
     float *moebuf = nullptr;
+    // batched prefill, allocated on first use for pf_cap tokens per chunk
+    uint32_t pf_cap = 0;
+    float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pattn = nullptr, *ptg = nullptr,
+          *ptu = nullptr, *pex = nullptr;
+    int8_t *pbq = nullptr;
     std::map<int, hipGraphExec_t> graphs;
     std::vector<void *> allocs;
 };
@@ -1470,6 +1543,7 @@ static void r_reset() {
     R.n_exp = R.top_k = R.window = 0;
     R.rope_conc = 1.0f;
     R.moebuf = nullptr;
+    R.pf_cap = 0;
 }
 
 static void r_invalidate_graphs() {
@@ -1784,6 +1858,175 @@ static int r_run(int mode, float penalty) {
     return 1;
 }
 
+// ---- batched prefill (forward_prefill_batch, src/model.rs:9917-10090) -----------
+// A chunk of T prompt tokens goes through every layer together: each weight
+// matrix is read once per chunk by the batched products on the matrix cores,
+// while RMSNorm, bias, RoPE, the KV store and attention stay per token with
+// the decode step's arithmetic.  The KV cache is linear (slot = position), so
+// the chunk's K/V rows are all stored before any of its tokens attends; each
+// token's range ends at its own position, which is the sequential order's
+// result exactly.  Every value written is bit-identical to decoding the
+// tokens one by one.
+#define PF_CHUNK 256
+
+static bool r_prefill_enabled() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("RUSTY_HIP_PREFILL");
+        on = (e && (e[0] == '0' || e[0] == 'n' || e[0] == 'N' || e[0] == 'f' || e[0] == 'F')) ? 0 : 1;
+    }
+    return on == 1;
+}
+
+// standard_prefill_batchable (src/model.rs:9869-9887): a standard model whose
+// seven projections are all K-quant, with K-quant-compatible widths.
+static bool r_prefill_batchable() {
+    if (!R.ready || R.moe || !R.has_embd) return false;
+    if (R.dim % 256 != 0 || (R.n_heads * R.vd) % 256 != 0 || R.hidden % 256 != 0) return false;
+    for (const RLayer &Ly : R.L)
+        for (int i = 0; i < 7; i++)
+            if (Ly.w[i].fmt != 12 && Ly.w[i].fmt != 14) return false;
+    return true;
+}
+
+static int r_prefill_alloc() {
+    if (R.pf_cap) return 1;
+    const size_t C = PF_CHUNK;
+    const size_t qd = (size_t)R.n_heads * R.hd, kd = (size_t)R.n_kv * R.hd, vdim = (size_t)R.n_kv * R.vd;
+    const size_t attn_cols = (size_t)R.n_heads * R.vd;
+    const size_t kmax = std::max<size_t>(std::max<size_t>(R.dim, attn_cols), R.hidden);
+    const size_t ex = exact_scratch_floats((int)R.n_kv, (int)(R.n_heads / R.n_kv), R.ex_cap);
+    if (!r_alloc((void **)&R.px, C * R.dim * 4) || !r_alloc((void **)&R.pq, C * qd * 4) ||
+        !r_alloc((void **)&R.pk, C * kd * 4) || !r_alloc((void **)&R.pv, C * vdim * 4) ||
+        !r_alloc((void **)&R.pattn, C * attn_cols * 4) || !r_alloc((void **)&R.ptg, C * R.hidden * 4) ||
+        !r_alloc((void **)&R.ptu, C * R.hidden * 4) || !r_alloc((void **)&R.pex, C * ex * 4) ||
+        !r_alloc((void **)&R.pbq, batch_xq_bytes((int)C, (int)kmax)))
+        return 0;
+    R.pf_cap = (uint32_t)C;
+    return 1;
+}
+
+static int r_rmsnorm_batch(const float *norm_w, int T, const BatchXq &b, hipStream_t s) {
+    ProfScope ps("rmsnorm_q8k_batch", s);
+    rh_launch(rmsnorm_q8k_batch_kernel, dim3(R.dim / 256, (unsigned)T), dim3(256), R.dim * 4, s, (const float *)R.px,
+              norm_w, R.eps, (int)R.dim, b.qs, b.dx, b.ldx);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// T (<= pf_cap) tokens from the device array tok at positions pos0.. .
+static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
+    const int dim = R.dim, qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd;
+    const int attn_cols = R.n_heads * R.vd, hid = R.hidden, kvm = R.n_heads / R.n_kv;
+    if (T <= 0 || (uint32_t)T > R.pf_cap) return 0;
+    {
+        ProfScope ps("embed_batch", s);
+        rh_launch(embed_batch_kernel, dim3((dim + 255) / 256, (unsigned)T), dim3(256), 0, s, R.embd.p, R.embd.stride,
+                  R.embd.fmt, dim, tok, R.px);
+        RH_LAUNCH_OK();
+    }
+    const BatchXq bd = batch_xq_at(R.pbq, T, dim), ba = batch_xq_at(R.pbq, T, attn_cols);
+    const BatchXq bh = batch_xq_at(R.pbq, T, hid);
+    const int cap = (pos0 + T + 63) / 64 * 64;
+    for (uint32_t l = 0; l < R.n_layers; l++) {
+        RLayer &Ly = R.L[l];
+        if (!r_rmsnorm_batch(Ly.attn_norm, T, bd, s)) return 0;
+        if (!gemm_kq_enqueue(Ly.w[0], bd, T, R.pq, qd, EPI_STORE, Ly.bias[0], s) ||
+            !gemm_kq_enqueue(Ly.w[1], bd, T, R.pk, kd, EPI_STORE, Ly.bias[1], s) ||
+            !gemm_kq_enqueue(Ly.w[2], bd, T, R.pv, vdim, EPI_STORE, Ly.bias[2], s))
+            return 0;
+        {
+            RopeArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.pq;
+            A.k = R.pk;
+            A.v = R.pv;
+            A.kcache = Ly.k;
+            A.vcache = Ly.v;
+            A.cos_t = R.cos_t;
+            A.sin_t = R.sin_t;
+            A.st = nullptr;
+            A.pos = pos0;
+            A.max_pos = R.storage;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.slots = R.storage;
+            A.ring = 0;
+            A.neox = R.neox;
+            A.q_tok = qd;
+            A.k_tok = kd;
+            A.v_tok = vdim;
+            const int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+            ProfScope ps("rope_kv_batch", s);
+            rh_launch(rope_kv_kernel, dim3((work + 255) / 256, (unsigned)T), dim3(256), 0, s, A);
+            RH_LAUNCH_OK();
+        }
+        {
+            AttnExactArgs E;
+            memset(&E, 0, sizeof(E));
+            E.q = R.pq;
+            E.k = Ly.k;
+            E.v = Ly.v;
+            E.out = R.pattn;
+            E.n_heads = R.n_heads;
+            E.n_kv = R.n_kv;
+            E.kv_mul = kvm;
+            E.hd = R.hd;
+            E.vd = R.vd;
+            E.key_stride = kd;
+            E.value_stride = vdim;
+            E.slot_count = R.storage;
+            E.start_t = 0;
+            E.window = 0;
+            E.cap = cap;
+            E.scale = 1.0f / sqrtf((float)R.hd);
+            E.n_tok = T;
+            E.pos0 = pos0;
+            E.q_tok = qd;
+            E.o_tok = attn_cols;
+            const float *den = nullptr;
+            if (!attn_exact_launch(E, R.pex, XQ{}, s, false, &den)) return 0;
+            ProfScope ps("attn_finish_batch", s);
+            rh_launch(attn_finish_q8k_batch_kernel, dim3(attn_cols / 256, (unsigned)T), dim3(256), 0, s,
+                      (const float *)R.pattn, den, (int64_t)exact_scratch_floats(R.n_kv, kvm, cap), (int)R.vd,
+                      attn_cols, ba.qs, ba.dx, ba.ldx);
+            RH_LAUNCH_OK();
+        }
+        if (!gemm_kq_enqueue(Ly.w[3], ba, T, R.px, dim, EPI_ADD, nullptr, s)) return 0;
+        if (!r_rmsnorm_batch(Ly.ffn_norm, T, bd, s)) return 0;
+        if (!gemm_kq_enqueue(Ly.w[4], bd, T, R.ptg, hid, EPI_STORE, nullptr, s) ||
+            !gemm_kq_enqueue(Ly.w[5], bd, T, R.ptu, hid, EPI_STORE, nullptr, s))
+            return 0;
+        {
+            ProfScope ps("silu_mul_batch", s);
+            rh_launch(silu_mul_q8k_batch_kernel, dim3(hid / 256, (unsigned)T), dim3(256), 0, s, (const float *)R.ptg,
+                      (const float *)R.ptu, hid, bh.qs, bh.dx, bh.ldx);
+            RH_LAUNCH_OK();
+        }
+        if (!gemm_kq_enqueue(Ly.w[6], bh, T, R.px, dim, EPI_ADD, nullptr, s)) return 0;
+    }
+    return 1;
+}
+
+// n tokens already in R.tokens[0..n) at positions pos0.. in chunks.
+static int r_prefill_tokens(int n, int pos0) {
+    if (!r_prefill_alloc()) return 0;
+    for (int c = 0; c < n; c += (int)R.pf_cap)
+        if (!r_prefill_chunk(R.tokens + c, std::min<int>((int)R.pf_cap, n - c), pos0 + c, g.s)) return 0;
+    return 1;
+}
+
+static int r_ensure_tokens(uint32_t need) {
+    if (R.tok_cap >= need) return 1;
+    need = std::max(need, std::min<uint32_t>(R.storage + 1, 8192));
+    if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
+    R.tok_cap = need;
+    r_invalidate_graphs();  // the greedy graph records the token pointer
+    return 1;
+}
+
 static int r_set_state(int pos, int start_t, int token, bool reset_recent) {
     StepState *h = R.st_host;
     RH_CHECK(hipStreamSynchronize(g.s));  // staging buffer reuse
@@ -2050,22 +2293,22 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
     if ((uint64_t)start_pos + n_prompt + n_gen > (uint64_t)R.storage + 1) return 0;
     for (uint32_t i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= R.vocab) return 0;
-    uint32_t need = std::max(n_prompt, n_gen) + 1;
-    if (R.tok_cap < need) {
-        need = std::max<uint32_t>(need, std::min<uint32_t>(R.storage + 1, 8192));
-        if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
-        R.tok_cap = need;
-        r_invalidate_graphs();  // greedy graph records the token pointer
-    }
+    if (!r_ensure_tokens(std::max(n_prompt, n_gen) + 1)) return 0;
     RH_CHECK(hipMemcpy(R.tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
     if (!r_set_state((int)start_pos, 0, prompt[0], true)) return 0;
+    // prefill_prompt_tokens (src/runtime.rs:3368-3420): every prompt token but
+    // the last in batched chunks when the model allows it, then the last one
+    // through the decode step for its logits.
+    const bool batched = n_prompt > 2 && r_prefill_enabled() && r_prefill_batchable();
+    if (batched && !r_prefill_tokens((int)n_prompt - 1, (int)start_pos)) return 0;
     // recent window = last <= 64 prompt tokens (recent_token_tail, src/runtime.rs:508-512)
     uint32_t tail = n_prompt > 64 ? n_prompt - 64 : 0;
     for (uint32_t i = 0; i < n_prompt; i++) {
+        if (batched && i < tail && i + 1 < n_prompt) continue;  // no state change, no decode step
         rh_launch(set_step_kernel, dim3(1), dim3(64), 0, g.s, R.st, R.tokens, (int)i, (int)(start_pos + i),
                            i >= tail ? 1 : 0);
         RH_LAUNCH_OK();
-        if (i + 1 < n_prompt) {
+        if (i + 1 < n_prompt && !batched) {
             if (!r_run(MODE_DEVTOK, 1.0f)) return 0;
         }
     }
@@ -2079,6 +2322,20 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
         RH_CHECK(hipMemcpyAsync(out_tokens, R.tokens, (size_t)n_gen * 4, hipMemcpyDeviceToHost, g.s));
     }
     if (logits_out) RH_CHECK(hipMemcpyAsync(logits_out, R.logits, (size_t)R.vocab * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!tokens || n_tokens == 0 || !r_prefill_batchable()) return 0;
+    if ((uint64_t)start_pos + n_tokens > (uint64_t)R.storage) return 0;
+    for (uint32_t i = 0; i < n_tokens; i++)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= R.vocab) return 0;
+    if (!r_ensure_tokens(n_tokens + 1)) return 0;
+    RH_CHECK(hipMemcpy(R.tokens, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice));
+    if (!r_prefill_tokens((int)n_tokens, (int)start_pos)) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
     return 1;
@@ -2190,65 +2447,6 @@ int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *rece
     RH_CHECK(hipMemcpyAsync(&hs, st, sizeof(hs), hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
     *token = hs.token;
-    return 1;
-}
-
-// ---- batched K-quant products (prefill) ------------------------------------------
-// Q8_K activations of T tokens in one buffer: quants [T][K], then the scales
-// token-minor [K/256][ldx] with ldx = T rounded up to the 64-token tile, so the
-// product kernel reads four tokens' scales per 16-byte load without a bound.
-struct BatchXq {
-    int8_t *qs;
-    float *dx;
-    int ldx;
-};
-static int64_t batch_ldx(int T) { return ((int64_t)T + 63) / 64 * 64; }
-static size_t batch_xq_bytes(int T, int K) { return (size_t)T * K + (size_t)(K / 256) * batch_ldx(T) * 4 + 256; }
-static BatchXq batch_xq_at(int8_t *buf, int T, int K) {
-    BatchXq b;
-    b.qs = buf;
-    b.dx = (float *)(buf + ((size_t)T * K + 255) / 256 * 256);
-    b.ldx = (int)batch_ldx(T);
-    return b;
-}
-
-static int quantize_batch_enqueue(const float *x, int ldxf, int T, int K, const BatchXq &b, hipStream_t s) {
-    if (K % 256 != 0 || T <= 0) return 0;
-    ProfScope ps("quantize_q8k_batch", s);
-    rh_launch(quantize_q8k_batch_kernel, dim3((unsigned)(K / 256), (unsigned)T), dim3(256), 0, s, x, K, ldxf, b.qs,
-              b.dx, b.ldx);
-    RH_LAUNCH_OK();
-    return 1;
-}
-
-// y[t * ldy + r] (=, or += with epi EPI_ADD) row r of W times token t, plus
-// bias[r] when given; rows of one wave tile are 32 weight rows, a workgroup
-// holds 4 tiles and covers 64 tokens.
-static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int ldy, int epi, const float *bias,
-                           hipStream_t s) {
-    if ((W.fmt != 12 && W.fmt != 14) || W.cols % 256 != 0 || W.stride % 16 != 0 || T <= 0 || ldy < W.rows)
-        return 0;
-    GemmArgs A;
-    memset(&A, 0, sizeof(A));
-    A.w = W.p;
-    A.row_stride = W.stride;
-    A.rows = W.rows;
-    A.K = W.cols;
-    A.T = T;
-    A.epi = epi;
-    A.xq = b.qs;
-    A.dx = b.dx;
-    A.ldx = b.ldx;
-    A.ldy = ldy;
-    A.y = y;
-    A.bias = bias;
-    const dim3 grid((unsigned)((W.rows + 127) / 128), (unsigned)((T + 32 * GEMM_NT - 1) / (32 * GEMM_NT)));
-    ProfScope ps(W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma", s);
-    if (W.fmt == 12)
-        rh_launch(gemm_kq_mfma_kernel<F_Q4_K>, grid, dim3(256), 0, s, A);
-    else
-        rh_launch(gemm_kq_mfma_kernel<F_Q6_K>, grid, dim3(256), 0, s, A);
-    RH_LAUNCH_OK();
     return 1;
 }
 

@@ -32,7 +32,7 @@ SYMBOLS = [
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
-    "rusty_hip_kquant_matvec_batch",
+    "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill",
 ]
 
 
@@ -91,6 +91,7 @@ _sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32,
      _f)
 _sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
 _sig("rusty_hip_kquant_matvec_batch", _i, _u32, _p, _u, _u, _u, _p, _u, _p, _u)
+_sig("rusty_hip_resident_prefill", _i, _p, _u32, _u32)
 _sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
      _p, _p)
 
@@ -317,6 +318,12 @@ class Resident:
         if ok != 1:
             raise RuntimeError("rusty_hip_resident_decode failed")
         return logits
+
+    def prefill(self, tokens, start_pos=0) -> bool:
+        """forward_prefill_batch: KV cache over tokens at start_pos.. (no
+        logits).  False when the model is not batchable."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        return lib.rusty_hip_resident_prefill(_ptr(t), t.size, start_pos) == 1
 
     def generate(self, prompt, n_gen, penalty=1.1, start_pos=0, want_logits=True):
         p = np.ascontiguousarray(prompt, np.int32)
