@@ -15,7 +15,10 @@ Also measured in the same run:
   stream during a profiling pass of the same decode;
 - cpu_baseline: the CPU oracle (C restatement of the reference's AVX2 path,
   oracle/) continuing the same decode from the GPU's KV cache on the host's
-  cores, for a bounded sample of tokens.
+  cores, for a bounded sample of tokens;
+- prefill: batched prefill of the first --prefill-tokens prompt tokens
+  (forward_prefill_batch on the device), tok/s and the int8 MFMA roofline of
+  its fused gate/up product.
 """
 from __future__ import annotations
 
@@ -59,6 +62,8 @@ def main():
     ap.add_argument("--kv-fill", choices=["prefill", "random"], default="prefill",
                     help="prefill: run the ctx random-id prompt through the decoder; random: write N(0,1) K/V "
                          "directly (same per-token decode work, far fewer dispatches, for profiler runs)")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="prompt length of the batched-prefill measurement (0: skip it)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy (y = x * 1) over this many MiB, 5 launches, and exit: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -90,8 +95,13 @@ def main():
     res = hip.Resident(model, storage_len=storage)
     log(f"uploaded to HBM in {time.time() - t0:.1f}s (storage {storage} slots)")
 
-    # KV prefill: ctx random-id positions, then `warmup` greedy tokens.
     prompt = synth.token_ids(args.seed + 1, args.ctx, cfg["vocab"]).astype(np.int32)
+    prefill = None
+    if args.prefill_tokens and args.kv_fill == "prefill":
+        prefill = measure_prefill(hip, res, prompt[:min(args.prefill_tokens, args.ctx)], cfg, log)
+
+    # KV prefill: ctx random-id positions (all but the last through batched
+    # prefill), then `warmup` greedy tokens.
     t0 = time.time()
     if args.kv_fill == "prefill":
         res.generate(prompt, args.warmup, penalty=args.penalty, want_logits=False)
@@ -113,7 +123,7 @@ def main():
     prof_ms = res.time_decode(args.profile_tokens, penalty=args.penalty)
     prof = hip.profile_results()
     hip.profile_enable(False)
-    fam_tot = sorted(prof.items(), key=lambda kv: -kv[1][0])
+    fam_tot = sorted(((k, v) for k, v in prof.items() if v[1] > 0), key=lambda kv: -kv[1][0])
     log("profile (per token): " + ", ".join(
         f"{k}={v[0] / args.profile_tokens:.3f}ms/{v[1] // args.profile_tokens}" for k, v in fam_tot))
 
@@ -173,8 +183,57 @@ def main():
         "profile_ms_per_token": {k: round(v[0] / args.profile_tokens, 4) for k, v in fam_tot},
         "profile_pass_ms_per_token": round(prof_ms / args.profile_tokens, 4),
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
+
+
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def measure_prefill(hip, res, toks, cfg, log):
+    """Batched prefill (rusty_hip_resident_prefill) of `toks` from position 0:
+    whole-call wall time (host clock around the synchronous call; the tokens
+    are uploaded inside it), then a profiling pass for per-launch times.  The
+    MFMA roofline is the fused gate/up batched product: 2*ffn*d_model*T int8
+    operations per launch, T = the chunk's tokens."""
+    n = int(toks.size)
+    res.prefill(toks, 0)  # warm-up (allocates the chunk buffers)
+    t0 = time.perf_counter()
+    ok = res.prefill(toks, 0)
+    sec = time.perf_counter() - t0
+    if not ok:
+        log("prefill: model not batchable")
+        return None
+    hip.profile_enable(True)
+    res.prefill(toks, 0)
+    prof = hip.profile_results()
+    hip.profile_enable(False)
+    chunk = min(n, 256)
+    tot, cnt = prof.get("pf_gemm_gate_up", (0.0, 0))
+    avg_ms = tot / cnt if cnt else float("nan")
+    ops = 2.0 * cfg["hidden_dim"] * cfg["dim"] * chunk
+    tops = ops / (avg_ms * 1e-3) / 1e12 if cnt else 0.0
+    log(f"prefill {n} tokens: {sec * 1e3:.1f} ms -> {n / sec:.1f} tok/s; gate/up product {avg_ms * 1e3:.1f} us "
+        f"= {tops:.1f} TOP/s")
+    return {
+        "tokens": n,
+        "tok_s": round(n / sec, 1),
+        "ms": round(sec * 1e3, 2),
+        "chunk": chunk,
+        "roofline": {
+            "kernel": "pf_gemm_gate_up (Q4_K %dx%d x %d tokens, i8 MFMA)" % (cfg["hidden_dim"], cfg["dim"], chunk),
+            "bound": "mfma",
+            "achieved": round(tops, 1),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s",
+            "frac": round(tops / INT8_PEAK_TOPS, 4),
+            "ops_per_launch": ops,
+            "avg_launch_us": round(avg_ms * 1e3, 2),
+            "launches": cnt,
+        },
+        "profile_ms": {k: round(v[0], 3) for k, v in sorted(prof.items(), key=lambda kv: -kv[1][0]) if v[1] > 0},
+    }
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_kquant_swiglu_llama3-8b-q4km_traffic.json")

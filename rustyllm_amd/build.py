@@ -19,6 +19,10 @@ SYNTH_LIB = os.path.join(HERE, "libsynth.so")
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in architectural VGPRs: the batched products feed every C
+    # element to VALU integer multiply-adds, which AGPR results would first
+    # have to copy out one register at a time
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

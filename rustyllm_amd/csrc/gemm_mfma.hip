@@ -42,8 +42,6 @@ struct GemmArgs {
     const float *bias;  // [rows] or null
 };
 
-#define GEMM_NT 2  // 32-token tiles per wave
-
 // Q6_K bytes q (0..63, four per dword) as signed q - 32: flip bit 5, then copy
 // it into bits 6 and 7.
 __device__ __forceinline__ uint32_t q6_signed4(uint32_t q) {
@@ -51,109 +49,205 @@ __device__ __forceinline__ uint32_t q6_signed4(uint32_t q) {
     return b | (s << 1) | (s << 2);
 }
 
+// One block of the lane's weight row, as the lane's MFMA B operands need it
+// (lane half h = lane / 32 takes k = 16h.. of each 32-element Q4_K sub-block,
+// k = 8h.. of each 16-element Q6_K group).
 template <int FMT>
+struct GemmW;
+template <>
+struct GemmW<F_Q4_K> {
+    uint4 hdr, qs[4];
+};
+template <>
+struct GemmW<F_Q6_K> {
+    uint2 ql[8], qh[4];
+    uint4 sc;
+    uint32_t d;
+};
+
+__device__ __forceinline__ void gemm_w_load(GemmW<F_Q4_K> &W, const uint8_t *blk, int half) {
+    W.hdr = *(const uint4 *)blk;  // 144-byte blocks of 16-aligned rows
+#pragma unroll
+    for (int q = 0; q < 4; q++) W.qs[q] = *(const uint4 *)(blk + 16 + 32 * q + 16 * half);
+}
+__device__ __forceinline__ void gemm_w_load(GemmW<F_Q6_K> &W, const uint8_t *blk, int half) {
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            W.qh[2 * g + h] = ld8(blk + 128 + 32 * g + 16 * h + 8 * half);
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) W.ql[4 * g + 2 * h + kk] = ld8(blk + 64 * g + 32 * kk + 16 * h + 8 * half);
+        }
+    W.sc = ld16(blk + 192);
+    W.d = ld2(blk + 208);
+}
+
+// LDS activation tile: one block (256 quants) of each of the workgroup's
+// tokens, rows padded to 272 bytes so the 32 token rows one MFMA operand read
+// touches start 4 banks apart.
+#define GEMM_XS 272
+
+// Integer sums of block b for the wave's 32 rows x 32*NT tokens: isum (and
+// for Q4_K imin) per C element, from the activation tile xs.
+template <int NT>
+__device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q4_K> &W, const int8_t *xs, int lane,
+                                                int (&isum)[NT][16], rh_v16i (&imin)[NT]) {
+    const int half = lane >> 5, n = lane & 31;
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+        imin[tt] = rh_v16i{};
+#pragma unroll
+        for (int i = 0; i < 16; i++) isum[tt][i] = 0;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int sc0, m0, sc1, m1;
+        scale_min_k4(2 * q, W.hdr.y, W.hdr.z, W.hdr.w, sc0, m0);
+        scale_min_k4(2 * q + 1, W.hdr.y, W.hdr.z, W.hdr.w, sc1, m1);
+        const uint4 qs = W.qs[q];
+        const rh_v4i blo = {(int)(qs.x & 0x0F0F0F0Fu), (int)(qs.y & 0x0F0F0F0Fu), (int)(qs.z & 0x0F0F0F0Fu),
+                            (int)(qs.w & 0x0F0F0F0Fu)};
+        const rh_v4i bhi = {(int)((qs.x >> 4) & 0x0F0F0F0Fu), (int)((qs.y >> 4) & 0x0F0F0F0Fu),
+                            (int)((qs.z >> 4) & 0x0F0F0F0Fu), (int)((qs.w >> 4) & 0x0F0F0F0Fu)};
+        const int mb0 = m0 * 0x01010101, mb1 = m1 * 0x01010101;
+        const rh_v4i bm0 = {mb0, mb0, mb0, mb0}, bm1 = {mb1, mb1, mb1, mb1};
+#pragma unroll
+        for (int tt = 0; tt < NT; tt++) {
+            const int8_t *xr = xs + (32 * tt + n) * GEMM_XS + 64 * q + 16 * half;
+            const rh_v4i a0 = *(const rh_v4i *)xr;
+            const rh_v4i a1 = *(const rh_v4i *)(xr + 32);
+            const rh_v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, blo, rh_v16i{}, 0, 0, 0);
+            const rh_v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bhi, rh_v16i{}, 0, 0, 0);
+            imin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bm0, imin[tt], 0, 0, 0);
+            imin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bm1, imin[tt], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                isum[tt][i] = __mul24(sc0, c0[i]) + isum[tt][i];
+                isum[tt][i] = __mul24(sc1, c1[i]) + isum[tt][i];
+            }
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q6_K> &W, const int8_t *xs, int lane,
+                                                int (&isum)[NT][16], rh_v16i (&imin)[NT]) {
+    const int half = lane >> 5, n = lane & 31;
+    (void)imin;
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) isum[tt][i] = 0;
+    const uint32_t scw[4] = {W.sc.x, W.sc.y, W.sc.z, W.sc.w};
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint2 qh = W.qh[2 * g + h];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint2 ql = W.ql[4 * g + 2 * h + (k & 1)];
+                const int sh = 4 * (k >> 1);
+                const uint32_t q0 = ((ql.x >> sh) & 0x0F0F0F0Fu) | (((qh.x >> (2 * k)) & 0x03030303u) << 4);
+                const uint32_t q1 = ((ql.y >> sh) & 0x0F0F0F0Fu) | (((qh.y >> (2 * k)) & 0x03030303u) << 4);
+                const long bq = (long)((uint64_t)q6_signed4(q0) | ((uint64_t)q6_signed4(q1) << 32));
+                const int si = 8 * g + 2 * k + h;  // scale of 16-element group (g, k, h)
+                const int sc = (int)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                const int e0 = 128 * g + 32 * k + 16 * h + 8 * half;
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) {
+                    const long a = *(const long *)(xs + (32 * tt + n) * GEMM_XS + e0);
+                    const rh_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, bq, rh_v16i{}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 16; i++) isum[tt][i] = __mul24(sc, c[i]) + isum[tt][i];
+                }
+            }
+        }
+}
+
+// Workgroup: 4 waves x 32 weight rows, 32*NT tokens.  Per block: the next
+// block's weights (registers) and activation tile (registers, then the other
+// LDS buffer) are loaded while this block's MFMAs and combine run; one
+// barrier per block.  Waves past the last row compute clamped rows and store
+// nothing, so every wave reaches every barrier.
+template <int FMT, int NT>
 __global__ __launch_bounds__(256) void gemm_kq_mfma_kernel(GemmArgs A) {
-    const int lane = threadIdx.x & 63, half = lane >> 5, n = lane & 31;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    extern __shared__ __align__(16) int8_t s_xs[];  // [2][32*NT][GEMM_XS]
+    constexpr int TOK = 32 * NT;
+    constexpr int NLD = TOK * 16 / 256;  // 16-byte activation pieces per thread per block
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, n = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r0 = (blockIdx.x * 4 + wave) * 32;
-    if (r0 >= A.rows) return;  // whole-wave exit: no barrier follows
-    const int t0 = blockIdx.y * 32 * GEMM_NT;
+    const int t0 = blockIdx.y * TOK;
     const int row = min(r0 + n, A.rows - 1);
     const uint8_t *wr = A.w + (int64_t)row * A.row_stride;
     const int nb = A.K >> 8;
-    // this lane's A-operand token per 32-token tile (clamped)
-    const int8_t *xrow[GEMM_NT];
+    constexpr int BB = FMT == F_Q4_K ? 144 : 210;
+    // activation pieces: thread -> (token, 16-byte part)
+    const int8_t *xsrc[NLD];
+    int xdst[NLD];
 #pragma unroll
-    for (int tt = 0; tt < GEMM_NT; tt++) xrow[tt] = A.xq + (int64_t)min(t0 + 32 * tt + n, A.T - 1) * A.K;
-    float acc[GEMM_NT][16];
+    for (int j = 0; j < NLD; j++) {
+        const int p = tid + 256 * j, tok = p >> 4, part = p & 15;
+        xsrc[j] = A.xq + (int64_t)min(t0 + tok, A.T - 1) * A.K + 16 * part;
+        xdst[j] = tok * GEMM_XS + 16 * part;
+    }
+    GemmW<FMT> W;
+    gemm_w_load(W, wr, half);
+    {
+        uint4 st[NLD];
 #pragma unroll
-    for (int tt = 0; tt < GEMM_NT; tt++)
+        for (int j = 0; j < NLD; j++) st[j] = *(const uint4 *)xsrc[j];
+#pragma unroll
+        for (int j = 0; j < NLD; j++) *(uint4 *)(s_xs + xdst[j]) = st[j];
+    }
+    __syncthreads();
+    float acc[NT][16];
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[tt][i] = 0.0f;
 
     for (int b = 0; b < nb; b++) {
-        int isum[GEMM_NT][16];
+        const bool more = b + 1 < nb;
+        const int bn = more ? b + 1 : b;
+        GemmW<FMT> Wn;
+        gemm_w_load(Wn, wr + (int64_t)bn * BB, half);
+        uint4 st[NLD];
 #pragma unroll
-        for (int tt = 0; tt < GEMM_NT; tt++)
+        for (int j = 0; j < NLD; j++) st[j] = *(const uint4 *)(xsrc[j] + 256 * bn);
+        // this block's activation scales, four consecutive tokens per load:
+        // token of C element i = 8*(i/4) + 4*half + i%4
+        float4 dv[NT][4];
 #pragma unroll
-            for (int i = 0; i < 16; i++) isum[tt][i] = 0;
+        for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+                dv[tt][g4] = *(const float4 *)(A.dx + (int64_t)b * A.ldx + t0 + 32 * tt + 4 * half + 8 * g4);
+        int isum[NT][16];
+        rh_v16i imin[NT];
+        gemm_block_ints<NT>(W, s_xs + (b & 1) * TOK * GEMM_XS, lane, isum, imin);
         float d, dmin = 0.0f;
-        rh_v16i cmin[GEMM_NT];
-        if (FMT == F_Q4_K) {
-            const uint8_t *blk = wr + b * 144;
-            const uint4 hdr = *(const uint4 *)blk;
-            d = h2f(hdr.x & 0xFFFF);
-            dmin = h2f(hdr.x >> 16);
-#pragma unroll
-            for (int tt = 0; tt < GEMM_NT; tt++) cmin[tt] = rh_v16i{};
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint4 qs = *(const uint4 *)(blk + 16 + 32 * q + 16 * half);
-                int sc0, m0, sc1, m1;
-                scale_min_k4(2 * q, hdr.y, hdr.z, hdr.w, sc0, m0);
-                scale_min_k4(2 * q + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
-                const rh_v4i blo = {(int)(qs.x & 0x0F0F0F0Fu), (int)(qs.y & 0x0F0F0F0Fu), (int)(qs.z & 0x0F0F0F0Fu),
-                                    (int)(qs.w & 0x0F0F0F0Fu)};
-                const rh_v4i bhi = {(int)((qs.x >> 4) & 0x0F0F0F0Fu), (int)((qs.y >> 4) & 0x0F0F0F0Fu),
-                                    (int)((qs.z >> 4) & 0x0F0F0F0Fu), (int)((qs.w >> 4) & 0x0F0F0F0Fu)};
-                const int mb0 = m0 * 0x01010101, mb1 = m1 * 0x01010101;
-                const rh_v4i bm0 = {mb0, mb0, mb0, mb0}, bm1 = {mb1, mb1, mb1, mb1};
-#pragma unroll
-                for (int tt = 0; tt < GEMM_NT; tt++) {
-                    const rh_v4i a0 = *(const rh_v4i *)(xrow[tt] + 256 * b + 64 * q + 16 * half);
-                    const rh_v4i a1 = *(const rh_v4i *)(xrow[tt] + 256 * b + 64 * q + 32 + 16 * half);
-                    const rh_v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, blo, rh_v16i{}, 0, 0, 0);
-                    const rh_v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bhi, rh_v16i{}, 0, 0, 0);
-                    cmin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bm0, cmin[tt], 0, 0, 0);
-                    cmin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bm1, cmin[tt], 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 16; i++) isum[tt][i] += __mul24(sc0, c0[i]) + __mul24(sc1, c1[i]);
-                }
-            }
+        if constexpr (FMT == F_Q4_K) {
+            d = h2f(W.hdr.x & 0xFFFF);
+            dmin = h2f(W.hdr.x >> 16);
         } else {
-            const uint8_t *blk = wr + b * 210;
-            d = ldh(blk + 208);
-#pragma unroll
-            for (int g = 0; g < 2; g++)
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    // qh bytes of positions 16h + 8*half .. +8 of half g
-                    const uint2 qh = ld8(blk + 128 + 32 * g + 16 * h + 8 * half);
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const uint2 ql = ld8(blk + 64 * g + 32 * (k & 1) + 16 * h + 8 * half);
-                        const int sh = 4 * (k >> 1);
-                        const uint32_t q0 = ((ql.x >> sh) & 0x0F0F0F0Fu) | (((qh.x >> (2 * k)) & 0x03030303u) << 4);
-                        const uint32_t q1 = ((ql.y >> sh) & 0x0F0F0F0Fu) | (((qh.y >> (2 * k)) & 0x03030303u) << 4);
-                        const long bq = (long)((uint64_t)q6_signed4(q0) | ((uint64_t)q6_signed4(q1) << 32));
-                        const int sc = (int)(int8_t)blk[192 + 8 * g + 2 * k + h];
-                        const int e0 = 128 * g + 32 * k + 16 * h + 8 * half;
-#pragma unroll
-                        for (int tt = 0; tt < GEMM_NT; tt++) {
-                            const long a = *(const long *)(xrow[tt] + 256 * b + e0);
-                            const rh_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, bq, rh_v16i{}, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 16; i++) isum[tt][i] += __mul24(sc, c[i]);
-                        }
-                    }
-                }
+            d = h2f(W.d & 0xFFFF);
         }
-        // combine, block b: token m_i = 8*(i/4) + 4*half + i%4; dx of four
-        // consecutive tokens per 16-byte load
+        // the reference's per-block combine, accumulated in block order
 #pragma unroll
-        for (int tt = 0; tt < GEMM_NT; tt++) {
-            const float *dxb = A.dx + (int64_t)b * A.ldx + t0 + 32 * tt + 4 * half;
+        for (int tt = 0; tt < NT; tt++)
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
-                const float4 dv = *(const float4 *)(dxb + 8 * g4);
-                const float dxs[4] = {dv.x, dv.y, dv.z, dv.w};
+                const float dxs[4] = {dv[tt][g4].x, dv[tt][g4].y, dv[tt][g4].z, dv[tt][g4].w};
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int i = 4 * g4 + r;
                     float v;
-                    if (FMT == F_Q4_K) {
+                    if constexpr (FMT == F_Q4_K) {
                         const float t1 = d * (float)isum[tt][i];
-                        const float t2 = dmin * (float)cmin[tt][i];
+                        const float t2 = dmin * (float)imin[tt][i];
                         v = dxs[r] * (t1 - t2);
                     } else {
                         v = (dxs[r] * d) * (float)isum[tt][i];
@@ -161,12 +255,17 @@ __global__ __launch_bounds__(256) void gemm_kq_mfma_kernel(GemmArgs A) {
                     acc[tt][i] += v;
                 }
             }
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < NLD; j++) *(uint4 *)(s_xs + ((b + 1) & 1) * TOK * GEMM_XS + xdst[j]) = st[j];
         }
+        __syncthreads();
+        W = Wn;
     }
     if (r0 + n >= A.rows) return;
     const float bias = A.bias ? A.bias[r0 + n] : 0.0f;
 #pragma unroll
-    for (int tt = 0; tt < GEMM_NT; tt++)
+    for (int tt = 0; tt < NT; tt++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int t = t0 + 32 * tt + 8 * (i >> 2) + 4 * half + (i & 3);

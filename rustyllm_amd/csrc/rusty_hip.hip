@@ -779,11 +779,21 @@ static int quantize_batch_enqueue(const float *x, int ldxf, int T, int K, const 
     return 1;
 }
 
+// RUSTY_HIP_GEMM_NT=1|2 pins the token tile (32 or 64 tokens) for sweeps.
+static int gemm_nt_override() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RUSTY_HIP_GEMM_NT");
+        v = (e && (e[0] == '1' || e[0] == '2')) ? e[0] - '0' : 0;
+    }
+    return v;
+}
+
 // y[t * ldy + r] (=, or += with epi EPI_ADD) row r of W times token t, plus
 // bias[r] when given; rows of one wave tile are 32 weight rows, a workgroup
 // holds 4 tiles and covers 64 tokens.
 static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int ldy, int epi, const float *bias,
-                           hipStream_t s) {
+                           hipStream_t s, const char *prof_name = nullptr) {
     if ((W.fmt != 12 && W.fmt != 14) || W.cols % 256 != 0 || W.stride % 16 != 0 || T <= 0 || ldy < W.rows)
         return 0;
     GemmArgs A;
@@ -800,12 +810,24 @@ static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int
     A.ldy = ldy;
     A.y = y;
     A.bias = bias;
-    const dim3 grid((unsigned)((W.rows + 127) / 128), (unsigned)((T + 32 * GEMM_NT - 1) / (32 * GEMM_NT)));
-    ProfScope ps(W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma", s);
-    if (W.fmt == 12)
-        rh_launch(gemm_kq_mfma_kernel<F_Q4_K>, grid, dim3(256), 0, s, A);
-    else
-        rh_launch(gemm_kq_mfma_kernel<F_Q6_K>, grid, dim3(256), 0, s, A);
+    // 64 tokens per workgroup where that still gives every SIMD two waves,
+    // else 32
+    const int64_t row_tiles = (W.rows + 127) / 128;
+    int nt = gemm_nt_override() ? gemm_nt_override()
+                                : (row_tiles * 4 * ((T + 63) / 64) >= (int64_t)g.n_cu * 8 ? 2 : 1);
+    if (W.fmt == 14) nt = 1;
+    const int tok = 32 * nt;
+    const dim3 grid((unsigned)row_tiles, (unsigned)((T + tok - 1) / tok));
+    const uint32_t lds = 2u * tok * GEMM_XS;
+    ProfScope ps(prof_name ? prof_name : (W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma"), s);
+    if (W.fmt == 12) {
+        if (nt == 2)
+            rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 2>, grid, dim3(256), lds, s, A);
+        else
+            rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 1>, grid, dim3(256), lds, s, A);
+    } else {
+        rh_launch(gemm_kq_mfma_kernel<F_Q6_K, 1>, grid, dim3(256), lds, s, A);
+    }
     RH_LAUNCH_OK();
     return 1;
 }
@@ -1931,9 +1953,9 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
     for (uint32_t l = 0; l < R.n_layers; l++) {
         RLayer &Ly = R.L[l];
         if (!r_rmsnorm_batch(Ly.attn_norm, T, bd, s)) return 0;
-        if (!gemm_kq_enqueue(Ly.w[0], bd, T, R.pq, qd, EPI_STORE, Ly.bias[0], s) ||
-            !gemm_kq_enqueue(Ly.w[1], bd, T, R.pk, kd, EPI_STORE, Ly.bias[1], s) ||
-            !gemm_kq_enqueue(Ly.w[2], bd, T, R.pv, vdim, EPI_STORE, Ly.bias[2], s))
+        if (!gemm_kq_enqueue(Ly.w[0], bd, T, R.pq, qd, EPI_STORE, Ly.bias[0], s, "pf_gemm_q") ||
+            !gemm_kq_enqueue(Ly.w[1], bd, T, R.pk, kd, EPI_STORE, Ly.bias[1], s, "pf_gemm_k") ||
+            !gemm_kq_enqueue(Ly.w[2], bd, T, R.pv, vdim, EPI_STORE, Ly.bias[2], s, "pf_gemm_v"))
             return 0;
         {
             RopeArgs A;
@@ -1994,10 +2016,10 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
                       attn_cols, ba.qs, ba.dx, ba.ldx);
             RH_LAUNCH_OK();
         }
-        if (!gemm_kq_enqueue(Ly.w[3], ba, T, R.px, dim, EPI_ADD, nullptr, s)) return 0;
+        if (!gemm_kq_enqueue(Ly.w[3], ba, T, R.px, dim, EPI_ADD, nullptr, s, "pf_gemm_o")) return 0;
         if (!r_rmsnorm_batch(Ly.ffn_norm, T, bd, s)) return 0;
-        if (!gemm_kq_enqueue(Ly.w[4], bd, T, R.ptg, hid, EPI_STORE, nullptr, s) ||
-            !gemm_kq_enqueue(Ly.w[5], bd, T, R.ptu, hid, EPI_STORE, nullptr, s))
+        if (!gemm_kq_enqueue(Ly.w[4], bd, T, R.ptg, hid, EPI_STORE, nullptr, s, "pf_gemm_gate_up") ||
+            !gemm_kq_enqueue(Ly.w[5], bd, T, R.ptu, hid, EPI_STORE, nullptr, s, "pf_gemm_gate_up"))
             return 0;
         {
             ProfScope ps("silu_mul_batch", s);
@@ -2005,7 +2027,9 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
                       (const float *)R.ptu, hid, bh.qs, bh.dx, bh.ldx);
             RH_LAUNCH_OK();
         }
-        if (!gemm_kq_enqueue(Ly.w[6], bh, T, R.px, dim, EPI_ADD, nullptr, s)) return 0;
+        if (!gemm_kq_enqueue(Ly.w[6], bh, T, R.px, dim, EPI_ADD, nullptr, s,
+                             Ly.w[6].fmt == 12 ? "pf_gemm_down_q4k" : "pf_gemm_down_q6k"))
+            return 0;
     }
     return 1;
 }
