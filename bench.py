@@ -64,6 +64,8 @@ def main():
                          "directly (same per-token decode work, far fewer dispatches, for profiler runs)")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="prompt length of the batched-prefill measurement (0: skip it)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the batched-prefill measurement and print its JSON object")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy (y = x * 1) over this many MiB, 5 launches, and exit: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -97,8 +99,11 @@ def main():
 
     prompt = synth.token_ids(args.seed + 1, args.ctx, cfg["vocab"]).astype(np.int32)
     prefill = None
-    if args.prefill_tokens and args.kv_fill == "prefill":
+    if args.prefill_tokens and (args.kv_fill == "prefill" or args.prefill_only):
         prefill = measure_prefill(hip, res, prompt[:min(args.prefill_tokens, args.ctx)], cfg, log)
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill}), flush=True)
+        return
 
     # KV prefill: ctx random-id positions (all but the last through batched
     # prefill), then `warmup` greedy tokens.
