@@ -148,7 +148,9 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     const AttnExactArgs A = tok_view(A0);
     extern __shared__ float s_dyn[];
     const int hd = A.hd, kvm = A.kv_mul;
-    const int ldk = hd + 1;  // padded row: no bank conflicts on column reads
+    // Row pitch hd + 8: the x4 path's 8-lane groups read 8 consecutive floats
+    // of four rows per half-wave, which then fall in 32 distinct banks.
+    const int ldk = hd + 8;
     float *s_q = s_dyn;                       // [kv_mul][hd]
     float *s_k = s_q + kvm * hd;              // [EX_TILE][hd+1]
     float *s_sc = s_k + EX_TILE * ldk;        // [kv_mul][EX_TILE]
@@ -162,15 +164,17 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     const int nt = min(EX_TILE, ctx - t_base);
     for (int i = tid; i < kvm * hd; i += 256) s_q[i] = A.q[(size_t)h * kvm * hd + i];
     const float *kh = A.k + (size_t)h * hd;
-    if (A.kvec) {
-        const int h4 = hd >> 2;
+    const int h4 = hd >> 2;
+    if (A.kvec && (256 % h4) == 0 && A.slot_count >= EX_TILE) {
+        // thread -> (row r0 + k*rstep, float4 column c): one division, and the
+        // ring wrap as a compare (a tile spans fewer rows than the ring)
+        const int r0 = tid / h4, c = (tid - r0 * h4) * 4, rstep = 256 / h4;
+        const int base = (s0 + t_base) % A.slot_count;
 #pragma unroll 8
-        for (int i = tid; i < nt * h4; i += 256) {
-            int tt = i / h4, c = (i - tt * h4) * 4;
-            int slot = (s0 + t_base + tt) % A.slot_count;
-            float4 v = *(const float4 *)(kh + (size_t)slot * A.key_stride + c);
-            float *d = s_k + tt * ldk + c;
-            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        for (int tt = r0; tt < nt; tt += rstep) {
+            int slot = base + tt;
+            if (slot >= A.slot_count) slot -= A.slot_count;
+            *(float4 *)(s_k + tt * ldk + c) = *(const float4 *)(kh + (size_t)slot * A.key_stride + c);
         }
     } else {
 #pragma unroll 4
@@ -184,13 +188,14 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     // x4 heads: 8 lanes per (head, position), one accumulator per lane,
     // chained over the hd/8 chunks, then hsum_avx.
     const int nx4 = (A.sinks == nullptr && (kvm == 4 || kvm == 6)) ? 4 : 0;
+    // (head g, row tt) pairs are numbered g*EX_TILE + tt, rows past nt idle
     {
-        const int pairs = nx4 * nt;
+        const int pairs = nx4 * EX_TILE;
         const int l = lane & 7;
-        for (int p0 = wave * 8; p0 < ((pairs + 7) / 8) * 8; p0 += 32) {
-            int p = p0 + (lane >> 3);
-            bool ok = p < pairs;
-            int g = ok ? p / nt : 0, tt = ok ? p % nt : 0;
+        for (int p0 = wave * 8; p0 < pairs; p0 += 32) {
+            const int p = p0 + (lane >> 3);
+            const int g = p / EX_TILE, tt = p % EX_TILE;
+            const bool ok = tt < nt;
             float s = 0.0f;
             if (ok) {
                 const float *qq = s_q + g * hd, *kk = s_k + tt * ldk;
@@ -211,13 +216,14 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     // tail, hsum_avx, then the scalar tail.
     {
         const int ng = kvm - nx4;
-        const int pairs = ng * nt;
+        const int pairs = ng * EX_TILE;
         const int L = lane & 31;
         const int main32 = hd / 32, tail8 = (hd - main32 * 32) / 8;
-        for (int p0 = wave * 2; p0 < ((pairs + 1) / 2) * 2; p0 += 8) {
-            int p = p0 + (lane >> 5);
-            bool ok = p < pairs;
-            int g = ok ? nx4 + p / nt : 0, tt = ok ? p % nt : 0;
+        for (int p0 = wave * 2; p0 < pairs; p0 += 8) {
+            const int p = p0 + (lane >> 5);
+            const int tt = p % EX_TILE;
+            const bool ok = tt < nt;
+            const int g = nx4 + p / EX_TILE;
             const float *qq = s_q + g * hd, *kk = s_k + tt * ldk;
             float acc = 0.0f;
             if (ok)
@@ -295,31 +301,11 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
 //   else:    out = fma(e, v, out);  den = den + e
 // in the reference's step order.  A wave's own instruction stream is the
 // limit here (one dependent FMA per step and lane, ~3 ns per instruction for
-// a wave alone on its SIMD), so each recurrence wave gets a SIMD to itself and
-// everything else is kept out of its stream.
-//
-// Chain workgroups, one per (query head, 64 value dims), one wave per SIMD:
-//   wave 0     the consumer, lane = value dim.  Per 16 positions it issues
-//              one ds_read_b32 of e (lane j of each 16-lane row holds
-//              position j; the FMAs take it through their DPP row_newbcast
-//              operand, so e costs no instruction of its own) and eight
-//              ds_read2st64_b32 of V position pairs.  It never has direct
-//              loads in flight, so nothing drains before its LDS reads.  A
-//              single consumer per CU: a second one would compete for LDS
-//              return bandwidth (256 B per wave read) and its SIMD's issue;
-//   waves 1-2  producers: direct global->LDS loads (global_load_lds) of V
-//              [64 positions][64 dims], e and the new-max words into a ring
-//              of CH_NT tiles, CH_P tiles ahead, waiting on their own vmcnt.
-// The query heads of a kv head sit on the same XCD (block % n_kv), so their
-// repeated V reads hit its L2.  Denominator workgroups, one per kv head:
-// wave 0 runs the heads' denominators (lane = head) as the same recurrence
-// with v = 1 (fma(e, 1, d) = d + e and fma(1, 1, d*e) = d*e + 1 round exactly
-// like the scalar ops); wave 1 loads e and the words.  One s_barrier per two
-// tiles publishes them and releases the slots of the pair read before it.
-#define CH_NT 8
-#define CH_P 6
-#define CH_MAXG 8    // query heads per kv head handled by this kernel
-#define CH_WAVES 3
+// a wave alone on its SIMD), so the recurrence waves issue nothing else but
+// their LDS reads: e enters each FMA through its DPP row_newbcast operand
+// (lane j of a 16-lane row holds step j), V comes from LDS, and producer
+// waves stream both into a ring by direct global->LDS loads.
+#define CH_MAXG 8    // query heads per kv head handled by the chain kernel
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
@@ -342,123 +328,6 @@ __device__ __forceinline__ void tile_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-}
-
-template <int IPT>
-__device__ __forceinline__ void wait_tiles_after(int n_after) {
-    // n_after: this producer's tiles issued after the one to be published
-    switch (n_after) {
-        case 5: RH_WAIT_VM(5 * IPT); break;
-        case 4: RH_WAIT_VM(4 * IPT); break;
-        case 3: RH_WAIT_VM(3 * IPT); break;
-        case 2: RH_WAIT_VM(2 * IPT); break;
-        case 1: RH_WAIT_VM(1 * IPT); break;
-        default: RH_WAIT_VM(0); break;
-    }
-}
-static_assert(CH_P - 1 <= 5, "wait_tiles_after covers at most 5 tiles");
-static_assert(9 * CH_P <= 63, "vmcnt is 6 bits");
-
-struct ChainLds {
-    float v[CH_NT][EX_TILE * 64];       // [slot][position][64 dims]
-    float e[CH_NT][CH_MAXG * EX_TILE];  // [slot][head row][position]
-    uint32_t m[CH_NT][2 * CH_MAXG];     // [slot][head row][2 words]
-};
-
-// Barrier j publishes tiles 2j and 2j+1 (CH_PER tiles per barrier); the slots
-// refilled after it held tiles 2j-2 and 2j-1, read before it.
-#define CH_PER 2
-template <int IPT, class Issue>
-__device__ __forceinline__ void chain_producer_loop(int ntiles, Issue &issue) {
-    const int ngroups = (ntiles + CH_PER - 1) / CH_PER;
-    for (int i = 0; i < min(CH_P, ntiles); i++) issue(i);
-    for (int j = 0; j < ngroups; j++) {
-        const int last = min(CH_PER * j + CH_PER - 1, ntiles - 1);   // newest tile to publish
-        const int issued = min(CH_P + CH_PER * j, ntiles);           // tiles issued so far
-        wait_tiles_after<IPT>(issued - 1 - last);
-        tile_barrier();
-        for (int t = 0; t < CH_PER; t++) {
-            const int i = CH_P + CH_PER * j + t;
-            if (i < ntiles) issue(i);
-        }
-    }
-}
-static_assert(CH_NT >= CH_P + CH_PER, "ring too small");
-
-// Chain workgroup producer P: V rows k = 8P..8P+7 of every tile (4 positions
-// each); P = 0 also loads the head's e, P = 1 its two new-max words.
-template <int P>
-__device__ void chain_producer(const AttnExactArgs &A, ChainLds &L, int s0, int ctx, int h, int g, int slice) {
-    constexpr int IPT = 9;
-    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
-    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
-    const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 64) + (lane & 15) * 16;
-    const uint32_t row_bytes = (uint32_t)A.value_stride * 4u;
-    const uint32_t wrap = (uint32_t)A.slot_count * row_bytes;
-    const uint32_t step = 64u * row_bytes;
-    uint32_t roff[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-        const int tt = 4 * (8 * P + kk) + (lane >> 4);
-        roff[kk] = (uint32_t)((s0 + tt) % A.slot_count) * row_bytes;
-    }
-    const char *e_base = (const char *)(A.e + e_index(A, h, g, 0)) + lane * 4;
-    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + g) * (A.cap / 32)) + (lane & 1) * 4;
-
-    auto issue = [&](int i) {
-        const int sl = i & (CH_NT - 1);
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            dma16(v_base + roff[kk], &L.v[sl][(8 * P + kk) * 256]);
-            roff[kk] += step;
-            if (roff[kk] >= wrap) roff[kk] -= wrap;
-        }
-        if (P == 0) dma4(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
-        if (P == 1)
-            if (lane < 2) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
-    };
-
-    chain_producer_loop<IPT>(ntiles, issue);
-}
-
-// Denominator workgroup producer: e rows of all kv_mul heads (two 4-head
-// loads) and their new-max words.
-__device__ void den_producer(const AttnExactArgs &A, ChainLds &L, int ctx, int h) {
-    constexpr int IPT = 3;
-    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
-    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
-    const int eg0 = min(lane >> 4, kvm - 1), eg1 = min(4 + (lane >> 4), kvm - 1);
-    const char *e0 = (const char *)(A.e + e_index(A, h, eg0, 0)) + (lane & 15) * 16;
-    const char *e1 = (const char *)(A.e + e_index(A, h, eg1, 0)) + (lane & 15) * 16;
-    const int mg = min((lane >> 1) & 7, kvm - 1);
-    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + mg) * (A.cap / 32)) + (lane & 1) * 4;
-    auto issue = [&](int i) {
-        const int sl = i & (CH_NT - 1);
-        dma16(e0 + (uint32_t)i * 256u, &L.e[sl][0]);
-        dma16(e1 + (uint32_t)i * 256u, &L.e[sl][256]);
-        if (lane < 16) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
-    };
-    chain_producer_loop<IPT>(ntiles, issue);
-}
-
-// Denominator wave: 16 steps of its own head's e (four b128 reads).
-__device__ __forceinline__ void den_load16(const float *et, int k, float *e) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float4 q = *(const float4 *)(et + k * 16 + 4 * j);
-        e[4 * j] = q.x;
-        e[4 * j + 1] = q.y;
-        e[4 * j + 2] = q.z;
-        e[4 * j + 3] = q.w;
-    }
-}
-
-// Consumer: 16 steps.  e16 holds e of step (lane & 15) in every 16-lane row
-// (one ds_read_b32); v[j] = v of step j for this lane's dim.
-__device__ __forceinline__ void cons_load16(const float *et, const float *vt, int k, int lane, float &e16, float *v) {
-    e16 = et[k * 16 + (lane & 15)];
-#pragma unroll
-    for (int j = 0; j < 16; j++) v[j] = vt[(k * 16 + j) * 64];
 }
 
 // e of step J broadcast from lane J of each row.
@@ -513,148 +382,255 @@ __device__ __forceinline__ void chain_steps16_flags(const float *e, const float 
     }
 }
 
-// Consumer chunk: plain steps through the DPP FMAs unless a flag is set.
+// C, four query heads per wave: chain workgroups, one per (kv head, group of
+// four query heads, 16 value dims).  The consumer wave's four 16-lane rows
+// are the four heads and lane % 16 the value dim, so all four rows read the
+// same V element (one LDS broadcast) and each row takes its own head's e
+// through row_newbcast.  V of a kv head is then streamed from HBM once per
+// layer, 64 B per position per workgroup.  What bounds the chain is how fast
+// a workgroup's value stream arrives (bytes in flight / load latency), not
+// the FMAs: one wave's direct loads complete at a fixed rate however many are
+// in flight (about 75 ns per contiguous KB), so a tile (4 KB of V, 1 KB of
+// e) is split over four producer waves, and the ring keeps C4_P tiles in
+// flight.  The denominators run in a second recurrence wave as the same DPP
+// chain with v = 1.
+#define C4_NT 16
+#define C4_P 10
+#define C4_PER 2
+
+struct Chain4Lds {
+    float v[C4_NT][EX_TILE * 16];       // [slot][position][16 dims]
+    float e[C4_NT][CH_MAXG * EX_TILE];  // [slot][head][position]
+    uint32_t m[C4_NT][2 * CH_MAXG];     // [slot][head][2 words]
+};
+
+template <int IPT>
+__device__ __forceinline__ void c4_wait_tiles_after(int n_after) {
+    switch (n_after) {
+        case 9: RH_WAIT_VM(9 * IPT); break;
+        case 8: RH_WAIT_VM(8 * IPT); break;
+        case 7: RH_WAIT_VM(7 * IPT); break;
+        case 6: RH_WAIT_VM(6 * IPT); break;
+        case 5: RH_WAIT_VM(5 * IPT); break;
+        case 4: RH_WAIT_VM(4 * IPT); break;
+        case 3: RH_WAIT_VM(3 * IPT); break;
+        case 2: RH_WAIT_VM(2 * IPT); break;
+        case 1: RH_WAIT_VM(1 * IPT); break;
+        default: RH_WAIT_VM(0); break;
+    }
+}
+static_assert(C4_P - 1 <= 9, "c4_wait_tiles_after covers at most 9 tiles");
+static_assert(2 * 9 <= 63, "vmcnt is 6 bits (two loads per producer per tile)");
+static_assert(C4_NT >= C4_P + C4_PER, "ring too small");
+
+// Same protocol as chain_producer_loop on the C4 ring; after(j) runs once
+// group j's tiles are published (and before the barrier that lets their
+// slots be refilled, three groups later).
+template <int IPT, class Issue, class After>
+__device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue, After &after) {
+    const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
+    for (int i = 0; i < min(C4_P, ntiles); i++) issue(i);
+    for (int j = 0; j < ngroups; j++) {
+        const int last = min(C4_PER * j + C4_PER - 1, ntiles - 1);
+        const int issued = min(C4_P + C4_PER * j, ntiles);
+        c4_wait_tiles_after<IPT>(issued - 1 - last);
+        tile_barrier();
+        for (int t = 0; t < C4_PER; t++) {
+            const int i = C4_P + C4_PER * j + t;
+            if (i < ntiles) issue(i);
+        }
+        after(j);
+    }
+}
+
+// Producer P (0..3) of a chain workgroup, per tile: the direct load of V
+// positions 16P..16P+15 (lane -> position 16P + lane/4, dims 4*(lane%4)..+3);
+// P = 0 also loads e (lane -> head g0 + lane/16, positions 4*(lane%16)..+3),
+// P = 1 the heads' new-max words.  A position's 16 dims are 64 bytes of a
+// 4 KB cache row, and a wave's direct loads cost about 8 ns per such piece,
+// so a tile's V is split four ways.
+template <int P>
+__device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int g0, int slice) {
+    constexpr int IPT = P < 2 ? 2 : 1;
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 16) + (lane & 3) * 16;
+    const uint32_t row_bytes = (uint32_t)A.value_stride * 4u;
+    const uint32_t wrap = (uint32_t)A.slot_count * row_bytes;
+    const uint32_t step = 64u * row_bytes;
+    uint32_t roff = (uint32_t)((s0 + 16 * P + (lane >> 2)) % A.slot_count) * row_bytes;
+    const int re = min(g0 + (lane >> 4), kvm - 1);
+    const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
+    const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
+    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
+    auto issue = [&](int i) {
+        const int sl = i & (C4_NT - 1);
+        dma16(v_base + roff, &L.v[sl][P * 256]);
+        roff += step;
+        if (roff >= wrap) roff -= wrap;
+        if (P == 0) dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
+        if (P == 1)
+            if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
+    };
+    auto none = [](int) {};
+    c4_producer_loop<IPT>(ntiles, issue, none);
+}
+
+// Producer of a denominator workgroup: e of the four heads and their
+// new-max words, the same slots as a chain workgroup's.
+__device__ void c4_den_producer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
+    constexpr int IPT = 2;
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int re = min(g0 + (lane >> 4), kvm - 1);
+    const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
+    const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
+    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
+    auto issue = [&](int i) {
+        const int sl = i & (C4_NT - 1);
+        dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
+        if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
+    };
+    auto none = [](int) {};
+    c4_producer_loop<IPT>(ntiles, issue, none);
+}
+
+// A wave with nothing to load still takes part in every barrier.
+__device__ void c4_idle(int ctx) {
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
+    for (int j = 0; j < ngroups; j++) tile_barrier();
+}
+
+// 16 steps of a 16-dim row: e16 = e of step (lane % 16) of this row's head,
+// v[j] = V of step j at this lane's dim (broadcast across the four rows), or
+// 1 for the denominators.
+template <bool DEN>
+__device__ __forceinline__ void c4_load16(const float *et, const float *vt, int k, int lane, float &e16, float *v) {
+    e16 = et[k * 16 + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = DEN ? 1.0f : vt[(k * 16 + j) * 16];
+}
+
+// Consumer chunk: all rows' flags clear -> the DPP FMA run; else every step
+// in the per-lane update forms (each row its own head's flags).  Branching
+// per step instead measured slower.
 template <bool X4>
-__device__ __forceinline__ void cons_steps16(float e16, const float *v, float &o, uint32_t bits) {
-    if (__builtin_amdgcn_readfirstlane(bits) == 0u) {
+__device__ __forceinline__ void c4_steps16(float e16, const float *v, float &o, uint32_t bits) {
+    if (!__any(bits != 0u)) {
         cons_fma16_dpp(e16, v, o);
     } else {
         float e[16];
         bcast16_all(e16, e);
-        chain_steps16_flags<false, X4>(e, v, o, __builtin_amdgcn_readfirstlane(bits));
+        chain_steps16_flags<false, X4>(e, v, o, bits);
     }
 }
 
-// Denominator chunk (per-lane flags).
-__device__ __forceinline__ void den_steps16(const float *e, float &o, uint32_t bits) {
-    if (!__any(bits != 0u)) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) o = fmaf(e[j], 1.0f, o);
-    } else {
-        chain_steps16_flags<true, true>(e, nullptr, o, bits);
-    }
-}
-
-// Consumer (DEN = false: e/flag row `row`, lane = value dim; the row's flags
-// are wave-uniform) or denominator wave (DEN = true: lane = head = row).
-// active = false only keeps the wave in step with the barriers.
-template <bool DEN, bool X4>
-__device__ void chain_consumer(const AttnExactArgs &A, ChainLds &L, int ctx, int row, bool active, float *dst) {
-    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+// The recurrence of one wave: DEN = false the outputs (lane = value dim of
+// its row's head), DEN = true the denominators, the same recurrence with
+// v = 1 (fma(e, 1, d) = d + e; on a new maximum fma(1, 1, d*e) = d*e + 1,
+// the x4 form), starting from 1 with sinks; no V is read.
+template <bool X4, bool DEN>
+__device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float *dst) {
+    const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
-    const int ngroups = (ntiles + CH_PER - 1) / CH_PER;
-    const int r = DEN ? min(lane, kvm - 1) : row;
+    const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
     float o = (DEN && A.sinks) ? 1.0f : 0.0f;
     for (int j = 0; j < ngroups; j++) {
         tile_barrier();
-        if (!active) continue;
-        const int i0 = CH_PER * j;
-        const bool full = i0 + CH_PER <= ntiles && ctx >= (i0 + CH_PER) * EX_TILE;
-        if (!DEN && full) {
-            // 8 chunks of 16 steps over the group's two tiles.  A chunk is 9
-            // LDS reads and lgkmcnt holds at most 15, so one chunk is in
-            // flight: each chunk's reads are issued after the previous chunk
-            // has landed and before that chunk's FMAs, which cover them.
-            const int sa = i0 & (CH_NT - 1), sb = (i0 + 1) & (CH_NT - 1);
-            const float *va = &L.v[sa][lane], *vb = &L.v[sb][lane];
-            const float *ea = &L.e[sa][r * EX_TILE], *eb = &L.e[sb][r * EX_TILE];
-            const uint32_t m0 = L.m[sa][2 * r], m1 = L.m[sa][2 * r + 1];
-            const uint32_t m2 = L.m[sb][2 * r], m3 = L.m[sb][2 * r + 1];
+        const int i0 = C4_PER * j;
+        const bool full = i0 + C4_PER <= ntiles && ctx >= (i0 + C4_PER) * EX_TILE;
+        if (full) {
+            const int sa = i0 & (C4_NT - 1), sb = (i0 + 1) & (C4_NT - 1);
+            const float *va = &L.v[sa][dcol], *vb = &L.v[sb][dcol];
+            const float *ea = &L.e[sa][row * EX_TILE], *eb = &L.e[sb][row * EX_TILE];
+            const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
+            const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
             float a0, a1, v0[16], v1[16];
-            cons_load16(ea, va, 0, lane, a0, v0);
+            c4_load16<DEN>(ea, va, 0, lane, a0, v0);
             __builtin_amdgcn_sched_barrier(0);
-#define CH_STEP(ET, VT, K, NA, NV, CA, CV, BITS)       \
+#define C4_STEP(ET, VT, K, NA, NV, CA, CV, BITS)       \
     RH_WAIT_LGKM0();                                   \
-    cons_load16(ET, VT, K, lane, NA, NV);              \
+    c4_load16<DEN>(ET, VT, K, lane, NA, NV);           \
     __builtin_amdgcn_sched_barrier(0);                 \
-    cons_steps16<X4>(CA, CV, o, BITS);                 \
+    c4_steps16<X4>(CA, CV, o, BITS);                   \
     __builtin_amdgcn_sched_barrier(0);
-            CH_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu)
-            CH_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16)
-            CH_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu)
-            CH_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16)
-            CH_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu)
-            CH_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16)
-            CH_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu)
-#undef CH_STEP
+            C4_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu)
+            C4_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16)
+            C4_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu)
+            C4_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16)
+            C4_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu)
+            C4_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16)
+            C4_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu)
+#undef C4_STEP
             RH_WAIT_LGKM0();
-            cons_steps16<X4>(a1, v1, o, m3 >> 16);
+            c4_steps16<X4>(a1, v1, o, m3 >> 16);
         } else {
-            for (int i = i0; i < min(i0 + CH_PER, ntiles); i++) {
-                const int sl = i & (CH_NT - 1);
+            for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
+                const int sl = i & (C4_NT - 1);
                 const int ntok = min(EX_TILE, ctx - i * EX_TILE);
-                const float *vt = &L.v[sl][lane];
-                const float *et = &L.e[sl][r * EX_TILE];
-                uint32_t mw0 = L.m[sl][2 * r], mw1 = L.m[sl][2 * r + 1];
-                if (DEN && lane >= kvm) mw0 = mw1 = 0u;
-                if (DEN && ntok == EX_TILE) {
-                    float e0[16], e1[16], e2[16];
-                    den_load16(et, 0, e0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_load16(et, 1, e1);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_load16(et, 2, e2);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_steps16(e0, o, mw0 & 0xFFFFu);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_load16(et, 3, e0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_steps16(e1, o, mw0 >> 16);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_steps16(e2, o, mw1 & 0xFFFFu);
-                    __builtin_amdgcn_sched_barrier(0);
-                    den_steps16(e0, o, mw1 >> 16);
-                } else {
-                    for (int t = 0; t < ntok; t++) {
-                        const uint32_t mw = t < 32 ? mw0 : mw1;
-                        const float e = et[t];
-                        const float v = DEN ? 1.0f : vt[t * 64];
-                        const float on = fmaf(e, v, o);
-                        const float ox = (DEN || X4) ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
-                        o = ((mw >> (t & 31)) & 1u) ? ox : on;
-                    }
+                const float *vt = &L.v[sl][dcol];
+                const float *et = &L.e[sl][row * EX_TILE];
+                const uint32_t mw0 = L.m[sl][2 * row], mw1 = L.m[sl][2 * row + 1];
+                for (int t = 0; t < ntok; t++) {
+                    const uint32_t mw = t < 32 ? mw0 : mw1;
+                    const float e = et[t];
+                    const float v = DEN ? 1.0f : vt[t * 16];
+                    const float on = fmaf(e, v, o);
+                    const float ox = X4 ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
+                    o = ((mw >> (t & 31)) & 1u) ? ox : on;
                 }
             }
         }
-        RH_WAIT_LGKM0();  // the group's LDS reads are done before its slots are reused
+        RH_WAIT_LGKM0();  // this group's LDS reads are done before its slots are reused
     }
-    if (active && dst) *dst = o;
+    if (dst) *dst = o;
 }
 
-// grid: n_heads * (vd/64) chain workgroups, then n_kv denominator
-// workgroups, CH_WAVES waves each; block b serves kv head b % n_kv, so the
-// heads of a kv head share an XCD.
-__global__ __launch_bounds__(64 * CH_WAVES) void attn_exact_chain_dma_kernel(AttnExactArgs A0) {
+// grid: n_kv * ceil(kv_mul/4) * (vd/16) chain workgroups (wave 0 the
+// outputs, waves 1-4 the producers), then n_kv * ceil(kv_mul/4) denominator
+// workgroups (wave 0 the four heads' denominators as the same DPP recurrence
+// with v = 1, wave 1 their producer, the rest idle); block b serves kv head
+// b % n_kv.
+#define C4_WAVES 5
+__global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
-    __shared__ ChainLds L;
+    __shared__ Chain4Lds L;
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
     if (ctx <= 0) return;
-    const int kvm = A.kv_mul, nsl = A.vd / 64;
+    const int kvm = A.kv_mul, ngrp = (kvm + 3) / 4, nsl = A.vd / 16;
     const int h = blockIdx.x % A.n_kv, r = blockIdx.x / A.n_kv;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (r < kvm * nsl) {
-        const int g = r / nsl, slice = r % nsl;
-        if (wave == 1) {
-            chain_producer<0>(A, L, s0, ctx, h, g, slice);
-        } else if (wave == 2) {
-            chain_producer<1>(A, L, s0, ctx, h, g, slice);
-        } else {
-            float *dst = A.out + (size_t)(h * kvm + g) * A.vd + slice * 64 + lane;
-            const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4;
-            if (x4)
-                chain_consumer<false, true>(A, L, ctx, 0, true, dst);
+    if (r < ngrp * nsl) {
+        const int g0 = 4 * (r / nsl), slice = r % nsl;
+        const int g = g0 + (lane >> 4);
+        if (wave == 0) {
+            float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
+            if (A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0)
+                c4_consumer<true, false>(A, L, ctx, dst);
             else
-                chain_consumer<false, false>(A, L, ctx, 0, true, dst);
+                c4_consumer<false, false>(A, L, ctx, dst);
+        } else if (wave == 1) {
+            c4_producer<0>(A, L, s0, ctx, h, g0, slice);
+        } else if (wave == 2) {
+            c4_producer<1>(A, L, s0, ctx, h, g0, slice);
+        } else if (wave == 3) {
+            c4_producer<2>(A, L, s0, ctx, h, g0, slice);
+        } else {
+            c4_producer<3>(A, L, s0, ctx, h, g0, slice);
         }
     } else {
-        if (wave == 1) {
-            den_producer(A, L, ctx, h);
+        const int g0 = 4 * (r - ngrp * nsl);
+        const int g = g0 + (lane >> 4);
+        if (wave == 0) {
+            c4_consumer<true, true>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
+        } else if (wave == 1) {
+            c4_den_producer(A, L, ctx, h, g0);
         } else {
-            float *dst = lane < kvm ? A.den + h * kvm + lane : nullptr;
-            chain_consumer<true, true>(A, L, ctx, 0, wave == 0, dst);
+            c4_idle(ctx);
         }
     }
 }

@@ -687,6 +687,7 @@ static int attn_fast_mode() {
 }
 
 static size_t exact_e_floats(int n_kv, int kv_mul, int cap) { return (size_t)n_kv * kv_mul * cap; }
+
 static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
     size_t n = (size_t)n_kv * kv_mul;
     return n * cap + exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
@@ -718,7 +719,7 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     if (xq.qs && n_out % 256 != 0) return 0;
     {
         ProfScope ps("attn_exact_scores", s);
-        size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 1) + (size_t)A.kv_mul * EX_TILE) *
+        size_t lds = ((size_t)A.kv_mul * A.hd + (size_t)EX_TILE * (A.hd + 8) + (size_t)A.kv_mul * EX_TILE) *
                      sizeof(float);
         rh_launch(attn_exact_scores_kernel, dim3(ntl, A.n_kv, nz), dim3(256), lds, s, A);
         RH_LAUNCH_OK();
@@ -730,12 +731,14 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     {
         ProfScope ps("attn_exact_chain", s);
-        const bool dma = A.vd % 64 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
-                         A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
-                         (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
-        if (dma) {
-            int blocks = A.n_kv * (A.kv_mul * (A.vd / 64) + 1);
-            rh_launch(attn_exact_chain_dma_kernel, dim3(blocks, 1, nz), dim3(64 * CH_WAVES), 0, s, A);
+        // the LDS-fed kernel needs 16-byte rows of 16-dim slices and a ring
+        // that fits the cache (its row offsets are 32-bit)
+        const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
+                        A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
+                        (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
+        if (c4) {
+            const int blocks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
+            rh_launch(attn_exact_chain4_kernel, dim3(blocks, 1, nz), dim3(64 * C4_WAVES), 0, s, A);
         } else {
             rh_launch(attn_exact_chain_kernel, dim3(A.n_heads, (A.vd + 63) / 64, nz), dim3(64), 0, s, A);
         }
