@@ -214,7 +214,7 @@ def measure_prefill(hip, res, toks, cfg, log):
     res.prefill(toks, 0)
     prof = hip.profile_results()
     hip.profile_enable(False)
-    chunk = min(n, 256)
+    chunk = min(n, int(os.environ.get("RUSTY_HIP_PREFILL_CHUNK", "512")))
     tot, cnt = prof.get("pf_gemm_gate_up", (0.0, 0))
     avg_ms = tot / cnt if cnt else float("nan")
     ops = 2.0 * cfg["hidden_dim"] * cfg["dim"] * chunk

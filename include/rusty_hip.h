@@ -191,7 +191,7 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
                                 float repeat_penalty, int32_t *out_tokens, float *logits_out);
 /* forward_prefill_batch (src/model.rs:9917-10090): advances the KV cache over
  * tokens[0..n_tokens) at positions start_pos.. without computing logits, in
- * chunks of up to 256 tokens that run each weight matrix once per chunk on
+ * chunks (512 tokens; RUSTY_HIP_PREFILL_CHUNK, 64..2048) that run each weight matrix once per chunk on
  * the matrix cores.  Needs the device embedding (set_embedding) and a model
  * that standard_prefill_batchable (:9869-9887) accepts: every projection
  * Q4_K or Q6_K, widths multiples of 256, no MoE; returns 0 otherwise (the

@@ -49,6 +49,9 @@ __device__ __forceinline__ uint32_t q6_signed4(uint32_t q) {
     return b | (s << 1) | (s << 2);
 }
 
+// Byte m (< 256) in all four bytes of a dword (one v_perm_b32).
+__device__ __forceinline__ int bcast_byte(int m) { return (int)__builtin_amdgcn_perm(0u, (uint32_t)m, 0u); }
+
 // One block of the lane's weight row, as the lane's MFMA B operands need it
 // (lane half h = lane / 32 takes k = 16h.. of each 32-element Q4_K sub-block,
 // k = 8h.. of each 16-element Q6_K group).
@@ -110,7 +113,7 @@ __device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q4_K> &W, const in
                             (int)(qs.w & 0x0F0F0F0Fu)};
         const rh_v4i bhi = {(int)((qs.x >> 4) & 0x0F0F0F0Fu), (int)((qs.y >> 4) & 0x0F0F0F0Fu),
                             (int)((qs.z >> 4) & 0x0F0F0F0Fu), (int)((qs.w >> 4) & 0x0F0F0F0Fu)};
-        const int mb0 = m0 * 0x01010101, mb1 = m1 * 0x01010101;
+        const int mb0 = bcast_byte(m0), mb1 = bcast_byte(m1);
         const rh_v4i bm0 = {mb0, mb0, mb0, mb0}, bm1 = {mb1, mb1, mb1, mb1};
 #pragma unroll
         for (int tt = 0; tt < NT; tt++) {

@@ -371,6 +371,7 @@ static int grid_cap() { return g.n_cu * 8; }
 // once per kernel instantiation), never more than the tiles need.
 template <class Kern>
 static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
+    // RUSTY_HIP_WG_PER_CU caps the resident workgroups per CU (sweeps)
     static std::map<const void *, int> occ;
     auto it = occ.find((const void *)kernel);
     int per_cu;
@@ -382,6 +383,12 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
     } else {
         per_cu = it->second;
     }
+    static int cap = -1;
+    if (cap < 0) {
+        const char *e = getenv("RUSTY_HIP_WG_PER_CU");
+        cap = e ? atoi(e) : 0;
+    }
+    if (cap > 0) per_cu = std::min(per_cu, cap);
     int need = (n_tiles + waves_per_wg - 1) / waves_per_wg;
     int grid = std::min(need, per_cu * g.n_cu);
     return grid < 1 ? 1 : grid;
@@ -782,16 +789,6 @@ static int quantize_batch_enqueue(const float *x, int ldxf, int T, int K, const 
     return 1;
 }
 
-// RUSTY_HIP_GEMM_NT=1|2 pins the token tile (32 or 64 tokens) for sweeps.
-static int gemm_nt_override() {
-    static int v = -1;
-    if (v < 0) {
-        const char *e = getenv("RUSTY_HIP_GEMM_NT");
-        v = (e && (e[0] == '1' || e[0] == '2')) ? e[0] - '0' : 0;
-    }
-    return v;
-}
-
 // y[t * ldy + r] (=, or += with epi EPI_ADD) row r of W times token t, plus
 // bias[r] when given; rows of one wave tile are 32 weight rows, a workgroup
 // holds 4 tiles and covers 64 tokens.
@@ -813,24 +810,17 @@ static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int
     A.ldy = ldy;
     A.y = y;
     A.bias = bias;
-    // 64 tokens per workgroup where that still gives every SIMD two waves,
-    // else 32
+    // 32 tokens per workgroup: a 64-token tile needs twice the registers
+    // (one wave per SIMD) and measured slower at every size tried
     const int64_t row_tiles = (W.rows + 127) / 128;
-    int nt = gemm_nt_override() ? gemm_nt_override()
-                                : (row_tiles * 4 * ((T + 63) / 64) >= (int64_t)g.n_cu * 8 ? 2 : 1);
-    if (W.fmt == 14) nt = 1;
-    const int tok = 32 * nt;
+    const int tok = 32;
     const dim3 grid((unsigned)row_tiles, (unsigned)((T + tok - 1) / tok));
     const uint32_t lds = 2u * tok * GEMM_XS;
     ProfScope ps(prof_name ? prof_name : (W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma"), s);
-    if (W.fmt == 12) {
-        if (nt == 2)
-            rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 2>, grid, dim3(256), lds, s, A);
-        else
-            rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 1>, grid, dim3(256), lds, s, A);
-    } else {
+    if (W.fmt == 12)
+        rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 1>, grid, dim3(256), lds, s, A);
+    else
         rh_launch(gemm_kq_mfma_kernel<F_Q6_K, 1>, grid, dim3(256), lds, s, A);
-    }
     RH_LAUNCH_OK();
     return 1;
 }
@@ -1892,7 +1882,17 @@ static int r_run(int mode, float penalty) {
 // token's range ends at its own position, which is the sequential order's
 // result exactly.  Every value written is bit-identical to decoding the
 // tokens one by one.
-#define PF_CHUNK 256
+// Tokens per chunk: RUSTY_HIP_PREFILL_CHUNK (64..2048), else 512 (a sweep
+// over 256/512/1024 on a 2048-token prompt put 512 first, by 2-4%).
+static int pf_chunk() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RUSTY_HIP_PREFILL_CHUNK");
+        v = e ? atoi(e) : 512;
+        v = std::max(64, std::min(2048, v));
+    }
+    return v;
+}
 
 static bool r_prefill_enabled() {
     static int on = -1;
@@ -1916,7 +1916,7 @@ static bool r_prefill_batchable() {
 
 static int r_prefill_alloc() {
     if (R.pf_cap) return 1;
-    const size_t C = PF_CHUNK;
+    const size_t C = (size_t)pf_chunk();
     const size_t qd = (size_t)R.n_heads * R.hd, kd = (size_t)R.n_kv * R.hd, vdim = (size_t)R.n_kv * R.vd;
     const size_t attn_cols = (size_t)R.n_heads * R.vd;
     const size_t kmax = std::max<size_t>(std::max<size_t>(R.dim, attn_cols), R.hidden);
