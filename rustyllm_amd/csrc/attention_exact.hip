@@ -211,31 +211,36 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
             }
         }
     }
-    // other heads: dot_f32_avx2 (src/simd.rs:6547-6586): 32 lanes = four
-    // 8-wide accumulators over 32-element chunks, (a0+a1)+(a2+a3), the 8-chunk
-    // tail, hsum_avx, then the scalar tail.
+    // other heads: dot_f32_avx2 (src/simd.rs:6547-6586): four 8-wide
+    // accumulators over 32-element chunks, (a0+a1)+(a2+a3), the 8-chunk tail,
+    // hsum_avx, then the scalar tail.  8 lanes per (head, position), lane l
+    // holding vector lane l of all four accumulators.
     {
         const int ng = kvm - nx4;
         const int pairs = ng * EX_TILE;
-        const int L = lane & 31;
+        const int l = lane & 7;
         const int main32 = hd / 32, tail8 = (hd - main32 * 32) / 8;
-        for (int p0 = wave * 2; p0 < pairs; p0 += 8) {
-            const int p = p0 + (lane >> 5);
+        for (int p0 = wave * 8; p0 < pairs; p0 += 32) {
+            const int p = p0 + (lane >> 3);
             const int tt = p % EX_TILE;
             const bool ok = tt < nt;
             const int g = nx4 + p / EX_TILE;
             const float *qq = s_q + g * hd, *kk = s_k + tt * ldk;
-            float acc = 0.0f;
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
             if (ok)
-                for (int c = 0; c < main32; c++) acc = fmaf(qq[32 * c + L], kk[32 * c + L], acc);
-            float x = acc + __shfl_xor(acc, 8, 64);   // lane l (<8): a0+a1; lane 16+l: a2+a3
-            float y = x + __shfl_xor(x, 16, 64);      // lane l: (a0+a1)+(a2+a3)
-            if (ok && L < 8)
-                for (int i = 0; i < tail8; i++) y = fmaf(qq[32 * main32 + 8 * i + L], kk[32 * main32 + 8 * i + L], y);
+                for (int c = 0; c < main32; c++) {
+                    a0 = fmaf(qq[32 * c + l], kk[32 * c + l], a0);
+                    a1 = fmaf(qq[32 * c + 8 + l], kk[32 * c + 8 + l], a1);
+                    a2 = fmaf(qq[32 * c + 16 + l], kk[32 * c + 16 + l], a2);
+                    a3 = fmaf(qq[32 * c + 24 + l], kk[32 * c + 24 + l], a3);
+                }
+            float y = (a0 + a1) + (a2 + a3);
+            if (ok)
+                for (int i = 0; i < tail8; i++) y = fmaf(qq[32 * main32 + 8 * i + l], kk[32 * main32 + 8 * i + l], y);
             float a = y + __shfl_xor(y, 4, 64);
             float b = a + __shfl_xor(a, 1, 64);
             float d = b + __shfl_xor(b, 2, 64);
-            if (ok && L == 0) {
+            if (ok && l == 0) {
                 for (int c = 32 * main32 + 8 * tail8; c < hd; c++) d += qq[c] * kk[c];
                 s_sc[g * EX_TILE + tt] = d * A.scale;
             }
