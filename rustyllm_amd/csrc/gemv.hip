@@ -749,6 +749,124 @@ __global__ __launch_bounds__(64) void gemv_f32x_kernel(GemvArgs A) {
     }
 }
 
+// MXFP4 rows in dot_mxfp4_f32_scalar's order (src/simd.rs:5886-5902): one
+// running sum per row over the elements in order, each term
+// (lut[nibble] * scale) * x.  The sum is a dependent chain of K adds, so a
+// row is one lane's work; the terms are independent.  A workgroup of five
+// waves serves 64 rows of one matrix: waves 1-4 compute the terms of one
+// 32-element block each (lane = row) into an LDS ring, wave 0 adds them in
+// order (lane = row), eight LDS reads and 32 adds per block.  One barrier per
+// four blocks: the adder reads blocks 4j..4j+3 while the producers write
+// 4j+4..4j+7 into the ring's other half.
+// Barrier that waits only for this wave's LDS operations (global loads stay in
+// flight across it); the asm statements keep the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unrestricted
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Ring layout: slot, row r, then the row's eight 4-term groups with group g
+// stored at g ^ (r % 8), so the adder's 16-byte reads of one group by eight
+// consecutive rows fall in 32 distinct banks.
+__global__ __launch_bounds__(320) void gemv_mxfp4_serial_kernel(GemvArgs A) {
+    extern __shared__ float s_x[];                   // [K]
+    __shared__ __align__(16) float s_t[8][64 * 32];  // [slot][row][8 groups of 4 terms]
+    __shared__ float s_lut[16];
+    const int K = A.K, nb = K >> 5, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = blockIdx.x;
+    int mi = 0;
+#pragma unroll
+    for (int t = 1; t < GEMV_MAX_MATS; t++)
+        if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+    const GemvMat M = mat_sel(A, mi);
+    const float *xs = M.x ? M.x : A.x;
+    if (tid < 16) s_lut[tid] = kMxfp4Lut[tid];
+    for (int i = 4 * tid; i < K; i += 4 * 320) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
+    const uint8_t *w = M.w;
+    const float *bias = M.bias;
+    if (M.sel) {
+        const int64_t e = *M.sel;
+        w += e * M.sel_w;
+        if (bias) bias += e * M.sel_b;
+    }
+    const int row = (tile - M.tile_begin) * 64 + lane;
+    const bool live = row < M.rows;
+    const uint8_t *rp = w + (int64_t)(live ? row : 0) * M.row_stride;
+    const int ngroups = (nb + 3) / 4;
+    // producer wave p = wave - 1 handles blocks 4j + p; each block's bytes
+    // are loaded a group ahead, and the barriers wait only for LDS, so that
+    // load stays in flight across them
+    const int pw = wave - 1;
+    auto load_blk = [&](int b, uint4 &q, uint32_t &e) {
+        const int bb = min(b, nb - 1);  // past the end: a clamped, unused load
+        q = ld16(rp + bb * 17);
+        e = rp[bb * 17 + 16];
+    };
+    auto produce = [&](int b, const uint4 &q, uint32_t e) {
+        if (b >= nb) return;
+        const float sc = mxfp4_scale(e);
+        const float *xb = s_x + b * 32;
+        float *dst = &s_t[b & 7][lane * 32];
+        const int sw = lane & 7;
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t byte = (wd[k] >> (8 * u)) & 0xFFu;
+                t[2 * u] = s_lut[byte & 0xFu] * sc * xb[8 * k + 2 * u];
+                t[2 * u + 1] = s_lut[byte >> 4] * sc * xb[8 * k + 2 * u + 1];
+            }
+            *(float4 *)(dst + 4 * ((2 * k) ^ sw)) = make_float4(t[0], t[1], t[2], t[3]);
+            *(float4 *)(dst + 4 * ((2 * k + 1) ^ sw)) = make_float4(t[4], t[5], t[6], t[7]);
+        }
+    };
+    uint4 qc = make_uint4(0, 0, 0, 0), qn = make_uint4(0, 0, 0, 0);
+    uint32_t ec = 0, en = 0;
+    if (wave > 0) {
+        load_blk(pw, qc, ec);
+        load_blk(4 + pw, qn, en);
+    }
+    __syncthreads();  // x and the LUT staged
+    if (wave > 0) produce(pw, qc, ec);
+    lds_barrier();
+    float sum = 0.0f;
+    for (int j = 0; j < ngroups; j++) {
+        if (wave == 0) {
+            for (int b = 4 * j; b < min(4 * j + 4, nb); b++) {
+                const float *src = &s_t[b & 7][lane * 32];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 v = *(const float4 *)(src + 4 * (k ^ (lane & 7)));
+                    sum += v.x;
+                    sum += v.y;
+                    sum += v.z;
+                    sum += v.w;
+                }
+            }
+        } else if (j + 1 < ngroups) {
+            qc = qn;
+            ec = en;
+            load_blk(4 * (j + 2) + pw, qn, en);
+            produce(4 * (j + 1) + pw, qc, ec);
+        }
+        lds_barrier();
+    }
+    if (wave == 0 && live) {
+        float out = sum;
+        if (bias) out += bias[row];
+        if (A.epi == EPI_ADD)
+            M.y[row] += out;
+        else
+            M.y[row] = out;
+    }
+}
+
 // ---- debug kernels: per-block integer parts (bit-exactness checks) -----------
 // Q4_K: out[row*nb*2 + 2b] = isum, +1 = imin.  Q6_K: out[row*nb + b] = isum.
 // Q8_0: out[row*nb32 + b] = s (int dot of the 32-block).

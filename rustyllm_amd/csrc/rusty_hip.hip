@@ -414,6 +414,14 @@ static int launch_q8i(const GemvArgs &A, hipStream_t s) {
 }
 template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
+    if (FMT == F_MXFP4 && A.K % 4 == 0 && A.K <= 16384) {
+        // one workgroup per 64-row tile: the serial row sums are spread over
+        // a summing wave and four term-producing waves
+        ProfScope ps("gemv_mxfp4", s);
+        rh_launch(gemv_mxfp4_serial_kernel, dim3(A.n_tiles), dim3(320), (uint32_t)(A.K * sizeof(float)), s, A);
+        RH_LAUNCH_OK();
+        return 1;
+    }
     auto kern = gemv_f32x_kernel<FMT>;
     int grid = std::min(A.n_tiles, g.n_cu * 8);
     ProfScope ps("gemv_f32x", s);
