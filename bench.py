@@ -66,6 +66,9 @@ def main():
                     help="prompt length of the batched-prefill measurement (0: skip it)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the batched-prefill measurement and print its JSON object")
+    ap.add_argument("--sweep", action="store_true",
+                    help="run only the isolated kernel sweep (BASELINE configs[1]): batch-1 GEMV per format and "
+                         "shape, and GQA decode attention at ctx 512/4096/32768; prints one JSON object")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy (y = x * 1) over this many MiB, 5 launches, and exit: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -78,6 +81,9 @@ def main():
 
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.sweep:
+        kernel_sweep(args)
         return
 
     import numpy as np
@@ -309,6 +315,81 @@ def measure_prefill(hip, res, toks, cfg, log):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_kquant_swiglu_llama3-8b-q4km_traffic.json")
+
+
+# (block elements, block bytes) per GGML type, and the kernel family that
+# serves a batch-1 GEMV of that type at K % 256 == 0
+SWEEP_FORMATS = {"q8_0": (8, 32, 34, "gemv_q8_0_int"), "q4_k": (12, 256, 144, "gemv_kquant"),
+                 "q6_k": (14, 256, 210, "gemv_kquant"), "mxfp4": (39, 32, 17, "gemv_mxfp4")}
+SWEEP_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+SWEEP_CTX = [512, 4096, 32768]
+COLD_BYTES = 640e6  # rotate inputs over more than the 256 MB memory-side cache + 32 MB of L2
+
+
+def kernel_sweep(args):
+    """Isolated kernel sweep.  Each GEMV streams
+    W ~ N(0, 0.02) quantized by this repo's quantizers, x ~ N(0, 1); x is
+    quantized to Q8_K on the device for Q8_0/Q4_K/Q6_K (all K here are
+    multiples of 256) and stays f32 for MXFP4, as in the reference.  Weights
+    and K/V rotate over enough device copies to exceed the caches.  Time per
+    launch is the dispatch-stamped kernel duration (profile families)."""
+    import numpy as np
+    from rustyllm_amd import hip, synth
+
+    if not hip.available():
+        raise SystemExit("rusty_hip_available() == 0: no gfx950 device")
+    gemv = []
+    for name, (t, be, bb, fam) in SWEEP_FORMATS.items():
+        for n, k in SWEEP_SHAPES:
+            w = synth.normal_quantized(t, args.seed + n + k, n, k, 0.02)
+            x = synth.normal_f32(args.seed + 1, 1, k, 1.0)[0]
+            alg = n * (k // be) * bb + 4 * k + 4 * n
+            copies = int(min(64, max(2, -(-COLD_BYTES // w.nbytes))))
+            iters = max(24, 2 * copies) if w.nbytes < 100e6 else 12
+            hip.bench_matvec(t, w, x, n, k, 2, 2)  # warm: upload, first launches
+            hip.profile_enable(True)
+            y = hip.bench_matvec(t, w, x, n, k, copies, iters)
+            prof = hip.profile_results()
+            hip.profile_enable(False)
+            hip.weight_cache_clear()
+            tot, cnt = prof.get(fam, (0.0, 0))
+            if not cnt or not np.all(np.isfinite(y)):
+                raise SystemExit(f"sweep {name} {n}x{k}: no {fam} launches recorded or non-finite output")
+            us = tot / cnt * 1e3
+            gbs = alg / (us * 1e-6) / 1e9
+            gemv.append({"format": name, "rows": n, "cols": k, "kernel": fam, "alg_bytes": alg,
+                         "avg_launch_us": round(us, 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "launches": cnt, "copies": copies})
+            log(f"gemv {name:5s} {n:6d}x{k:5d}: {us:8.2f} us  {gbs:7.1f} GB/s  frac {gbs / HBM_PEAK_GBS:.3f}")
+    attn = []
+    heads, kv_mul, hd = 32, 4, 128
+    n_kv = heads // kv_mul
+    fams = {"exact": ["attn_exact_scores", "attn_exact_coef", "attn_exact_chain", "attn_exact_finish"],
+            "fast": ["attn_partial", "attn_combine"]}
+    for ctx in SWEEP_CTX:
+        alg = ctx * n_kv * (hd + hd) * 4 + 4 * heads * (hd + hd)
+        copies = int(min(256, max(2, -(-COLD_BYTES // (ctx * n_kv * hd * 8)))))
+        for mode in ("exact", "fast"):
+            iters = max(8, copies) if ctx <= 4096 else 8
+            hip.bench_attention(heads, kv_mul, hd, ctx, 1, 2, args.seed, mode)
+            hip.profile_enable(True)
+            o = hip.bench_attention(heads, kv_mul, hd, ctx, copies, iters, args.seed, mode)
+            prof = hip.profile_results()
+            hip.profile_enable(False)
+            parts = {f: prof[f][0] / prof[f][1] * 1e3 for f in fams[mode] if f in prof and prof[f][1]}
+            if len(parts) != len(fams[mode]) or not np.all(np.isfinite(o)):
+                raise SystemExit(f"sweep attention {mode} ctx {ctx}: missing launches or non-finite output")
+            us = sum(parts.values())
+            gbs = alg / (us * 1e-6) / 1e9
+            attn.append({"mode": mode, "ctx": ctx, "heads": [heads, n_kv], "head_dim": hd, "alg_bytes": alg,
+                         "us_per_call": round(us, 3), "kernel_us": {k: round(v, 3) for k, v in parts.items()},
+                         "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies})
+            log(f"attention {mode:5s} ctx {ctx:6d}: {us:9.2f} us  {gbs:7.1f} GB/s  frac {gbs / HBM_PEAK_GBS:.3f}  "
+                + " ".join(f"{k}={v:.1f}" for k, v in parts.items()))
+    print(json.dumps({"sweep": {"peak_GBps": HBM_PEAK_GBS, "gemv": gemv, "attention": attn,
+                                "workload": "BASELINE configs[1]: batch-1 GEMV per format/shape, GQA decode "
+                                            "attention 32q/8kv/128 (pseudo-normal K/V, linear slots)"}}),
+          flush=True)
 
 
 def recorded_traffic(args):

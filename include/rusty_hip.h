@@ -262,6 +262,20 @@ int rusty_hip_profile_get(int i, char *name, double *total_ms, int64_t *count);
  * two HIP events on the library stream; returns elapsed ms via *ms. */
 int rusty_hip_resident_time_decode(uint32_t n_tokens, float repeat_penalty, double *ms);
 
+/* Kernel sweep (bench only; no reference counterpart: the reference's own
+ * kernel bench, runtime.rs:2639 and :5448-5474, times its CPU kernels).
+ * Each runs `iters` launches on device-resident inputs rotated over `copies`
+ * device copies (so launches stream from HBM, not from caches), recording
+ * kernel durations in the profile families when profiling is on, and returns
+ * the last launch's output.  bench_matvec: y = W x for one GGML type
+ * (x quantized on the device as the reference does).  bench_attention:
+ * decode attention over ctx linear slots of pseudo-normal K/V (head_dim =
+ * value_dim, scale 1/sqrt(head_dim)); mode 0 exact, 1 split-K. */
+int rusty_hip_bench_matvec(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, const float *x,
+                           uintptr_t rows, uintptr_t cols, uint32_t copies, uint32_t iters, float *out);
+int rusty_hip_bench_attention(uint32_t heads, uint32_t kv_mul, uint32_t head_dim, uint32_t ctx, uint32_t copies,
+                              uint32_t iters, uint32_t seed, int mode, float *out);
+
 /* Test hooks (device results of single stages, for bit-exactness checks). */
 int rusty_hip_debug_quantize_q8k(const float *x, uintptr_t n, int8_t *qs, float *d, int16_t *bsums);
 int rusty_hip_debug_dequant(uint32_t ggml_type, const uint8_t *weights, uintptr_t weights_len, uintptr_t rows,

@@ -18,14 +18,19 @@
 namespace rh {
 
 #define ATT_MAX_KVMUL 8
-#define ATT_CHUNK_MAX 256
+#define ATT_TP 64  // positions per sub-tile of a split
+#define ATT_CB 16  // partials a combine lane loads before merging them
+
+// Floats per (split, query head) partial: vd outputs, then m and l, padded so
+// every partial starts 16-byte aligned.
+__host__ __device__ constexpr int att_pstride(int vd) { return vd + 4; }
 
 struct AttnArgs {
     const float *q;       // [n_heads * hd]
     const float *k;       // cache: slot s, kv head h at k + s*key_stride + h*hd
     const float *v;       // cache: v + s*value_stride + h*vd
     const float *sinks;   // [n_heads] or null
-    float *part;          // [n_kv][n_chunks][kv_mul][vd + 2]
+    float *part;          // [n_kv][n_chunks][kv_mul][att_pstride(vd)]
     float *out;           // [n_heads * vd]
     XQ xq;                // optional Q8_K of out (xq.qs == null: skip)
     const StepState *st;  // optional: positions come from the device
@@ -48,200 +53,265 @@ __device__ __forceinline__ void attn_range(const AttnArgs &A, int &start_t, int 
     }
 }
 
-// HD = head dim (key), VD = value dim; both multiples of 4, <= 256.  A chunk
-// of any length is scanned in sub-chunks of ATT_CHUNK_MAX positions with a
-// running max / denominator, so no position is ever dropped.
-template <int HD, int VD, int KVMUL>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs A) {
-    constexpr int LPT = HD / 4;         // lanes per token for the score pass
-    constexpr int TPW = 64 / LPT;       // tokens per wave step (score pass)
-    constexpr int LPV = VD / 4;         // lanes per token for the value pass
-    constexpr int TPV = 64 / LPV;
-    __shared__ float s_p[KVMUL][ATT_CHUNK_MAX];
-    __shared__ float s_o[4][KVMUL][VD];
-    __shared__ float s_run[KVMUL][3];  // running max, running denominator, rescale
+// xor-1 / xor-2 lane exchange inside a quad (DPP quad_perm).
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
 
-    const int c = blockIdx.x, h = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
+// Pass 1: workgroup (split c, kv head h) covers `per` positions (a multiple
+// of ATT_TP) of the range for all KVMUL query heads of h, so every K/V row
+// is read from HBM once per token.  Per sub-tile of ATT_TP positions all of
+// its K and V loads are issued first, each 64-lane load instruction reading
+// whole 128-byte lines (K: 8 lanes per position, 32 positions per pass; V:
+// TV lanes per row), then:
+//   scores: the 8 lanes of a position split the head dim, q from LDS, the
+//           partial dots summed across the 8 lanes;
+//   softmax: tile max per head (wave shuffles + LDS), p = exp(s - m),
+//            running (m, l) rescaled as in online softmax;
+//   values: acc[g] += p * v with p broadcast from LDS.
+// Outputs (m, l, o) per head; the combine merges the splits.
+template <int HD, int KVMUL>
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs A) {
+    constexpr int KF = HD / 32;        // float4 of a K row per lane (8 lanes per row)
+    constexpr int NP = ATT_TP / 32;    // K passes (32 positions each)
+    constexpr int QS = 4 * KF + 4;     // LDS stride of a lane's q slice (padded: slices hit distinct banks)
+    constexpr int TV = HD / 4;         // threads per V row
+    constexpr int PG = 256 / TV;       // V position groups
+    constexpr int PPG = ATT_TP / PG;   // positions per V group
+    constexpr int PS = att_pstride(HD);
+    __shared__ __align__(16) float s_q[KVMUL][8][QS];
+    __shared__ float s_p[KVMUL][ATT_TP];
+    __shared__ float s_mx[4][KVMUL], s_sm[4][KVMUL];
+    __shared__ __align__(16) float s_o[4][KVMUL][HD];
+
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int start_t, end_t;
     attn_range(A, start_t, end_t);
     const int ctx = end_t - start_t + 1;
-    int chunk = (ctx + A.n_chunks - 1) / A.n_chunks;
-    if (chunk < 16) chunk = 16;
-    const int t0 = start_t + c * chunk;
-    const int t1 = min(end_t + 1, t0 + chunk);
-    float *part = A.part + ((size_t)h * A.n_chunks + c) * KVMUL * (VD + 2);
+    const int per = ((ctx + A.n_chunks - 1) / A.n_chunks + ATT_TP - 1) / ATT_TP * ATT_TP;
+    const int t0 = c * per, t1 = min(ctx, t0 + per);  // positions relative to start_t
+    float *part = A.part + ((size_t)h * A.n_chunks + c) * KVMUL * PS;
     if (ctx <= 0 || t0 >= t1) {
-        if (tid < KVMUL) {
-            part[tid * (VD + 2) + VD] = -INFINITY;
-            part[tid * (VD + 2) + VD + 1] = 0.0f;
-        }
+        for (int i = tid; i < KVMUL * PS; i += 256) part[i] = (i % PS) == HD ? -INFINITY : 0.0f;
         return;
     }
-
-    const int sub = lane / LPT, dl = lane % LPT;
-    const int vsub = lane / LPV, vl = lane % LPV;
-    float4 qv[KVMUL];
-#pragma unroll
-    for (int g = 0; g < KVMUL; g++) qv[g] = *(const float4 *)(A.q + (size_t)(h * KVMUL + g) * HD + dl * 4);
+    // lane j8 of a position holds dims (8i + j8)*4 .. +3, i < KF
+    for (int i = tid; i < KVMUL * HD; i += 256) {
+        const int g = i / HD, d = i % HD, f = d >> 2;
+        s_q[g][f & 7][4 * (f >> 3) + (d & 3)] = A.q[(size_t)(h * KVMUL + g) * HD + d];
+    }
+    const int pk = tid >> 3, j8 = tid & 7;    // score pass: position within a pass, lane of the position
+    const int d4 = tid % TV, pg = tid / TV;   // value pass: float4 column, position group
+    const float *kb = A.k + (size_t)h * HD + 4 * j8;
+    const float *vb = A.v + (size_t)h * HD + d4 * 4;
+    float m_run[KVMUL], l_run[KVMUL];
     float4 acc[KVMUL];
 #pragma unroll
-    for (int g = 0; g < KVMUL; g++) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < KVMUL) {
-        s_run[tid][0] = -INFINITY;
-        s_run[tid][1] = 0.0f;
+    for (int g = 0; g < KVMUL; g++) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.0f;
+        acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-
-    for (int s0 = t0; s0 < t1; s0 += ATT_CHUNK_MAX) {
-        const int n = min(ATT_CHUNK_MAX, t1 - s0);
-        // ---- scores ----------------------------------------------------------
-        for (int base = wave * TPW; base < n; base += 4 * TPW) {
-            int tl = base + sub;
-            bool ok = tl < n;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (ok) {
-                int slot = (s0 + tl) % A.slot_count;
-                kv = *(const float4 *)(A.k + (size_t)slot * A.key_stride + (size_t)h * HD + dl * 4);
-            }
-            float dot[KVMUL];
+    __syncthreads();
+    for (int s0 = t0; s0 < t1; s0 += ATT_TP) {
+        float4 kr[NP][KF], vr[PPG];
 #pragma unroll
-            for (int g = 0; g < KVMUL; g++) {
-                float d = qv[g].x * kv.x;
-                d = fmaf(qv[g].y, kv.y, d);
-                d = fmaf(qv[g].z, kv.z, d);
-                d = fmaf(qv[g].w, kv.w, d);
-                if (LPT >= 2) d += swz_xor<1>(d);
-                if (LPT >= 4) d += swz_xor<2>(d);
-                if (LPT >= 8) d += swz_xor<4>(d);
-                if (LPT >= 16) d += swz_xor<8>(d);
-                if (LPT >= 32) d += swz_xor<16>(d);
-                if (LPT >= 64) d += __shfl_xor(d, 32, 64);
-                dot[g] = d;
-            }
-            if (ok && dl == 0) {
+        for (int r = 0; r < NP; r++) {
+            const int slot = (start_t + min(s0 + 32 * r + pk, t1 - 1)) % A.slot_count;
+            const float *kp = kb + (size_t)slot * A.key_stride;
 #pragma unroll
-                for (int g = 0; g < KVMUL; g++) s_p[g][tl] = dot[g] * A.scale;
-            }
+            for (int i = 0; i < KF; i++) kr[r][i] = *(const float4 *)(kp + 32 * i);
         }
-        __syncthreads();
-        // ---- running softmax statistics, one wave per head -----------------
-        for (int g = wave; g < KVMUL; g += 4) {
-            float m = -INFINITY;
-            for (int i = lane; i < n; i += 64) m = fmaxf(m, s_p[g][i]);
-            m = wave_max(m);
-            float m_old = s_run[g][0];
-            float m_new = fmaxf(m_old, m);
-            float l = 0.0f;
-            for (int i = lane; i < n; i += 64) {
-                float p = expf(s_p[g][i] - m_new);
-                s_p[g][i] = p;
-                l += p;
-            }
-            l = wave_sum(l);
-            if (lane == 0) {
-                float alpha = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
-                s_run[g][0] = m_new;
-                s_run[g][1] = s_run[g][1] * alpha + l;
-                s_run[g][2] = alpha;
-            }
+#pragma unroll
+        for (int i = 0; i < PPG; i++) {
+            const int sl = (start_t + min(s0 + pg * PPG + i, t1 - 1)) % A.slot_count;
+            vr[i] = *(const float4 *)(vb + (size_t)sl * A.value_stride);
         }
-        __syncthreads();
-        // ---- weighted values --------------------------------------------------
+        float sc[NP][KVMUL], tmx[KVMUL];
 #pragma unroll
         for (int g = 0; g < KVMUL; g++) {
-            float al = s_run[g][2];
-            acc[g].x *= al;
-            acc[g].y *= al;
-            acc[g].z *= al;
-            acc[g].w *= al;
-        }
-        for (int base = wave * TPV; base < n; base += 4 * TPV) {
-            int tl = base + vsub;
-            if (tl < n) {
-                int slot = (s0 + tl) % A.slot_count;
-                float4 vv = *(const float4 *)(A.v + (size_t)slot * A.value_stride + (size_t)h * VD + vl * 4);
+            float m = -INFINITY;
 #pragma unroll
-                for (int g = 0; g < KVMUL; g++) {
-                    float p = s_p[g][tl];
-                    acc[g].x = fmaf(p, vv.x, acc[g].x);
-                    acc[g].y = fmaf(p, vv.y, acc[g].y);
-                    acc[g].z = fmaf(p, vv.z, acc[g].z);
-                    acc[g].w = fmaf(p, vv.w, acc[g].w);
+            for (int r = 0; r < NP; r++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < KF; i++) {
+                    const float4 qv = *(const float4 *)&s_q[g][j8][4 * i];
+                    d = fmaf(qv.x, kr[r][i].x, d);
+                    d = fmaf(qv.y, kr[r][i].y, d);
+                    d = fmaf(qv.z, kr[r][i].z, d);
+                    d = fmaf(qv.w, kr[r][i].w, d);
                 }
+                d += quad_xor1(d);
+                d += quad_xor2(d);
+                d += __shfl_xor(d, 4, 64);
+                sc[r][g] = (s0 + 32 * r + pk < t1) ? d * A.scale : -INFINITY;
+                m = fmaxf(m, sc[r][g]);
+            }
+            m = fmaxf(m, __shfl_xor(m, 8, 64));
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            tmx[g] = m;
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int g = 0; g < KVMUL; g++) s_mx[wave][g] = tmx[g];
+        __syncthreads();
+        float alpha[KVMUL], psum[KVMUL];
+#pragma unroll
+        for (int g = 0; g < KVMUL; g++) {
+            const float t = fmaxf(fmaxf(s_mx[0][g], s_mx[1][g]), fmaxf(s_mx[2][g], s_mx[3][g]));
+            const float mn = fmaxf(m_run[g], t);
+            alpha[g] = m_run[g] == -INFINITY ? 0.0f : __expf(m_run[g] - mn);
+            m_run[g] = mn;
+            float v = 0.0f;
+#pragma unroll
+            for (int r = 0; r < NP; r++) {
+                const float pe = sc[r][g] == -INFINITY ? 0.0f : __expf(sc[r][g] - mn);
+                if ((g & 7) == j8) s_p[g][32 * r + pk] = pe;
+                v += j8 == 0 ? pe : 0.0f;
+            }
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            psum[g] = v;
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int g = 0; g < KVMUL; g++) s_sm[wave][g] = psum[g];
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < KVMUL; g++) {
+            l_run[g] = l_run[g] * alpha[g] + ((s_sm[0][g] + s_sm[1][g]) + (s_sm[2][g] + s_sm[3][g]));
+            acc[g].x *= alpha[g];
+            acc[g].y *= alpha[g];
+            acc[g].z *= alpha[g];
+            acc[g].w *= alpha[g];
+        }
+#pragma unroll
+        for (int i = 0; i < PPG; i++) {
+            const int pos = pg * PPG + i;
+#pragma unroll
+            for (int g = 0; g < KVMUL; g++) {
+                const float pp = s_p[g][pos];
+                acc[g].x = fmaf(pp, vr[i].x, acc[g].x);
+                acc[g].y = fmaf(pp, vr[i].y, acc[g].y);
+                acc[g].z = fmaf(pp, vr[i].z, acc[g].z);
+                acc[g].w = fmaf(pp, vr[i].w, acc[g].w);
             }
         }
-        __syncthreads();
+        __syncthreads();  // s_p, s_mx and s_sm are rewritten by the next sub-tile
     }
-    // fold the TPV token groups of each wave, then the four waves
+    // fold the position groups: inside the wave, then the four waves
 #pragma unroll
     for (int g = 0; g < KVMUL; g++) {
-        for (int o = LPV; o < 64; o <<= 1) {
+        for (int o = TV; o < 64; o <<= 1) {
             acc[g].x += __shfl_xor(acc[g].x, o, 64);
             acc[g].y += __shfl_xor(acc[g].y, o, 64);
             acc[g].z += __shfl_xor(acc[g].z, o, 64);
             acc[g].w += __shfl_xor(acc[g].w, o, 64);
         }
-        if (vsub == 0) *(float4 *)&s_o[wave][g][vl * 4] = acc[g];
+        if (lane < TV) *(float4 *)&s_o[wave][g][4 * d4] = acc[g];
     }
     __syncthreads();
-    for (int i = tid; i < KVMUL * VD; i += 256) {
-        int g = i / VD, d = i % VD;
-        float o = (s_o[0][g][d] + s_o[1][g][d]) + (s_o[2][g][d] + s_o[3][g][d]);
-        part[g * (VD + 2) + d] = o;
+    for (int i = tid; i < KVMUL * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        part[g * PS + d] = (s_o[0][g][d] + s_o[1][g][d]) + (s_o[2][g][d] + s_o[3][g][d]);
     }
     if (tid < KVMUL) {
-        part[tid * (VD + 2) + VD] = s_run[tid][0];
-        part[tid * (VD + 2) + VD + 1] = s_run[tid][1];
+        part[tid * PS + HD] = m_run[tid];
+        part[tid * PS + HD + 1] = l_run[tid];
     }
 }
 
-// One workgroup per 256 output elements (a Q8_K block); thread = element.
+// Online merge of one partial (m, l, o) into (M, L, acc).
+__device__ __forceinline__ void att_merge(float &M, float &L, float4 &acc, float m, float l, float4 o) {
+    if (m == -INFINITY) return;
+    const float mn = fmaxf(M, m);
+    const float a = M == -INFINITY ? 0.0f : __expf(M - mn);
+    const float b = __expf(m - mn);
+    L = L * a + l * b;
+    acc.x = acc.x * a + o.x * b;
+    acc.y = acc.y * a + o.y * b;
+    acc.z = acc.z * a + o.z * b;
+    acc.w = acc.w * a + o.w * b;
+    M = mn;
+}
+
+// Pass 2: one workgroup per 256 outputs (a Q8_K block), lane = four outputs
+// of one head, wave w = the splits c = w mod 4 (ATT_CB partials in flight per
+// lane), then the four waves merged through LDS, the sink logit joining as a
+// partial with l = 1 and a zero value row (model.rs:5754-5755).  Wave 0
+// writes the f32 outputs and, when requested, their Q8_K quantization.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs A) {
-    __shared__ float red[4];
-    const int e = blockIdx.x * 256 + threadIdx.x;
-    const int total = A.n_heads * A.vd;
-    float o = 0.0f;
-    if (e < total) {
-        int head = e / A.vd, d = e % A.vd;
-        int h = head / A.kv_mul, g = head % A.kv_mul;
-        const float *p0 = A.part + (size_t)h * A.n_chunks * A.kv_mul * (A.vd + 2) + (size_t)g * (A.vd + 2);
-        const size_t cstride = (size_t)A.kv_mul * (A.vd + 2);
-        float M = A.sinks ? A.sinks[head] : -INFINITY;
-        for (int c = 0; c < A.n_chunks; c++) M = fmaxf(M, p0[c * cstride + A.vd]);
-        float L = A.sinks ? expf(A.sinks[head] - M) : 0.0f;
-        float acc = 0.0f;
-        if (M != -INFINITY) {
-            for (int c = 0; c < A.n_chunks; c++) {
-                const float *pc = p0 + c * cstride;
-                float l = pc[A.vd + 1];
-                if (l > 0.0f) {
-                    float w = expf(pc[A.vd] - M);
-                    L = fmaf(w, l, L);
-                    acc = fmaf(w, pc[d], acc);
-                }
-            }
-        }
-        o = L > 0.0f ? acc / L : 0.0f;
-        A.out[e] = o;
+    __shared__ float s_m[4][64], s_l[4][64];
+    __shared__ float4 s_a[4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int total = A.n_heads * A.vd, PS = att_pstride(A.vd);
+    const int e0 = blockIdx.x * 256 + 4 * lane;
+    const bool ok = e0 < total;
+    const int head = ok ? e0 / A.vd : 0, d = e0 % A.vd;
+    const int h = head / A.kv_mul, g = head % A.kv_mul;
+    const size_t cst = (size_t)A.kv_mul * PS;
+    const float *p0 = A.part + (size_t)h * A.n_chunks * cst + (size_t)g * PS;
+    float M = -INFINITY, L = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (wave == 0 && A.sinks && ok) {
+        M = A.sinks[head];
+        L = 1.0f;
     }
+    for (int base = wave; base < A.n_chunks; base += 4 * ATT_CB) {
+        float mm[ATT_CB], ll[ATT_CB];
+        float4 oo[ATT_CB];
+#pragma unroll
+        for (int k = 0; k < ATT_CB; k++) {
+            const int cc = min(base + 4 * k, A.n_chunks - 1);
+            const float *pc = p0 + cc * cst;
+            mm[k] = pc[A.vd];
+            ll[k] = pc[A.vd + 1];
+            oo[k] = *(const float4 *)(pc + d);
+        }
+#pragma unroll
+        for (int k = 0; k < ATT_CB; k++)
+            if (base + 4 * k < A.n_chunks) att_merge(M, L, acc, mm[k], ll[k], oo[k]);
+    }
+    s_m[wave][lane] = M;
+    s_l[wave][lane] = L;
+    s_a[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < 4; w++) att_merge(M, L, acc, s_m[w][lane], s_l[w][lane], s_a[w][lane]);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (L > 0.0f) {
+        const float inv = 1.0f / L;
+        o = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
+    if (ok) *(float4 *)(A.out + e0) = o;
     if (A.xq.qs == nullptr) return;
     // Q8_K of this 256-block (total is a multiple of 256 when requested)
-    float amax = block_max_256(fabsf(o), red);
-    float dsc = amax * (1.0f / 127.0f);
-    float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-    int q = (int)__builtin_rintf(o * id);
-    q = max(-128, min(127, q));
-    A.xq.qs[e] = (int8_t)q;
-    if (threadIdx.x == 0) A.xq.d[blockIdx.x] = dsc;
-    int s = q;
+    const float amax = wave_max(fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+    const float ov[4] = {o.x, o.y, o.z, o.w};
+    int qv[4], s = 0;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        qv[i] = max(-128, min(127, (int)__builtin_rintf(ov[i] * id)));
+        s += qv[i];
+        packed |= (uint32_t)(qv[i] & 0xFF) << (8 * i);
+    }
+    *(uint32_t *)(A.xq.qs + e0) = packed;
+    if (lane == 0) A.xq.d[blockIdx.x] = amax * (1.0f / 127.0f);
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
+    if ((lane & 3) == 0) A.xq.sums16[e0 >> 4] = (int16_t)s;
     s += __shfl_xor(s, 4, 64);
-    s += __shfl_xor(s, 8, 64);
-    if ((threadIdx.x & 15) == 0) A.xq.sums16[e >> 4] = (int16_t)s;
-    s += __shfl_xor(s, 16, 64);
-    if ((threadIdx.x & 31) == 0) A.xq.bsums[e >> 5] = (int16_t)s;
+    if ((lane & 7) == 0) A.xq.bsums[e0 >> 5] = (int16_t)s;
 }
 
 }  // namespace rh

@@ -358,10 +358,10 @@ enum Cat { CAT_KQ = 1, CAT_Q8I = 2, CAT_F32 = 3 };
 static int cat_of(int fmt, int K) {
     if (fmt == 12 || fmt == 14) return K % 256 == 0 && K <= KMAX ? CAT_KQ : 0;
     if (fmt == 8) {
-        if (K % 256 == 0 && K <= 8192) return CAT_Q8I;
+        if (K % 256 == 0 && K <= KMAX) return CAT_Q8I;
         return K % 32 == 0 && K <= 12288 ? CAT_F32 : 0;
     }
-    if (fmt == 39) return K % 32 == 0 && K <= 12288 ? CAT_F32 : 0;
+    if (fmt == 39) return K % 32 == 0 && K <= KMAX ? CAT_F32 : 0;
     return 0;
 }
 
@@ -543,6 +543,8 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
         case 2: return launch_q8i<2, 2>(A, s);
         case 3: return launch_q8i<3, 1>(A, s);
         case 4: return launch_q8i<4, 1>(A, s);
+        case 6: return launch_q8i<6, 1>(A, s);
+        case 8: return launch_q8i<8, 1>(A, s);
         default: return 0;
         }
     }
@@ -661,7 +663,7 @@ static int attn_launch(const AttnArgs &A, hipStream_t s) {
         ProfScope ps("attn_partial", s);
 #define RH_ATT(HD, KM)                                                                            \
     if (A.hd == HD && A.vd == HD && A.kv_mul == KM) {                                            \
-        rh_launch((attn_partial_kernel<HD, HD, KM>), grid, dim3(256), 0, s, A);          \
+        rh_launch((attn_partial_kernel<HD, KM>), grid, dim3(256), 0, s, A);              \
         goto launched;                                                                            \
     }
         RH_ATT(128, 1) RH_ATT(128, 2) RH_ATT(128, 4) RH_ATT(128, 5) RH_ATT(128, 6) RH_ATT(128, 8)
@@ -683,9 +685,11 @@ static bool attn_supported(int hd, int vd, int kv_mul) {
     return hd == vd && (hd == 64 || hd == 128) &&
            (kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 5 || kv_mul == 6 || kv_mul == 8);
 }
+// Splits per kv head: up to four workgroups per CU (the partial kernel's
+// occupancy), each at least one ATT_TP-position sub-tile.
 static int attn_chunks(int n_kv, int max_ctx) {
-    int want = (2 * g.n_cu + n_kv - 1) / n_kv;
-    int by_ctx = (max_ctx + 15) / 16;
+    int want = (4 * g.n_cu + n_kv - 1) / n_kv;
+    int by_ctx = (max_ctx + ATT_TP - 1) / ATT_TP;
     int c = std::min(want, by_ctx);
     return c < 1 ? 1 : c;
 }
@@ -1200,7 +1204,7 @@ int rusty_hip_attention(const float *query, uintptr_t query_len, const float *ke
     A.n_chunks = attn_chunks((int)n_kv, (int)(end_t - start_t + 1));
     A.scale = scale;
     if (attn_fast_mode()) {
-        if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * (value_dim + 2))) return 0;
+        if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * att_pstride((int)value_dim))) return 0;
         A.part = g.part;
         if (!attn_launch(A, g.s)) return 0;
     } else {
@@ -2116,7 +2120,7 @@ static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n
             return 0;
     }
     R.n_chunks = attn_chunks((int)n_kv_heads, (int)storage_len);
-    if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * (value_dim + 2) * 4))
+    if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * att_pstride((int)value_dim) * 4))
         return 0;
     R.ex_cap = (int)((storage_len + 63) / 64 * 64);
     if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_kv_heads, (int)(n_heads / n_kv_heads), R.ex_cap) * 4)) return 0;
@@ -2511,6 +2515,148 @@ int rusty_hip_kquant_matvec_batch(uint32_t kind, const uint8_t *w, uintptr_t w_l
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
     return 1;
+}
+
+
+// ---- kernel sweep (bench.py --sweep) ------------------------------------------------
+// Both exports time kernels on device-resident inputs: nothing crosses PCIe
+// inside the loop, and the inputs rotate over `copies` device copies so a
+// launch streams from HBM rather than from the caches a previous launch
+// filled.  Kernel durations are recorded by the profile (its families) when
+// profiling is on; the result of the last launch is returned.
+
+// iters GEMV launches y = W x (x quantized to Q8_K once, on the device, where
+// the reference quantizes it).
+int rusty_hip_bench_matvec(uint32_t t, const uint8_t *w, uintptr_t wl, const float *x, uintptr_t rows, uintptr_t cols,
+                           uint32_t copies, uint32_t iters, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !w || !x || !out || rows == 0 || cols == 0 || copies == 0 || copies > 64 || iters == 0)
+        return 0;
+    const int fmt = dt_to_fmt(t);
+    const int cat = fmt > 0 ? cat_of(fmt, (int)cols) : 0;
+    if (!cat) return 0;
+    DevW W;
+    if (!get_weight(w, wl, (int64_t)rows, (int64_t)cols, fmt, &W)) return 0;
+    const size_t bytes = (size_t)W.rows * W.stride;
+    std::vector<uint8_t *> cp(copies, nullptr);
+    cp[0] = (uint8_t *)W.p;
+    int ok = 1;
+    for (uint32_t i = 1; i < copies && ok; i++) {
+        if (hipMalloc((void **)&cp[i], bytes) != hipSuccess ||
+            hipMemcpyAsync(cp[i], W.p, bytes, hipMemcpyDeviceToDevice, g.s) != hipSuccess)
+            ok = 0;
+    }
+    if (ok) ok = stage_x(x, cols) && ensure(&g.y, &g.y_cap, rows);
+    ActSpec act = act_xq(XQ{}, g.x);  // g.x as staged above
+    if (ok && (cat == CAT_KQ || cat == CAT_Q8I)) {
+        ok = ensure_xq(&g.xq, &g.xq_cap, cols) && launch_quant(g.x, (int)cols, g.xq, g.s);
+        act = act_xq(g.xq, g.x);
+    }
+    for (uint32_t i = 0; i < iters && ok; i++) {
+        DevW Wi = W;
+        Wi.p = cp[i % copies];
+        MatSpec m = {Wi, g.y, nullptr};
+        ok = gemv_cat(&m, 1, (int)cols, EPI_STORE, act, g.s);
+    }
+    if (ok) ok = hipMemcpyAsync(out, g.y, rows * 4, hipMemcpyDeviceToHost, g.s) == hipSuccess;
+    (void)hipStreamSynchronize(g.s);
+    for (uint32_t i = 1; i < copies; i++)
+        if (cp[i]) (void)hipFree(cp[i]);
+    prof_drain();
+    return ok;
+}
+
+// Pseudo-normal fill (sum of four hashed uniforms, variance 1) for the
+// attention sweep's K, V and q.
+__global__ void bench_fill_kernel(float *p, size_t n, uint32_t seed) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t h = (uint32_t)i * 0x9E3779B1u ^ (seed + 0x85EBCA77u * (uint32_t)(k + 1)) ^ (uint32_t)(i >> 32);
+            h ^= h >> 16;
+            h *= 0x7FEB352Du;
+            h ^= h >> 15;
+            h *= 0x846CA68Bu;
+            h ^= h >> 16;
+            acc += (float)(h >> 8) * (1.0f / 16777216.0f);
+        }
+        p[i] = (acc - 2.0f) * 1.7320508f;
+    }
+}
+
+// iters decode-attention launches: heads query heads over kv_mul-way grouped
+// K/V of ctx positions (linear slots), head_dim = value_dim, scale
+// 1/sqrt(head_dim); mode 0 = the exact kernels, 1 = split-K.  out receives
+// the last launch's heads*head_dim outputs.
+int rusty_hip_bench_attention(uint32_t heads, uint32_t kv_mul, uint32_t head_dim, uint32_t ctx, uint32_t copies,
+                              uint32_t iters, uint32_t seed, int mode, float *out) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !out || heads == 0 || kv_mul == 0 || heads % kv_mul != 0 || ctx == 0 || copies == 0 ||
+        copies > 256 || iters == 0 || !attn_supported((int)head_dim, (int)head_dim, (int)kv_mul))
+        return 0;
+    const int n_kv = (int)(heads / kv_mul), hd = (int)head_dim;
+    const size_t per = (size_t)ctx * n_kv * hd;  // floats of K (and of V) per copy
+    const size_t qn = (size_t)heads * hd;
+    float *kv = nullptr;
+    if (hipMalloc((void **)&kv, (2 * per * copies + qn) * sizeof(float)) != hipSuccess) return 0;
+    float *q = kv + 2 * per * copies;
+    int ok = 1;
+    rh_launch(bench_fill_kernel, dim3(2048), dim3(256), 0, g.s, kv, 2 * per * copies + qn, seed);
+    if (hipGetLastError() != hipSuccess) ok = 0;
+    if (ok) ok = ensure(&g.y, &g.y_cap, qn);
+    if (ok && mode == 1) {
+        const int chunks = attn_chunks(n_kv, (int)ctx);
+        ok = ensure(&g.part, &g.part_cap, (size_t)n_kv * chunks * kv_mul * att_pstride((int)head_dim));
+    }
+    const int cap = (int)((ctx + 63) / 64 * 64);
+    if (ok && mode == 0) ok = ensure(&g.ex, &g.ex_cap, exact_scratch_floats(n_kv, (int)kv_mul, cap));
+    for (uint32_t i = 0; i < iters && ok; i++) {
+        const float *k = kv + 2 * per * (i % copies), *v = k + per;
+        if (mode == 1) {
+            AttnArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = q;
+            A.k = k;
+            A.v = v;
+            A.part = g.part;
+            A.out = g.y;
+            A.n_heads = (int)heads;
+            A.n_kv = n_kv;
+            A.kv_mul = (int)kv_mul;
+            A.hd = A.vd = hd;
+            A.key_stride = A.value_stride = (int64_t)n_kv * hd;
+            A.slot_count = (int)ctx;
+            A.start_t = 0;
+            A.end_t = (int)ctx - 1;
+            A.n_chunks = attn_chunks(n_kv, (int)ctx);
+            A.scale = 1.0f / sqrtf((float)hd);
+            ok = attn_launch(A, g.s);
+        } else {
+            AttnExactArgs E;
+            memset(&E, 0, sizeof(E));
+            E.q = q;
+            E.k = k;
+            E.v = v;
+            E.out = g.y;
+            E.n_heads = (int)heads;
+            E.n_kv = n_kv;
+            E.kv_mul = (int)kv_mul;
+            E.hd = E.vd = hd;
+            E.key_stride = E.value_stride = (int64_t)n_kv * hd;
+            E.slot_count = (int)ctx;
+            E.start_t = 0;
+            E.end_t = (int)ctx - 1;
+            E.cap = cap;
+            E.scale = 1.0f / sqrtf((float)hd);
+            ok = attn_exact_launch(E, g.ex, XQ{}, g.s);
+        }
+    }
+    if (ok) ok = hipMemcpyAsync(out, g.y, qn * 4, hipMemcpyDeviceToHost, g.s) == hipSuccess;
+    (void)hipStreamSynchronize(g.s);
+    (void)hipFree(kv);
+    prof_drain();
+    return ok;
 }
 
 }  // extern "C"

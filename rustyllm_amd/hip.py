@@ -32,7 +32,8 @@ SYMBOLS = [
     "rusty_hip_debug_rmsnorm", "rusty_hip_debug_silu_mul", "rusty_hip_debug_rope", "rusty_hip_debug_greedy",
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
-    "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill",
+    "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
+    "rusty_hip_bench_attention",
 ]
 
 
@@ -92,6 +93,8 @@ _sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32,
 _sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
 _sig("rusty_hip_kquant_matvec_batch", _i, _u32, _p, _u, _u, _u, _p, _u, _p, _u)
 _sig("rusty_hip_resident_prefill", _i, _p, _u32, _u32)
+_sig("rusty_hip_bench_matvec", _i, _u32, _p, _u, _p, _u, _u, _u32, _u32, _p)
+_sig("rusty_hip_bench_attention", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i, _p)
 _sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
      _p, _p)
 
@@ -422,6 +425,28 @@ def profile_results():
     while lib.rusty_hip_profile_get(i, name, C.byref(tot), C.byref(cnt)) == 1:
         out[name.value.decode()] = (tot.value, cnt.value)
         i += 1
+    return out
+
+
+def bench_matvec(ggml_type: int, weights: np.ndarray, x: np.ndarray, rows: int, cols: int, copies: int,
+                 iters: int) -> np.ndarray:
+    """iters device-resident GEMV launches over `copies` rotated weight copies
+    (kernel sweep); returns the last output.  Durations land in the profile."""
+    w, x = _u8(weights), _f32(x)
+    out = np.empty(rows, np.float32)
+    if lib.rusty_hip_bench_matvec(ggml_type, _ptr(w), w.nbytes, _ptr(x), rows, cols, copies, iters, _ptr(out)) != 1:
+        raise RuntimeError("rusty_hip_bench_matvec failed")
+    return out
+
+
+def bench_attention(heads: int, kv_mul: int, head_dim: int, ctx: int, copies: int, iters: int, seed: int,
+                    mode: str = "exact") -> np.ndarray:
+    """iters decode-attention launches over `copies` rotated device K/V sets
+    of ctx positions (kernel sweep); returns the last output."""
+    out = np.empty(heads * head_dim, np.float32)
+    code = {"exact": 0, "fast": 1}[mode]
+    if lib.rusty_hip_bench_attention(heads, kv_mul, head_dim, ctx, copies, iters, seed, code, _ptr(out)) != 1:
+        raise RuntimeError("rusty_hip_bench_attention failed")
     return out
 
 

@@ -112,7 +112,8 @@ def test_block_ints_random(hip, t):
 
 
 BIT_EXACT_SHAPES = [(12, 33, 512), (12, 4096, 4096), (12, 1024, 14336), (14, 1024, 4096), (14, 513, 14336),
-                    (14, 300, 5120), (12, 300, 13824), (8, 2048, 2048), (8, 256, 5632), (8, 77, 4096)]
+                    (14, 300, 5120), (12, 300, 13824), (8, 2048, 2048), (8, 256, 5632), (8, 77, 4096),
+                    (8, 129, 8192), (8, 300, 14336)]
 
 
 @pytest.mark.parametrize("t,rows,cols", BIT_EXACT_SHAPES)
@@ -125,7 +126,8 @@ def test_gemv_bit_exact(hip, t, rows, cols):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), np.max(np.abs(out - ref))
 
 
-@pytest.mark.parametrize("t,rows,cols", [(39, 2880, 2880), (39, 513, 4096), (39, 70, 96), (8, 4096, 2880),
+@pytest.mark.parametrize("t,rows,cols", [(39, 2880, 2880), (39, 513, 4096), (39, 200, 14336), (39, 70, 96),
+                                         (8, 4096, 2880),
                                          (8, 201, 2880), (8, 9, 160)])
 def test_gemv_f32_paths_bit_exact(hip, t, rows, cols):
     """f32-activation rows (MXFP4 always; Q8_0 when K % 256 != 0) in the
