@@ -44,9 +44,16 @@ struct GemvMat {
 
 #define GEMV_MAX_MATS 8
 
-// The Q8_K activation a launch consumes is always prepared by a standalone
-// kernel (host ActSpec); building it inside every GEMV workgroup was measured
-// slower (each workgroup repeats the work ahead of its first tile).
+// Where a K-quant launch's Q8_K activation comes from.  KQ_ACT_XQ: a Q8_K
+// vector in memory (xq).  The others build it in every workgroup's prologue,
+// from f32 data, while the first tiles' weights are in flight, which saves
+// the standalone kernel (and its launch) that would otherwise produce it:
+//   KQ_ACT_NORM: RMSNorm of act_x with act_w (rms_norm_into), then Q8_K;
+//   KQ_ACT_DEN:  attention normalisation act_x[e] * (1/act_den[e/act_group])
+//                where the denominator is positive, then Q8_K.
+enum KqAct : int { KQ_ACT_XQ = 0, KQ_ACT_NORM = 1, KQ_ACT_DEN = 2 };
+#define KQ_ACT_KMAX 4096  // widest activation a prologue builds: one 16-element chunk per thread
+
 struct GemvArgs {
     GemvMat m[GEMV_MAX_MATS];
     int32_t n_mats;
@@ -56,6 +63,13 @@ struct GemvArgs {
     int32_t tile_rows;  // K-quant kernel: rows per wave tile (per matrix for SWIGLU)
     XQ xq;              // Q8_K activation (int paths)
     const float *x;     // f32 activation (f32 paths)
+    // K-quant prologue activation (KqAct != KQ_ACT_XQ)
+    const float *act_x;
+    const float *act_w;
+    const float *act_den;
+    float act_eps;
+    int32_t act_group;
+    int32_t act_store;  // prologue modes: workgroup 0 also writes the Q8_K vector it built to xq
 };
 
 // Matrix mi of a launch with mi wave-uniform.  The byval kernel argument
@@ -324,6 +338,40 @@ __device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, cons
 // 272 bytes: the four quads a ds_read_b128 pass serves read four different
 // blocks at the same in-block offset, which would otherwise share banks.
 #define KQ_XQ_STRIDE 68
+#define KQ_XQ_WORDS (NB256_MAX * KQ_XQ_STRIDE > KQ_ACT_KMAX ? NB256_MAX * KQ_XQ_STRIDE : KQ_ACT_KMAX)
+
+// Q8_K of chunk c (16 consecutive elements v) into the LDS staging, exactly
+// as quantize_row_q8k (src/simd.rs:5013-5101): a block's 16 chunks sit in 16
+// consecutive lanes, which exchange the block maximum; the chunk's own sum is
+// its per-16 sum and a lane pair's the per-32 bsum.  Every lane of the wave
+// takes part (chunks past the end hold zeros and store nothing).
+__device__ __forceinline__ void kq_quant_chunk(const float (&v)[16], int c, bool valid, int32_t *s_xq, float *s_dx,
+                                               int16_t *s_bs, int16_t *s_s16) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+    int sum = 0;
+    uint32_t w4[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int q = max(-128, min(127, (int)__builtin_rintf(v[i] * id)));
+        sum += q;
+        w4[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+    }
+    const int pair = sum + __shfl_xor(sum, 1, 64);
+    if (valid) {
+        const int b = c >> 4;
+        *(int4 *)(s_xq + b * KQ_XQ_STRIDE + (c & 15) * 4) = make_int4((int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]);
+        s_s16[c] = (int16_t)sum;
+        if ((c & 1) == 0) s_bs[c >> 1] = (int16_t)pair;
+        if ((c & 15) == 0) s_dx[b] = amax * (1.0f / 127.0f);
+    }
+}
 
 struct KqTile {
     GemvMat M;  // the tile's matrix (SWIGLU: the gate matrix)
@@ -483,9 +531,11 @@ __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int 
 
 // FMT: every matrix of the launch has this format (Q4_K or Q6_K).  KQ_U:
 // units per lane (a wave tile is 64*KQ_U quarter-block units).
-template <int FMT, bool SWIGLU, int KQ_U>
+template <int FMT, bool SWIGLU, int KQ_U, int ACT>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
-    __shared__ int32_t s_xq[NB256_MAX * KQ_XQ_STRIDE];
+    __shared__ __align__(16) int32_t s_xq[KQ_XQ_WORDS];
+    __shared__ __align__(16) float s_wf[ACT == KQ_ACT_NORM ? KQ_ACT_KMAX : 4];
+    __shared__ float s_red[40];
     __shared__ float s_dx[NB256_MAX];
     __shared__ int16_t s_bs[NB32_MAX];
     __shared__ int16_t s_s16[KMAX / 16];
@@ -509,23 +559,44 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
     const int n16 = K >> 4;
     const int nbs = K >> 8;   // int4 chunks of bsums (8 per 256)
     const int ns16 = K >> 7;  // int4 chunks of sums16 (16 per 256)
-    const int4 *src = (const int4 *)A.xq.qs;
-    const int4 x0 = src[min(tid, n16 - 1)];
-    const int4 x1 = src[min(tid + 256, n16 - 1)];
-    const int4 x2 = src[min(tid + 512, n16 - 1)];
-    const int4 x3 = src[min(tid + 768, n16 - 1)];
-    const int4 bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
-    const int4 s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
-    const float dxr = A.xq.d[min(tid, nb - 1)];
+    int4 x0, x1, x2, x3, bsr, s16r;
+    float dxr;
+    float4 xf[ACT == KQ_ACT_NORM ? 8 : 1];  // this thread's 16-element chunk of x, then of w (NORM)
+    float4 xd[ACT == KQ_ACT_DEN ? 4 : 1];  // this thread's 16-element chunk (DEN)
+    float dd = 0.0f;
+    if (ACT == KQ_ACT_XQ) {
+        const int4 *src = (const int4 *)A.xq.qs;
+        x0 = src[min(tid, n16 - 1)];
+        x1 = src[min(tid + 256, n16 - 1)];
+        x2 = src[min(tid + 512, n16 - 1)];
+        x3 = src[min(tid + 768, n16 - 1)];
+        bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
+        s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
+        dxr = A.xq.d[min(tid, nb - 1)];
+    } else if (ACT == KQ_ACT_NORM) {
+        const int c = min(tid, n16 - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xf[i] = ((const float4 *)A.act_x)[4 * c + i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) xf[4 + i] = ((const float4 *)A.act_w)[4 * c + i];
+    } else {
+        const int c = min(tid, n16 - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xd[i] = ((const float4 *)A.act_x)[4 * c + i];
+        dd = A.act_den[(16 * c) / A.act_group];
+    }
 
     UnitLoad L0[KQ_U], L1[KQ_U];
     KqTile T0 = kq_tile_info<SWIGLU>(A, tile, tr);
     kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
     KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
     KqTile T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
-    kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
-    KqEpi E1 = kq_epi_load<SWIGLU>(T1, lane);
-    {
+    KqEpi E1;
+    if (ACT != KQ_ACT_NORM) {
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
+        E1 = kq_epi_load<SWIGLU>(T1, lane);
+    }
+    if (ACT == KQ_ACT_XQ) {
         // 16-byte chunk c of the activation goes to block c/16, padded stride
         int4 *dst = (int4 *)s_xq;
         const int d0 = (tid >> 4) * (KQ_XQ_STRIDE / 4) + (tid & 15);
@@ -536,8 +607,62 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
         if (tid < nbs) ((int4 *)s_bs)[tid] = bsr;
         if (tid < ns16) ((int4 *)s_s16)[tid] = s16r;
         if (tid < nb) s_dx[tid] = dxr;
+    } else if (ACT == KQ_ACT_NORM) {
+        // rms_norm_into (src/model.rs:5429-5437): x staged as f32 in the
+        // quant buffer, sum of squares in the reference's AVX2 order, then
+        // (x * scale) * w per element and Q8_K of the result
+        // x and w were loaded ahead of the first tile's weights; they go to
+        // LDS before the second tile's loads are issued, so their registers
+        // are free again by then
+        float *s_xf = (float *)s_xq;
+        if (tid < n16) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ((float4 *)s_xf)[4 * tid + i] = xf[i];
+                ((float4 *)s_wf)[4 * tid + i] = xf[4 + i];
+            }
+        }
+        kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
+        E1 = kq_epi_load<SWIGLU>(T1, lane);
+        __syncthreads();
+        const float ss = sumsq_avx2_order(s_xf, K, s_red);
+        const float scale = 1.0f / sqrtf(ss / (float)K + A.act_eps);
+        float v[16];
+        const int c = min(tid, n16 - 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 xv = ((const float4 *)s_xf)[4 * c + i];
+            const float4 wv = ((const float4 *)s_wf)[4 * c + i];
+            v[4 * i + 0] = xv.x * scale * wv.x;
+            v[4 * i + 1] = xv.y * scale * wv.y;
+            v[4 * i + 2] = xv.z * scale * wv.z;
+            v[4 * i + 3] = xv.w * scale * wv.w;
+        }
+        __syncthreads();  // every read of the f32 staging precedes the quant stores over it
+        kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
+    } else {
+        // attention normalisation (out *= 1/den where den > 0, as the
+        // reference's final scale) and Q8_K
+        float v[16];
+        const float inv = dd > 0.0f ? 1.0f / dd : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 a = xd[i];
+            v[4 * i + 0] = dd > 0.0f ? a.x * inv : a.x;
+            v[4 * i + 1] = dd > 0.0f ? a.y * inv : a.y;
+            v[4 * i + 2] = dd > 0.0f ? a.z * inv : a.z;
+            v[4 * i + 3] = dd > 0.0f ? a.w * inv : a.w;
+        }
+        kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
     }
     __syncthreads();
+    if (ACT != KQ_ACT_XQ && A.act_store && blockIdx.x == 0) {
+        // the same vector for a later launch that consumes it as is
+        if (tid < n16) ((int4 *)A.xq.qs)[tid] = ((const int4 *)s_xq)[(tid >> 4) * (KQ_XQ_STRIDE / 4) + (tid & 15)];
+        if (tid < nbs) ((int4 *)A.xq.bsums)[tid] = ((const int4 *)s_bs)[tid];
+        if (tid < ns16) ((int4 *)A.xq.sums16)[tid] = ((const int4 *)s_s16)[tid];
+        if (tid < nb) A.xq.d[tid] = s_dx[tid];
+    }
 
     while (T0.valid) {
         kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T0, E0, G, S, tr, nb, nbp, lane, L0, s_xq, s_dx, s_bs, s_s16,

@@ -32,53 +32,6 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *x, int n
     q8k_block_store(v, blockIdx.x, e, xq, red);
 }
 
-// sum(x*x) in the exact order of dot_f32_avx2(x, x) (src/simd.rs:6547-6586):
-// 32 lanes = four 8-wide FMA accumulators over 32-element chunks, combined as
-// (acc0+acc1)+(acc2+acc3), then the 8-element tail chunks, the hsum_avx tree
-// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)), then the scalar tail.  x is read
-// from LDS (s_x, already staged); every workgroup computes the same value.
-// red needs 33 floats.
-__device__ float sumsq_avx2_order(const float *s_x, int n, float *red) {
-    const int main32 = n / 32;
-    if (threadIdx.x < 32) {
-        const int L = threadIdx.x;
-        float acc = 0.0f;
-        int c = 0;
-        for (; c + 8 <= main32; c += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = s_x[32 * (c + j) + L];
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc = fmaf(v[j], v[j], acc);
-        }
-        for (; c < main32; c++) {
-            float v = s_x[32 * c + L];
-            acc = fmaf(v, v, acc);
-        }
-        red[L] = acc;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float t[8];
-#pragma unroll
-        for (int l = 0; l < 8; l++) t[l] = (red[l] + red[8 + l]) + (red[16 + l] + red[24 + l]);
-        const int ts = main32 * 32, tail8 = (n - ts) / 8;
-        for (int i = 0; i < tail8; i++)
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                float v = s_x[ts + 8 * i + l];
-                t[l] = fmaf(v, v, t[l]);
-            }
-        float sum = ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
-        for (int i = ts + tail8 * 8; i < n; i++) sum += s_x[i] * s_x[i];
-        red[32] = sum;
-    }
-    __syncthreads();
-    float r = red[32];
-    __syncthreads();
-    return r;
-}
-
 // RMSNorm (rms_norm_into, src/model.rs:5429-5437): ss = sum(x^2)/n,
 // scale = 1/sqrt(ss + eps), out = (x*scale)*w, with the sum in the
 // reference's order (so scale, and everything after it, matches bit for

@@ -394,14 +394,20 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
     return grid < 1 ? 1 : grid;
 }
 
-template <int FMT, bool SW, int U>
-static int launch_kq(const GemvArgs &A, hipStream_t s) {
-    auto kern = gemv_kq_kernel<FMT, SW, U>;
+template <int FMT, bool SW, int U, int ACT>
+static int launch_kq_act(const GemvArgs &A, hipStream_t s) {
+    auto kern = gemv_kq_kernel<FMT, SW, U, ACT>;
     int grid = persistent_grid(kern, A.n_tiles, 4);
     ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
     rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
     return 1;
+}
+template <int FMT, bool SW, int U>
+static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
+    if (act == KQ_ACT_NORM) return launch_kq_act<FMT, SW, U, KQ_ACT_NORM>(A, s);
+    if (act == KQ_ACT_DEN) return launch_kq_act<FMT, SW, U, KQ_ACT_DEN>(A, s);
+    return launch_kq_act<FMT, SW, U, KQ_ACT_XQ>(A, s);
 }
 template <int IT, int R>
 static int launch_q8i(const GemvArgs &A, hipStream_t s) {
@@ -479,6 +485,21 @@ static void pick_iters(int cat, int K, int *it, int *r) {
     }
 }
 
+// The prologue mode a K-quant launch uses to build act itself, or -1 when a
+// standalone kernel has to produce the Q8_K vector first.
+static int kq_prologue_act(const ActSpec &a, int K) {
+    static int off = -1;
+    if (off < 0) {
+        const char *e = getenv("RUSTY_HIP_ACT_PROLOGUE");  // 0: always the standalone kernels
+        off = (e && atoi(e) == 0) ? 1 : 0;
+    }
+    if (a.mode == ACT_XQ) return KQ_ACT_XQ;
+    if (off || K % 256 != 0 || K > KQ_ACT_KMAX) return -1;
+    if (a.mode == ACT_RMSNORM && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.norm_w & 15) == 0) return KQ_ACT_NORM;
+    if (a.mode == ACT_DEN && a.group > 0 && a.group % 16 == 0 && ((uintptr_t)a.x & 15) == 0) return KQ_ACT_DEN;
+    return -1;
+}
+
 // Launches y_i = W_i x for matrices of one category.
 static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
     if (n <= 0 || n > GEMV_MAX_MATS) return 0;
@@ -494,7 +515,8 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
         it = kq_units_per_lane(K, rows, epi == EPI_SWIGLU);
         r = kq_tile_rows(K, it, epi == EPI_SWIGLU);
     }
-    if (act.mode != ACT_XQ) return 0;
+    const int kact = cat == CAT_KQ ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
+    if (kact < 0) return 0;
     GemvArgs A;
     memset(&A, 0, sizeof(A));
     A.K = K;
@@ -502,6 +524,12 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     A.xq = act.xq;
     A.x = act.x;
     A.n_mats = n;
+    A.act_x = act.x;
+    A.act_w = act.norm_w;
+    A.act_den = act.den;
+    A.act_eps = act.eps;
+    A.act_group = act.group;
+    A.act_store = (kact > 0 && act.xq.qs) ? 1 : 0;
     int tiles = 0;
     int rows_per_tile = (cat == CAT_KQ) ? r : (cat == CAT_F32) ? (ms[0].w.fmt == 8 ? 8 : 64) : 4 * r;
     if (cat == CAT_F32)
@@ -530,8 +558,9 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
         const bool q4 = A.m[0].fmt == 12;
 #define RH_KQ_U(U)                                                                                     \
     if (it == U) {                                                                                     \
-        if (epi == EPI_SWIGLU) return q4 ? launch_kq<F_Q4_K, true, U>(A, s) : launch_kq<F_Q6_K, true, U>(A, s); \
-        return q4 ? launch_kq<F_Q4_K, false, U>(A, s) : launch_kq<F_Q6_K, false, U>(A, s);             \
+        if (epi == EPI_SWIGLU)                                                                         \
+            return q4 ? launch_kq<F_Q4_K, true, U>(A, kact, s) : launch_kq<F_Q6_K, true, U>(A, kact, s); \
+        return q4 ? launch_kq<F_Q4_K, false, U>(A, kact, s) : launch_kq<F_Q6_K, false, U>(A, kact, s);   \
     }
         RH_KQ_U(1) RH_KQ_U(2) RH_KQ_U(3) RH_KQ_U(4)
 #undef RH_KQ_U
@@ -585,8 +614,17 @@ static int act_materialize(const ActSpec &a, int K, ActSpec *out, hipStream_t s)
 // Splits a list of matrices into launch groups (one per category; K-quant
 // groups also share one format) and launches each.
 static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
-    ActSpec use;
-    if (!act_materialize(act, K, &use, s)) return 0;
+    // every launch group K-quant and the prologue able to build act: no
+    // standalone activation kernel
+    bool prologue = kq_prologue_act(act, K) > 0;
+    for (int i = 0; i < n && prologue; i++) prologue = cat_of(ms[i].w.fmt, K) == CAT_KQ;
+    ActSpec use = act;
+    if (!prologue && !act_materialize(act, K, &use, s)) return 0;
+    // with a prologue, the first launch group publishes the Q8_K vector it
+    // builds (act.xq) and later groups read it instead of building it again
+    const bool share = prologue && act.xq.qs != nullptr;
+    ActSpec later = act_xq(act.xq, act.x);
+    int launched = 0;
     int done[GEMV_MAX_MATS] = {0};
     for (int i = 0; i < n; i++) {
         if (done[i]) continue;
@@ -599,7 +637,8 @@ static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpe
                 grp[ng++] = ms[j];
                 done[j] = 1;
             }
-        if (!gemv_cat(grp, ng, K, epi, use, s)) return 0;
+        if (!gemv_cat(grp, ng, K, epi, (share && launched > 0) ? later : use, s)) return 0;
+        launched++;
     }
     return 1;
 }
@@ -644,8 +683,8 @@ static int gemv_swiglu_act(const DevW &gate, const DevW &up, int K, const ActSpe
                            float *tmp_g, float *tmp_u, hipStream_t s) {
     if (cat_of(gate.fmt, K) == CAT_KQ && gate.fmt == up.fmt && gate.rows == up.rows && K / 256 <= 32) {
         MatSpec ms[2] = {{gate, hidden, nullptr}, {up, hidden, nullptr}};
-        ActSpec use;
-        if (!act_materialize(act, K, &use, s)) return 0;
+        ActSpec use = act;
+        if (kq_prologue_act(act, K) < 0 && !act_materialize(act, K, &use, s)) return 0;
         return gemv_cat(ms, 2, K, EPI_SWIGLU, use, s);
     }
     MatSpec ms[2] = {{gate, tmp_g, nullptr}, {up, tmp_u, nullptr}};
