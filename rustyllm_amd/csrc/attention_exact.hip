@@ -520,15 +520,29 @@ __device__ __forceinline__ void c4_load16(const float *et, const float *vt, int 
 // Consumer chunk: all rows' flags clear -> the DPP FMA run; else every step
 // in the per-lane update forms (each row its own head's flags).  Branching
 // per step instead measured slower.
+// slow: wave-uniform (an SGPR bit of the group's chunk mask), so the common
+// case costs one scalar test and branch; a vector compare feeding the branch
+// (VCC from a VALU, right after the flag words arrive from LDS) measured
+// about 115 clocks per 16-step chunk on its own.
 template <bool X4>
-__device__ __forceinline__ void c4_steps16(float e16, const float *v, float &o, uint32_t bits) {
-    if (!__any(bits != 0u)) {
+__device__ __forceinline__ void c4_steps16(float e16, const float *v, float &o, uint32_t bits, bool slow) {
+    if (!slow) {
         cons_fma16_dpp(e16, v, o);
     } else {
         float e[16];
         bcast16_all(e16, e);
         chain_steps16_flags<false, X4>(e, v, o, bits);
     }
+}
+
+// Bit k (k < 8) set when chunk k of a two-tile group has a new maximum in any
+// of the wave's four rows; the row words m0..m3 are lane-varying by row.
+__device__ __forceinline__ uint32_t c4_group_mask(uint32_t m0, uint32_t m1, uint32_t m2, uint32_t m3) {
+    uint32_t f = ((m0 & 0xFFFFu) ? 1u : 0u) | ((m0 >> 16) ? 2u : 0u) | ((m1 & 0xFFFFu) ? 4u : 0u) |
+                 ((m1 >> 16) ? 8u : 0u) | ((m2 & 0xFFFFu) ? 16u : 0u) | ((m2 >> 16) ? 32u : 0u) |
+                 ((m3 & 0xFFFFu) ? 64u : 0u) | ((m3 >> 16) ? 128u : 0u);
+    return __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) | __builtin_amdgcn_readlane(f, 32) |
+           __builtin_amdgcn_readlane(f, 48);
 }
 
 // The recurrence of one wave: DEN = false the outputs (lane = value dim of
@@ -551,25 +565,47 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
             const float *ea = &L.e[sa][row * EX_TILE], *eb = &L.e[sb][row * EX_TILE];
             const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
             const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
+            const uint32_t gm = c4_group_mask(m0, m1, m2, m3);
             float a0, a1, v0[16], v1[16];
             c4_load16<DEN>(ea, va, 0, lane, a0, v0);
             __builtin_amdgcn_sched_barrier(0);
-#define C4_STEP(ET, VT, K, NA, NV, CA, CV, BITS)       \
+            if (gm == 0u) {
+                // no new maximum in any of the group's 128 steps (the common
+                // case past the first tiles): straight-line FMA runs
+#define C4_FAST(ET, VT, K, NA, NV, CA, CV)   \
+    RH_WAIT_LGKM0();                         \
+    c4_load16<DEN>(ET, VT, K, lane, NA, NV); \
+    __builtin_amdgcn_sched_barrier(0);       \
+    cons_fma16_dpp(CA, CV, o);               \
+    __builtin_amdgcn_sched_barrier(0);
+                C4_FAST(ea, va, 1, a1, v1, a0, v0)
+                C4_FAST(ea, va, 2, a0, v0, a1, v1)
+                C4_FAST(ea, va, 3, a1, v1, a0, v0)
+                C4_FAST(eb, vb, 0, a0, v0, a1, v1)
+                C4_FAST(eb, vb, 1, a1, v1, a0, v0)
+                C4_FAST(eb, vb, 2, a0, v0, a1, v1)
+                C4_FAST(eb, vb, 3, a1, v1, a0, v0)
+#undef C4_FAST
+                RH_WAIT_LGKM0();
+                cons_fma16_dpp(a1, v1, o);
+            } else {
+#define C4_STEP(ET, VT, K, NA, NV, CA, CV, BITS, C)    \
     RH_WAIT_LGKM0();                                   \
     c4_load16<DEN>(ET, VT, K, lane, NA, NV);           \
     __builtin_amdgcn_sched_barrier(0);                 \
-    c4_steps16<X4>(CA, CV, o, BITS);                   \
+    c4_steps16<X4>(CA, CV, o, BITS, (gm >> (C)) & 1u); \
     __builtin_amdgcn_sched_barrier(0);
-            C4_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu)
-            C4_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16)
-            C4_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu)
-            C4_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16)
-            C4_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu)
-            C4_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16)
-            C4_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu)
+                C4_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu, 0)
+                C4_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16, 1)
+                C4_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu, 2)
+                C4_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16, 3)
+                C4_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu, 4)
+                C4_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16, 5)
+                C4_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu, 6)
 #undef C4_STEP
-            RH_WAIT_LGKM0();
-            c4_steps16<X4>(a1, v1, o, m3 >> 16);
+                RH_WAIT_LGKM0();
+                c4_steps16<X4>(a1, v1, o, m3 >> 16, (gm >> 7) & 1u);
+            }
         } else {
             for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
                 const int sl = i & (C4_NT - 1);
