@@ -17,6 +17,9 @@
 //      before every step from the tile maxima and an in-tile prefix max, so
 //      each step's branch and expf argument are known up front; expf is
 //      glibc's (restated below, checked against glibc on all 2^32 inputs).
+//      Each step gets a coefficient a and a multiplier m: (a, m) = (w, 1) on
+//      an ordinary step and (1, old) on a new maximum, so the grouped form
+//      is o = fma(a, v, o*m) on every step (o*1 is exact).
 //   C  attn_exact_chain:   the FMA recurrences, one lane per (head, dim),
 //      V streamed into LDS by direct global->LDS loads; the denominators run
 //      as the same recurrence with v = 1.
@@ -80,7 +83,8 @@ struct AttnExactArgs {
     const float *v;
     const float *sinks;  // [n_heads] or null
     float *scores;       // [n_heads][cap]   q.k * scale per position
-    float *e;            // [n_heads][cap]   the step's expf value (see below)
+    float *e;            // [n_heads][cap]   the step's coefficient a: expf(s - max), or 1 on a new max
+    float *mul;          // [n_heads][cap]   the step's multiplier m: 1, or expf(old max - s) on a new max
     float *tmax;         // [n_heads][cap/64] max score of each 64-position tile
     uint32_t *newmask;   // [n_heads][cap/32] bit t%32 set when step t sets a new max
     float *den;          // [n_heads]         final denominators
@@ -110,6 +114,7 @@ __device__ __forceinline__ AttnExactArgs tok_view(const AttnExactArgs &A0) {
     A.out += (int64_t)z * A0.o_tok;
     A.scores += sc;
     A.e += sc;
+    A.mul += sc;
     A.tmax += sc;
     A.newmask += sc;
     A.den += sc;
@@ -261,9 +266,10 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
 // B: one wave per (tile of 64 positions, query head).  The running max before
 // each step is max(initial, maxima of the earlier tiles, prefix max inside the
 // tile), so every step's branch and expf argument are known without a serial
-// scan.  e[t] = isfinite(run) ? expf(run - s) : 0 on a new max (the factor the
-// old output and denominator are scaled by), expf(s - run) otherwise; the
-// new-max steps are marked in newmask.
+// scan.  On a new max the multiplier is isfinite(run) ? expf(run - s) : 0
+// (the factor the old output and denominator are scaled by) and the
+// coefficient 1; otherwise the coefficient is expf(s - run) and the
+// multiplier 1.  The new-max steps are also marked in newmask.
 __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     int s0, e0;
@@ -289,13 +295,16 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
     float prev = __shfl_up(p, 1, 64);
     const float run = lane == 0 ? m : fmaxf(m, prev);
     const bool flag = valid && s > run;
-    float e = 0.0f;
-    if (flag)
-        e = __builtin_isfinite(run) ? expf_glibc(run - s) : 0.0f;
-    else if (valid)
+    float e = 0.0f, mlt = 1.0f;
+    if (flag) {
+        mlt = __builtin_isfinite(run) ? expf_glibc(run - s) : 0.0f;
+        e = 1.0f;
+    } else if (valid) {
         e = expf_glibc(s - run);
+    }
     const int kvm = A.kv_mul, g = head % kvm;
     A.e[e_index(A, head / kvm, g, t)] = e;
+    A.mul[e_index(A, head / kvm, g, t)] = mlt;
     const unsigned long long bits = __ballot(flag);
     if (lane < 2) A.newmask[(size_t)head * (A.cap / 32) + 2 * tile + lane] = (uint32_t)(bits >> (32 * lane));
 }
@@ -374,15 +383,35 @@ __device__ __forceinline__ void cons_fma16_dpp(float e16, const float *v, float 
           "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
 }
 
+// 16 steps of the grouped update form on every step, o = fma(a_j, v_j, o*m_j)
+// (the reference's affine_add_f32x4 with its new-max and ordinary cases, and
+// the denominators with v = 1): a_j and m_j come from lane j of the row via
+// row_newbcast, so a group holding new maxima runs branch-free in two DPP
+// instructions per step.
+__device__ __forceinline__ void cons_affine16_dpp(float a16, float m16, const float *v, float &o) {
+#define RH_AFF(J, VJ)                                                               \
+    "v_mul_f32_dpp %0, %2, %0 row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_fmac_f32_dpp %0, %1, %" #VJ " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n\t"
+    asm("s_nop 1\n\t"
+        RH_AFF(0, 3) RH_AFF(1, 4) RH_AFF(2, 5) RH_AFF(3, 6) RH_AFF(4, 7) RH_AFF(5, 8) RH_AFF(6, 9) RH_AFF(7, 10)
+        RH_AFF(8, 11) RH_AFF(9, 12) RH_AFF(10, 13) RH_AFF(11, 14) RH_AFF(12, 15) RH_AFF(13, 16) RH_AFF(14, 17)
+        RH_AFF(15, 18)
+        : "+v"(o)
+        : "v"(a16), "v"(m16), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]),
+          "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
+#undef RH_AFF
+}
+
 // 16 recurrence steps with per-step new-max flags `bits`: the update forms
 // selected per step (rare: only chunks holding a new maximum come here).
 template <bool DEN, bool X4>
-__device__ __forceinline__ void chain_steps16_flags(const float *e, const float *v, float &o, uint32_t bits) {
+__device__ __forceinline__ void chain_steps16_flags(const float *e, const float *m, const float *v, float &o,
+                                                    uint32_t bits) {
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const float vj = DEN ? 1.0f : v[j];
         const float on = fmaf(e[j], vj, o);
-        const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * e[j]) : fmaf(o, e[j], vj);
+        const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * m[j]) : fmaf(o, m[j], vj);
         o = ((bits >> j) & 1u) ? ox : on;
     }
 }
@@ -405,7 +434,8 @@ __device__ __forceinline__ void chain_steps16_flags(const float *e, const float 
 
 struct Chain4Lds {
     float v[C4_NT][EX_TILE * 16];       // [slot][position][16 dims]
-    float e[C4_NT][CH_MAXG * EX_TILE];  // [slot][head][position]
+    float e[C4_NT][CH_MAXG * EX_TILE];  // [slot][head][position] coefficients
+    float mu[C4_NT][CH_MAXG * EX_TILE]; // [slot][head][position] multipliers
     uint32_t m[C4_NT][2 * CH_MAXG];     // [slot][head][2 words]
 };
 
@@ -425,7 +455,7 @@ __device__ __forceinline__ void c4_wait_tiles_after(int n_after) {
     }
 }
 static_assert(C4_P - 1 <= 9, "c4_wait_tiles_after covers at most 9 tiles");
-static_assert(2 * 9 <= 63, "vmcnt is 6 bits (two loads per producer per tile)");
+static_assert(3 * 9 <= 63, "vmcnt is 6 bits (up to three loads per producer per tile)");
 static_assert(C4_NT >= C4_P + C4_PER, "ring too small");
 
 // Same protocol as chain_producer_loop on the C4 ring; after(j) runs once
@@ -456,7 +486,7 @@ __device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue, After
 // so a tile's V is split four ways.
 template <int P>
 __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int g0, int slice) {
-    constexpr int IPT = P < 2 ? 2 : 1;
+    constexpr int IPT = P < 3 ? 2 : 1;
     const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 16) + (lane & 3) * 16;
@@ -466,6 +496,7 @@ __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ct
     uint32_t roff = (uint32_t)((s0 + 16 * P + (lane >> 2)) % A.slot_count) * row_bytes;
     const int re = min(g0 + (lane >> 4), kvm - 1);
     const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
+    const char *mu_base = (const char *)(A.mul + e_index(A, h, re, 0)) + (lane & 15) * 16;
     const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
     const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
     auto issue = [&](int i) {
@@ -476,6 +507,7 @@ __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ct
         if (P == 0) dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
         if (P == 1)
             if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
+        if (P == 2) dma16(mu_base + (uint32_t)i * 256u, &L.mu[sl][0]);
     };
     auto none = [](int) {};
     c4_producer_loop<IPT>(ntiles, issue, none);
@@ -484,16 +516,18 @@ __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ct
 // Producer of a denominator workgroup: e of the four heads and their
 // new-max words, the same slots as a chain workgroup's.
 __device__ void c4_den_producer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
-    constexpr int IPT = 2;
+    constexpr int IPT = 3;
     const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const int re = min(g0 + (lane >> 4), kvm - 1);
     const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
+    const char *mu_base = (const char *)(A.mul + e_index(A, h, re, 0)) + (lane & 15) * 16;
     const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
     const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
     auto issue = [&](int i) {
         const int sl = i & (C4_NT - 1);
         dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
+        dma16(mu_base + (uint32_t)i * 256u, &L.mu[sl][0]);
         if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
     };
     auto none = [](int) {};
@@ -516,6 +550,12 @@ __device__ __forceinline__ void c4_load16(const float *et, const float *vt, int 
 #pragma unroll
     for (int j = 0; j < 16; j++) v[j] = DEN ? 1.0f : vt[(k * 16 + j) * 16];
 }
+template <bool DEN>
+__device__ __forceinline__ void c4_load16m(const float *et, const float *mt, const float *vt, int k, int lane,
+                                           float &e16, float &m16, float *v) {
+    m16 = mt[k * 16 + (lane & 15)];
+    c4_load16<DEN>(et, vt, k, lane, e16, v);
+}
 
 // Consumer chunk: all rows' flags clear -> the DPP FMA run; else every step
 // in the per-lane update forms (each row its own head's flags).  Branching
@@ -525,13 +565,14 @@ __device__ __forceinline__ void c4_load16(const float *et, const float *vt, int 
 // (VCC from a VALU, right after the flag words arrive from LDS) measured
 // about 115 clocks per 16-step chunk on its own.
 template <bool X4>
-__device__ __forceinline__ void c4_steps16(float e16, const float *v, float &o, uint32_t bits, bool slow) {
+__device__ __forceinline__ void c4_steps16(float e16, float m16, const float *v, float &o, uint32_t bits, bool slow) {
     if (!slow) {
         cons_fma16_dpp(e16, v, o);
     } else {
-        float e[16];
+        float e[16], m[16];
         bcast16_all(e16, e);
-        chain_steps16_flags<false, X4>(e, v, o, bits);
+        bcast16_all(m16, m);
+        chain_steps16_flags<false, X4>(e, m, v, o, bits);
     }
 }
 
@@ -588,23 +629,49 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
 #undef C4_FAST
                 RH_WAIT_LGKM0();
                 cons_fma16_dpp(a1, v1, o);
-            } else {
-#define C4_STEP(ET, VT, K, NA, NV, CA, CV, BITS, C)    \
-    RH_WAIT_LGKM0();                                   \
-    c4_load16<DEN>(ET, VT, K, lane, NA, NV);           \
-    __builtin_amdgcn_sched_barrier(0);                 \
-    c4_steps16<X4>(CA, CV, o, BITS, (gm >> (C)) & 1u); \
+            } else if (X4 || DEN) {
+                // a group holding new maxima, grouped form: every step as
+                // o = fma(a, v, o*m), straight-line
+                const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
+                float u0, u1;
+                u0 = ma[lane & 15];
+#define C4_AFF(ET, MT, VT, K, NA, NU, NV, CA, CU, CV) \
+    RH_WAIT_LGKM0();                                  \
+    c4_load16m<DEN>(ET, MT, VT, K, lane, NA, NU, NV); \
+    __builtin_amdgcn_sched_barrier(0);                \
+    cons_affine16_dpp(CA, CU, CV, o);                 \
     __builtin_amdgcn_sched_barrier(0);
-                C4_STEP(ea, va, 1, a1, v1, a0, v0, m0 & 0xFFFFu, 0)
-                C4_STEP(ea, va, 2, a0, v0, a1, v1, m0 >> 16, 1)
-                C4_STEP(ea, va, 3, a1, v1, a0, v0, m1 & 0xFFFFu, 2)
-                C4_STEP(eb, vb, 0, a0, v0, a1, v1, m1 >> 16, 3)
-                C4_STEP(eb, vb, 1, a1, v1, a0, v0, m2 & 0xFFFFu, 4)
-                C4_STEP(eb, vb, 2, a0, v0, a1, v1, m2 >> 16, 5)
-                C4_STEP(eb, vb, 3, a1, v1, a0, v0, m3 & 0xFFFFu, 6)
+                C4_AFF(ea, ma, va, 1, a1, u1, v1, a0, u0, v0)
+                C4_AFF(ea, ma, va, 2, a0, u0, v0, a1, u1, v1)
+                C4_AFF(ea, ma, va, 3, a1, u1, v1, a0, u0, v0)
+                C4_AFF(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1)
+                C4_AFF(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0)
+                C4_AFF(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1)
+                C4_AFF(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0)
+#undef C4_AFF
+                RH_WAIT_LGKM0();
+                cons_affine16_dpp(a1, u1, v1, o);
+            } else {
+                // scale_add heads: each step in its own form, chunk by chunk
+                const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
+                float u0, u1;
+                u0 = ma[lane & 15];
+#define C4_STEP(ET, MT, VT, K, NA, NU, NV, CA, CU, CV, BITS, C) \
+    RH_WAIT_LGKM0();                                            \
+    c4_load16m<DEN>(ET, MT, VT, K, lane, NA, NU, NV);           \
+    __builtin_amdgcn_sched_barrier(0);                          \
+    c4_steps16<X4>(CA, CU, CV, o, BITS, (gm >> (C)) & 1u);      \
+    __builtin_amdgcn_sched_barrier(0);
+                C4_STEP(ea, ma, va, 1, a1, u1, v1, a0, u0, v0, m0 & 0xFFFFu, 0)
+                C4_STEP(ea, ma, va, 2, a0, u0, v0, a1, u1, v1, m0 >> 16, 1)
+                C4_STEP(ea, ma, va, 3, a1, u1, v1, a0, u0, v0, m1 & 0xFFFFu, 2)
+                C4_STEP(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1, m1 >> 16, 3)
+                C4_STEP(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0, m2 & 0xFFFFu, 4)
+                C4_STEP(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1, m2 >> 16, 5)
+                C4_STEP(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0, m3 & 0xFFFFu, 6)
 #undef C4_STEP
                 RH_WAIT_LGKM0();
-                c4_steps16<X4>(a1, v1, o, m3 >> 16, (gm >> 7) & 1u);
+                c4_steps16<X4>(a1, u1, v1, o, m3 >> 16, (gm >> 7) & 1u);
             }
         } else {
             for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
@@ -612,13 +679,14 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 const int ntok = min(EX_TILE, ctx - i * EX_TILE);
                 const float *vt = &L.v[sl][dcol];
                 const float *et = &L.e[sl][row * EX_TILE];
+                const float *mt = &L.mu[sl][row * EX_TILE];
                 const uint32_t mw0 = L.m[sl][2 * row], mw1 = L.m[sl][2 * row + 1];
                 for (int t = 0; t < ntok; t++) {
                     const uint32_t mw = t < 32 ? mw0 : mw1;
-                    const float e = et[t];
+                    const float e = et[t], mlt = mt[t];
                     const float v = DEN ? 1.0f : vt[t * 16];
                     const float on = fmaf(e, v, o);
-                    const float ox = X4 ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
+                    const float ox = X4 ? fmaf(v, 1.0f, o * mlt) : fmaf(o, mlt, v);
                     o = ((mw >> (t & 31)) & 1u) ? ox : on;
                 }
             }
@@ -691,19 +759,21 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) 
     const bool dim_ok = dim < A.vd;
     const bool x4 = is_x4(A, g);
     const float *ef = A.e + e_index(A, h, g, 0);
+    const float *mf = A.mul + e_index(A, h, g, 0);
     const uint32_t *mk = A.newmask + (size_t)head * (A.cap / 32);
     const float *vbase = A.v + (size_t)h * A.vd + (dim_ok ? dim : 0);
     float o = 0.0f;
     float d = A.sinks ? 1.0f : 0.0f;
     for (int t0 = 0; t0 < ctx; t0 += 32) {
         const int n = min(32, ctx - t0);
-        float vb[32], eb[32];
+        float vb[32], eb[32], mb[32];
 #pragma unroll
         for (int j = 0; j < 32; j++) {
             int t = t0 + j < ctx ? t0 + j : ctx - 1;
             int slot = (s0 + t) % A.slot_count;
             vb[j] = vbase[(size_t)slot * A.value_stride];
             eb[j] = ef[t];
+            mb[j] = mf[t];
         }
         const uint32_t bits = mk[t0 >> 5];
         if (bits == 0 && n == 32) {
@@ -718,10 +788,10 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) 
                 if (j < n) {
                     if ((bits >> j) & 1u) {
                         if (x4)
-                            o = fmaf(vb[j], 1.0f, o * eb[j]);  // affine_add: fma(value, 1, out*old)
+                            o = fmaf(vb[j], 1.0f, o * mb[j]);  // affine_add: fma(value, 1, out*old)
                         else
-                            o = fmaf(o, eb[j], vb[j]);         // scale_add: fma(out, old, value)
-                        float p = d * eb[j];
+                            o = fmaf(o, mb[j], vb[j]);         // scale_add: fma(out, old, value)
+                        float p = d * mb[j];
                         d = p + 1.0f;
                     } else {
                         o = fmaf(eb[j], vb[j], o);             // axpy / affine_add with mul 1

@@ -748,7 +748,7 @@ static size_t exact_e_floats(int n_kv, int kv_mul, int cap) { return (size_t)n_k
 
 static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
     size_t n = (size_t)n_kv * kv_mul;
-    return n * cap + exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
+    return n * cap + 2 * exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
 }
 
 // Launches the exact attention kernels; cap = positions reserved per head
@@ -769,7 +769,8 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     A.scores = scratch;
     A.e = scratch + nh * cap;
-    A.tmax = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
+    A.mul = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
+    A.tmax = A.mul + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
     A.newmask = (uint32_t *)(A.tmax + nh * (cap / 64));
     A.den = (float *)(A.newmask + nh * (cap / 32));
     A.kvec = (A.key_stride % 4 == 0 && A.hd % 4 == 0 && ((uintptr_t)A.k & 15) == 0) ? 1 : 0;
