@@ -101,6 +101,12 @@ struct AttnExactArgs {
     // n_tok = 0: one token, ranges from st or start_t/end_t.
     int32_t n_tok, pos0;
     int64_t q_tok, o_tok, tok_scratch;
+    // Optional transposed V copy [n_kv*vd][vt_stride] (position fastest):
+    // with a range starting on a multiple of 4 positions and not wrapping,
+    // the chain kernel streams V from it so that one 16-byte LDS read gives a
+    // lane four steps of its value dim.  null: V only.
+    const float *vt;
+    int32_t vt_stride;
 };
 
 // The single-token view of token blockIdx.z of a multi-token launch: its
@@ -484,12 +490,17 @@ __device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue, After
 // P = 1 the heads' new-max words.  A position's 16 dims are 64 bytes of a
 // 4 KB cache row, and a wave's direct loads cost about 8 ns per such piece,
 // so a tile's V is split four ways.
-template <int P>
+template <int P, bool VT>
 __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int g0, int slice) {
     constexpr int IPT = P < 3 ? 2 : 1;
     const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 16) + (lane & 3) * 16;
+    // VT: lane -> dim lane%16 of the slice, positions 16P + 4*(lane/16) ..+3
+    // of the tile (the range starts on a multiple of 4 and does not wrap)
+    const char *vt_base = VT ? (const char *)(A.vt + (size_t)(h * A.vd + slice * 16 + (lane & 15)) * A.vt_stride +
+                                              s0 + 16 * P + 4 * (lane >> 4))
+                             : nullptr;
     const uint32_t row_bytes = (uint32_t)A.value_stride * 4u;
     const uint32_t wrap = (uint32_t)A.slot_count * row_bytes;
     const uint32_t step = 64u * row_bytes;
@@ -501,9 +512,13 @@ __device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ct
     const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
     auto issue = [&](int i) {
         const int sl = i & (C4_NT - 1);
-        dma16(v_base + roff, &L.v[sl][P * 256]);
-        roff += step;
-        if (roff >= wrap) roff -= wrap;
+        if (VT) {
+            dma16(vt_base + (uint32_t)i * 256u, &L.v[sl][P * 256]);
+        } else {
+            dma16(v_base + roff, &L.v[sl][P * 256]);
+            roff += step;
+            if (roff >= wrap) roff -= wrap;
+        }
         if (P == 0) dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
         if (P == 1)
             if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
@@ -544,17 +559,31 @@ __device__ void c4_idle(int ctx) {
 // 16 steps of a 16-dim row: e16 = e of step (lane % 16) of this row's head,
 // v[j] = V of step j at this lane's dim (broadcast across the four rows), or
 // 1 for the denominators.
-template <bool DEN>
+// V tile layouts in LDS: VT = false [position][16 dims] (vt = &v[dcol], one
+// value per read); VT = true [position/4][16 dims][4 positions] (vt =
+// &v[4*dcol], four steps of the lane's dim per 16-byte read).
+template <bool DEN, bool VT>
 __device__ __forceinline__ void c4_load16(const float *et, const float *vt, int k, int lane, float &e16, float *v) {
     e16 = et[k * 16 + (lane & 15)];
+    if (VT && !DEN) {
 #pragma unroll
-    for (int j = 0; j < 16; j++) v[j] = DEN ? 1.0f : vt[(k * 16 + j) * 16];
+        for (int q = 0; q < 4; q++) {
+            const float4 f = *(const float4 *)(vt + (4 * k + q) * 64);
+            v[4 * q] = f.x;
+            v[4 * q + 1] = f.y;
+            v[4 * q + 2] = f.z;
+            v[4 * q + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = DEN ? 1.0f : vt[(k * 16 + j) * 16];
+    }
 }
-template <bool DEN>
+template <bool DEN, bool VT>
 __device__ __forceinline__ void c4_load16m(const float *et, const float *mt, const float *vt, int k, int lane,
                                            float &e16, float &m16, float *v) {
     m16 = mt[k * 16 + (lane & 15)];
-    c4_load16<DEN>(et, vt, k, lane, e16, v);
+    c4_load16<DEN, VT>(et, vt, k, lane, e16, v);
 }
 
 // Consumer chunk: all rows' flags clear -> the DPP FMA run; else every step
@@ -590,7 +619,7 @@ __device__ __forceinline__ uint32_t c4_group_mask(uint32_t m0, uint32_t m1, uint
 // its row's head), DEN = true the denominators, the same recurrence with
 // v = 1 (fma(e, 1, d) = d + e; on a new maximum fma(1, 1, d*e) = d*e + 1,
 // the x4 form), starting from 1 with sinks; no V is read.
-template <bool X4, bool DEN>
+template <bool X4, bool DEN, bool VT>
 __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float *dst) {
     const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
@@ -602,20 +631,20 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
         const bool full = i0 + C4_PER <= ntiles && ctx >= (i0 + C4_PER) * EX_TILE;
         if (full) {
             const int sa = i0 & (C4_NT - 1), sb = (i0 + 1) & (C4_NT - 1);
-            const float *va = &L.v[sa][dcol], *vb = &L.v[sb][dcol];
+            const float *va = &L.v[sa][VT ? 4 * dcol : dcol], *vb = &L.v[sb][VT ? 4 * dcol : dcol];
             const float *ea = &L.e[sa][row * EX_TILE], *eb = &L.e[sb][row * EX_TILE];
             const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
             const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
             const uint32_t gm = c4_group_mask(m0, m1, m2, m3);
             float a0, a1, v0[16], v1[16];
-            c4_load16<DEN>(ea, va, 0, lane, a0, v0);
+            c4_load16<DEN, VT>(ea, va, 0, lane, a0, v0);
             __builtin_amdgcn_sched_barrier(0);
             if (gm == 0u) {
                 // no new maximum in any of the group's 128 steps (the common
                 // case past the first tiles): straight-line FMA runs
-#define C4_FAST(ET, VT, K, NA, NV, CA, CV)   \
+#define C4_FAST(ET, VP, K, NA, NV, CA, CV)   \
     RH_WAIT_LGKM0();                         \
-    c4_load16<DEN>(ET, VT, K, lane, NA, NV); \
+    c4_load16<DEN, VT>(ET, VP, K, lane, NA, NV); \
     __builtin_amdgcn_sched_barrier(0);       \
     cons_fma16_dpp(CA, CV, o);               \
     __builtin_amdgcn_sched_barrier(0);
@@ -635,9 +664,9 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
                 float u0, u1;
                 u0 = ma[lane & 15];
-#define C4_AFF(ET, MT, VT, K, NA, NU, NV, CA, CU, CV) \
+#define C4_AFF(ET, MT, VP, K, NA, NU, NV, CA, CU, CV) \
     RH_WAIT_LGKM0();                                  \
-    c4_load16m<DEN>(ET, MT, VT, K, lane, NA, NU, NV); \
+    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV); \
     __builtin_amdgcn_sched_barrier(0);                \
     cons_affine16_dpp(CA, CU, CV, o);                 \
     __builtin_amdgcn_sched_barrier(0);
@@ -656,9 +685,9 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
                 float u0, u1;
                 u0 = ma[lane & 15];
-#define C4_STEP(ET, MT, VT, K, NA, NU, NV, CA, CU, CV, BITS, C) \
+#define C4_STEP(ET, MT, VP, K, NA, NU, NV, CA, CU, CV, BITS, C) \
     RH_WAIT_LGKM0();                                            \
-    c4_load16m<DEN>(ET, MT, VT, K, lane, NA, NU, NV);           \
+    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV);           \
     __builtin_amdgcn_sched_barrier(0);                          \
     c4_steps16<X4>(CA, CU, CV, o, BITS, (gm >> (C)) & 1u);      \
     __builtin_amdgcn_sched_barrier(0);
@@ -684,7 +713,7 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 for (int t = 0; t < ntok; t++) {
                     const uint32_t mw = t < 32 ? mw0 : mw1;
                     const float e = et[t], mlt = mt[t];
-                    const float v = DEN ? 1.0f : vt[t * 16];
+                    const float v = DEN ? 1.0f : (VT ? L.v[sl][(t >> 2) * 64 + 4 * dcol + (t & 3)] : vt[t * 16]);
                     const float on = fmaf(e, v, o);
                     const float ox = X4 ? fmaf(v, 1.0f, o * mlt) : fmaf(o, mlt, v);
                     o = ((mw >> (t & 31)) & 1u) ? ox : on;
@@ -713,29 +742,39 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
     const int h = blockIdx.x % A.n_kv, r = blockIdx.x / A.n_kv;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    // V from the transposed copy when the range starts on a multiple of 4
+    // positions, does not wrap, and its tiles stay inside the copy's rows
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const bool vt_ok = A.vt != nullptr && (s0 & 3) == 0 && e0 < A.slot_count && s0 + ntiles * EX_TILE <= A.vt_stride;
     if (r < ngrp * nsl) {
         const int g0 = 4 * (r / nsl), slice = r % nsl;
         const int g = g0 + (lane >> 4);
         if (wave == 0) {
             float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
-            if (A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0)
-                c4_consumer<true, false>(A, L, ctx, dst);
-            else
-                c4_consumer<false, false>(A, L, ctx, dst);
-        } else if (wave == 1) {
-            c4_producer<0>(A, L, s0, ctx, h, g0, slice);
-        } else if (wave == 2) {
-            c4_producer<1>(A, L, s0, ctx, h, g0, slice);
-        } else if (wave == 3) {
-            c4_producer<2>(A, L, s0, ctx, h, g0, slice);
+            const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
+            if (vt_ok) {
+                if (x4) c4_consumer<true, false, true>(A, L, ctx, dst);
+                else c4_consumer<false, false, true>(A, L, ctx, dst);
+            } else {
+                if (x4) c4_consumer<true, false, false>(A, L, ctx, dst);
+                else c4_consumer<false, false, false>(A, L, ctx, dst);
+            }
+        } else if (vt_ok) {
+            if (wave == 1) c4_producer<0, true>(A, L, s0, ctx, h, g0, slice);
+            else if (wave == 2) c4_producer<1, true>(A, L, s0, ctx, h, g0, slice);
+            else if (wave == 3) c4_producer<2, true>(A, L, s0, ctx, h, g0, slice);
+            else c4_producer<3, true>(A, L, s0, ctx, h, g0, slice);
         } else {
-            c4_producer<3>(A, L, s0, ctx, h, g0, slice);
+            if (wave == 1) c4_producer<0, false>(A, L, s0, ctx, h, g0, slice);
+            else if (wave == 2) c4_producer<1, false>(A, L, s0, ctx, h, g0, slice);
+            else if (wave == 3) c4_producer<2, false>(A, L, s0, ctx, h, g0, slice);
+            else c4_producer<3, false>(A, L, s0, ctx, h, g0, slice);
         }
     } else {
         const int g0 = 4 * (r - ngrp * nsl);
         const int g = g0 + (lane >> 4);
         if (wave == 0) {
-            c4_consumer<true, true>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
+            c4_consumer<true, true, false>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
         } else if (wave == 1) {
             c4_den_producer(A, L, ctx, h, g0);
         } else {

@@ -84,6 +84,8 @@ struct RopeArgs {
     int32_t max_pos;      // rows of the cos/sin table
     int32_t n_heads, n_kv, hd, vd, slots, ring, neox;
     int32_t q_tok, k_tok, v_tok;  // per-token row strides of q/k/v (prefill: token blockIdx.y at pos + y)
+    float *vtcache;       // optional transposed V copy [n_kv*vd][vt_stride] (slot fastest), or null
+    int32_t vt_stride;
 };
 
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
@@ -127,7 +129,9 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
             }
         } else {
             int j = i - nq - nk;
-            A.vcache[(size_t)slot * vvd + j] = A.v[j];
+            const float v = A.v[j];
+            A.vcache[(size_t)slot * vvd + j] = v;
+            if (A.vtcache) A.vtcache[(size_t)j * A.vt_stride + slot] = v;
         }
     }
 }

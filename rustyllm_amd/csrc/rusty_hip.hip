@@ -1540,6 +1540,7 @@ struct RLayer {
     float *attn_norm = nullptr, *ffn_norm = nullptr;  // gpt-oss: ffn_norm is post_attn_norm
     float *bias[3] = {nullptr, nullptr, nullptr};
     float *k = nullptr, *v = nullptr;
+    float *vt = nullptr;  // transposed V copy [n_kv*vd][vt_stride] (standard layers)
     // gpt-oss
     float *bo = nullptr, *sinks = nullptr;
     MoeDev moe{};
@@ -1549,6 +1550,7 @@ struct Resident {
     bool configured = false, ready = false;
     uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, vd = 0, hidden = 0, vocab = 0, storage = 0;
     uint32_t neox = 0;
+    uint32_t vt_stride = 0;  // positions per row of the transposed V copies (storage rounded up to 64)
     float eps = 1e-5f;
     std::vector<RLayer> L;
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
@@ -1644,6 +1646,15 @@ static ActSpec r_act_norm(const float *norm_w) {
     return a;
 }
 
+// V rows [slot][w] of slots slot0..slot0+n-1 into the transposed copy
+// vt[j][slot] (row length vt_stride).
+__global__ void kv_transpose_kernel(const float *v, int w, int slot0, int n, float *vt, int vt_stride) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * w) return;
+    const int t = (int)(i / w), j = (int)(i % w);
+    vt[(int64_t)j * vt_stride + slot0 + t] = v[(int64_t)(slot0 + t) * w + j];
+}
+
 // One token through the layer stack (and head / greedy by mode) on stream s.
 static int r_enqueue_moe(int mode, float penalty, hipStream_t s);
 static int r_enqueue(int mode, float penalty, hipStream_t s) {
@@ -1668,6 +1679,8 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.v = R.v;
             A.kcache = Ly.k;
             A.vcache = Ly.v;
+            A.vtcache = Ly.vt;
+            A.vt_stride = (int32_t)R.vt_stride;
             A.cos_t = R.cos_t;
             A.sin_t = R.sin_t;
             A.st = R.st;
@@ -1715,6 +1728,8 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.q = R.q;
             E.k = Ly.k;
             E.v = Ly.v;
+            E.vt = Ly.vt;
+            E.vt_stride = (int32_t)R.vt_stride;
             E.out = R.attn;
             E.st = R.st;
             E.n_heads = R.n_heads;
@@ -2020,6 +2035,8 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
             A.v = R.pv;
             A.kcache = Ly.k;
             A.vcache = Ly.v;
+            A.vtcache = Ly.vt;
+            A.vt_stride = (int32_t)R.vt_stride;
             A.cos_t = R.cos_t;
             A.sin_t = R.sin_t;
             A.st = nullptr;
@@ -2046,6 +2063,8 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
             E.q = R.pq;
             E.k = Ly.k;
             E.v = Ly.v;
+            E.vt = Ly.vt;
+            E.vt_stride = (int32_t)R.vt_stride;
             E.out = R.pattn;
             E.n_heads = R.n_heads;
             E.n_kv = R.n_kv;
@@ -2303,6 +2322,9 @@ int rusty_hip_resident_set_layer(uint32_t l, const RustyResidentLayerDesc *d) {
         return 0;
     RH_CHECK(hipMemset(Ly.k, 0, (size_t)R.storage * kd * 4));
     RH_CHECK(hipMemset(Ly.v, 0, (size_t)R.storage * vdim * 4));
+    R.vt_stride = (R.storage + 63) / 64 * 64;
+    if (!r_alloc((void **)&Ly.vt, (size_t)R.vt_stride * vdim * 4)) return 0;
+    RH_CHECK(hipMemset(Ly.vt, 0, (size_t)R.vt_stride * vdim * 4));
     r_invalidate_graphs();
     return 1;
 }
@@ -2488,6 +2510,12 @@ int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint
     if (!dst) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
     RH_CHECK(hipMemcpy(dst + (size_t)slot0 * w, host_in, (size_t)n_slots * w * 4, hipMemcpyHostToDevice));
+    if (which && R.L[l].vt && n_slots > 0) {
+        rh_launch(kv_transpose_kernel, dim3((n_slots * w + 255) / 256), dim3(256), 0, g.s, (const float *)dst, (int)w,
+                  (int)slot0, (int)n_slots, R.L[l].vt, (int)R.vt_stride);
+        RH_LAUNCH_OK();
+        RH_CHECK(hipStreamSynchronize(g.s));
+    }
     return 1;
 }
 
