@@ -147,6 +147,7 @@ __device__ __forceinline__ bool is_x4(const AttnExactArgs &A, int g) {
 }
 
 #define EX_TILE 64
+#define CH_MAXG 8    // query heads per kv head handled by the lane-sliced scores and chain kernels
 
 // e of (kv head h, head g of its group, position t).
 __device__ __forceinline__ size_t e_index(const AttnExactArgs &A, int h, int g, int t) {
@@ -269,6 +270,104 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     }
 }
 
+// A, head dims that are multiples of 32 up to 128: the K tile is staged in
+// LDS per row as [AVX2 lane l][m] (element 8m + l), so lane l of an 8-lane
+// group reads its hd/8 elements with hd/32 16-byte reads; q's slice for the
+// same lane sits in registers.  One wave per query head (64 positions x 8
+// lanes), the per-lane accumulation in the reference's order:
+//   dot_f32x4_avx2 (heads 0..3 of kv_mul 4/6): acc = fma(q, k, acc) over m;
+//   dot_f32_avx2 (the others): four accumulators over m = 4c + j, then
+//   (a0 + a1) + (a2 + a3);
+// then hsum_avx across the 8 lanes.  Writes the same scores and tile maxima
+// as attn_exact_scores_kernel.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A0) {
+    constexpr int M = HD / 8;        // elements per lane
+    constexpr int LS = M + 4;        // LDS floats per lane slice (padded: a row's 8 slices hit distinct banks)
+    constexpr int RS = 8 * LS;       // LDS floats per K row
+    const AttnExactArgs A = tok_view(A0);
+    __shared__ __align__(16) float s_k[EX_TILE * RS];
+    __shared__ float s_sc[CH_MAXG * EX_TILE];
+    int s0, e0;
+    exact_range(A, s0, e0);
+    const int ctx = e0 - s0 + 1;
+    const int t_base = blockIdx.x * EX_TILE;
+    if (ctx <= 0 || t_base >= ctx) return;
+    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, kvm = A.kv_mul;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nt = min(EX_TILE, ctx - t_base);
+    const float *kh = A.k + (size_t)h * HD;
+    {
+        // thread -> (row r0 + k*rstep, float4 column c4); element 4*c4 + i
+        // goes to lane slice (4*c4 + i) % 8, position (4*c4 + i) / 8
+        constexpr int H4 = HD / 4, RSTEP = 256 / H4;
+        const int r0 = tid / H4, c4 = tid - r0 * H4;
+        const int lbase = (4 * c4) & 7, m = (4 * c4) >> 3;
+        const int base = (s0 + t_base) % A.slot_count;
+#pragma unroll
+        for (int tt = r0; tt < EX_TILE; tt += RSTEP) {
+            int slot = base + min(tt, nt - 1);
+            if (slot >= A.slot_count) slot -= A.slot_count;
+            const float4 v = *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
+            float *d = s_k + tt * RS + m;
+            d[(lbase + 0) * LS] = v.x;
+            d[(lbase + 1) * LS] = v.y;
+            d[(lbase + 2) * LS] = v.z;
+            d[(lbase + 3) * LS] = v.w;
+        }
+    }
+    const int l = lane & 7, sub = lane >> 3;
+    __syncthreads();
+    for (int g = wave; g < kvm; g += 4) {
+        const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4;
+        const float *qg = A.q + (size_t)(h * kvm + g) * HD;
+        float q[M];
+#pragma unroll
+        for (int mm = 0; mm < M; mm++) q[mm] = qg[8 * mm + l];
+#pragma unroll
+        for (int it = 0; it < EX_TILE / 8; it++) {
+            const int tt = 8 * it + sub;
+            const float *kr = s_k + tt * RS + l * LS;
+            float k[M];
+#pragma unroll
+            for (int r = 0; r < M / 4; r++) {
+                const float4 f = *(const float4 *)(kr + 4 * r);
+                k[4 * r] = f.x;
+                k[4 * r + 1] = f.y;
+                k[4 * r + 2] = f.z;
+                k[4 * r + 3] = f.w;
+            }
+            float y;
+            if (x4) {
+                y = 0.0f;
+#pragma unroll
+                for (int mm = 0; mm < M; mm++) y = fmaf(q[mm], k[mm], y);
+            } else {
+                float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c = 0; c < M / 4; c++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) a[j] = fmaf(q[4 * c + j], k[4 * c + j], a[j]);
+                y = (a[0] + a[1]) + (a[2] + a[3]);
+            }
+            const float a = y + __shfl_xor(y, 4, 64);
+            const float b = a + __shfl_xor(a, 1, 64);
+            const float d = b + __shfl_xor(b, 2, 64);
+            if (l == 0) s_sc[g * EX_TILE + tt] = d * A.scale;
+        }
+    }
+    __syncthreads();
+    // coalesced score rows + tile maxima (max is exact in any order)
+    const int ntl = A.cap / EX_TILE;
+    for (int g = wave; g < kvm; g += 4) {
+        const int head = h * kvm + g;
+        float v = lane < nt ? s_sc[g * EX_TILE + lane] : -INFINITY;
+        if (lane < nt) A.scores[(size_t)head * A.cap + t_base + lane] = v;
+        float mx = wave_max(v);
+        if (lane == 0) A.tmax[(size_t)head * ntl + blockIdx.x] = mx;
+    }
+}
+
 // B: one wave per (tile of 64 positions, query head).  The running max before
 // each step is max(initial, maxima of the earlier tiles, prefix max inside the
 // tile), so every step's branch and expf argument are known without a serial
@@ -325,7 +424,6 @@ __global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
 // their LDS reads: e enters each FMA through its DPP row_newbcast operand
 // (lane j of a 16-lane row holds step j), V comes from LDS, and producer
 // waves stream both into a ring by direct global->LDS loads.
-#define CH_MAXG 8    // query heads per kv head handled by the chain kernel
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ void dma16(const void *src, void *lds) {
