@@ -370,7 +370,7 @@ static int grid_cap() { return g.n_cu * 8; }
 // Persistent grid: as many workgroups as fit on the device at once (queried
 // once per kernel instantiation), never more than the tiles need.
 template <class Kern>
-static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
+static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, bool prologue = false) {
     // RUSTY_HIP_WG_PER_CU caps the resident workgroups per CU (sweeps)
     static std::map<const void *, int> occ;
     auto it = occ.find((const void *)kernel);
@@ -383,16 +383,18 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
     } else {
         per_cu = it->second;
     }
-    // Two resident workgroups per CU by default: each wave then runs more
-    // tiles through its two-deep load pipeline, which amortises the
-    // activation prologue (measured on the 8B decode: 290 -> 298 tok/s
-    // against the occupancy limit of three).
+    // Launches that build their activation in a prologue run two resident
+    // workgroups per CU: each wave then takes more tiles through its two-deep
+    // load pipeline, which amortises the prologue (8B decode: 290 -> 298
+    // tok/s); the others keep the occupancy limit, which streams faster on
+    // its own (Q4_K 14336x4096: 11.0 against 12.6 us).
     static int cap = -1;
     if (cap < 0) {
         const char *e = getenv("RUSTY_HIP_WG_PER_CU");
-        cap = e ? atoi(e) : 2;
+        cap = e ? atoi(e) : 0;
     }
     if (cap > 0) per_cu = std::min(per_cu, cap);
+    else if (prologue) per_cu = std::min(per_cu, 2);
     int need = (n_tiles + waves_per_wg - 1) / waves_per_wg;
     int grid = std::min(need, per_cu * g.n_cu);
     return grid < 1 ? 1 : grid;
@@ -401,7 +403,7 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg) {
 template <int FMT, bool SW, int U, int ACT>
 static int launch_kq_act(const GemvArgs &A, hipStream_t s) {
     auto kern = gemv_kq_kernel<FMT, SW, U, ACT>;
-    int grid = persistent_grid(kern, A.n_tiles, 4);
+    int grid = persistent_grid(kern, A.n_tiles, 4, ACT != KQ_ACT_XQ);
     ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
     rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
