@@ -143,7 +143,7 @@ def main():
 
     dim, hid = cfg["dim"], cfg["hidden_dim"]
     nb = dim // 256
-    swiglu_bytes = 2 * hid * nb * 144 + dim * 4 + hid * 4  # gate+up blocks, x (f32 units), y
+    swiglu_bytes = 2 * hid * nb * 144 + 2 * dim * 4 + hid * 4  # gate+up blocks, x and the norm weights, y
     tot, cnt = prof.get("gemv_kquant_swiglu", (0.0, 0))
     avg_ms = tot / cnt if cnt else float("nan")
     achieved = swiglu_bytes / (avg_ms * 1e-3) / 1e9 if cnt else 0.0
