@@ -757,27 +757,51 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 RH_WAIT_LGKM0();
                 cons_fma16_dpp(a1, v1, o);
             } else if (X4 || DEN) {
-                // a group holding new maxima, grouped form: every step as
-                // o = fma(a, v, o*m), straight-line
+                // a group holding new maxima: each of its two tiles runs the
+                // straight-line FMA form when it has none, else the grouped
+                // form o = fma(a, v, o*m) on every step
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
-                float u0, u1;
-                u0 = ma[lane & 15];
-#define C4_AFF(ET, MT, VP, K, NA, NU, NV, CA, CU, CV) \
-    RH_WAIT_LGKM0();                                  \
-    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV); \
-    __builtin_amdgcn_sched_barrier(0);                \
-    cons_affine16_dpp(CA, CU, CV, o);                 \
+                float u0 = 1.0f, u1 = 1.0f;
+#define C4_FAST(ET, VP, K, NA, NV, CA, CV)       \
+    RH_WAIT_LGKM0();                             \
+    c4_load16<DEN, VT>(ET, VP, K, lane, NA, NV); \
+    __builtin_amdgcn_sched_barrier(0);           \
+    cons_fma16_dpp(CA, CV, o);                   \
     __builtin_amdgcn_sched_barrier(0);
-                C4_AFF(ea, ma, va, 1, a1, u1, v1, a0, u0, v0)
-                C4_AFF(ea, ma, va, 2, a0, u0, v0, a1, u1, v1)
-                C4_AFF(ea, ma, va, 3, a1, u1, v1, a0, u0, v0)
-                C4_AFF(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1)
-                C4_AFF(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0)
-                C4_AFF(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1)
-                C4_AFF(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0)
+#define C4_AFF(ET, MT, VP, K, NA, NU, NV, CA, CU, CV)     \
+    RH_WAIT_LGKM0();                                      \
+    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV); \
+    __builtin_amdgcn_sched_barrier(0);                    \
+    cons_affine16_dpp(CA, CU, CV, o);                     \
+    __builtin_amdgcn_sched_barrier(0);
+                if ((gm & 0x0Fu) == 0u) {
+                    C4_FAST(ea, va, 1, a1, v1, a0, v0)
+                    C4_FAST(ea, va, 2, a0, v0, a1, v1)
+                    C4_FAST(ea, va, 3, a1, v1, a0, v0)
+                    C4_FAST(eb, vb, 0, a0, v0, a1, v1)
+                } else {
+                    u0 = ma[lane & 15];
+                    C4_AFF(ea, ma, va, 1, a1, u1, v1, a0, u0, v0)
+                    C4_AFF(ea, ma, va, 2, a0, u0, v0, a1, u1, v1)
+                    C4_AFF(ea, ma, va, 3, a1, u1, v1, a0, u0, v0)
+                    C4_AFF(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1)
+                }
+                if ((gm & 0xF0u) == 0u) {
+                    C4_FAST(eb, vb, 1, a1, v1, a0, v0)
+                    C4_FAST(eb, vb, 2, a0, v0, a1, v1)
+                    C4_FAST(eb, vb, 3, a1, v1, a0, v0)
+                    RH_WAIT_LGKM0();
+                    cons_fma16_dpp(a1, v1, o);
+                } else {
+                    u0 = mb[lane & 15];
+                    C4_AFF(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0)
+                    C4_AFF(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1)
+                    C4_AFF(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0)
+                    RH_WAIT_LGKM0();
+                    cons_affine16_dpp(a1, u1, v1, o);
+                }
+#undef C4_FAST
 #undef C4_AFF
-                RH_WAIT_LGKM0();
-                cons_affine16_dpp(a1, u1, v1, o);
             } else {
                 // scale_add heads: each step in its own form, chunk by chunk
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
