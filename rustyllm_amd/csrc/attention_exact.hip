@@ -107,7 +107,31 @@ struct AttnExactArgs {
     // lane four steps of its value dim.  null: V only.
     const float *vt;
     int32_t vt_stride;
+    // Decode only (n_tok = 0): the lane-sliced scores kernel also does the
+    // RoPE + KV store of the current position (rope_kv_kernel's work) from
+    // the raw q/k/v in rope, so that launch is not needed.
+    RopeArgs rope;
+    int32_t fuse_rope;
 };
+
+// Element e of a head vector x after RoPE with the row's cos/sin, exactly as
+// rope_kv_kernel computes it (interleaved pairs (2p, 2p+1) or NeoX pairs
+// (p, p + hd/2); r0 = v0*c - v1*s, r1 = v0*s + v1*c).
+__device__ __forceinline__ float rope_elem(const float *x, int e, int half, bool neox, const float *ct,
+                                           const float *st) {
+    int p, i0, i1;
+    if (neox) {
+        p = e < half ? e : e - half;
+        i0 = p;
+        i1 = p + half;
+    } else {
+        p = e >> 1;
+        i0 = 2 * p;
+        i1 = i0 + 1;
+    }
+    const float c = ct[p], s = st[p], v0 = x[i0], v1 = x[i1];
+    return e == i0 ? v0 * c - v1 * s : v0 * s + v1 * c;
+}
 
 // The single-token view of token blockIdx.z of a multi-token launch: its
 // range is start_t (or the window's start) ..= pos0 + z.
@@ -287,6 +311,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     constexpr int RS = 8 * LS;       // LDS floats per K row
     const AttnExactArgs A = tok_view(A0);
     __shared__ __align__(16) float s_k[EX_TILE * RS];
+    __shared__ __align__(16) float s_q[CH_MAXG * RS];  // the heads' q, lane-sliced like a K row
     __shared__ float s_sc[CH_MAXG * EX_TILE];
     int s0, e0;
     exact_range(A, s0, e0);
@@ -297,6 +322,21 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nt = min(EX_TILE, ctx - t_base);
     const float *kh = A.k + (size_t)h * HD;
+    // fused RoPE: the current position e0 and its cos/sin row
+    const RopeArgs &RA = A.rope;
+    const bool fuse = A.fuse_rope != 0 && e0 < RA.max_pos;
+    const int half = HD / 2;
+    const float *ct = RA.cos_t + (size_t)e0 * half, *stb = RA.sin_t + (size_t)e0 * half;
+    {
+        // q of the kv head's query heads (rotated here when RoPE is fused),
+        // element e of head g at lane slice e % 8, position e / 8
+        const float *qsrc = (fuse ? RA.q : A.q) + (size_t)h * kvm * HD;
+        for (int i = tid; i < kvm * HD; i += 256) {
+            const int g = i / HD, e = i - g * HD;
+            const float v = fuse ? rope_elem(qsrc + (size_t)g * HD, e, half, RA.neox != 0, ct, stb) : qsrc[i];
+            s_q[g * RS + (e & 7) * LS + (e >> 3)] = v;
+        }
+    }
     {
         // thread -> (row r0 + k*rstep, float4 column c4); element 4*c4 + i
         // goes to lane slice (4*c4 + i) % 8, position (4*c4 + i) / 8
@@ -317,13 +357,39 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         }
     }
     const int l = lane & 7, sub = lane >> 3;
+    const int tt_cur = e0 - s0 - t_base;  // the current position's row, if in this tile
+    if (fuse && tt_cur >= 0 && tt_cur < EX_TILE) {
+        // k rotated into the tile (over the cache row staged above) and both
+        // cache rows of the current position stored, as rope_kv_kernel does
+        __syncthreads();
+        const int slot = RA.ring ? e0 % RA.slots : e0;
+        const int kvd = RA.n_kv * HD, vvd = RA.n_kv * RA.vd;
+        for (int e = tid; e < HD; e += 256) {
+            const float kr = rope_elem(RA.k + (size_t)h * HD, e, half, RA.neox != 0, ct, stb);
+            s_k[tt_cur * RS + (e & 7) * LS + (e >> 3)] = kr;
+            RA.kcache[(size_t)slot * kvd + h * HD + e] = kr;
+        }
+        for (int e = tid; e < RA.vd; e += 256) {
+            const float v = RA.v[(size_t)h * RA.vd + e];
+            RA.vcache[(size_t)slot * vvd + h * RA.vd + e] = v;
+            if (RA.vtcache) RA.vtcache[(size_t)(h * RA.vd + e) * RA.vt_stride + slot] = v;
+        }
+    }
     __syncthreads();
     for (int g = wave; g < kvm; g += 4) {
         const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4;
-        const float *qg = A.q + (size_t)(h * kvm + g) * HD;
         float q[M];
+        {
+            const float *qr = s_q + g * RS + l * LS;
 #pragma unroll
-        for (int mm = 0; mm < M; mm++) q[mm] = qg[8 * mm + l];
+            for (int r = 0; r < M / 4; r++) {
+                const float4 f = *(const float4 *)(qr + 4 * r);
+                q[4 * r] = f.x;
+                q[4 * r + 1] = f.y;
+                q[4 * r + 2] = f.z;
+                q[4 * r + 3] = f.w;
+            }
+        }
 #pragma unroll
         for (int it = 0; it < EX_TILE / 8; it++) {
             const int tt = 8 * it + sub;

@@ -782,10 +782,18 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     A.kvec = (A.key_stride % 4 == 0 && A.hd % 4 == 0 && ((uintptr_t)A.k & 15) == 0) ? 1 : 0;
     const int n_out = A.n_heads * A.vd;
     if (xq.qs && n_out % 256 != 0) return 0;
+    // the lane-sliced scores kernel: 16-byte K rows, kv_mul <= 8, hd 64 or 128
+    const bool s8 = A.kvec && A.kv_mul <= CH_MAXG && (A.hd == 64 || A.hd == 128) && A.slot_count >= EX_TILE;
+    if (A.fuse_rope && (!s8 || A.n_tok > 0 || A.rope.hd != A.hd)) {
+        // the RoPE + KV store the scores kernel would have done
+        ProfScope ps("rope_kv", s);
+        const int work = A.rope.n_heads * (A.rope.hd / 2) + A.rope.n_kv * (A.rope.hd / 2) + A.rope.n_kv * A.rope.vd;
+        rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A.rope);
+        RH_LAUNCH_OK();
+        A.fuse_rope = 0;
+    }
     {
         ProfScope ps("attn_exact_scores", s);
-        // the lane-sliced kernel: 16-byte K rows, kv_mul <= 8, hd 64 or 128
-        const bool s8 = A.kvec && A.kv_mul <= CH_MAXG && (A.hd == 64 || A.hd == 128) && A.slot_count >= EX_TILE;
         if (s8 && A.hd == 128) {
             rh_launch(attn_exact_scores8_kernel<128>, dim3(ntl, A.n_kv, nz), dim3(256), 0, s, A);
         } else if (s8) {
@@ -1685,6 +1693,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
         RLayer &Ly = R.L[l];
         MatSpec qkv[3] = {{Ly.w[0], R.q, Ly.bias[0]}, {Ly.w[1], R.k, Ly.bias[1]}, {Ly.w[2], R.v, Ly.bias[2]}};
         if (!gemv_multi_act(qkv, 3, dim, EPI_STORE, r_act_norm(Ly.attn_norm), s)) return 0;
+        RopeArgs r_rope;
         {
             RopeArgs A;
             memset(&A, 0, sizeof(A));
@@ -1706,10 +1715,13 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.slots = R.storage;
             A.ring = 0;
             A.neox = R.neox;
-            int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
-            ProfScope ps("rope_kv", s);
-            rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
-            RH_LAUNCH_OK();
+            r_rope = A;
+            if (attn_fast_mode()) {
+                int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+                ProfScope ps("rope_kv", s);
+                rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
+                RH_LAUNCH_OK();
+            }
         }
         ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
         act_o.xq = attn_cols % 256 == 0 ? R.xq_attn : XQ{};
@@ -1757,6 +1769,8 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.window = 0;
             E.cap = R.ex_cap;
             E.scale = 1.0f / sqrtf((float)R.hd);
+            E.rope = r_rope;  // RoPE + KV store inside the scores launch
+            E.fuse_rope = 1;
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
             act_o.mode = ACT_DEN;
