@@ -434,30 +434,34 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     }
 }
 
-// B: one wave per (tile of 64 positions, query head).  The running max before
+// B: one wave per (tile of 64 positions, query head), four tiles per workgroup.  The running max before
 // each step is max(initial, maxima of the earlier tiles, prefix max inside the
 // tile), so every step's branch and expf argument are known without a serial
 // scan.  On a new max the multiplier is isfinite(run) ? expf(run - s) : 0
 // (the factor the old output and denominator are scaled by) and the
 // coefficient 1; otherwise the coefficient is expf(s - run) and the
 // multiplier 1.  The new-max steps are also marked in newmask.
-__global__ __launch_bounds__(64) void attn_exact_coef_kernel(AttnExactArgs A0) {
+__global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
-    const int tile = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+    // four tiles per workgroup, one per wave
+    const int lane = threadIdx.x & 63, head = blockIdx.y;
+    const int tile = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (ctx <= 0 || tile * EX_TILE >= ctx) return;
     const int ntl = A.cap / EX_TILE;
     const float *tm = A.tmax + (size_t)head * ntl;
+    // both loads in flight together: this tile's scores and the maxima of
+    // the tiles before it
+    const int t = tile * EX_TILE + lane;
+    const bool valid = t < ctx;
+    const float s = A.scores[(size_t)head * A.cap + min(t, ctx - 1)];
     float m = -INFINITY;
     for (int j = lane; j < tile; j += 64) m = fmaxf(m, tm[j]);
     m = wave_max(m);
     if (A.sinks) m = fmaxf(A.sinks[head], m);
-    const int t = tile * EX_TILE + lane;
-    const bool valid = t < ctx;
-    const float s = valid ? A.scores[(size_t)head * A.cap + t] : -INFINITY;
-    float p = s;  // inclusive prefix max over lanes
+    float p = valid ? s : -INFINITY;  // inclusive prefix max over lanes
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         float q = __shfl_up(p, o, 64);

@@ -807,7 +807,7 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     {
         ProfScope ps("attn_exact_coef", s);
-        rh_launch(attn_exact_coef_kernel, dim3(ntl, A.n_heads, nz), dim3(64), 0, s, A);
+        rh_launch(attn_exact_coef_kernel, dim3((ntl + 3) / 4, A.n_heads, nz), dim3(256), 0, s, A);
         RH_LAUNCH_OK();
     }
     {
