@@ -975,6 +975,96 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
     }
 }
 
+// C for many query tokens at once (prefill: grid z = token): a token's
+// recurrence is short (its own position), so the launch is bound by
+// throughput, not by one chain's latency.  Each wave is one independent task
+// (token, kv head, group of four query heads, 16 value dims) or the group's
+// denominators, with no LDS ring: V comes straight from the cache (the
+// transposed copy gives four steps of a lane's dim per 16-byte load), the
+// coefficients, multipliers and new-max words from global memory, and many
+// waves per SIMD hide the latency.  The update forms are the chain4
+// consumer's, step for step.
+__global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
+    int s0, e0;
+    exact_range(A, s0, e0);
+    const int ctx = e0 - s0 + 1;
+    const int kvm = A.kv_mul, ngrp = (kvm + 3) / 4, nsl = A.vd / 16;
+    const int n_chain = A.n_kv * ngrp * nsl, n_task = n_chain + A.n_kv * ngrp;
+    const int task = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (ctx <= 0 || task >= n_task) return;
+    const bool den = task >= n_chain;
+    const int r = den ? task - n_chain : task;
+    const int h = r % A.n_kv, rr = r / A.n_kv;
+    const int g0 = 4 * (den ? rr : rr / nsl), slice = den ? 0 : rr % nsl;
+    const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
+    const int g = g0 + row, gr = min(g, kvm - 1);
+    const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
+    const float *ef = A.e + e_index(A, h, gr, 0), *mf = A.mul + e_index(A, h, gr, 0);
+    const uint32_t *mk = A.newmask + (size_t)(h * kvm + gr) * (A.cap / 32);
+    const int dim = h * A.vd + slice * 16 + dcol;
+    const bool vt = A.vt != nullptr && (s0 & 3) == 0 && e0 < A.slot_count &&
+                    s0 + (ctx + EX_TILE - 1) / EX_TILE * EX_TILE <= A.vt_stride;
+    const float *vtr = vt ? A.vt + (size_t)dim * A.vt_stride + s0 : nullptr;
+    float o = (den && A.sinks) ? 1.0f : 0.0f;
+    for (int k = 0; 16 * k < ctx; k++) {
+        const int n = min(16, ctx - 16 * k);
+        const float e16 = ef[16 * k + dcol], m16 = mf[16 * k + dcol];
+        const uint32_t bits = (mk[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+        float v[16];
+        if (den) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = 1.0f;
+        } else if (vt) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4 *)(vtr + 16 * k + 4 * q);
+                v[4 * q] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int slot = (s0 + 16 * k + min(j, n - 1)) % A.slot_count;
+                v[j] = A.v[(size_t)slot * A.value_stride + dim];
+            }
+        }
+        if (n == 16) {
+            const uint32_t f = bits ? 1u : 0u;
+            const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
+                                 __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
+            if (any == 0u) {
+                cons_fma16_dpp(e16, v, o);
+            } else if (x4 || den) {
+                cons_affine16_dpp(e16, m16, v, o);
+            } else {
+                float ee[16], mm[16];
+                bcast16_all(e16, ee);
+                bcast16_all(m16, mm);
+                chain_steps16_flags<false, false>(ee, mm, v, o, bits);
+            }
+        } else {
+            // the last, partial chunk: step by step in its own form
+            for (int j = 0; j < n; j++) {
+                const float e = ef[16 * k + j], mlt = mf[16 * k + j];
+                const float vj = v[j];
+                const float on = fmaf(e, vj, o);
+                const float ox = (x4 || den) ? fmaf(vj, 1.0f, o * mlt) : fmaf(o, mlt, vj);
+                o = ((bits >> j) & 1u) ? ox : on;
+            }
+        }
+    }
+    if (g < kvm) {
+        if (den) {
+            if (dcol == 0) A.den[h * kvm + g] = o;
+        } else {
+            A.out[(size_t)(h * kvm + g) * A.vd + slice * 16 + dcol] = o;
+        }
+    }
+}
+
 // C (any layout): one wave per (query head, 64 value dims), grid (n_heads,
 // ceil(vd/64)); V read straight from the cache, 32 steps per batch.  The
 // denominator runs in every lane beside the output; slice 0 stores it.

@@ -817,7 +817,11 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
                         A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
                         (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
-        if (c4) {
+        if (c4 && A.n_tok > 0) {
+            // many query tokens: one independent wave per task, no LDS ring
+            const int tasks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
+            rh_launch(attn_exact_chain_tok_kernel, dim3((tasks + 3) / 4, 1, nz), dim3(256), 0, s, A);
+        } else if (c4) {
             const int blocks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
             rh_launch(attn_exact_chain4_kernel, dim3(blocks, 1, nz), dim3(64 * C4_WAVES), 0, s, A);
         } else {
