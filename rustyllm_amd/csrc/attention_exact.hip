@@ -327,6 +327,21 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     const bool fuse = A.fuse_rope != 0 && e0 < RA.max_pos;
     const int half = HD / 2;
     const float *ct = RA.cos_t + (size_t)e0 * half, *stb = RA.sin_t + (size_t)e0 * half;
+    // the K tile's loads first (registers), so their latency overlaps the q
+    // staging below; element 4*c4 + i of a row goes to lane slice
+    // (4*c4 + i) % 8, position (4*c4 + i) / 8
+    constexpr int H4 = HD / 4, RSTEP = 256 / H4, NKR = EX_TILE / RSTEP;
+    const int r0 = tid / H4, c4 = tid - r0 * H4;
+    float4 kreg[NKR];
+    {
+        const int base = (s0 + t_base) % A.slot_count;
+#pragma unroll
+        for (int i = 0; i < NKR; i++) {
+            int slot = base + min(r0 + i * RSTEP, nt - 1);
+            if (slot >= A.slot_count) slot -= A.slot_count;
+            kreg[i] = *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
+        }
+    }
     {
         // q of the kv head's query heads (rotated here when RoPE is fused),
         // element e of head g at lane slice e % 8, position e / 8
@@ -338,22 +353,14 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         }
     }
     {
-        // thread -> (row r0 + k*rstep, float4 column c4); element 4*c4 + i
-        // goes to lane slice (4*c4 + i) % 8, position (4*c4 + i) / 8
-        constexpr int H4 = HD / 4, RSTEP = 256 / H4;
-        const int r0 = tid / H4, c4 = tid - r0 * H4;
         const int lbase = (4 * c4) & 7, m = (4 * c4) >> 3;
-        const int base = (s0 + t_base) % A.slot_count;
 #pragma unroll
-        for (int tt = r0; tt < EX_TILE; tt += RSTEP) {
-            int slot = base + min(tt, nt - 1);
-            if (slot >= A.slot_count) slot -= A.slot_count;
-            const float4 v = *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
-            float *d = s_k + tt * RS + m;
-            d[(lbase + 0) * LS] = v.x;
-            d[(lbase + 1) * LS] = v.y;
-            d[(lbase + 2) * LS] = v.z;
-            d[(lbase + 3) * LS] = v.w;
+        for (int i = 0; i < NKR; i++) {
+            float *d = s_k + (r0 + i * RSTEP) * RS + m;
+            d[(lbase + 0) * LS] = kreg[i].x;
+            d[(lbase + 1) * LS] = kreg[i].y;
+            d[(lbase + 2) * LS] = kreg[i].z;
+            d[(lbase + 3) * LS] = kreg[i].w;
         }
     }
     const int l = lane & 7, sub = lane >> 3;
