@@ -322,3 +322,29 @@ def test_greedy_matches_reference(hip):
     for lg, rec, pen in cases:
         tok_ref, _ = O.greedy(lg, rec, pen)
         assert hip.debug_greedy(lg, rec, pen) == tok_ref
+
+
+@pytest.mark.parametrize("t,rows,cols", [(12, 4096, 4096), (14, 1024, 14336), (8, 512, 14336), (39, 300, 4096)])
+def test_bench_matvec_equals_oracle_rows(hip, t, rows, cols):
+    """The sweep's device-resident GEMV (rusty_hip_bench_matvec, weights
+    rotated over device copies) returns the reference rows bit for bit, as
+    the per-op export does."""
+    w = _synth_weight(t, rows, cols, rows + 3 * cols + t)
+    x = np.random.default_rng(cols + t).standard_normal(cols).astype(np.float32)
+    got = hip.bench_matvec(t, w, x, rows, cols, 3, 4)
+    hip.weight_cache_clear()
+    ref = O.matvec(t, w, x, rows, cols, threads=8)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), np.max(np.abs(got - ref))
+
+
+@pytest.mark.parametrize("ctx", [100, 4096])
+def test_bench_attention_exact_and_split_k_agree(hip, ctx):
+    """The sweep's attention on device-generated K/V: the exact kernels and
+    the split-K kernels (two independent orders of the same softmax) agree
+    within 1e-4 x ||o_h|| per head, and both are finite."""
+    nh, kvm, hd = 32, 4, 128
+    ex = hip.bench_attention(nh, kvm, hd, ctx, 2, 3, 11, "exact").reshape(nh, hd)
+    fa = hip.bench_attention(nh, kvm, hd, ctx, 2, 3, 11, "fast").reshape(nh, hd)
+    assert np.all(np.isfinite(ex)) and np.all(np.isfinite(fa))
+    err = np.abs(ex - fa).max(axis=1)
+    assert np.all(err <= 1e-4 * np.linalg.norm(ex, axis=1) + 1e-7), err.max()
