@@ -730,10 +730,16 @@ static bool attn_supported(int hd, int vd, int kv_mul) {
     return hd == vd && (hd == 64 || hd == 128) &&
            (kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 5 || kv_mul == 6 || kv_mul == 8);
 }
-// Splits per kv head: up to four workgroups per CU (the partial kernel's
-// occupancy), each at least one ATT_TP-position sub-tile.
+// Splits per kv head: two workgroups per CU (measured at ctx 32768: 63.6 us
+// against 69.5 at four and 71.2 at one), each at least one ATT_TP-position
+// sub-tile.  RUSTY_HIP_SPLITK_PER_CU overrides it for sweeps.
 static int attn_chunks(int n_kv, int max_ctx) {
-    int want = (4 * g.n_cu + n_kv - 1) / n_kv;
+    static int per_cu = -1;
+    if (per_cu < 0) {
+        const char *e = getenv("RUSTY_HIP_SPLITK_PER_CU");
+        per_cu = e ? std::max(1, atoi(e)) : 2;
+    }
+    int want = (per_cu * g.n_cu + n_kv - 1) / n_kv;
     int by_ctx = (max_ctx + ATT_TP - 1) / ATT_TP;
     int c = std::min(want, by_ctx);
     return c < 1 ? 1 : c;
