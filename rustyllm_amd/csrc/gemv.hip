@@ -340,6 +340,35 @@ __device__ __forceinline__ float unit_block_value(const UnitLoad &L, int q, cons
 #define KQ_XQ_STRIDE 68
 #define KQ_XQ_WORDS (NB256_MAX * KQ_XQ_STRIDE > KQ_ACT_KMAX ? NB256_MAX * KQ_XQ_STRIDE : KQ_ACT_KMAX)
 
+// sum(x*x) in dot_f32_avx2's order (as sumsq_avx2_order) from x staged
+// transposed: xt[L * ld + c] = x[32c + L], so accumulator lane L (0..31) reads
+// four steps of its chain per 16-byte read.  n % 32 == 0, n/32 % 4 == 0.
+// red needs 33 floats; every thread receives the sum.
+__device__ float kq_sumsq_t(const float *xt, int ld, int n, float *red) {
+    const int C = n >> 5;
+    if (threadIdx.x < 32) {
+        const float *r = xt + threadIdx.x * ld;
+        float acc = 0.0f;
+        for (int c = 0; c < C; c += 4) {
+            const float4 f = *(const float4 *)(r + c);
+            acc = fmaf(f.x, f.x, acc);
+            acc = fmaf(f.y, f.y, acc);
+            acc = fmaf(f.z, f.z, acc);
+            acc = fmaf(f.w, f.w, acc);
+        }
+        red[threadIdx.x] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) t[l] = (red[l] + red[8 + l]) + (red[16 + l] + red[24 + l]);
+        red[32] = ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
+    }
+    __syncthreads();
+    return red[32];
+}
+
 // Q8_K of chunk c (16 consecutive elements v) into the LDS staging, exactly
 // as quantize_row_q8k (src/simd.rs:5013-5101): a block's 16 chunks sit in 16
 // consecutive lanes, which exchange the block maximum; the chunk's own sum is
@@ -534,7 +563,6 @@ __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int 
 template <int FMT, bool SWIGLU, int KQ_U, int ACT>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
     __shared__ __align__(16) int32_t s_xq[KQ_XQ_WORDS];
-    __shared__ __align__(16) float s_wf[ACT == KQ_ACT_NORM ? KQ_ACT_KMAX : 4];
     __shared__ float s_red[40];
     __shared__ float s_dx[NB256_MAX];
     __shared__ int16_t s_bs[NB32_MAX];
@@ -611,28 +639,31 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
         // rms_norm_into (src/model.rs:5429-5437): x staged as f32 in the
         // quant buffer, sum of squares in the reference's AVX2 order, then
         // (x * scale) * w per element and Q8_K of the result
-        // x and w were loaded ahead of the first tile's weights; they go to
-        // LDS before the second tile's loads are issued, so their registers
-        // are free again by then
-        float *s_xf = (float *)s_xq;
+        // x and w (this thread's 16-element chunk, loaded ahead of the first
+        // tile's weights) stay in registers; x is also staged transposed
+        // (element 32c + L at L*ld + c) for the sum of squares
+        float *s_xt = (float *)s_xq;
+        const int ld = (K >> 5) + 4;
         if (tid < n16) {
+            const int c = tid >> 1, l0 = 16 * (tid & 1);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                ((float4 *)s_xf)[4 * tid + i] = xf[i];
-                ((float4 *)s_wf)[4 * tid + i] = xf[4 + i];
+                s_xt[(l0 + 4 * i + 0) * ld + c] = xf[i].x;
+                s_xt[(l0 + 4 * i + 1) * ld + c] = xf[i].y;
+                s_xt[(l0 + 4 * i + 2) * ld + c] = xf[i].z;
+                s_xt[(l0 + 4 * i + 3) * ld + c] = xf[i].w;
             }
         }
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
         E1 = kq_epi_load<SWIGLU>(T1, lane);
         __syncthreads();
-        const float ss = sumsq_avx2_order(s_xf, K, s_red);
+        const float ss = kq_sumsq_t(s_xt, ld, K, s_red);
         const float scale = 1.0f / sqrtf(ss / (float)K + A.act_eps);
         float v[16];
-        const int c = min(tid, n16 - 1);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float4 xv = ((const float4 *)s_xf)[4 * c + i];
-            const float4 wv = ((const float4 *)s_wf)[4 * c + i];
+            const float4 xv = xf[i];
+            const float4 wv = xf[4 + i];
             v[4 * i + 0] = xv.x * scale * wv.x;
             v[4 * i + 1] = xv.y * scale * wv.y;
             v[4 * i + 2] = xv.z * scale * wv.z;
