@@ -780,14 +780,19 @@ __device__ __forceinline__ void c4_steps16(float e16, float m16, const float *v,
     }
 }
 
-// Bit k (k < 8) set when chunk k of a two-tile group has a new maximum in any
-// of the wave's four rows; the row words m0..m3 are lane-varying by row.
-__device__ __forceinline__ uint32_t c4_group_mask(uint32_t m0, uint32_t m1, uint32_t m2, uint32_t m3) {
-    uint32_t f = ((m0 & 0xFFFFu) ? 1u : 0u) | ((m0 >> 16) ? 2u : 0u) | ((m1 & 0xFFFFu) ? 4u : 0u) |
-                 ((m1 >> 16) ? 8u : 0u) | ((m2 & 0xFFFFu) ? 16u : 0u) | ((m2 >> 16) ? 32u : 0u) |
-                 ((m3 & 0xFFFFu) ? 64u : 0u) | ((m3 >> 16) ? 128u : 0u);
-    return __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) | __builtin_amdgcn_readlane(f, 32) |
-           __builtin_amdgcn_readlane(f, 48);
+// New-max summary of a two-tile group for the wave's four rows.  w: lane
+// l < 16 holds new-max word l & 1 of head (l >> 1) & 3 in tile l >> 3 of the
+// group (0 in the other lanes); bit l of lo (hi) is set when that word has a
+// new maximum in its low (high) 16 positions.  Chunk c of the group (16
+// positions) is tile c >> 2, word (c >> 1) & 1, half c & 1, so its bits are
+// c4_chunk_slow's four-head mask of the ballot of that half.
+__device__ __forceinline__ void c4_group_ballots(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    lo = (uint32_t)__builtin_amdgcn_ballot_w64((w & 0xFFFFu) != 0u);
+    hi = (uint32_t)__builtin_amdgcn_ballot_w64((w >> 16) != 0u);
+}
+template <int C>
+__device__ __forceinline__ bool c4_chunk_slow(uint32_t lo, uint32_t hi) {
+    return (((C & 1) ? hi : lo) & (0x55u << (8 * (C >> 2) + ((C >> 1) & 1)))) != 0u;
 }
 
 // The recurrence of one wave: DEN = false the outputs (lane = value dim of
@@ -808,13 +813,15 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
             const int sa = i0 & (C4_NT - 1), sb = (i0 + 1) & (C4_NT - 1);
             const float *va = &L.v[sa][VT ? 4 * dcol : dcol], *vb = &L.v[sb][VT ? 4 * dcol : dcol];
             const float *ea = &L.e[sa][row * EX_TILE], *eb = &L.e[sb][row * EX_TILE];
-            const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
-            const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
-            const uint32_t gm = c4_group_mask(m0, m1, m2, m3);
+            // the group's new-max words first, then chunk 0, so the mask
+            // is ready while chunk 0 is still in flight
+            const uint32_t wraw = L.m[(lane & 8) ? sb : sa][lane & 7];
             float a0, a1, v0[16], v1[16];
             c4_load16<DEN, VT>(ea, va, 0, lane, a0, v0);
             __builtin_amdgcn_sched_barrier(0);
-            if (gm == 0u) {
+            uint32_t glo, ghi;
+            c4_group_ballots(lane < 16 ? wraw : 0u, glo, ghi);
+            if ((glo | ghi) == 0u) {
                 // no new maximum in any of the group's 128 steps (the common
                 // case past the first tiles): straight-line FMA runs
 #define C4_FAST(ET, VP, K, NA, NV, CA, CV)   \
@@ -834,9 +841,6 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 RH_WAIT_LGKM0();
                 cons_fma16_dpp(a1, v1, o);
             } else if (X4 || DEN) {
-                // a group holding new maxima: each of its two tiles runs the
-                // straight-line FMA form when it has none, else the grouped
-                // form o = fma(a, v, o*m) on every step
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
                 float u0 = 1.0f, u1 = 1.0f;
 #define C4_FAST(ET, VP, K, NA, NV, CA, CV)       \
@@ -851,7 +855,7 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
     __builtin_amdgcn_sched_barrier(0);                    \
     cons_affine16_dpp(CA, CU, CV, o);                     \
     __builtin_amdgcn_sched_barrier(0);
-                if ((gm & 0x0Fu) == 0u) {
+                if (((glo | ghi) & 0xFFu) == 0u) {
                     C4_FAST(ea, va, 1, a1, v1, a0, v0)
                     C4_FAST(ea, va, 2, a0, v0, a1, v1)
                     C4_FAST(ea, va, 3, a1, v1, a0, v0)
@@ -863,7 +867,7 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                     C4_AFF(ea, ma, va, 3, a1, u1, v1, a0, u0, v0)
                     C4_AFF(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1)
                 }
-                if ((gm & 0xF0u) == 0u) {
+                if (((glo | ghi) & 0xFF00u) == 0u) {
                     C4_FAST(eb, vb, 1, a1, v1, a0, v0)
                     C4_FAST(eb, vb, 2, a0, v0, a1, v1)
                     C4_FAST(eb, vb, 3, a1, v1, a0, v0)
@@ -882,13 +886,15 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
             } else {
                 // scale_add heads: each step in its own form, chunk by chunk
                 const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
+                const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
+                const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
                 float u0, u1;
                 u0 = ma[lane & 15];
 #define C4_STEP(ET, MT, VP, K, NA, NU, NV, CA, CU, CV, BITS, C) \
     RH_WAIT_LGKM0();                                            \
     c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV);           \
     __builtin_amdgcn_sched_barrier(0);                          \
-    c4_steps16<X4>(CA, CU, CV, o, BITS, (gm >> (C)) & 1u);      \
+    c4_steps16<X4>(CA, CU, CV, o, BITS, c4_chunk_slow<C>(glo, ghi)); \
     __builtin_amdgcn_sched_barrier(0);
                 C4_STEP(ea, ma, va, 1, a1, u1, v1, a0, u0, v0, m0 & 0xFFFFu, 0)
                 C4_STEP(ea, ma, va, 2, a0, u0, v0, a1, u1, v1, m0 >> 16, 1)
@@ -899,7 +905,7 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
                 C4_STEP(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0, m3 & 0xFFFFu, 6)
 #undef C4_STEP
                 RH_WAIT_LGKM0();
-                c4_steps16<X4>(a1, u1, v1, o, m3 >> 16, (gm >> 7) & 1u);
+                c4_steps16<X4>(a1, u1, v1, o, m3 >> 16, c4_chunk_slow<7>(glo, ghi));
             }
         } else {
             for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
