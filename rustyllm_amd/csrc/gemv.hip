@@ -71,16 +71,20 @@ struct GemvArgs {
     int32_t act_group;
     int32_t act_store;  // prologue modes: workgroup 0 also writes the Q8_K vector it built to xq
 };
+// byte offset of a kernel's second GemvArgs argument in its argument segment
+constexpr int KARG_SECOND = (int)((sizeof(GemvArgs) + alignof(GemvArgs) - 1) / alignof(GemvArgs) * alignof(GemvArgs));
 
 // Matrix mi of a launch with mi wave-uniform.  The byval kernel argument
 // must not be indexed with a run-time value (the compiler then copies it to
 // scratch and reads it back with vector loads followed by vmcnt(0) waits,
 // which drain every weight load in flight).  The descriptor is read instead
-// through the kernarg segment pointer: GemvArgs is each kernel's first
-// argument, at offset 0, so these are scalar loads at a uniform offset.
+// through the kernarg segment pointer, at the argument's offset KOFF (0 for
+// a kernel's first argument), so these are scalar loads at a uniform offset.
 typedef const __attribute__((address_space(4))) GemvArgs KGemvArgs;
+template <int KOFF = 0>
 __device__ __forceinline__ GemvMat mat_sel(const GemvArgs &, int mi) {
-    KGemvArgs *ka = (KGemvArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    KGemvArgs *ka =
+        (KGemvArgs *)((const __attribute__((address_space(4))) char *)__builtin_amdgcn_kernarg_segment_ptr() + KOFF);
     GemvMat r;
     r.w = ka->m[mi].w;
     r.row_stride = ka->m[mi].row_stride;
@@ -543,7 +547,7 @@ __device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <bool SWIGLU>
+template <bool SWIGLU, int KOFF = 0>
 __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int tr) {
     KqTile T;
     T.valid = tile < A.n_tiles;
@@ -553,31 +557,37 @@ __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int 
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
     }
-    T.M = mat_sel(A, mi);
+    T.M = mat_sel<KOFF>(A, mi);
     T.row0 = (tile - T.M.tile_begin) * tr;
     return T;
 }
 
 // FMT: every matrix of the launch has this format (Q4_K or Q6_K).  KQ_U:
 // units per lane (a wave tile is 64*KQ_U quarter-block units).
-template <int FMT, bool SWIGLU, int KQ_U, int ACT>
-__global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
-    __shared__ __align__(16) int32_t s_xq[KQ_XQ_WORDS];
-    __shared__ float s_red[40];
-    __shared__ float s_dx[NB256_MAX];
-    __shared__ int16_t s_bs[NB32_MAX];
-    __shared__ int16_t s_s16[KMAX / 16];
-    __shared__ __align__(16) float s_v[4][64];
+struct KqShared {
+    __align__(16) int32_t xq[KQ_XQ_WORDS];
+    float red[40];
+    float dx[NB256_MAX];
+    int16_t bs[NB32_MAX];
+    int16_t s16[KMAX / 16];
+    __align__(16) float v[4][64];
+};
+
+// One workgroup's share of a launch: workgroup blk of the nblk that serve
+// A's tiles (the whole grid for a one-group launch).
+template <int FMT, bool SWIGLU, int KQ_U, int ACT, int KOFF>
+__device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqShared &SH) {
+    int32_t *s_xq = SH.xq;
+    float *s_red = SH.red;
+    float *s_dx = SH.dx;
+    int16_t *s_bs = SH.bs;
+    int16_t *s_s16 = SH.s16;
+    float(*s_v)[64] = SH.v;
 
     const int K = A.K, nb = K >> 8, nbp = (nb + 3) & ~3;
     const int tr = A.tile_rows;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
-    const int step = gridDim.x * 4;
-    int tile = blockIdx.x * 4 + wave;
-    const KqGeo<KQ_U> G = kq_geo<FMT, SWIGLU, KQ_U>(tr, nb, nbp, A.m[0].row_stride, lane);
-    const Q4KScaleSel S = q4k_scale_sel(lane & 3);
-
     // Prologue: the activation's loads first, then the first two tiles'
     // weights and epilogue operands, so that staging the activation in LDS
     // waits only for its own loads and both tiles are in flight from the
@@ -614,11 +624,18 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
         dd = A.act_den[(16 * c) / A.act_group];
     }
 
+    // the activation's loads are issued before the tile geometry's arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    const int step = nblk * 4;
+    int tile = blk * 4 + wave;
+    const KqGeo<KQ_U> G = kq_geo<FMT, SWIGLU, KQ_U>(tr, nb, nbp, A.m[0].row_stride, lane);
+    const Q4KScaleSel S = q4k_scale_sel(lane & 3);
+
     UnitLoad L0[KQ_U], L1[KQ_U];
-    KqTile T0 = kq_tile_info<SWIGLU>(A, tile, tr);
+    KqTile T0 = kq_tile_info<SWIGLU, KOFF>(A, tile, tr);
     kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
     KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
-    KqTile T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+    KqTile T1 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
     KqEpi E1;
     if (ACT != KQ_ACT_NORM) {
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
@@ -687,7 +704,7 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
         kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
     }
     __syncthreads();
-    if (ACT != KQ_ACT_XQ && A.act_store && blockIdx.x == 0) {
+    if (ACT != KQ_ACT_XQ && A.act_store && blk == 0) {
         // the same vector for a later launch that consumes it as is
         if (tid < n16) ((int4 *)A.xq.qs)[tid] = ((const int4 *)s_xq)[(tid >> 4) * (KQ_XQ_STRIDE / 4) + (tid & 15)];
         if (tid < nbs) ((int4 *)A.xq.bsums)[tid] = ((const int4 *)s_bs)[tid];
@@ -700,17 +717,36 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
                                            s_v[wave]);
         tile += step;
         if (!T1.valid) break;
-        T0 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+        T0 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
         E0 = kq_epi_load<SWIGLU>(T0, lane);
         kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T1, E1, G, S, tr, nb, nbp, lane, L1, s_xq, s_dx, s_bs, s_s16,
                                            s_v[wave]);
         tile += step;
         if (!T0.valid) break;
-        T1 = kq_tile_info<SWIGLU>(A, tile + step, tr);
+        T1 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
         E1 = kq_epi_load<SWIGLU>(T1, lane);
     }
+}
+
+template <int FMT, bool SWIGLU, int KQ_U, int ACT>
+__global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
+    __shared__ KqShared sh;
+    kq_run<FMT, SWIGLU, KQ_U, ACT, 0>(A, blockIdx.x, gridDim.x, sh);
+}
+
+// Two launch groups of different formats that build the same activation in
+// their prologue (a layer's wq/wk in Q4_K and wv in Q6_K): workgroups below
+// grid_a serve A, the rest B, so the layer's q/k/v products take one launch.
+// Every tile is computed exactly as in the one-group kernel.
+template <int FA, int UA, int FB, int UB, int ACT>
+__global__ __launch_bounds__(256) void gemv_kq2_kernel(GemvArgs A, GemvArgs B, int grid_a) {
+    __shared__ KqShared sh;
+    if ((int)blockIdx.x < grid_a)
+        kq_run<FA, false, UA, ACT, 0>(A, blockIdx.x, grid_a, sh);
+    else
+        kq_run<FB, false, UB, ACT, KARG_SECOND>(B, blockIdx.x - grid_a, gridDim.x - grid_a, sh);
 }
 
 // ---- 32-element-block formats: Q8_0 (int / f32) and MXFP4 --------------------

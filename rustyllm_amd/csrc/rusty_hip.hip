@@ -506,8 +506,10 @@ static int kq_prologue_act(const ActSpec &a, int K) {
     return -1;
 }
 
-// Launches y_i = W_i x for matrices of one category.
-static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
+// The launch arguments for y_i = W_i x over matrices of one category: the
+// category, units per lane (it) and activation mode (kact) of the launch.
+static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, GemvArgs &A, int &cat_out,
+                         int &it_out, int &kact_out) {
     if (n <= 0 || n > GEMV_MAX_MATS) return 0;
     int cat = cat_of(ms[0].w.fmt, K);
     if (!cat) return 0;
@@ -523,7 +525,6 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     }
     const int kact = cat == CAT_KQ ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
     if (kact < 0) return 0;
-    GemvArgs A;
     memset(&A, 0, sizeof(A));
     A.K = K;
     A.epi = epi;
@@ -558,9 +559,21 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     }
     A.n_tiles = tiles;
     A.tile_rows = r;
-    if (cat == CAT_KQ) {
+    if (cat == CAT_KQ)
         for (int i = 1; i < n; i++)  // gemv_multi groups by format; the kernel assumes one row stride
             if (A.m[i].fmt != A.m[0].fmt || A.m[i].row_stride != A.m[0].row_stride) return 0;
+    cat_out = cat;
+    it_out = it;
+    kact_out = kact;
+    return 1;
+}
+
+// Launches y_i = W_i x for matrices of one category.
+static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
+    GemvArgs A;
+    int cat, it, kact;
+    if (!gemv_cat_args(ms, n, K, epi, act, A, cat, it, kact)) return 0;
+    if (cat == CAT_KQ) {
         const bool q4 = A.m[0].fmt == 12;
 #define RH_KQ_U(U)                                                                                     \
     if (it == U) {                                                                                     \
@@ -617,6 +630,49 @@ static int act_materialize(const ActSpec &a, int K, ActSpec *out, hipStream_t s)
     return 0;
 }
 
+// Two K-quant launch groups of different formats (a Q4_K group and a Q6_K
+// group) that both build act in their prologue, as one launch: the
+// persistent grid is split between them in proportion to their weight bytes.
+// Returns 0 (nothing launched) for combinations without an instantiation.
+template <int UA, int UB>
+static int launch_kq2(const GemvArgs &A, const GemvArgs &B, int bytes_a, int bytes_b, hipStream_t s) {
+    auto kern = gemv_kq2_kernel<F_Q4_K, UA, F_Q6_K, UB, KQ_ACT_NORM>;
+    const int need_a = (A.n_tiles + 3) / 4, need_b = (B.n_tiles + 3) / 4;
+    const int total = persistent_grid(kern, A.n_tiles + B.n_tiles, 4, true);
+    int grid_a = (int)((double)total * bytes_a / ((double)bytes_a + bytes_b) + 0.5);
+    grid_a = std::max(1, std::min(grid_a, std::min(need_a, total - 1)));
+    const int grid_b = std::max(1, std::min(total - grid_a, need_b));
+    ProfScope ps("gemv_kquant", s);
+    rh_launch(kern, dim3(grid_a + grid_b), dim3(256), 0, s, A, B, grid_a);
+    RH_LAUNCH_OK();
+    return 1;
+}
+static int gemv_kq2(const MatSpec *ga, int na, const MatSpec *gb, int nb, int K, const ActSpec &act, hipStream_t s) {
+    static int off = -1;
+    if (off < 0) {
+        const char *e = getenv("RUSTY_HIP_KQ2");  // 0: one launch per format group
+        off = (e && atoi(e) == 0) ? 1 : 0;
+    }
+    if (off) return 0;
+    if (ga[0].w.fmt == 14) std::swap(ga, gb), std::swap(na, nb);
+    if (ga[0].w.fmt != 12 || gb[0].w.fmt != 14) return 0;
+    GemvArgs A, B;
+    int ca, ia, ka, cb, ib, kb;
+    if (!gemv_cat_args(ga, na, K, EPI_STORE, act, A, ca, ia, ka)) return 0;
+    if (!gemv_cat_args(gb, nb, K, EPI_STORE, act, B, cb, ib, kb)) return 0;
+    if (ca != CAT_KQ || cb != CAT_KQ || ka != KQ_ACT_NORM || kb != KQ_ACT_NORM) return 0;
+    B.act_store = 0;  // A's first workgroup publishes the vector
+    long long bytes_a = 0, bytes_b = 0;
+    for (int i = 0; i < na; i++) bytes_a += (long long)ga[i].w.rows * ga[i].w.stride;
+    for (int i = 0; i < nb; i++) bytes_b += (long long)gb[i].w.rows * gb[i].w.stride;
+    const int ba = (int)(bytes_a >> 10), bb = (int)(bytes_b >> 10);
+    if (ia == 1 && ib == 1) return launch_kq2<1, 1>(A, B, ba, bb, s);
+    if (ia == 2 && ib == 1) return launch_kq2<2, 1>(A, B, ba, bb, s);
+    if (ia == 1 && ib == 2) return launch_kq2<1, 2>(A, B, ba, bb, s);
+    if (ia == 2 && ib == 2) return launch_kq2<2, 2>(A, B, ba, bb, s);
+    return 0;
+}
+
 // Splits a list of matrices into launch groups (one per category; K-quant
 // groups also share one format) and launches each.
 static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, hipStream_t s) {
@@ -630,22 +686,27 @@ static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpe
     // builds (act.xq) and later groups read it instead of building it again
     const bool share = prologue && act.xq.qs != nullptr;
     ActSpec later = act_xq(act.xq, act.x);
-    int launched = 0;
     int done[GEMV_MAX_MATS] = {0};
+    MatSpec grp[GEMV_MAX_MATS][GEMV_MAX_MATS];
+    int ngrp[GEMV_MAX_MATS], n_groups = 0;
     for (int i = 0; i < n; i++) {
         if (done[i]) continue;
         int cat = cat_of(ms[i].w.fmt, K);
         if (!cat) return 0;
-        MatSpec grp[GEMV_MAX_MATS];
         int ng = 0;
         for (int j = i; j < n; j++)
             if (!done[j] && cat_of(ms[j].w.fmt, K) == cat && (cat == CAT_Q8I || ms[j].w.fmt == ms[i].w.fmt)) {
-                grp[ng++] = ms[j];
+                grp[n_groups][ng++] = ms[j];
                 done[j] = 1;
             }
-        if (!gemv_cat(grp, ng, K, epi, (share && launched > 0) ? later : use, s)) return 0;
-        launched++;
+        ngrp[n_groups++] = ng;
     }
+    // two K-quant groups sharing a prologue: one launch when the pair has an
+    // instantiation
+    if (n_groups == 2 && prologue && epi == EPI_STORE && gemv_kq2(grp[0], ngrp[0], grp[1], ngrp[1], K, use, s))
+        return 1;
+    for (int g = 0; g < n_groups; g++)
+        if (!gemv_cat(grp[g], ngrp[g], K, epi, (share && g > 0) ? later : use, s)) return 0;
     return 1;
 }
 
