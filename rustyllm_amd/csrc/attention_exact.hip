@@ -304,6 +304,32 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
 //   (a0 + a1) + (a2 + a3);
 // then hsum_avx across the 8 lanes.  Writes the same scores and tile maxima
 // as attn_exact_scores_kernel.
+// v of lane i + N of this lane's 16-lane row (lanes whose source lies past
+// the row end are not used by the callers).
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x100 + N, 0xF, 0xF, false));
+}
+
+// max over the wave, in every lane: DPP shifts inside each 16-lane row
+// leave the row's max in its lane 15, row_bcast:15 and :31 carry rows 0-1 and
+// 2-3 into lane 63 (a lane with no source keeps its own value).  Max is exact
+// in any order.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int o = __builtin_bit_cast(int, v);
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(o, o, CTRL, ROWS, 0xF, false)));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = dpp_max<0x111, 0xF>(v);  // row_shr:1
+    v = dpp_max<0x112, 0xF>(v);  // row_shr:2
+    v = dpp_max<0x114, 0xF>(v);  // row_shr:4
+    v = dpp_max<0x118, 0xF>(v);  // row_shr:8
+    v = dpp_max<0x142, 0xA>(v);  // row_bcast:15
+    v = dpp_max<0x143, 0xC>(v);  // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A0) {
     constexpr int M = HD / 8;        // elements per lane
@@ -423,9 +449,13 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
                     for (int j = 0; j < 4; j++) a[j] = fmaf(q[4 * c + j], k[4 * c + j], a[j]);
                 y = (a[0] + a[1]) + (a[2] + a[3]);
             }
-            const float a = y + __shfl_xor(y, 4, 64);
-            const float b = a + __shfl_xor(a, 1, 64);
-            const float d = b + __shfl_xor(b, 2, 64);
+            // hsum_avx of the 8 lanes, needed in lane l = 0 only: lane i
+            // takes lane i + N of its row (DPP row_shl), so lanes 0 and 8 of
+            // every row get (y0 + y4) + (y1 + y5) and (y2 + y6) + (y3 + y7)
+            // and their sum, as the xor-4/1/2 butterfly gives there
+            const float a = y + row_shl<4>(y);
+            const float b = a + row_shl<1>(a);
+            const float d = b + row_shl<2>(b);
             if (l == 0) s_sc[g * EX_TILE + tt] = d * A.scale;
         }
     }
@@ -436,7 +466,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         const int head = h * kvm + g;
         float v = lane < nt ? s_sc[g * EX_TILE + lane] : -INFINITY;
         if (lane < nt) A.scores[(size_t)head * A.cap + t_base + lane] = v;
-        float mx = wave_max(v);
+        const float mx = wave_max_dpp(v);
         if (lane == 0) A.tmax[(size_t)head * ntl + blockIdx.x] = mx;
     }
 }
