@@ -496,15 +496,20 @@ __global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) 
     const float s = A.scores[(size_t)head * A.cap + min(t, ctx - 1)];
     float m = -INFINITY;
     for (int j = lane; j < tile; j += 64) m = fmaxf(m, tm[j]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     if (A.sinks) m = fmaxf(A.sinks[head], m);
-    float p = valid ? s : -INFINITY;  // inclusive prefix max over lanes
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        float q = __shfl_up(p, o, 64);
-        if (lane >= o) p = fmaxf(p, q);
-    }
-    float prev = __shfl_up(p, 1, 64);
+    // inclusive prefix max over lanes (DPP scan: within rows, then row 0-1
+    // and 0-2 totals carried up; max is exact in any order), then each
+    // lane's exclusive prefix from lane - 1 (wave_shr:1)
+    float p = valid ? s : -INFINITY;
+    p = dpp_max<0x111, 0xF>(p);
+    p = dpp_max<0x112, 0xF>(p);
+    p = dpp_max<0x114, 0xF>(p);
+    p = dpp_max<0x118, 0xF>(p);
+    p = dpp_max<0x142, 0xA>(p);
+    p = dpp_max<0x143, 0xC>(p);
+    const float prev = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, p), __builtin_bit_cast(int, p), 0x138, 0xF, 0xF, false));
     const float run = lane == 0 ? m : fmaxf(m, prev);
     const bool flag = valid && s > run;
     float e = 0.0f, mlt = 1.0f;
