@@ -311,25 +311,6 @@ __device__ __forceinline__ float row_shl(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x100 + N, 0xF, 0xF, false));
 }
 
-// max over the wave, in every lane: DPP shifts inside each 16-lane row
-// leave the row's max in its lane 15, row_bcast:15 and :31 carry rows 0-1 and
-// 2-3 into lane 63 (a lane with no source keeps its own value).  Max is exact
-// in any order.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_max(float v) {
-    const int o = __builtin_bit_cast(int, v);
-    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(o, o, CTRL, ROWS, 0xF, false)));
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    v = dpp_max<0x111, 0xF>(v);  // row_shr:1
-    v = dpp_max<0x112, 0xF>(v);  // row_shr:2
-    v = dpp_max<0x114, 0xF>(v);  // row_shr:4
-    v = dpp_max<0x118, 0xF>(v);  // row_shr:8
-    v = dpp_max<0x142, 0xA>(v);  // row_bcast:15
-    v = dpp_max<0x143, 0xC>(v);  // row_bcast:31
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 template <int HD>
 __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A0) {
     constexpr int M = HD / 8;        // elements per lane
@@ -466,7 +447,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         const int head = h * kvm + g;
         float v = lane < nt ? s_sc[g * EX_TILE + lane] : -INFINITY;
         if (lane < nt) A.scores[(size_t)head * A.cap + t_base + lane] = v;
-        const float mx = wave_max_dpp(v);
+        const float mx = wave_max(v);
         if (lane == 0) A.tmax[(size_t)head * ntl + blockIdx.x] = mx;
     }
 }
@@ -496,7 +477,7 @@ __global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) 
     const float s = A.scores[(size_t)head * A.cap + min(t, ctx - 1)];
     float m = -INFINITY;
     for (int j = lane; j < tile; j += 64) m = fmaxf(m, tm[j]);
-    m = wave_max_dpp(m);
+    m = wave_max(m);
     if (A.sinks) m = fmaxf(A.sinks[head], m);
     // inclusive prefix max over lanes (DPP scan: within rows, then row 0-1
     // and 0-2 totals carried up; max is exact in any order), then each

@@ -63,8 +63,43 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// max over the wave, in every lane: DPP shifts inside each 16-lane row
+// leave the row's max in its lane 15, row_bcast:15 and :31 carry rows 0-1 and
+// 2-3 into lane 63 (a lane with no source keeps its own value).  Max is exact
+// in any order.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max(float v) {
+    const int o = __builtin_bit_cast(int, v);
+    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(o, o, CTRL, ROWS, 0xF, false)));
+}
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = dpp_max<0x111, 0xF>(v);  // row_shr:1
+    v = dpp_max<0x112, 0xF>(v);  // row_shr:2
+    v = dpp_max<0x114, 0xF>(v);  // row_shr:4
+    v = dpp_max<0x118, 0xF>(v);  // row_shr:8
+    v = dpp_max<0x142, 0xA>(v);  // row_bcast:15
+    v = dpp_max<0x143, 0xC>(v);  // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Within each 16-lane row, every lane gets the row's max / integer sum:
+// quad_perm xor 1 and xor 2, then row_ror 4 and 8 (all sources valid).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0xB1>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x4E>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x124>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_i<0x128>(__builtin_bit_cast(int, v))));
+    return v;
+}
+__device__ __forceinline__ int row_sum16_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x124>(v);
+    v += dpp_i<0x128>(v);
     return v;
 }
 __device__ __forceinline__ int wave_sum_i32(int v) {

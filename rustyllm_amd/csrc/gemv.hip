@@ -383,10 +383,7 @@ __device__ __forceinline__ void kq_quant_chunk(const float (&v)[16], int c, bool
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+    amax = row_max16(amax);
     const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
     int sum = 0;
     uint32_t w4[4] = {0u, 0u, 0u, 0u};
@@ -396,7 +393,7 @@ __device__ __forceinline__ void kq_quant_chunk(const float (&v)[16], int c, bool
         sum += q;
         w4[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
     }
-    const int pair = sum + __shfl_xor(sum, 1, 64);
+    const int pair = sum + dpp_i<0xB1>(sum);  // quad_perm: the partner lane c ^ 1
     if (valid) {
         const int b = c >> 4;
         *(int4 *)(s_xq + b * KQ_XQ_STRIDE + (c & 15) * 4) = make_int4((int)w4[0], (int)w4[1], (int)w4[2], (int)w4[3]);

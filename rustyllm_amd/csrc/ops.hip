@@ -15,13 +15,12 @@ __device__ __forceinline__ void q8k_block_store(float v, int blk, int e, XQ xq, 
     q = max(-128, min(127, q));
     xq.qs[e] = (int8_t)q;
     if (threadIdx.x == 0) xq.d[blk] = amax * (1.0f / 127.0f);
-    int s = q;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
-    s += __shfl_xor(s, 8, 64);
+    // integer sums (exact in any order): per 16 lanes, then rows 0+1 and 2+3
+    int s = row_sum16_i(q);
     if ((threadIdx.x & 15) == 0) xq.sums16[e >> 4] = (int16_t)s;
-    s += __shfl_xor(s, 16, 64);
+    const int lane = threadIdx.x & 63;
+    const int r1 = __builtin_amdgcn_readlane(s, 16), r3 = __builtin_amdgcn_readlane(s, 48);
+    s += lane < 32 ? r1 : r3;
     if ((threadIdx.x & 31) == 0) xq.bsums[e >> 5] = (int16_t)s;
 }
 
