@@ -320,35 +320,43 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     __shared__ __align__(16) float s_k[EX_TILE * RS];
     __shared__ __align__(16) float s_q[CH_MAXG * RS];  // the heads' q, lane-sliced like a K row
     __shared__ float s_sc[CH_MAXG * EX_TILE];
-    int s0, e0;
-    exact_range(A, s0, e0);
-    const int ctx = e0 - s0 + 1;
     const int t_base = blockIdx.x * EX_TILE;
-    if (ctx <= 0 || t_base >= ctx) return;
     const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, kvm = A.kv_mul;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nt = min(EX_TILE, ctx - t_base);
     const float *kh = A.k + (size_t)h * HD;
-    // fused RoPE: the current position e0 and its cos/sin row
-    const RopeArgs &RA = A.rope;
-    const bool fuse = A.fuse_rope != 0 && e0 < RA.max_pos;
-    const int half = HD / 2;
-    const float *ct = RA.cos_t + (size_t)e0 * half, *stb = RA.sin_t + (size_t)e0 * half;
     // the K tile's loads first (registers), so their latency overlaps the q
     // staging below; element 4*c4 + i of a row goes to lane slice
     // (4*c4 + i) % 8, position (4*c4 + i) / 8
     constexpr int H4 = HD / 4, RSTEP = 256 / H4, NKR = EX_TILE / RSTEP;
     const int r0 = tid / H4, c4 = tid - r0 * H4;
     float4 kreg[NKR];
-    {
-        const int base = (s0 + t_base) % A.slot_count;
+    auto load_k = [&](int start, int rows) {
+        const int base = (start + t_base) % A.slot_count;
 #pragma unroll
         for (int i = 0; i < NKR; i++) {
-            int slot = base + min(r0 + i * RSTEP, nt - 1);
+            int slot = base + min(r0 + i * RSTEP, rows - 1);
             if (slot >= A.slot_count) slot -= A.slot_count;
             kreg[i] = *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
         }
-    }
+    };
+    // Without a window the range starts at start_t, which the host passes as
+    // a hint (A.start_t) when the range comes from the device state: the
+    // tile's K loads are issued before that state arrives, every row of the
+    // tile (slots wrap, so any start is in bounds; rows past the range are
+    // never used), and issued again below if the range starts elsewhere.
+    const bool spec = A.window == 0;
+    if (spec) load_k(A.start_t, EX_TILE);
+    int s0, e0;
+    exact_range(A, s0, e0);
+    const int ctx = e0 - s0 + 1;
+    if (ctx <= 0 || t_base >= ctx) return;
+    const int nt = min(EX_TILE, ctx - t_base);
+    if (!spec || s0 != A.start_t) load_k(s0, nt);
+    // fused RoPE: the current position e0 and its cos/sin row
+    const RopeArgs &RA = A.rope;
+    const bool fuse = A.fuse_rope != 0 && e0 < RA.max_pos;
+    const int half = HD / 2;
+    const float *ct = RA.cos_t + (size_t)e0 * half, *stb = RA.sin_t + (size_t)e0 * half;
     {
         // q of the kv head's query heads (rotated here when RoPE is fused),
         // element e of head g at lane slice e % 8, position e / 8

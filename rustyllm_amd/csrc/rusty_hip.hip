@@ -1842,6 +1842,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.scale = 1.0f / sqrtf((float)R.hd);
             E.rope = r_rope;  // RoPE + KV store inside the scores launch
             E.fuse_rope = 1;
+            E.start_t = R.st_host ? R.st_host->start_t : 0;  // the range's start as of this enqueue (a hint)
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
             act_o.mode = ACT_DEN;
