@@ -213,7 +213,16 @@ int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint
  * (as rusty_hip_moe_ffn) into the residual.  Configure with this call, then
  * set every layer with rusty_hip_resident_set_moe_layer, then
  * rusty_hip_resident_set_output / _set_embedding; decode, generate, kv_read
- * and time_decode work as for the standard decoder.  value_dim = head_dim. */
+ * and time_decode work as for the standard decoder.  value_dim = head_dim.
+ * storage_len is the cache's max_len (positions accepted).  With
+ * sliding_window > 0 the KV cache is the reference's ring of
+ * min(sliding_window, max_len) slots, position p in slot p % slots
+ * (KVCache::with_sliding_window / slot_for_pos, src/model.rs:1363-1464), and
+ * every layer reads it with slot_count = slots: the even layers over the
+ * window, the odd layers from position 0 (src/model.rs:6786-6810), which
+ * revisits slots once pos >= slots exactly as the reference's slot walk
+ * does.  kv_read / kv_write address ring slots.  forward_gpt_oss_into has no
+ * start position, so resident_decode ignores start_t in this mode. */
 typedef struct {
     const uint8_t *w[4];       /* wq, wk, wv, wo */
     uintptr_t w_len[4];
@@ -243,10 +252,13 @@ int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *desc);
  * Returns the previous mode; other values only query. */
 int rusty_hip_attention_mode(int mode);
 
-/* Frees every cached device weight copy (no reference counterpart: the
- * Metal cache lives as long as the process because the reference's weights
- * are mmap'd and never freed).  Call it before freeing host weight memory
- * whose addresses may be reused; rusty_hip_resident_configure also clears. */
+/* Frees every device weight copy cached for the per-op exports (no reference
+ * counterpart: the Metal cache lives as long as the process because the
+ * reference's weights are mmap'd and never freed).  Call it before freeing
+ * host weight memory whose addresses may be reused.  The resident decoder
+ * holds copies of its own, uploaded by set_layer / set_moe_layer /
+ * set_output / set_embedding and freed by the next configure, so this call
+ * leaves a configured decoder working. */
 int rusty_hip_weight_cache_clear(void);
 
 /* Timing on the library's stream (the stream every kernel is launched on). */

@@ -868,6 +868,37 @@ void orc_build_rope_inv_freq(float theta, int64_t head_dim, float scaling, float
     }
 }
 
+/* build_rope_inv_freq_gpt_oss, model.rs:3059-3098: YaRN inverse frequencies
+ * (a linear ramp between the extrapolated 1/base and the interpolated
+ * 1/(scaling*base) over pairs low..high) and the concentration
+ * 0.1*ln(scaling) + 1, in f32 with libm logf/powf as Rust's f32::ln/powf. */
+void orc_build_rope_inv_freq_gpt_oss(float theta, int64_t head_dim, float scaling, int64_t orig_ctx, float *inv,
+                                     float *concentration) {
+    const float pi = 3.14159265358979323846f;
+    float d_half = (float)head_dim / 2.0f;
+    float low = 0.0f, high = 0.0f;
+    if (scaling > 1.0f) {
+        low = d_half * (logf((float)orig_ctx / (32.0f * 2.0f * pi)) / logf(theta));
+        high = d_half * (logf((float)orig_ctx / (1.0f * 2.0f * pi)) / logf(theta));
+    }
+    *concentration = scaling > 1.0f ? 0.1f * logf(scaling) + 1.0f : 1.0f;
+    for (int64_t pair = 0; pair < head_dim / 2; pair++) {
+        float i = (float)(pair * 2);
+        float base_freq = powf(theta, i / (float)head_dim);
+        if (scaling > 1.0f) {
+            float idx = (float)pair;
+            float ramp = (idx - low) / (high - low);
+            ramp = ramp < 0.0f ? 0.0f : (ramp > 1.0f ? 1.0f : ramp);
+            float mask = 1.0f - ramp;
+            float interpolation = 1.0f / (scaling * base_freq);
+            float extrapolation = 1.0f / base_freq;
+            inv[pair] = interpolation * (1.0f - mask) + extrapolation * mask;
+        } else {
+            inv[pair] = 1.0f / base_freq;
+        }
+    }
+}
+
 /* apply_rope_qk, model.rs:5562-5603 (adjacent pairs) */
 void orc_rope_qk(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq) {
     int64_t last = hd - (hd % 2);
@@ -1144,7 +1175,11 @@ static void add_bias(float *out, const float *b, uint32_t len) {
     for (uint32_t i = 0; i < len; i++) out[i] += b[i];
 }
 
-void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits, int want_logits) {
+/* forward_into (model.rs:7177-7358).  start_t >= 0 fixes every layer's
+ * attention start as the Metal resident decoder's start_t argument does
+ * (metal_backend.m:2167-2189); start_t < 0 takes attention_start_pos. */
+void orc_model_forward_from(orc_model *m, uint32_t token, int64_t pos, int64_t start_t, float *logits,
+                            int want_logits) {
     const orc_config *c = &m->c;
     int64_t dim = c->dim, hd = c->head_dim, vd = c->value_dim;
     int64_t kdim = (int64_t)c->n_kv_heads * hd, vdim = (int64_t)c->n_kv_heads * vd;
@@ -1170,7 +1205,7 @@ void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits,
         memcpy(m->k[l] + slot * kdim, m->kk, (size_t)kdim * 4);
         memcpy(m->v[l] + slot * vdim, m->vv, (size_t)vdim * 4);
         float scale = 1.0f / sqrtf((float)hd);
-        int64_t start = orc_attention_start_pos(pos, window);
+        int64_t start = start_t >= 0 ? start_t : orc_attention_start_pos(pos, window);
         orc_attention_over_kv_heads(m->q, m->k[l], m->v[l], kdim, vdim, c->storage_len, hd, vd, c->n_kv_heads,
                                     kv_mul, start, pos, scale, m->attn);
         orc_matvec((int)L->w_type[3], L->w[3], m->attn, L->w_rows[3], (int64_t)c->n_heads * vd, m->proj, th);
@@ -1185,6 +1220,10 @@ void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits,
     if (!want_logits) return;
     orc_rms_norm(m->x, m->output_norm, c->eps, dim, m->xn);
     orc_matvec((int)m->output_type, m->output_w, m->xn, c->vocab, dim, logits, th);
+}
+
+void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits, int want_logits) {
+    orc_model_forward_from(m, token, pos, -1, logits, want_logits);
 }
 
 int64_t orc_model_generate(orc_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t start_pos, int64_t n_gen,

@@ -94,6 +94,8 @@ int64_t orc_attention_start_pos(int64_t pos, int64_t window);
 /* ---- small ops ------------------------------------------------------------ */
 void orc_rms_norm(const float *x, const float *w, float eps, int64_t n, float *out);
 void orc_build_rope_inv_freq(float theta, int64_t head_dim, float scaling, float *inv);
+void orc_build_rope_inv_freq_gpt_oss(float theta, int64_t head_dim, float scaling, int64_t orig_ctx, float *inv,
+                                     float *concentration);
 void orc_rope_qk(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq);
 void orc_rope_qk_neox(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, const float *inv_freq);
 void orc_rope_gpt_oss(float *q, float *k, int64_t pos, int64_t hd, int64_t nh, int64_t nkv, float concentration,
@@ -137,6 +139,8 @@ int orc_model_set_layer(orc_model *m, int32_t l, const orc_layer *layer);
 int orc_model_set_output(orc_model *m, const float *output_norm, const uint8_t *output_w,
                          uint32_t output_type, const uint8_t *embd, uint32_t embd_type,
                          const float *inv_freq);
+void orc_model_forward_from(orc_model *m, uint32_t token, int64_t pos, int64_t start_t, float *logits,
+                            int want_logits);
 void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits, int want_logits);
 float *orc_model_kv(orc_model *m, int32_t layer, int32_t which);
 /* prefill prompt (per token) then greedy-decode n_gen tokens. Returns count. */

@@ -74,6 +74,7 @@ _sig("orc_build_rope_inv_freq", None, _f, _i64, _f, _p)
 _sig("orc_rope_qk", None, _p, _p, _i64, _i64, _i64, _i64, _p)
 _sig("orc_rope_qk_neox", None, _p, _p, _i64, _i64, _i64, _i64, _p)
 _sig("orc_rope_gpt_oss", None, _p, _p, _i64, _i64, _i64, _i64, _f, _p)
+_sig("orc_build_rope_inv_freq_gpt_oss", None, _f, _i64, _f, _i64, _p, _p)
 _sig("orc_silu_mul_avx2", None, _p, _p, _p, _i64)
 _sig("orc_silu_mul_scalar", None, _p, _p, _p, _i64)
 _sig("orc_swiglu_gpt_oss", _f, _f, _f)
@@ -88,6 +89,7 @@ _sig("orc_model_free", None, _p)
 _sig("orc_model_set_layer", C.c_int, _p, C.c_int32, _p)
 _sig("orc_model_set_output", C.c_int, _p, _p, _p, C.c_uint32, _p, C.c_uint32, _p)
 _sig("orc_model_forward", None, _p, C.c_uint32, _i64, _p, C.c_int)
+_sig("orc_model_forward_from", None, _p, C.c_uint32, _i64, _i64, _p, C.c_int)
 _sig("orc_model_kv", C.POINTER(C.c_float), _p, C.c_int32, C.c_int32)
 _sig("orc_model_generate", _i64, _p, _p, _i64, _i64, _i64, _f, _p, _p)
 _sig("orc_make_q4k_weights", None, _i64, _i64, C.c_uint8, _p)
@@ -232,6 +234,14 @@ def top_k_router(logits, k):
     return idx, val, probs
 
 
+def rope_inv_freq_gpt_oss(theta: float, head_dim: int, scaling: float, orig_ctx: int):
+    """build_rope_inv_freq_gpt_oss (model.rs:3059-3098): (inv_freq, concentration)."""
+    inv = np.zeros(head_dim // 2, np.float32)
+    conc = C.c_float(0.0)
+    lib.orc_build_rope_inv_freq_gpt_oss(theta, head_dim, scaling, orig_ctx, ptr(inv), C.addressof(conc))
+    return inv, float(conc.value)
+
+
 def rope_gpt_oss(q, k, pos, hd, nh, nkv, concentration, inv_freq):
     q, k, inv = f32(q).copy(), f32(k).copy(), f32(inv_freq)
     lib.orc_rope_gpt_oss(ptr(q), ptr(k), pos, hd, nh, nkv, concentration, ptr(inv))
@@ -275,17 +285,29 @@ def moe_block(x, router, router_t, router_bias, experts, experts_t, hidden, bias
 
 class OracleGptOss:
     """forward_gpt_oss_into (model.rs:6733-6908) composed from the C
-    restatements, with the KV cache on the host (linear slots).  Test
-    infrastructure only."""
+    restatements, with the KV cache on the host.  The cache is the
+    reference's KVCache::with_sliding_window(max_len, window)
+    (model.rs:1363-1385): with a window it is a ring of
+    storage_len_for(max_len, window) = min(window, max_len) slots and
+    position p lives in slot p % storage (slot_for_pos, :1458-1464); every
+    layer's attention scans that ring with slot_count = storage
+    (:6793-6810), the full (odd) layers from position 0.  Test infrastructure
+    only."""
 
-    def __init__(self, model, storage_len: int):
+    def __init__(self, model, max_len: int):
         self.m = model
         c = self.c = model["config"]
-        self.storage = storage_len
+        self.max_len = max(1, max_len)
+        w = c.get("window", 0)
+        self.storage = min(w, self.max_len) if w > 0 else self.max_len
+        self.ring = w > 0
         self.kd = c["n_kv_heads"] * c["head_dim"]
         self.vdim = c["n_kv_heads"] * c["value_dim"]
-        self.kc = [np.zeros(storage_len * self.kd, np.float32) for _ in model["layers"]]
-        self.vc = [np.zeros(storage_len * self.vdim, np.float32) for _ in model["layers"]]
+        self.kc = [np.zeros(self.storage * self.kd, np.float32) for _ in model["layers"]]
+        self.vc = [np.zeros(self.storage * self.vdim, np.float32) for _ in model["layers"]]
+
+    def slot(self, pos: int) -> int:
+        return pos % self.storage if self.ring else pos
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         m, c = self.m, self.c
@@ -299,8 +321,9 @@ class OracleGptOss:
             k = (matvec(L["wk"][1], L["wk"][0], xn, nkv * hd, dim) + L["bk"]).astype(np.float32)
             v = (matvec(L["wv"][1], L["wv"][0], xn, nkv * vd, dim) + L["bv"]).astype(np.float32)
             q, k = rope_gpt_oss(q, k, pos, hd, nh, nkv, m["concentration"], m["inv_freq"])
-            self.kc[l][pos * self.kd:(pos + 1) * self.kd] = k
-            self.vc[l][pos * self.vdim:(pos + 1) * self.vdim] = v
+            sl = self.slot(pos)
+            self.kc[l][sl * self.kd:(sl + 1) * self.kd] = k
+            self.vc[l][sl * self.vdim:(sl + 1) * self.vdim] = v
             start = int(lib.orc_attention_start_pos(pos, c["window"])) if l % 2 == 0 else 0
             attn = attention(q, self.kc[l], self.vc[l], nh, nkv, hd, vd, self.kd, self.vdim, self.storage, start,
                              pos, scale, sinks=L["sinks"])
@@ -424,9 +447,11 @@ class OracleModel:
         lib.orc_model_set_output(self.h, ptr(model["output_norm"]), ptr(out_w), out_dt, ptr(emb_w), emb_dt,
                                  ptr(model["inv_freq"]))
 
-    def forward(self, token: int, pos: int, want_logits: bool = True):
+    def forward(self, token: int, pos: int, want_logits: bool = True, start_t: int = -1):
+        """start_t >= 0: every layer attends start_t..pos (the resident
+        decoder's start_t); -1: the model's own range."""
         logits = np.zeros(self.vocab, np.float32)
-        lib.orc_model_forward(self.h, token, pos, ptr(logits), 1 if want_logits else 0)
+        lib.orc_model_forward_from(self.h, token, pos, start_t, ptr(logits), 1 if want_logits else 0)
         return logits
 
     def kv(self, layer: int, storage_len: int):

@@ -42,7 +42,7 @@ def build_hip() -> str:
 
 def build_synth() -> str:
     tmp = SYNTH_LIB + ".tmp"
-    _run(["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-mf16c", "-o", tmp,
+    _run(["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-mf16c", "-ffp-contract=off", "-o", tmp,
           os.path.join(CSRC, "synth.cpp")])
     os.replace(tmp, SYNTH_LIB)
     return SYNTH_LIB

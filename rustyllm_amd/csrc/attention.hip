@@ -38,7 +38,7 @@ struct AttnArgs {
     int64_t key_stride, value_stride;
     int32_t slot_count;
     int32_t start_t, end_t;  // used when st == null
-    int32_t window;          // with st: start = max(0, pos+1-window) if window>0 else 0
+    int32_t window;          // with st: start = max(0, pos+1-window) if window>0 else st->start_t
     int32_t n_chunks;
     float scale;
 };
@@ -46,7 +46,7 @@ struct AttnArgs {
 __device__ __forceinline__ void attn_range(const AttnArgs &A, int &start_t, int &end_t) {
     if (A.st) {
         end_t = A.st->pos;
-        start_t = A.window > 0 ? max(0, end_t + 1 - A.window) : 0;
+        start_t = A.window > 0 ? max(0, end_t + 1 - A.window) : A.st->start_t;
     } else {
         start_t = A.start_t;
         end_t = A.end_t;

@@ -194,14 +194,44 @@ static uint64_t fingerprint(const uint8_t *p, size_t len) {
     return h;
 }
 
-// Device copy of a host weight, cached by (pointer, length) and checked
-// against a sampled fingerprint of the bytes.  Rows are padded to a 16-byte
-// stride; block bytes are copied unchanged.
-static int get_weight(const uint8_t *host, size_t len, int64_t rows, int64_t cols, int fmt, DevW *out) {
-    if (!host || rows <= 0 || cols <= 0) return 0;
+static bool weight_shape_ok(const uint8_t *host, size_t len, int64_t rows, int64_t cols, int fmt) {
+    if (!host || rows <= 0 || cols <= 0) return false;
     int64_t rb = row_bytes_of(fmt, cols);
-    if (rb <= 0 || cols % block_elems(fmt) != 0) return 0;
-    if ((int64_t)len < rows * rb) return 0;
+    if (rb <= 0 || cols % block_elems(fmt) != 0) return false;
+    return (int64_t)len >= rows * rb;
+}
+
+// A new device copy of a host weight (the caller owns it).  Rows are padded
+// to a 16-byte stride; block bytes are copied unchanged.
+static int upload_weight(const uint8_t *host, int64_t rows, int64_t cols, int fmt, uint64_t fp, DevW *out) {
+    const int64_t rb = row_bytes_of(fmt, cols);
+    const int64_t stride = (rb + 15) / 16 * 16;
+    uint8_t *d = nullptr;
+    RH_CHECK(hipMalloc((void **)&d, (size_t)(rows * stride)));
+    hipError_t e = stride == rb ? hipMemcpy(d, host, (size_t)(rows * rb), hipMemcpyHostToDevice)
+                                : hipMemcpy2D(d, (size_t)stride, host, (size_t)rb, (size_t)rb, (size_t)rows,
+                                              hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        RH_CHECK(e);
+    }
+    DevW w;
+    w.p = d;
+    w.stride = stride;
+    w.rows = (int32_t)rows;
+    w.cols = (int32_t)cols;
+    w.fmt = fmt;
+    w.fp = fp;
+    *out = w;
+    return 1;
+}
+
+// Device copy of a host weight for the per-op exports, cached by (pointer,
+// length) and checked against a sampled fingerprint of the bytes.  The
+// resident decoder keeps copies of its own (r_weight), so neither eviction
+// here nor rusty_hip_weight_cache_clear can pull memory from under it.
+static int get_weight(const uint8_t *host, size_t len, int64_t rows, int64_t cols, int fmt, DevW *out) {
+    if (!weight_shape_ok(host, len, rows, cols, fmt)) return 0;
     auto key = std::make_pair((const void *)host, len);
     auto it = g.wcache.find(key);
     uint64_t fp = fingerprint(host, len);
@@ -214,21 +244,8 @@ static int get_weight(const uint8_t *host, size_t len, int64_t rows, int64_t col
         (void)hipFree((void *)it->second.p);
         g.wcache.erase(it);
     }
-    int64_t stride = (rb + 15) / 16 * 16;
-    uint8_t *d = nullptr;
-    RH_CHECK(hipMalloc((void **)&d, (size_t)(rows * stride)));
-    if (stride == rb) {
-        RH_CHECK(hipMemcpy(d, host, (size_t)(rows * rb), hipMemcpyHostToDevice));
-    } else {
-        RH_CHECK(hipMemcpy2D(d, (size_t)stride, host, (size_t)rb, (size_t)rb, (size_t)rows, hipMemcpyHostToDevice));
-    }
     DevW w;
-    w.p = d;
-    w.stride = stride;
-    w.rows = (int32_t)rows;
-    w.cols = (int32_t)cols;
-    w.fmt = fmt;
-    w.fp = fp;
+    if (!upload_weight(host, rows, cols, fmt, fp, &w)) return 0;
     g.wcache[key] = w;
     *out = w;
     return 1;
@@ -1641,7 +1658,14 @@ struct RLayer {
 
 struct Resident {
     bool configured = false, ready = false;
-    uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, vd = 0, hidden = 0, vocab = 0, storage = 0;
+    uint32_t n_layers = 0, dim = 0, n_heads = 0, n_kv = 0, hd = 0, vd = 0, hidden = 0, vocab = 0;
+    // storage: KV slots per layer; max_pos: positions the decoder accepts
+    // (rows of the RoPE table, the longest attention range).  They differ
+    // only for a ring cache (gpt-oss with a sliding window: storage =
+    // min(window, max_pos), slot = pos % storage, KVCache::storage_len_for /
+    // slot_for_pos, src/model.rs:1450-1464).
+    uint32_t storage = 0, max_pos = 0;
+    bool ring = false;
     uint32_t neox = 0;
     uint32_t vt_stride = 0;  // positions per row of the transposed V copies (storage rounded up to 64)
     float eps = 1e-5f;
@@ -1676,8 +1700,9 @@ struct Resident {
     float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pattn = nullptr, *ptg = nullptr,
           *ptu = nullptr, *pex = nullptr;
     int8_t *pbq = nullptr;
-    std::map<int, hipGraphExec_t> graphs;
+    std::map<std::pair<int, uint32_t>, hipGraphExec_t> graphs;  // by (mode, penalty bits)
     std::vector<void *> allocs;
+    std::vector<std::pair<const void *, DevW>> wown;  // weight copies owned by the decoder
 };
 static Resident R;
 
@@ -1689,12 +1714,30 @@ static int r_alloc(void **p, size_t bytes) {
     return 1;
 }
 
+// The resident decoder's own device copy of a weight, freed only by the next
+// configure: a tensor given twice (a tied output head) is copied once.
+static int r_weight(const uint8_t *host, size_t len, int64_t rows, int64_t cols, int fmt, DevW *out) {
+    if (!weight_shape_ok(host, len, rows, cols, fmt)) return 0;
+    for (const auto &e : R.wown)
+        if (e.first == (const void *)host && e.second.rows == rows && e.second.cols == cols && e.second.fmt == fmt) {
+            *out = e.second;
+            return 1;
+        }
+    DevW w;
+    if (!upload_weight(host, rows, cols, fmt, 0, &w)) return 0;
+    R.allocs.push_back((void *)w.p);
+    R.wown.emplace_back((const void *)host, w);
+    *out = w;
+    return 1;
+}
+
 static void r_reset() {
     if (g.s) (void)hipStreamSynchronize(g.s);
     for (auto &kv : R.graphs) (void)hipGraphExecDestroy(kv.second);
     R.graphs.clear();
     for (void *p : R.allocs) (void)hipFree(p);
     R.allocs.clear();
+    R.wown.clear();
     if (R.st_host) (void)hipHostFree(R.st_host);
     R.st_host = nullptr;
     R.L.clear();
@@ -1778,7 +1821,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.cos_t = R.cos_t;
             A.sin_t = R.sin_t;
             A.st = R.st;
-            A.max_pos = R.storage;
+            A.max_pos = R.max_pos;
             A.n_heads = R.n_heads;
             A.n_kv = R.n_kv;
             A.hd = R.hd;
@@ -1910,12 +1953,13 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
             A.cos_t = R.cos_t;
             A.sin_t = R.sin_t;
             A.st = R.st;
-            A.max_pos = R.storage;
+            A.max_pos = R.max_pos;
             A.n_heads = R.n_heads;
             A.n_kv = R.n_kv;
             A.hd = R.hd;
             A.vd = R.vd;
             A.slots = R.storage;
+            A.ring = R.ring ? 1 : 0;  // KVCache::k_offset(pos) (src/model.rs:6778-6783)
             A.neox = 0;
             int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
             ProfScope ps("rope_kv", s);
@@ -2015,11 +2059,11 @@ static bool use_graphs() {
 
 // Runs one token in `mode`, via a cached graph when allowed.  The penalty is
 // baked into the greedy graph, so graphs are keyed by (mode, penalty bits).
-static int r_run(int mode, float penalty) {
-    if (!use_graphs()) return r_enqueue(mode, penalty, g.s);
+// The token graph for (mode, penalty), captured on first use.
+static int r_graph(int mode, float penalty, hipGraphExec_t *out) {
     uint32_t pb;
     memcpy(&pb, &penalty, 4);
-    int key = mode ^ (int)(pb * 2654435761u & 0x7ffffff8u);
+    const auto key = std::make_pair(mode, pb);
     auto it = R.graphs.find(key);
     if (it == R.graphs.end()) {
         hipGraph_t graph;
@@ -2036,7 +2080,15 @@ static int r_run(int mode, float penalty) {
         RH_CHECK(ie);
         it = R.graphs.emplace(key, exec).first;
     }
-    RH_CHECK(hipGraphLaunch(it->second, g.s));
+    *out = it->second;
+    return 1;
+}
+
+static int r_run(int mode, float penalty) {
+    if (!use_graphs()) return r_enqueue(mode, penalty, g.s);
+    hipGraphExec_t exec;
+    if (!r_graph(mode, penalty, &exec)) return 0;
+    RH_CHECK(hipGraphLaunch(exec, g.s));
     return 1;
 }
 
@@ -2141,7 +2193,7 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
             A.sin_t = R.sin_t;
             A.st = nullptr;
             A.pos = pos0;
-            A.max_pos = R.storage;
+            A.max_pos = R.max_pos;
             A.n_heads = R.n_heads;
             A.n_kv = R.n_kv;
             A.hd = R.hd;
@@ -2218,7 +2270,7 @@ static int r_prefill_tokens(int n, int pos0) {
 
 static int r_ensure_tokens(uint32_t need) {
     if (R.tok_cap >= need) return 1;
-    need = std::max(need, std::min<uint32_t>(R.storage + 1, 8192));
+    need = std::max(need, std::min<uint32_t>(R.max_pos + 1, 8192));
     if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
     R.tok_cap = need;
     r_invalidate_graphs();  // the greedy graph records the token pointer
@@ -2245,11 +2297,12 @@ extern "C" {
 }  // extern "C"
 
 // Resident buffers for a model shape (shared by both configure calls).
+// storage_len KV slots per layer, max_pos positions (max_pos > storage_len
+// only for a ring cache).
 static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                   uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab, uint32_t storage_len, float eps,
-                   uint32_t neox) {
+                   uint32_t value_dim, uint32_t hidden_dim, uint32_t vocab, uint32_t storage_len, uint32_t max_pos,
+                   float eps, uint32_t neox) {
     r_reset();
-    wcache_clear();  // a new model: cached copies keyed by old host addresses are stale
     R.n_layers = n_layers;
     R.dim = dim;
     R.n_heads = n_heads;
@@ -2259,6 +2312,8 @@ static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n
     R.hidden = hidden_dim;
     R.vocab = vocab;
     R.storage = storage_len;
+    R.max_pos = max_pos;
+    R.ring = max_pos > storage_len;
     R.eps = eps;
     R.neox = neox;
     R.L.resize(n_layers);
@@ -2278,10 +2333,10 @@ static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n
             !r_alloc((void **)&xqs[i]->bsums, nb * 16) || !r_alloc((void **)&xqs[i]->sums16, nb * 32))
             return 0;
     }
-    R.n_chunks = attn_chunks((int)n_kv_heads, (int)storage_len);
+    R.n_chunks = attn_chunks((int)n_kv_heads, (int)max_pos);
     if (!r_alloc((void **)&R.part, (size_t)n_kv_heads * R.n_chunks * (n_heads / n_kv_heads) * att_pstride((int)value_dim) * 4))
         return 0;
-    R.ex_cap = (int)((storage_len + 63) / 64 * 64);
+    R.ex_cap = (int)((max_pos + 63) / 64 * 64);  // a range is at most max_pos positions
     if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_kv_heads, (int)(n_heads / n_kv_heads), R.ex_cap) * 4)) return 0;
     R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
     if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
@@ -2307,8 +2362,8 @@ int rusty_hip_resident_configure(uint32_t n_layers, uint32_t dim, uint32_t n_hea
     if (head_dim == 0 || head_dim > 256 || value_dim == 0 || value_dim > 256) return 0;
     if (dim % 256 != 0 || hidden_dim % 256 != 0 || storage_len == 0 || vocab == 0) return 0;
     if (!attn_supported((int)head_dim, (int)value_dim, (int)(n_heads / n_kv_heads))) return 0;
-    return r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, value_dim, hidden_dim, vocab, storage_len, eps,
-                   neox);
+    return r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, value_dim, hidden_dim, vocab, storage_len,
+                   storage_len, eps, neox);
 }
 
 int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n_kv_heads,
@@ -2325,7 +2380,12 @@ int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n
         top_k > n_experts)
         return 0;
     if (!attn_supported((int)head_dim, (int)head_dim, (int)(n_heads / n_kv_heads))) return 0;
-    if (!r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, head_dim, hidden_dim, vocab, storage_len, eps, 0))
+    // storage_len is the cache's max_len; with a window the cache is a ring
+    // of min(window, max_len) slots (KVCache::with_sliding_window,
+    // src/model.rs:1363-1385, storage_len_for :1450-1455)
+    const uint32_t slots = sliding_window > 0 ? std::min(sliding_window, storage_len) : storage_len;
+    if (!r_setup(n_layers, dim, n_heads, n_kv_heads, head_dim, head_dim, hidden_dim, vocab, slots, storage_len, eps,
+                 0))
         return 0;
     R.moe = true;
     R.n_exp = n_experts;
@@ -2346,7 +2406,7 @@ int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *d) {
     for (int i = 0; i < 4; i++) {
         const int fmt = dt_to_fmt(d->w_dt[i]);
         if (!d->w[i] || fmt < 0 || !cat_of(fmt, (int)cols[i])) return 0;
-        if (!get_weight(d->w[i], d->w_len[i], rows[i], cols[i], fmt, &Ly.w[i])) return 0;
+        if (!r_weight(d->w[i], d->w_len[i], rows[i], cols[i], fmt, &Ly.w[i])) return 0;
     }
     auto upload = [&](const float *h, size_t n, float **dst) {
         if (!h) return 0;
@@ -2366,12 +2426,12 @@ int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *d) {
     M.hidden = (int)R.hidden;
     const int rfmt = dt_to_fmt(d->router_dt), efmt = dt_to_fmt(d->exps_dt);
     if (rfmt < 0 || efmt < 0 || !d->router) return 0;
-    if (!get_weight(d->router, d->router_len, R.n_exp, R.dim, rfmt, &M.router)) return 0;
+    if (!r_weight(d->router, d->router_len, R.n_exp, R.dim, rfmt, &M.router)) return 0;
     const uint32_t erows[3] = {R.n_exp * R.hidden, R.n_exp * R.hidden, R.n_exp * R.dim};
     const uint32_t ecols[3] = {R.dim, R.dim, R.hidden};
     DevW *ew[3] = {&M.gate, &M.up, &M.down};
     for (int i = 0; i < 3; i++)
-        if (!d->exps[i] || !get_weight(d->exps[i], d->exps_len[i], erows[i], ecols[i], efmt, ew[i])) return 0;
+        if (!d->exps[i] || !r_weight(d->exps[i], d->exps_len[i], erows[i], ecols[i], efmt, ew[i])) return 0;
     float *rb = nullptr, *gb = nullptr, *ub = nullptr, *db = nullptr;
     if (d->router_bias && !upload(d->router_bias, R.n_exp, &rb)) return 0;
     if (d->exps_bias[0] && !upload(d->exps_bias[0], (size_t)R.n_exp * R.hidden, &gb)) return 0;
@@ -2401,7 +2461,7 @@ int rusty_hip_resident_set_layer(uint32_t l, const RustyResidentLayerDesc *d) {
     for (int i = 0; i < 7; i++) {
         int fmt = dt_to_fmt(d->w_dt[i]);
         if (!d->w[i] || fmt < 0 || d->w_rows[i] != want_rows[i] || !cat_of(fmt, (int)cols[i])) return 0;
-        if (!get_weight(d->w[i], d->w_len[i], d->w_rows[i], cols[i], fmt, &Ly.w[i])) return 0;
+        if (!r_weight(d->w[i], d->w_len[i], d->w_rows[i], cols[i], fmt, &Ly.w[i])) return 0;
     }
     if (!d->attn_norm || !d->ffn_norm) return 0;
     if (!r_alloc((void **)&Ly.attn_norm, R.dim * 4) || !r_alloc((void **)&Ly.ffn_norm, R.dim * 4)) return 0;
@@ -2437,14 +2497,14 @@ int rusty_hip_resident_set_output(const float *output_norm, const uint8_t *outpu
     if (inv_freq_len < R.hd / 2) return 0;
     int fmt = dt_to_fmt(output_dt);
     if (fmt < 0 || !cat_of(fmt, (int)R.dim)) return 0;
-    if (!get_weight(output_w, output_w_len, output_rows, R.dim, fmt, &R.out_w)) return 0;
+    if (!r_weight(output_w, output_w_len, output_rows, R.dim, fmt, &R.out_w)) return 0;
     if (!r_alloc((void **)&R.out_norm, R.dim * 4)) return 0;
     RH_CHECK(hipMemcpy(R.out_norm, output_norm, R.dim * 4, hipMemcpyHostToDevice));
     // RoPE table: the reference's angle (float)pos * inv_freq[i] and libm
     // sinf/cosf (apply_rope_qk, src/model.rs:5574-5575).
     size_t half = R.hd / 2;
-    std::vector<float> ct((size_t)R.storage * half), stb((size_t)R.storage * half);
-    for (size_t p = 0; p < R.storage; p++)
+    std::vector<float> ct((size_t)R.max_pos * half), stb((size_t)R.max_pos * half);
+    for (size_t p = 0; p < R.max_pos; p++)
         for (size_t i = 0; i < half; i++) {
             float ang = (float)p * inv_freq[i];
             // gpt-oss scales both by the YaRN concentration (apply_rope_gpt_oss,
@@ -2467,7 +2527,7 @@ int rusty_hip_resident_set_embedding(const uint8_t *embd, uintptr_t embd_len, ui
     if (!R.configured || !embd) return 0;
     int fmt = (int)t;
     if (row_bytes_of(fmt, R.dim) <= 0) return 0;
-    if (!get_weight(embd, embd_len, R.vocab, R.dim, fmt, &R.embd)) return 0;
+    if (!r_weight(embd, embd_len, R.vocab, R.dim, fmt, &R.embd)) return 0;
     R.has_embd = true;
     r_invalidate_graphs();
     return 1;
@@ -2476,8 +2536,10 @@ int rusty_hip_resident_set_embedding(const uint8_t *embd, uintptr_t embd_len, ui
 int rusty_hip_resident_decode(const float *x_embed, uint32_t pos, uint32_t start_t, int want_logits,
                               float *logits_out) {
     std::lock_guard<std::mutex> lk(g.mu);
-    if (!R.ready || !x_embed || pos >= R.storage) return 0;
+    if (!R.ready || !x_embed || pos >= R.max_pos) return 0;
     if (want_logits && !logits_out) return 0;
+    // forward_gpt_oss_into has no start_t: its full layers scan from 0
+    if (R.moe) start_t = 0;
     if (!r_set_state((int)pos, (int)start_t, 0, false)) return 0;
     RH_CHECK(hipMemcpyAsync(R.x, x_embed, R.dim * 4, hipMemcpyHostToDevice, g.s));
     if (!r_run(want_logits ? MODE_LOGITS : 0, 1.0f)) return 0;
@@ -2491,7 +2553,7 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
                                 float penalty, int32_t *out_tokens, float *logits_out) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (!R.ready || !R.has_embd || !prompt || n_prompt == 0 || (n_gen > 0 && !out_tokens)) return 0;
-    if ((uint64_t)start_pos + n_prompt + n_gen > (uint64_t)R.storage + 1) return 0;
+    if ((uint64_t)start_pos + n_prompt + n_gen > (uint64_t)R.max_pos + 1) return 0;
     for (uint32_t i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= R.vocab) return 0;
     if (!r_ensure_tokens(std::max(n_prompt, n_gen) + 1)) return 0;
@@ -2546,33 +2608,20 @@ int rusty_hip_resident_time_decode(uint32_t n_tokens, float penalty, double *ms)
     std::lock_guard<std::mutex> lk(g.mu);
     if (!R.ready || !R.has_embd || !ms) return 0;
     if (R.tok_cap < n_tokens + 1) {
-        uint32_t need = std::max<uint32_t>(n_tokens + 1, std::min<uint32_t>(R.storage + 1, 8192));
+        uint32_t need = std::max<uint32_t>(n_tokens + 1, std::min<uint32_t>(R.max_pos + 1, 8192));
         if (!r_alloc((void **)&R.tokens, (size_t)need * 4)) return 0;
         R.tok_cap = need;
         r_invalidate_graphs();
     }
     RH_CHECK(hipStreamSynchronize(g.s));
     RH_CHECK(hipMemcpy(R.st_host, R.st, sizeof(StepState), hipMemcpyDeviceToHost));
-    if ((uint64_t)R.st_host->pos + n_tokens > R.storage) return 0;
+    if ((uint64_t)R.st_host->pos + n_tokens > R.max_pos) return 0;
     RH_CHECK(hipMemsetAsync(R.out_idx, 0, 4, g.s));
     // make sure the graph exists before timing
     if (use_graphs()) {
-        uint32_t pb;
-        memcpy(&pb, &penalty, 4);
-        int key = (MODE_DEVTOK | MODE_GREEDY) ^ (int)(pb * 2654435761u & 0x7ffffff8u);
-        if (R.graphs.find(key) == R.graphs.end()) {
-            // capture only (no launch): replay below is timed
-            hipGraph_t graph;
-            RH_CHECK(hipStreamBeginCapture(g.s, hipStreamCaptureModeThreadLocal));
-            int ok = r_enqueue(MODE_DEVTOK | MODE_GREEDY, penalty, g.s);
-            hipError_t e = hipStreamEndCapture(g.s, &graph);
-            if (!ok || e != hipSuccess) return 0;
-            hipGraphExec_t exec;
-            hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(graph);
-            RH_CHECK(ie);
-            R.graphs.emplace(key, exec);
-        }
+        // capture only (no launch): the replays below are timed
+        hipGraphExec_t exec;
+        if (!r_graph(MODE_DEVTOK | MODE_GREEDY, penalty, &exec)) return 0;
     }
     hipEvent_t a, b;
     RH_CHECK(hipEventCreate(&a));

@@ -265,4 +265,31 @@ void synth_rope_inv_freq(float theta, int64_t head_dim, float scaling, float *ou
         out[pair] = 1.0f / (scaling * base * 1.0f);
     }
 }
+
+// gpt-oss YaRN table as the reference's loader builds it
+// (build_rope_inv_freq_gpt_oss, src/model.rs:3059-3098): pairs below `low`
+// keep 1/base, pairs above `high` get 1/(scaling*base), a linear ramp in
+// between; concentration = 0.1 ln(scaling) + 1.  f32 arithmetic with libm
+// logf/powf (Rust's f32::ln / powf), nothing contracted.
+void synth_rope_inv_freq_gpt_oss(float theta, int64_t head_dim, float scaling, int64_t orig_ctx, float *out,
+                                 float *concentration) {
+    const bool yarn = scaling > 1.0f;
+    const float two_pi = 2.0f * 3.14159265358979323846f;
+    const float half = (float)head_dim / 2.0f;
+    // 32 and 1 are the fast/slow rotation counts of the ramp's ends
+    const float lo = yarn ? half * (logf((float)orig_ctx / (32.0f * two_pi)) / logf(theta)) : 0.0f;
+    const float hi = yarn ? half * (logf((float)orig_ctx / two_pi) / logf(theta)) : 0.0f;
+    *concentration = yarn ? 0.1f * logf(scaling) + 1.0f : 1.0f;
+    for (int64_t pair = 0; pair < head_dim / 2; pair++) {
+        const float base = powf(theta, (float)(2 * pair) / (float)head_dim);
+        if (!yarn) {
+            out[pair] = 1.0f / base;
+            continue;
+        }
+        float r = ((float)pair - lo) / (hi - lo);
+        r = std::min(1.0f, std::max(0.0f, r));
+        const float keep = 1.0f - r;  // weight of the extrapolated frequency
+        out[pair] = (1.0f / (scaling * base)) * (1.0f - keep) + (1.0f / base) * keep;
+    }
+}
 }

@@ -287,28 +287,42 @@ class Resident:
                                               storage_len, cfg["eps"], 1 if cfg.get("neox") else 0)
         if ok != 1:
             raise RuntimeError("rusty_hip_resident_configure failed")
+        # every host array handed over stays referenced until the call returns
+        self._keep = []
+
+        def hold(a, conv):
+            a = conv(a)
+            self._keep.append(a)
+            return _ptr(a)
+
         for l, layer in enumerate(model["layers"]):
             d = ResidentLayerDesc()
             for i, (arr, dt, rows) in enumerate(layer["w"]):
-                d.w[i] = _ptr(arr)
+                d.w[i] = hold(arr, _u8)
                 d.w_len[i] = arr.nbytes
                 d.w_rows[i] = rows
                 d.w_dt[i] = dt
-            d.attn_norm = _ptr(layer["attn_norm"])
-            d.ffn_norm = _ptr(layer["ffn_norm"])
+            d.attn_norm = hold(layer["attn_norm"], _f32)
+            d.ffn_norm = hold(layer["ffn_norm"], _f32)
             for nm in ("bq", "bk", "bv"):
                 b = layer.get(nm)
                 if b is not None:
-                    setattr(d, nm, _ptr(b))
-                    setattr(d, nm + "_len", b.size)
+                    setattr(d, nm, hold(b, _f32))
+                    setattr(d, nm + "_len", np.asarray(b).size)
             if lib.rusty_hip_resident_set_layer(l, C.byref(d)) != 1:
                 raise RuntimeError(f"rusty_hip_resident_set_layer({l}) failed")
+        self._set_output(model)
+        self._keep = []
+
+    def _set_output(self, model):
+        cfg = self.cfg
         out_w, out_dt = model["output"]
-        inv = _f32(model["inv_freq"])
-        if lib.rusty_hip_resident_set_output(_ptr(model["output_norm"]), _ptr(out_w), out_w.nbytes, cfg["vocab"],
-                                             out_dt, _ptr(inv), inv.size) != 1:
+        out_w, inv, norm = _u8(out_w), _f32(model["inv_freq"]), _f32(model["output_norm"])
+        if lib.rusty_hip_resident_set_output(_ptr(norm), _ptr(out_w), out_w.nbytes, cfg["vocab"], out_dt, _ptr(inv),
+                                             inv.size) != 1:
             raise RuntimeError("rusty_hip_resident_set_output failed")
         emb, emb_dt = model["token_embd"]
+        emb = _u8(emb)
         if lib.rusty_hip_resident_set_embedding(_ptr(emb), emb.nbytes, emb_dt) != 1:
             raise RuntimeError("rusty_hip_resident_set_embedding failed")
         self.vocab = cfg["vocab"]
@@ -374,41 +388,45 @@ class ResidentGptOss(Resident):
     """The resident decoder in gpt-oss mode over a model from
     rustyllm_amd.synth.make_gptoss (rusty_hip_resident_configure_moe)."""
 
-    def __init__(self, model, storage_len: int):
+    def __init__(self, model, max_len: int):
+        """max_len: positions the cache holds (the reference's KVCache
+        max_len); with a sliding window the device keeps a ring of
+        min(window, max_len) slots."""
         cfg = self.cfg = model["config"]
-        self.storage_len = storage_len
+        self.storage_len = max_len
+        w = cfg.get("window", 0)
+        self.slots = min(w, max_len) if w > 0 else max_len
         self._keep = []
+
+        def hold(a, conv):
+            a = conv(a)
+            self._keep.append(a)
+            return _ptr(a)
+
         ok = lib.rusty_hip_resident_configure_moe(cfg["n_layers"], cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"],
                                                   cfg["head_dim"], cfg["hidden_dim"], cfg["n_experts"],
-                                                  cfg["top_k"], cfg["vocab"], storage_len, cfg["window"],
-                                                  cfg["eps"], model["concentration"])
+                                                  cfg["top_k"], cfg["vocab"], max_len, w, cfg["eps"],
+                                                  model["concentration"])
         if ok != 1:
             raise RuntimeError("rusty_hip_resident_configure_moe failed")
+        router_dt = model.get("router_type", Q8_0)
+        exps_dt = model.get("experts_type", MXFP4)
         for l, L in enumerate(model["layers"]):
             d = MoeLayerDesc()
             for i, nm in enumerate(("wq", "wk", "wv", "wo")):
                 arr, t = L[nm]
-                d.w[i], d.w_len[i], d.w_dt[i] = _ptr(arr), arr.nbytes, t
+                d.w[i], d.w_len[i], d.w_dt[i] = hold(arr, _u8), arr.nbytes, t
             for nm in ("bq", "bk", "bv", "bo", "sinks", "attn_norm", "post_attn_norm", "router_bias"):
-                setattr(d, nm, _ptr(_f32(L[nm])))
-            d.router, d.router_len, d.router_dt = _ptr(L["router"]), L["router"].nbytes, Q8_0
+                setattr(d, nm, hold(L[nm], _f32))
+            d.router, d.router_len, d.router_dt = hold(L["router"], _u8), L["router"].nbytes, router_dt
             for i, nm in enumerate(("gate_exps", "up_exps", "down_exps")):
-                d.exps[i], d.exps_len[i] = _ptr(L[nm]), L[nm].nbytes
-                b = np.ascontiguousarray(L[nm + "_bias"], np.float32)
-                self._keep.append(b)
-                d.exps_bias[i] = _ptr(b)
-            d.exps_dt = MXFP4
+                d.exps[i], d.exps_len[i] = hold(L[nm], _u8), L[nm].nbytes
+                d.exps_bias[i] = hold(L[nm + "_bias"], _f32)
+            d.exps_dt = exps_dt
             if lib.rusty_hip_resident_set_moe_layer(l, C.byref(d)) != 1:
                 raise RuntimeError(f"rusty_hip_resident_set_moe_layer({l}) failed")
-        out_w, out_dt = model["output"]
-        inv = _f32(model["inv_freq"])
-        if lib.rusty_hip_resident_set_output(_ptr(model["output_norm"]), _ptr(out_w), out_w.nbytes, cfg["vocab"],
-                                             out_dt, _ptr(inv), inv.size) != 1:
-            raise RuntimeError("rusty_hip_resident_set_output failed")
-        emb, emb_dt = model["token_embd"]
-        if lib.rusty_hip_resident_set_embedding(_ptr(emb), emb.nbytes, emb_dt) != 1:
-            raise RuntimeError("rusty_hip_resident_set_embedding failed")
-        self.vocab = cfg["vocab"]
+        self._set_output(model)
+        self._keep = []
 
 
 # ---- profiling -------------------------------------------------------------------------

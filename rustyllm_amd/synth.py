@@ -66,6 +66,8 @@ def _load():
     lib.synth_token_ids.argtypes = [C.c_uint64, C.c_int64, C.c_uint32, C.c_void_p]
     lib.synth_rope_inv_freq.restype = None
     lib.synth_rope_inv_freq.argtypes = [C.c_float, C.c_int64, C.c_float, C.c_void_p]
+    lib.synth_rope_inv_freq_gpt_oss.restype = None
+    lib.synth_rope_inv_freq_gpt_oss.argtypes = [C.c_float, C.c_int64, C.c_float, C.c_int64, C.c_void_p, C.c_void_p]
     return lib
 
 
@@ -175,6 +177,11 @@ GPTOSS_CONFIGS = {
     "tiny-gptoss": dict(n_layers=3, dim=160, n_heads=4, n_kv_heads=2, head_dim=64, hidden_dim=96, n_experts=6,
                         top_k=2, vocab=500, window=8, theta=150000.0, rope_scaling=32.0, rope_orig_ctx=4096,
                         eps=1e-5),
+    # the same with the real 128-position window: the ring then has enough
+    # slots for the main (LDS-tiled) attention kernels
+    "tiny-gptoss-w128": dict(n_layers=3, dim=160, n_heads=4, n_kv_heads=2, head_dim=64, hidden_dim=96, n_experts=6,
+                             top_k=2, vocab=500, window=128, theta=150000.0, rope_scaling=32.0, rope_orig_ctx=4096,
+                             eps=1e-5),
     "gpt-oss-20b": dict(n_layers=24, dim=2880, n_heads=64, n_kv_heads=8, head_dim=64, hidden_dim=2880,
                         n_experts=32, top_k=4, vocab=201088, window=128, theta=150000.0, rope_scaling=32.0,
                         rope_orig_ctx=4096, eps=1e-5),
@@ -183,27 +190,12 @@ GPTOSS_CONFIGS = {
 
 def rope_gpt_oss(theta: float, head_dim: int, scaling: float, orig_ctx: int):
     """build_rope_inv_freq_gpt_oss (src/model.rs:3059-3098): YaRN frequencies
-    and the concentration 0.1 ln(scaling) + 1, in f32 arithmetic."""
-    f = np.float32
-    d_half = f(head_dim) / f(2.0)
-    low = high = f(0.0)
-    if scaling > 1.0:
-        two_pi = f(2.0) * f(np.pi)
-        low = d_half * (np.log(f(orig_ctx) / (f(32.0) * two_pi)) / np.log(f(theta)))
-        high = d_half * (np.log(f(orig_ctx) / (f(1.0) * two_pi)) / np.log(f(theta)))
-    conc = f(0.1) * np.log(f(scaling)) + f(1.0) if scaling > 1.0 else f(1.0)
-    inv = np.zeros(head_dim // 2, np.float32)
-    for pair in range(head_dim // 2):
-        base = np.power(f(theta), f(pair * 2) / f(head_dim))
-        if scaling > 1.0:
-            ramp = np.clip((f(pair) - low) / (high - low), f(0.0), f(1.0))
-            mask = f(1.0) - ramp
-            interp = f(1.0) / (f(scaling) * base)
-            extrap = f(1.0) / base
-            inv[pair] = interp * (f(1.0) - mask) + extrap * mask
-        else:
-            inv[pair] = f(1.0) / base
-    return inv, float(conc)
+    and the concentration 0.1 ln(scaling) + 1, in f32 with libm logf/powf
+    (csrc/synth.cpp)."""
+    inv = np.empty(head_dim // 2, np.float32)
+    conc = C.c_float(0.0)
+    lib.synth_rope_inv_freq_gpt_oss(theta, head_dim, scaling, orig_ctx, inv.ctypes.data, C.addressof(conc))
+    return inv, float(conc.value)
 
 
 def make_gptoss(name_or_cfg, seed: int = 1234) -> dict:

@@ -196,3 +196,104 @@ def forward_model(model, tokens, start_pos=0):
         int_path = out_t in (12, 14) or (out_t == 8 and dim % 256 == 0)
         logits_all.append(Wo @ (q8k_dequant(xn) if int_path else xn))
     return np.array(logits_all)
+
+
+def forward_gptoss(model, tokens, max_len, ring=True):
+    """float64 restatement of forward_gpt_oss_into (src/model.rs:6733-6908)
+    for a rustyllm_amd.synth.make_gptoss model; returns every position's
+    logits.  Written from the semantics, not the oracle's loops:
+    - the KV cache is a ring of S = min(window, max_len) slots
+      (KVCache::with_sliding_window, model.rs:1363-1385); after position pos
+      is stored, slot s holds the newest position p <= pos with p % S == s;
+    - every layer scans steps t = start..pos reading slot t % S (the
+      reference's incrementing-slot walk), start = pos + 1 - window on even
+      layers and 0 on odd ones, so an odd layer past S positions sees each
+      slot's newest entry, cyclically, pos + 1 times in all;
+    - softmax over those scores plus the head's sink logit (zero value row)."""
+    c = model["config"]
+    dim, hd, vd = c["dim"], c["head_dim"], c.get("value_dim", c["head_dim"])
+    nh, nkv, hid = c["n_heads"], c["n_kv_heads"], c["hidden_dim"]
+    W = c["window"]
+    # ring=False: a linear cache of max_len slots (for showing that the ring matters)
+    S = min(W, max_len) if (W > 0 and ring) else max_len
+    kv_mul = nh // nkv
+    eps, conc, inv = c["eps"], float(model["concentration"]), np.asarray(model["inv_freq"], np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    emb_w, emb_t = model["token_embd"]
+    E = deq_matrix(emb_w, emb_t, c["vocab"], dim)
+    out_w, out_t = model["output"]
+    Wout = deq_matrix(out_w, out_t, c["vocab"], dim)
+    ne = c["n_experts"]
+
+    def mv(Wm, x, t, cols):
+        int_path = t in (12, 14) or (t == 8 and cols % 256 == 0)
+        return Wm @ (q8k_dequant(x) if int_path else x)
+
+    def rms(x, w):
+        return x / np.sqrt((x * x).mean() + eps) * np.asarray(w, np.float64)
+
+    def rope(x, n, pos):
+        x = x.reshape(n, hd).copy()
+        ang = (np.float32(pos) * inv).astype(np.float64)
+        cs, sn = np.cos(ang) * conc, np.sin(ang) * conc
+        a, b = x[:, 0::2].copy(), x[:, 1::2].copy()
+        x[:, 0::2], x[:, 1::2] = a * cs - b * sn, a * sn + b * cs
+        return x.reshape(-1)
+
+    def swiglu(g, u):
+        g = np.minimum(g, 7.0)
+        u = np.clip(u, -7.0, 7.0)
+        return g / (1.0 + np.exp(-1.702 * g)) * (u + 1.0)
+
+    layers = []
+    for L in model["layers"]:
+        D = {nm: deq_matrix(L[nm][0], L[nm][1], r, cl) for nm, r, cl in
+             (("wq", nh * hd, dim), ("wk", nkv * hd, dim), ("wv", nkv * vd, dim), ("wo", dim, nh * vd))}
+        D["router"] = deq_matrix(L["router"], 8, ne, dim)
+        D["gate"] = deq_matrix(L["gate_exps"], 39, ne * hid, dim).reshape(ne, hid, dim)
+        D["up"] = deq_matrix(L["up_exps"], 39, ne * hid, dim).reshape(ne, hid, dim)
+        D["down"] = deq_matrix(L["down_exps"], 39, ne * dim, hid).reshape(ne, dim, hid)
+        layers.append(D)
+    hist_k = [[] for _ in layers]
+    hist_v = [[] for _ in layers]
+    logits_all = []
+    for pos, tok in enumerate(tokens):
+        x = E[tok].copy()
+        for l, (L, D) in enumerate(zip(model["layers"], layers)):
+            xn = rms(x, L["attn_norm"])
+            q = mv(D["wq"], xn, L["wq"][1], dim) + L["bq"]
+            k = mv(D["wk"], xn, L["wk"][1], dim) + L["bk"]
+            v = mv(D["wv"], xn, L["wv"][1], dim) + L["bv"]
+            q, k = rope(q, nh, pos), rope(k, nkv, pos)
+            hist_k[l].append(k.reshape(nkv, hd))
+            hist_v[l].append(v.reshape(nkv, vd))
+            start = max(0, pos + 1 - W) if (l % 2 == 0 and W > 0) else 0
+            steps = np.arange(start, pos + 1)
+            slots = steps % S if W > 0 else steps
+            # newest position stored in each slot by now
+            newest = pos - ((pos - slots) % S) if W > 0 else slots
+            Kc = np.array([hist_k[l][p] for p in newest])
+            Vc = np.array([hist_v[l][p] for p in newest])
+            qh = q.reshape(nh, hd)
+            att = np.zeros((nh, vd))
+            for h in range(nh):
+                s = Kc[:, h // kv_mul, :] @ qh[h] * scale
+                sink = float(L["sinks"][h])
+                m = max(s.max(), sink)
+                w = np.exp(s - m)
+                att[h] = (w @ Vc[:, h // kv_mul, :]) / (w.sum() + np.exp(sink - m))
+            x = x + mv(D["wo"], att.reshape(-1), L["wo"][1], nh * vd) + L["bo"]
+            xn2 = rms(x, L["post_attn_norm"])
+            r = mv(D["router"], xn2, 8, dim) + L["router_bias"]
+            sel = np.argsort(-r, kind="stable")[: c["top_k"]]
+            p = np.exp(r[sel] - r[sel].max())
+            p /= p.sum()
+            moe = np.zeros(dim)
+            for e, pe in zip(sel, p):
+                g = D["gate"][e] @ xn2 + L["gate_exps_bias"][e]
+                u = D["up"][e] @ xn2 + L["up_exps_bias"][e]
+                moe += (D["down"][e] @ swiglu(g, u) + L["down_exps_bias"][e]) * pe
+            x = x + moe
+        xn = rms(x, model["output_norm"])
+        logits_all.append(mv(Wout, xn, out_t, dim))
+    return np.array(logits_all)

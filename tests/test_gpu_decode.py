@@ -110,3 +110,41 @@ def test_tinyllama_config1_stream(hip, exact):
     o_toks, o_logits = orc.generate(prompt, 64, penalty=1.1)
     assert list(g_toks) == list(o_toks)
     assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))
+
+
+def test_start_t_changes_between_graph_replays(hip, exact):
+    """rusty_hip_resident_decode's start_t (the Metal decoder's attention start,
+    metal_backend.m:2167-2189) varying between replays of one captured graph:
+    the scores kernel issues its K loads from the start current at capture
+    and must reload when the device state starts elsewhere."""
+    model, res, orc = _pair("tiny-q4km", 128, seed=13)
+    emb, emb_t = model["token_embd"]
+    dim = model["config"]["dim"]
+    toks = synth.token_ids(6, 72, model["config"]["vocab"])
+    starts = [0] * 8 + [p // 3 for p in range(8, 40)] + [0, 5, 0, 17, 64, 3, 70, 1] + [p - 1 for p in range(48, 72)]
+    for pos, (t, st) in enumerate(zip(toks, starts)):
+        st = min(st, pos)
+        x = O.dequant_row(emb_t, emb[int(t) * O.row_bytes(emb_t, dim):], dim)
+        g = res.decode(x, pos, st, True)
+        r = orc.forward(int(t), pos, start_t=st)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (pos, st, np.max(np.abs(g - r)))
+
+
+def test_weight_cache_clear_leaves_resident_working(hip, exact):
+    """The resident decoder owns its weight copies: dropping the per-op cache
+    (as an integrator does before unmapping host weights) must not touch them."""
+    model, res, orc = _pair("tiny-q8", 64, seed=2)
+    emb, emb_t = model["token_embd"]
+    dim = model["config"]["dim"]
+    toks = synth.token_ids(5, 20, model["config"]["vocab"])
+    for pos, t in enumerate(toks):
+        if pos == 10:
+            hip.weight_cache_clear()
+        x = O.dequant_row(emb_t, emb[int(t) * O.row_bytes(emb_t, dim):], dim)
+        g = res.decode(x, pos, 0, True)
+        r = orc.forward(int(t), pos)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), pos
+    g_toks, _ = res.generate(toks[:4], 8, penalty=1.1, start_pos=20)
+    hip.weight_cache_clear()
+    g2, _ = res.generate(toks[:4], 8, penalty=1.1, start_pos=20)
+    assert list(g_toks) == list(g2)

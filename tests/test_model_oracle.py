@@ -1,6 +1,8 @@
 """Pins the oracle's decode forward (forward_into, src/model.rs:7177-7358) and
 decode loop (greedy + repeat penalty, src/runtime.rs:3266-3342) against an
 independent float64 numpy restatement on small synthetic models."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -43,3 +45,76 @@ def test_generate_matches_manual_loop():
             logits = b.forward(tok, pos)
             pos += 1
     assert list(toks) == manual
+
+
+def test_gptoss_forward_vs_f64_with_ring():
+    """OracleGptOss (forward_gpt_oss_into with the reference's window-sized KV
+    ring) against the float64 restatement, past three ring lengths: the odd
+    layers then scan the ring from slot 0 cyclically (pos + 1 steps)."""
+    model = synth.make_gptoss("tiny-gptoss", seed=5)
+    c = model["config"]
+    W = c["window"]
+    n = 3 * W + 5
+    toks = [int(t) for t in synth.token_ids(17, n, c["vocab"])]
+    orc = O.OracleGptOss(model, 64)
+    assert orc.storage == W and orc.ring
+    got = np.array([orc.forward(t, p) for p, t in enumerate(toks)])
+    ref = npref.forward_gptoss(model, toks, 64)
+    scale = np.abs(ref).max()
+    assert np.max(np.abs(got - ref)) < 5e-4 * scale, (np.max(np.abs(got - ref)), scale)
+    # the check is sensitive to the ring: a linear cache agrees up to the
+    # first wrap and then departs by far more than the tolerance
+    lin = npref.forward_gptoss(model, toks, 64, ring=False)
+    assert np.max(np.abs(lin[:W] - ref[:W])) < 1e-9 * scale
+    assert np.max(np.abs(lin[W + 1:] - ref[W + 1:])) > 1e-2 * scale
+
+
+def test_gptoss_short_cache_is_linear():
+    """max_len below the window: storage_len_for gives max_len slots and no
+    position ever wraps."""
+    model = synth.make_gptoss("tiny-gptoss", seed=6)
+    c = model["config"]
+    toks = [int(t) for t in synth.token_ids(3, 6, c["vocab"])]
+    orc = O.OracleGptOss(model, 6)
+    assert orc.storage == 6
+    got = np.array([orc.forward(t, p) for p, t in enumerate(toks)])
+    ref = npref.forward_gptoss(model, toks, 6)
+    assert np.max(np.abs(got - ref)) < 5e-4 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("theta,hd,scaling,orig", [(150000.0, 64, 32.0, 4096), (10000.0, 128, 4.0, 8192),
+                                                   (150000.0, 64, 1.0, 4096)])
+def test_yarn_table(theta, hd, scaling, orig):
+    """build_rope_inv_freq_gpt_oss (model.rs:3059-3098): the synthetic model's
+    table (csrc/synth.cpp) equals the oracle's bit for bit, and the oracle is
+    pinned by the ramp's closed form: pairs below `low` keep 1/base, pairs
+    above `high` get 1/(scaling*base) (both exactly, in f32), the ramp in
+    between within 1e-6 of float64, the concentration 0.1 ln(s) + 1."""
+    inv, conc = O.rope_inv_freq_gpt_oss(theta, hd, scaling, orig)
+    s_inv, s_conc = synth.rope_gpt_oss(theta, hd, scaling, orig)
+    assert np.array_equal(inv.view(np.uint32), s_inv.view(np.uint32)) and conc == s_conc
+    f = np.float32
+    # libm powf itself (numpy's float32 power can differ from it in the last bit)
+    libm = ctypes.CDLL("libm.so.6")
+    libm.powf.restype = ctypes.c_float
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    base = np.array([libm.powf(theta, float(f(2 * i) / f(hd))) for i in range(hd // 2)], np.float32)
+    if scaling <= 1.0:
+        assert conc == 1.0
+        assert np.array_equal(inv, (f(1.0) / base).astype(np.float32))
+        assert np.array_equal(inv, O.rope_inv_freq(theta, hd, 1.0))
+        return
+    assert abs(conc - (0.1 * np.log(scaling) + 1.0)) < 1e-6
+    half = hd / 2
+    low = half * np.log(orig / (32 * 2 * np.pi)) / np.log(theta)
+    high = half * np.log(orig / (2 * np.pi)) / np.log(theta)
+    b64 = np.power(np.float64(theta), np.arange(hd // 2) * 2.0 / hd)
+    ramp = np.clip((np.arange(hd // 2) - low) / (high - low), 0.0, 1.0)
+    ref = (1.0 / (scaling * b64)) * ramp + (1.0 / b64) * (1.0 - ramp)
+    assert np.max(np.abs(inv - ref) / ref) < 1e-5
+    lo_pairs = np.arange(hd // 2) < np.floor(low) - 1
+    hi_pairs = np.arange(hd // 2) > np.ceil(high) + 1
+    assert lo_pairs.any() and hi_pairs.any()
+    assert np.array_equal(inv[lo_pairs], (f(1.0) / base[lo_pairs]).astype(np.float32))
+    assert np.array_equal(inv[hi_pairs], (f(1.0) / (f(scaling) * base[hi_pairs])).astype(np.float32))
+    assert np.all(np.diff(inv) < 0)
