@@ -245,6 +245,23 @@ int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n
                                      float rope_concentration);
 int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *desc);
 
+/* No reference counterpart: rusty_hip_attention for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, checks, numerics and
+ * attention mode as rusty_hip_attention, but query, keys, values, sinks and
+ * out are DEVICE pointers, and the call makes no allocation: its scratch (the
+ * exact order's scores, coefficients and masks, or the split-K partials) is
+ * one fixed 16 MiB device array per GPU, held until the process ends.
+ * Returns 0, with a message on stderr, when a call needs more than that
+ * (exact order: about 12 bytes per query head per attended position, so
+ * heads x positions up to ~1.3 M, e.g. 40 heads over 32768 positions).  Calls
+ * that overlap on one GPU share the array and race.  Synchronous. */
+int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
+                                const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,
+                                float *out, uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim,
+                                uintptr_t value_dim, uintptr_t key_stride, uintptr_t value_stride,
+                                uintptr_t slot_count, uintptr_t start_t, uintptr_t end_t, float scale, int use_sink);
+
 /* Attention order for every later call (no reference counterpart).
  * 0 (default): the reference's serial online-softmax order with glibc's expf,
  * bit for bit (src/model.rs:5739-6198); 1: split-K flash decode, within

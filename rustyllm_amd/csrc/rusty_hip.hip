@@ -27,6 +27,14 @@
 
 #include "../../include/rusty_hip.h"
 
+// Device scratch of rusty_hip_attention_noalloc: the exact-attention scores,
+// coefficients and masks, or the split-K partials, of one call.  Every GPU
+// holds its own copy for the life of the process; host code uses the address
+// hipGetSymbolAddress returns for the current device (Ctx::noalloc), never
+// this name, which on the host is only a stand-in.
+#define RH_NOALLOC_SCRATCH_BYTES (16u << 20)
+static __device__ __align__(256) float scratch[RH_NOALLOC_SCRATCH_BYTES / 4];
+
 namespace rh {
 
 // ---- errors -------------------------------------------------------------------
@@ -112,6 +120,7 @@ struct Ctx {
     size_t bx_cap = 0, by_cap = 0;
     int attn_fast = -1;   // -1: read RUSTY_HIP_ATTN once; 0 exact, 1 split-K
     Profile prof;
+    float *noalloc[16] = {};  // device address of `scratch`, per device (set up by init)
 };
 static Ctx g;
 
@@ -141,6 +150,13 @@ static int init_locked() {
     }
     g.n_cu = prop.multiProcessorCount;
     RH_CHECK(hipStreamCreateWithFlags(&g.s, hipStreamNonBlocking));
+    // the no-allocation entry point's scratch on this device (device 0 is current)
+    void *sp = nullptr;
+    if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) != hipSuccess || !sp) {
+        if (debug_on()) fprintf(stderr, "[rusty_hip] no address for the no-allocation scratch\n");
+        sp = nullptr;
+    }
+    g.noalloc[g.dev] = (float *)sp;
     g.state = 1;
     return 1;
 }
@@ -1294,22 +1310,114 @@ int rusty_hip_mistral_post_attention_ffn(const uint8_t *ow, uintptr_t ol, const 
     return 1;
 }
 
+}  // extern "C"
+
+namespace rh {
+// Argument checks of rusty_metal_attention (src/metal.rs:277-299; *_len are
+// byte lengths, metal_backend.m:2082-2086), shared by both attention exports.
+static bool attn_export_args_ok(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
+                                const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,
+                                const float *out, uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul,
+                                uintptr_t head_dim, uintptr_t value_dim, uintptr_t key_stride, uintptr_t value_stride,
+                                uintptr_t slot_count, uintptr_t start_t, uintptr_t end_t, int use_sink) {
+    if (!query || !keys || !values || !out || heads == 0 || kv_mul == 0 || head_dim == 0 || value_dim == 0 ||
+        slot_count == 0 || head_dim > 256 || value_dim > 256)
+        return false;
+    if (heads % kv_mul != 0 || !attn_supported((int)head_dim, (int)value_dim, (int)kv_mul)) return false;
+    if (key_stride % 4 != 0 || value_stride % 4 != 0) return false;
+    const size_t n_kv = heads / kv_mul;
+    if (key_stride < n_kv * head_dim || value_stride < n_kv * value_dim) return false;
+    if (query_len < heads * head_dim * 4 || keys_len < slot_count * key_stride * 4 ||
+        values_len < slot_count * value_stride * 4 || out_len < heads * value_dim * 4 ||
+        (use_sink && (!sinks || sinks_len < heads * 4)))
+        return false;
+    // positions and slots travel as int32 in the kernels
+    if (end_t >= (uintptr_t)INT32_MAX || slot_count >= (uintptr_t)INT32_MAX) return false;
+    return true;
+}
+
+// One attention call over device buffers on the library stream: the scratch
+// it needs (floats), and the launches.  Exact mode: scores, coefficients and
+// masks of a cap-position range (exact_scratch_floats); split-K: the
+// per-chunk partials.
+struct AttnCall {
+    AttnArgs A;
+    bool fast;
+    int cap;
+    size_t scratch_floats;
+};
+static AttnCall attn_call_plan(const float *q, const float *k, const float *v, const float *sinks, float *out,
+                               uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim, uintptr_t value_dim,
+                               uintptr_t key_stride, uintptr_t value_stride, uintptr_t slot_count, uintptr_t start_t,
+                               uintptr_t end_t, float scale) {
+    AttnCall C;
+    memset(&C, 0, sizeof(C));
+    AttnArgs &A = C.A;
+    A.q = q;
+    A.k = k;
+    A.v = v;
+    A.sinks = sinks;
+    A.out = out;
+    A.n_heads = (int)heads;
+    A.n_kv = (int)(heads / kv_mul);
+    A.kv_mul = (int)kv_mul;
+    A.hd = (int)head_dim;
+    A.vd = (int)value_dim;
+    A.key_stride = (int64_t)key_stride;
+    A.value_stride = (int64_t)value_stride;
+    A.slot_count = (int)slot_count;
+    A.start_t = (int)start_t;
+    A.end_t = (int)end_t;
+    A.scale = scale;
+    const int ctx = (int)(end_t - start_t + 1);
+    A.n_chunks = attn_chunks(A.n_kv, ctx);
+    C.fast = attn_fast_mode() != 0;
+    C.cap = (ctx + 63) / 64 * 64;
+    C.scratch_floats = C.fast ? (size_t)A.n_kv * A.n_chunks * A.kv_mul * att_pstride(A.vd)
+                              : exact_scratch_floats(A.n_kv, A.kv_mul, C.cap);
+    return C;
+}
+static int attn_call_launch(AttnCall C, float *scratch, hipStream_t s) {
+    const AttnArgs &A = C.A;
+    if (C.fast) {
+        C.A.part = scratch;
+        return attn_launch(C.A, s);
+    }
+    AttnExactArgs E;
+    memset(&E, 0, sizeof(E));
+    E.q = A.q;
+    E.k = A.k;
+    E.v = A.v;
+    E.sinks = A.sinks;
+    E.out = A.out;
+    E.n_heads = A.n_heads;
+    E.n_kv = A.n_kv;
+    E.kv_mul = A.kv_mul;
+    E.hd = A.hd;
+    E.vd = A.vd;
+    E.key_stride = A.key_stride;
+    E.value_stride = A.value_stride;
+    E.slot_count = A.slot_count;
+    E.start_t = A.start_t;
+    E.end_t = A.end_t;
+    E.scale = A.scale;
+    E.cap = C.cap;
+    return attn_exact_launch(E, scratch, XQ{}, s);
+}
+}  // namespace rh
+
+extern "C" {
+
 int rusty_hip_attention(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
                         const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len, float *out,
                         uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim, uintptr_t value_dim,
                         uintptr_t key_stride, uintptr_t value_stride, uintptr_t slot_count, uintptr_t start_t,
                         uintptr_t end_t, float scale, int use_sink) {
     std::lock_guard<std::mutex> lk(g.mu);
-    if (!init_locked() || !query || !keys || !values || !out || heads == 0 || kv_mul == 0 || head_dim == 0 ||
-        value_dim == 0 || slot_count == 0 || head_dim > 256 || value_dim > 256)
-        return 0;
-    if (heads % kv_mul != 0 || !attn_supported((int)head_dim, (int)value_dim, (int)kv_mul)) return 0;
-    if (key_stride % 4 != 0 || value_stride % 4 != 0) return 0;
-    size_t n_kv = heads / kv_mul;
-    if (key_stride < n_kv * head_dim || value_stride < n_kv * value_dim) return 0;
-    if (query_len < heads * head_dim * 4 || keys_len < slot_count * key_stride * 4 ||
-        values_len < slot_count * value_stride * 4 || out_len < heads * value_dim * 4 ||
-        (use_sink && (!sinks || sinks_len < heads * 4)))
+    if (!init_locked() ||
+        !attn_export_args_ok(query, query_len, keys, keys_len, values, values_len, sinks, sinks_len, out, out_len,
+                             heads, kv_mul, head_dim, value_dim, key_stride, value_stride, slot_count, start_t, end_t,
+                             use_sink))
         return 0;
     if (start_t > end_t) {  // empty range: the reference leaves out untouched
         return 1;
@@ -1334,54 +1442,52 @@ int rusty_hip_attention(const float *query, uintptr_t query_len, const float *ke
     if (!ensure(&g.x, &g.x_cap, qn + heads) || !ensure(&g.y, &g.y_cap, on)) return 0;
     RH_CHECK(hipMemcpyAsync(g.x, query, qn * 4, hipMemcpyHostToDevice, g.s));
     if (use_sink) RH_CHECK(hipMemcpyAsync(g.x + qn, sinks, heads * 4, hipMemcpyHostToDevice, g.s));
-    AttnArgs A;
-    memset(&A, 0, sizeof(A));
-    A.q = g.x;
-    A.k = g.kv_k;
-    A.v = g.kv_v;
-    A.sinks = use_sink ? g.x + qn : nullptr;
-    A.out = g.y;
-    A.n_heads = (int)heads;
-    A.n_kv = (int)n_kv;
-    A.kv_mul = (int)kv_mul;
-    A.hd = (int)head_dim;
-    A.vd = (int)value_dim;
-    A.key_stride = (int64_t)key_stride;
-    A.value_stride = (int64_t)value_stride;
-    A.slot_count = (int)slot_count;
-    A.start_t = (int)start_t;
-    A.end_t = (int)end_t;
-    A.n_chunks = attn_chunks((int)n_kv, (int)(end_t - start_t + 1));
-    A.scale = scale;
-    if (attn_fast_mode()) {
-        if (!ensure(&g.part, &g.part_cap, (size_t)n_kv * A.n_chunks * kv_mul * att_pstride((int)value_dim))) return 0;
-        A.part = g.part;
-        if (!attn_launch(A, g.s)) return 0;
+    AttnCall C = attn_call_plan(g.x, g.kv_k, g.kv_v, use_sink ? g.x + qn : nullptr, g.y, heads, kv_mul, head_dim,
+                                value_dim, key_stride, value_stride, slot_count, start_t, end_t, scale);
+    float *scr;
+    if (C.fast) {
+        if (!ensure(&g.part, &g.part_cap, C.scratch_floats)) return 0;
+        scr = g.part;
     } else {
-        AttnExactArgs E;
-        memset(&E, 0, sizeof(E));
-        E.q = A.q;
-        E.k = A.k;
-        E.v = A.v;
-        E.sinks = A.sinks;
-        E.out = A.out;
-        E.n_heads = A.n_heads;
-        E.n_kv = A.n_kv;
-        E.kv_mul = A.kv_mul;
-        E.hd = A.hd;
-        E.vd = A.vd;
-        E.key_stride = A.key_stride;
-        E.value_stride = A.value_stride;
-        E.slot_count = A.slot_count;
-        E.start_t = A.start_t;
-        E.end_t = A.end_t;
-        E.scale = scale;
-        int ctx = (int)(end_t - start_t + 1);
-        E.cap = (ctx + 63) / 64 * 64;
-        if (!ensure(&g.ex, &g.ex_cap, exact_scratch_floats(E.n_kv, E.kv_mul, E.cap))) return 0;
-        if (!attn_exact_launch(E, g.ex, XQ{}, g.s)) return 0;
+        if (!ensure(&g.ex, &g.ex_cap, C.scratch_floats)) return 0;
+        scr = g.ex;
     }
+    if (!attn_call_launch(C, scr, g.s)) return 0;
     RH_CHECK(hipMemcpyAsync(out, g.y, on * 4, hipMemcpyDeviceToHost, g.s));
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+// rusty_hip_attention over device buffers with no allocation: the scratch is
+// the static `scratch` array of this device (its address taken at init).
+// Calls that overlap on one GPU share that array and race; each call
+// writes every scratch word it later reads, so nothing needs clearing.
+int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
+                                const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,
+                                float *out, uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim,
+                                uintptr_t value_dim, uintptr_t key_stride, uintptr_t value_stride,
+                                uintptr_t slot_count, uintptr_t start_t, uintptr_t end_t, float scale, int use_sink) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() ||
+        !attn_export_args_ok(query, query_len, keys, keys_len, values, values_len, sinks, sinks_len, out, out_len,
+                             heads, kv_mul, head_dim, value_dim, key_stride, value_stride, slot_count, start_t, end_t,
+                             use_sink))
+        return 0;
+    float *scr = g.noalloc[g.dev];
+    if (!scr) return 0;
+    if (start_t > end_t) return 1;  // empty range: out untouched, as the reference
+    AttnCall C = attn_call_plan(query, keys, values, use_sink ? sinks : nullptr, out, heads, kv_mul, head_dim,
+                                value_dim, key_stride, value_stride, slot_count, start_t, end_t, scale);
+    if (C.scratch_floats * sizeof(float) > RH_NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr,
+                "[rusty_hip] rusty_hip_attention_noalloc: %zu bytes of scratch needed for %zu heads over %zu "
+                "positions, above the fixed %u-byte maximum; call rusty_hip_attention instead\n",
+                C.scratch_floats * sizeof(float), (size_t)heads, (size_t)(end_t - start_t + 1),
+                (unsigned)RH_NOALLOC_SCRATCH_BYTES);
+        return 0;
+    }
+    if (!attn_call_launch(C, scr, g.s)) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
     return 1;

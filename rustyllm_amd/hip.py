@@ -33,7 +33,7 @@ SYMBOLS = [
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
     "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
-    "rusty_hip_bench_attention",
+    "rusty_hip_bench_attention", "rusty_hip_attention_noalloc",
 ]
 
 
@@ -65,6 +65,8 @@ for _n in ("rusty_hip_q6k_matvec3", "rusty_hip_q4k_matvec3", "rusty_hip_q4k_q4k_
 _sig("rusty_hip_q4k_q4k_q6k_ffn", _i, _p, _u, _p, _u, _p, _u, _p, _u, _u, _u, _u, _p)
 _sig("rusty_hip_mistral_post_attention_ffn", _i, _p, _u, _p, _u, _p, _u, _p, _u, _p, _u, _p, _u, _p, _f, _u, _u, _u)
 _sig("rusty_hip_attention", _i, _p, _u, _p, _u, _p, _u, _p, _u, _p, _u, _u, _u, _u, _u, _u, _u, _u, _u, _u, _f, _i)
+_sig("rusty_hip_attention_noalloc", _i, _p, _u, _p, _u, _p, _u, _p, _u, _p, _u, _u, _u, _u, _u, _u, _u, _u, _u, _u, _f,
+     _i)
 _sig("rusty_hip_resident_configure", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f, _u32)
 _sig("rusty_hip_resident_set_layer", _i, _u32, _p)
 _sig("rusty_hip_resident_set_output", _i, _p, _p, _u, _u32, _u32, _p, _u32)
@@ -238,6 +240,19 @@ def attention_with_sink_into(query, keys, values, sinks, out, heads, kv_mul, hea
                              value_stride, slot_count, start_t, end_t, scale) -> bool:
     return _attention(query, keys, values, sinks, out, heads, kv_mul, head_dim, value_dim, key_stride, value_stride,
                       slot_count, start_t, end_t, scale)
+
+
+def attention_noalloc_dev(q_ptr, k_ptr, v_ptr, sinks_ptr, out_ptr, heads, kv_mul, head_dim, value_dim, key_stride,
+                          value_stride, slot_count, start_t, end_t, scale) -> bool:
+    """rusty_hip_attention_noalloc on device buffers given by address (e.g. a
+    torch tensor's data_ptr()); the library allocates nothing for the call."""
+    n_kv = heads // kv_mul
+    ql, kl, vl = heads * head_dim * 4, slot_count * key_stride * 4, slot_count * value_stride * 4
+    ol, sl = heads * value_dim * 4, (heads * 4 if sinks_ptr else 0)
+    assert key_stride >= n_kv * head_dim and value_stride >= n_kv * value_dim
+    return lib.rusty_hip_attention_noalloc(q_ptr, ql, k_ptr, kl, v_ptr, vl, sinks_ptr or None, sl, out_ptr, ol, heads,
+                                           kv_mul, head_dim, value_dim, key_stride, value_stride, slot_count,
+                                           start_t, end_t, scale, 1 if sinks_ptr else 0) == 1
 
 
 # ---- resident decoder (src/metal.rs:302-360) --------------------------------------------
