@@ -262,6 +262,39 @@ int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const f
                                 uintptr_t value_dim, uintptr_t key_stride, uintptr_t value_stride,
                                 uintptr_t slot_count, uintptr_t start_t, uintptr_t end_t, float scale, int use_sink);
 
+/* ===== GGUF on-disk path (src/gguf.rs; src/model.rs:40-120, 3573-3860,
+ * 5180-5420) ============================================================== */
+
+/* What the reference's parser and loaders read from a GGUF v3 file
+ * (GGUFFile::parse, Config::from_gguf and load_model's head/value dim
+ * override from the attn_q / attn_v shapes).  Host only: needs no GPU. */
+typedef struct {
+    char arch[32];              /* general.architecture (default "llama") */
+    uint32_t version, n_tensors;
+    uint64_t data_offset;       /* start of tensor data (general.alignment, default 32) */
+    uint32_t n_layers, dim, n_heads, n_kv_heads, head_dim, value_dim, hidden_dim, vocab;
+    uint32_t context_length, sliding_window, n_experts, top_k, rope_orig_ctx;
+    float rope_theta, rms_eps, rope_scaling;
+    uint32_t tied_output;       /* no output.weight: the head reuses token_embd (src/model.rs:3653-3667) */
+    uint32_t fused_qkv;         /* blk.N.attn_qkv.weight instead of attn_q/k/v (:3795-3859) */
+    uint32_t qkv_bias;
+} RustyGgufSummary;
+int rusty_hip_gguf_summary(const char *path, RustyGgufSummary *out);
+
+/* Configures the resident decoder from a GGUF file (no reference
+ * counterpart: the reference's Rust loader would call the resident exports
+ * itself).  llama / qwen2 / qwen3 files go through rusty_hip_resident_configure
+ * and set_layer as load_model maps them (tied output, fused attn_qkv split by
+ * rows, the shape override of head/value dim); gpt-oss files through
+ * configure_moe / set_moe_layer as load_gpt_oss_model maps them.  RoPE
+ * tables are built as the reference's DecodeBuffer does (build_rope_inv_freq,
+ * or the YaRN table for gpt-oss).  max_len is the cache length.  The file is
+ * mapped read-only and unmapped before the call returns; weights are copied
+ * through pinned staging buffers into the decoder's own device copies.
+ * Returns 0 for an unreadable file, a missing tensor or a shape the decoder
+ * does not take (RUSTY_HIP_DEBUG=1 prints which). */
+int rusty_hip_resident_load_gguf(const char *path, uint32_t max_len);
+
 /* Attention order for every later call (no reference counterpart).
  * 0 (default): the reference's serial online-softmax order with glibc's expf,
  * bit for bit (src/model.rs:5739-6198); 1: split-K flash decode, within

@@ -11,6 +11,7 @@
 #include "moe.hip"
 #include "gemm_mfma.hip"
 #include "prefill.hip"
+#include "gguf.hpp"
 
 #include <hip/hip_ext.h>
 
@@ -121,6 +122,8 @@ struct Ctx {
     int attn_fast = -1;   // -1: read RUSTY_HIP_ATTN once; 0 exact, 1 split-K
     Profile prof;
     float *noalloc[16] = {};  // device address of `scratch`, per device (set up by init)
+    uint8_t *stage[2] = {nullptr, nullptr};  // pinned staging of weight uploads
+    hipEvent_t stage_ev[2] = {nullptr, nullptr};
 };
 static Ctx g;
 
@@ -217,6 +220,33 @@ static bool weight_shape_ok(const uint8_t *host, size_t len, int64_t rows, int64
     return (int64_t)len >= rows * rb;
 }
 
+// rows x rb host bytes (pageable, e.g. a mapped file) into device rows of
+// `stride` bytes through two pinned buffers: while the DMA of one chunk runs,
+// the host copies (and pages in) the next.  Synchronous.
+#define RH_STAGE_BYTES ((size_t)32 << 20)
+static hipError_t staged_upload(uint8_t *d, int64_t stride, const uint8_t *host, int64_t rb, int64_t rows) {
+    if (!g.stage[0]) {
+        for (int i = 0; i < 2; i++) {
+            hipError_t e = hipHostMalloc((void **)&g.stage[i], RH_STAGE_BYTES, hipHostMallocDefault);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&g.stage_ev[i], hipEventDisableTiming);
+            if (e != hipSuccess) return e;
+        }
+    }
+    const int64_t per = std::max<int64_t>(1, (int64_t)RH_STAGE_BYTES / rb);
+    int i = 0;
+    for (int64_t r0 = 0; r0 < rows; r0 += per, i ^= 1) {
+        const int64_t n = std::min(per, rows - r0);
+        hipError_t e = hipEventSynchronize(g.stage_ev[i]);  // this buffer's previous DMA is done
+        if (e != hipSuccess) return e;
+        memcpy(g.stage[i], host + r0 * rb, (size_t)(n * rb));
+        e = hipMemcpy2DAsync(d + r0 * stride, (size_t)stride, g.stage[i], (size_t)rb, (size_t)rb, (size_t)n,
+                             hipMemcpyHostToDevice, g.s);
+        if (e == hipSuccess) e = hipEventRecord(g.stage_ev[i], g.s);
+        if (e != hipSuccess) return e;
+    }
+    return hipStreamSynchronize(g.s);
+}
+
 // A new device copy of a host weight (the caller owns it).  Rows are padded
 // to a 16-byte stride; block bytes are copied unchanged.
 static int upload_weight(const uint8_t *host, int64_t rows, int64_t cols, int fmt, uint64_t fp, DevW *out) {
@@ -224,9 +254,13 @@ static int upload_weight(const uint8_t *host, int64_t rows, int64_t cols, int fm
     const int64_t stride = (rb + 15) / 16 * 16;
     uint8_t *d = nullptr;
     RH_CHECK(hipMalloc((void **)&d, (size_t)(rows * stride)));
-    hipError_t e = stride == rb ? hipMemcpy(d, host, (size_t)(rows * rb), hipMemcpyHostToDevice)
-                                : hipMemcpy2D(d, (size_t)stride, host, (size_t)rb, (size_t)rb, (size_t)rows,
-                                              hipMemcpyHostToDevice);
+    hipError_t e;
+    if ((size_t)(rows * rb) >= ((size_t)4 << 20) && (size_t)rb <= RH_STAGE_BYTES)
+        e = staged_upload(d, stride, host, rb, rows);
+    else
+        e = stride == rb ? hipMemcpy(d, host, (size_t)(rows * rb), hipMemcpyHostToDevice)
+                         : hipMemcpy2D(d, (size_t)stride, host, (size_t)rb, (size_t)rb, (size_t)rows,
+                                       hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(d);
         RH_CHECK(e);
@@ -2980,6 +3014,315 @@ int rusty_hip_bench_attention(uint32_t heads, uint32_t kv_mul, uint32_t head_dim
     (void)hipFree(kv);
     prof_drain();
     return ok;
+}
+
+// ---- GGUF on-disk path (src/gguf.rs, src/model.rs:3573-3860, :5180-5420) -------------
+
+// Model facts of a GGUF file as the reference's loaders see them.
+int rusty_hip_gguf_summary(const char *path, RustyGgufSummary *out) {
+    if (!path || !out) return 0;
+    GgufFile G;
+    if (!G.open_path(path)) {
+        if (debug_on()) fprintf(stderr, "[rusty_hip] %s: %s\n", path, G.error.c_str());
+        return 0;
+    }
+    GgufConfig c = gguf_config(G);
+    memset(out, 0, sizeof(*out));
+    snprintf(out->arch, sizeof(out->arch), "%s", c.arch.c_str());
+    out->version = G.version;
+    out->n_tensors = (uint32_t)G.tensors.size();
+    out->data_offset = G.data_offset;
+    out->n_layers = c.n_layers;
+    out->dim = c.dim;
+    out->n_heads = c.n_heads;
+    out->n_kv_heads = c.n_kv;
+    out->head_dim = c.head_dim;
+    out->value_dim = c.value_dim;
+    out->hidden_dim = c.hidden;
+    out->vocab = c.vocab;
+    out->context_length = c.ctx;
+    out->sliding_window = c.window;
+    out->n_experts = c.n_experts;
+    out->top_k = c.top_k;
+    out->rope_orig_ctx = c.rope_orig_ctx;
+    out->rope_theta = c.theta;
+    out->rms_eps = c.eps;
+    out->rope_scaling = c.rope_scaling;
+    // load_model's shape override of head_dim / value_dim (src/model.rs:3668-3724)
+    for (uint32_t l = 0; l < c.n_layers && c.arch != "gpt-oss"; l++) {
+        const GgufTensor *q = G.find("blk." + std::to_string(l) + ".attn_q.weight");
+        const GgufTensor *v = G.find("blk." + std::to_string(l) + ".attn_v.weight");
+        bool hq = false, hv = false;
+        if (q && q->dims.size() >= 2 && q->dims[0] == c.dim && c.n_heads && q->dims[1] % c.n_heads == 0) {
+            out->head_dim = (uint32_t)(q->dims[1] / c.n_heads);
+            hq = true;
+        }
+        if (v && v->dims.size() >= 2 && v->dims[0] == c.dim && c.n_kv && v->dims[1] % c.n_kv == 0) {
+            out->value_dim = (uint32_t)(v->dims[1] / c.n_kv);
+            hv = true;
+        }
+        if (hq && hv) break;
+    }
+    out->tied_output = G.find("output.weight") ? 0 : 1;
+    out->fused_qkv = G.find("blk.0.attn_qkv.weight") ? 1 : 0;
+    out->qkv_bias = (G.find("blk.0.attn_q.bias") || G.find("blk.0.attn_qkv.bias")) ? 1 : 0;
+    return 1;
+}
+
+}  // extern "C"
+
+namespace rh {
+// A float vector tensor (F32, F16 or BF16) as f32, n elements.
+static bool gguf_f32(const GgufFile &G, const std::string &name, size_t n, std::vector<float> *out) {
+    const GgufTensor *t = G.find(name);
+    if (!t || t->numel() < n) return false;
+    int64_t len;
+    const uint8_t *p = G.data(*t, &len);
+    if (!p) return false;
+    out->resize(n);
+    if (t->type == 0) {
+        memcpy(out->data(), p, n * 4);
+    } else if (t->type == 1) {
+        for (size_t i = 0; i < n; i++) (*out)[i] = f16_to_f32_host((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
+    } else if (t->type == 30) {
+        for (size_t i = 0; i < n; i++) {
+            uint32_t b = (uint32_t)(p[2 * i] | (p[2 * i + 1] << 8)) << 16;
+            memcpy(&(*out)[i], &b, 4);
+        }
+    } else {
+        return false;
+    }
+    return true;
+}
+
+struct GgufMat {
+    const uint8_t *p = nullptr;
+    int64_t len = 0, rows = 0, cols = 0;
+    uint32_t type = 0;
+};
+// A 2-D (or expert-major 3-D) block tensor: rows = product of dims[1..].
+static bool gguf_mat(const GgufFile &G, const std::string &name, GgufMat *m) {
+    const GgufTensor *t = G.find(name);
+    if (!t || t->dims.size() < 2) return false;
+    m->p = G.data(*t, &m->len);
+    if (!m->p) return false;
+    m->cols = (int64_t)t->dims[0];
+    m->rows = 1;
+    for (size_t i = 1; i < t->dims.size(); i++) m->rows *= (int64_t)t->dims[i];
+    m->type = t->type;
+    return true;
+}
+
+static void gguf_note(const char *path, const std::string &what) {
+    if (debug_on()) fprintf(stderr, "[rusty_hip] %s: %s\n", path, what.c_str());
+}
+
+// build_rope_inv_freq (src/model.rs:3031-3057) and build_rope_inv_freq_gpt_oss
+// (:3059-3098) with libm powf / logf on f32, as Rust's f32::powf / ln.
+static std::vector<float> rope_table(const GgufConfig &c, bool yarn, float *concentration) {
+    const uint32_t half = c.head_dim / 2;
+    std::vector<float> inv(half);
+    *concentration = 1.0f;
+    const bool scaled = yarn && c.rope_scaling > 1.0f;
+    float lo = 0.0f, hi = 0.0f;
+    if (scaled) {
+        const float two_pi = 2.0f * 3.14159265358979323846f;
+        const float dh = (float)c.head_dim / 2.0f;
+        lo = dh * (logf((float)c.rope_orig_ctx / (32.0f * two_pi)) / logf(c.theta));
+        hi = dh * (logf((float)c.rope_orig_ctx / two_pi) / logf(c.theta));
+        *concentration = 0.1f * logf(c.rope_scaling) + 1.0f;
+    }
+    for (uint32_t i = 0; i < half; i++) {
+        const float base = powf(c.theta, (float)(2 * i) / (float)c.head_dim);
+        if (!yarn) {
+            inv[i] = 1.0f / (1.0f * base * 1.0f);
+        } else if (!scaled) {
+            inv[i] = 1.0f / base;
+        } else {
+            float r = ((float)i - lo) / (hi - lo);
+            r = std::min(1.0f, std::max(0.0f, r));
+            const float keep = 1.0f - r;
+            inv[i] = (1.0f / (c.rope_scaling * base)) * (1.0f - keep) + (1.0f / base) * keep;
+        }
+    }
+    return inv;
+}
+}  // namespace rh
+
+extern "C" {
+
+int rusty_hip_resident_load_gguf(const char *path, uint32_t max_len) {
+    if (!path || max_len == 0) return 0;
+    GgufFile G;
+    if (!G.open_path(path)) {
+        gguf_note(path, G.error);
+        return 0;
+    }
+    GgufConfig c = gguf_config(G);
+    auto blk = [](uint32_t l, const char *nm) { return "blk." + std::to_string(l) + "." + nm; };
+    std::vector<std::vector<float>> keep;  // host vectors alive until each call has uploaded them
+    auto vec = [&](const std::string &name, size_t n, const float **dst) {
+        keep.emplace_back();
+        if (!gguf_f32(G, name, n, &keep.back())) {
+            gguf_note(path, "missing or bad f32 tensor " + name);
+            return false;
+        }
+        *dst = keep.back().data();
+        return true;
+    };
+    auto mat = [&](const std::string &name, GgufMat *m) {
+        if (gguf_mat(G, name, m)) return true;
+        gguf_note(path, "missing or bad tensor " + name);
+        return false;
+    };
+    GgufMat emb, outw;
+    if (!mat("token_embd.weight", &emb)) return 0;
+    std::vector<float> out_norm;  // kept apart: `keep` is cleared after every layer
+    if (!gguf_f32(G, "output_norm.weight", c.dim, &out_norm)) {
+        gguf_note(path, "missing or bad f32 tensor output_norm.weight");
+        return 0;
+    }
+    float conc = 1.0f;
+    if (c.arch == "gpt-oss") {
+        if (!mat("output.weight", &outw)) return 0;
+        (void)rope_table(c, true, &conc);
+        if (!rusty_hip_resident_configure_moe(c.n_layers, c.dim, c.n_heads, c.n_kv, c.head_dim, c.hidden,
+                                              c.n_experts, c.top_k, c.vocab, max_len, c.window, c.eps, conc))
+            return 0;
+        for (uint32_t l = 0; l < c.n_layers; l++) {
+            RustyMoeLayerDesc d;
+            memset(&d, 0, sizeof(d));
+            const char *wn[4] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight"};
+            for (int i = 0; i < 4; i++) {
+                GgufMat m;
+                if (!mat(blk(l, wn[i]), &m)) return 0;
+                d.w[i] = m.p;
+                d.w_len[i] = (uintptr_t)m.len;
+                d.w_dt[i] = m.type;
+            }
+            const uint32_t qd = c.n_heads * c.head_dim, kd = c.n_kv * c.head_dim;
+            if (!vec(blk(l, "attn_q.bias"), qd, &d.bq) || !vec(blk(l, "attn_k.bias"), kd, &d.bk) ||
+                !vec(blk(l, "attn_v.bias"), kd, &d.bv) || !vec(blk(l, "attn_output.bias"), c.dim, &d.bo) ||
+                !vec(blk(l, "attn_sinks.weight"), c.n_heads, &d.sinks) ||
+                !vec(blk(l, "attn_norm.weight"), c.dim, &d.attn_norm) ||
+                !vec(blk(l, "post_attention_norm.weight"), c.dim, &d.post_attn_norm) ||
+                !vec(blk(l, "ffn_gate_inp.bias"), c.n_experts, &d.router_bias))
+                return 0;
+            GgufMat r;
+            if (!mat(blk(l, "ffn_gate_inp.weight"), &r)) return 0;
+            d.router = r.p;
+            d.router_len = (uintptr_t)r.len;
+            d.router_dt = r.type;
+            const char *en[3] = {"ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"};
+            const char *bn[3] = {"ffn_gate_exps.bias", "ffn_up_exps.bias", "ffn_down_exps.bias"};
+            const size_t bl[3] = {(size_t)c.n_experts * c.hidden, (size_t)c.n_experts * c.hidden,
+                                  (size_t)c.n_experts * c.dim};
+            for (int i = 0; i < 3; i++) {
+                GgufMat m;
+                if (!mat(blk(l, en[i]), &m)) return 0;
+                d.exps[i] = m.p;
+                d.exps_len[i] = (uintptr_t)m.len;
+                d.exps_dt = m.type;
+                if (!vec(blk(l, bn[i]), bl[i], &d.exps_bias[i])) return 0;
+            }
+            if (!rusty_hip_resident_set_moe_layer(l, &d)) return 0;
+            keep.clear();
+        }
+    } else {
+        // load_model (src/model.rs:3573-3860): head / value dims from the
+        // attn_q / attn_v shapes, fused attn_qkv split by rows, tied output
+        for (uint32_t l = 0; l < c.n_layers; l++) {
+            const GgufTensor *q = G.find(blk(l, "attn_q.weight")), *v = G.find(blk(l, "attn_v.weight"));
+            bool hq = false, hv = false;
+            if (q && q->dims.size() >= 2 && q->dims[0] == c.dim && c.n_heads && q->dims[1] % c.n_heads == 0) {
+                c.head_dim = (uint32_t)(q->dims[1] / c.n_heads);
+                hq = true;
+            }
+            if (v && v->dims.size() >= 2 && v->dims[0] == c.dim && c.n_kv && v->dims[1] % c.n_kv == 0) {
+                c.value_dim = (uint32_t)(v->dims[1] / c.n_kv);
+                hv = true;
+            }
+            if (hq && hv) break;
+        }
+        const bool neox = c.arch == "qwen2" || c.arch == "qwen3";
+        if (!rusty_hip_resident_configure(c.n_layers, c.dim, c.n_heads, c.n_kv, c.head_dim, c.value_dim, c.hidden,
+                                          c.vocab, max_len, c.eps, neox ? 1 : 0))
+            return 0;
+        const uint32_t rows[7] = {c.n_heads * c.head_dim, c.n_kv * c.head_dim, c.n_kv * c.value_dim, c.dim,
+                                  c.hidden, c.hidden, c.dim};
+        for (uint32_t l = 0; l < c.n_layers; l++) {
+            RustyResidentLayerDesc d;
+            memset(&d, 0, sizeof(d));
+            if (G.find(blk(l, "attn_q.weight"))) {
+                const char *nm[3] = {"attn_q.weight", "attn_k.weight", "attn_v.weight"};
+                const char *bn[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+                const float **bd[3] = {&d.bq, &d.bk, &d.bv};
+                uint32_t *bln[3] = {&d.bq_len, &d.bk_len, &d.bv_len};
+                for (int i = 0; i < 3; i++) {
+                    GgufMat m;
+                    if (!mat(blk(l, nm[i]), &m)) return 0;
+                    d.w[i] = m.p;
+                    d.w_len[i] = (uintptr_t)m.len;
+                    d.w_rows[i] = (uint32_t)m.rows;
+                    d.w_dt[i] = m.type;
+                    if (G.find(blk(l, bn[i]))) {
+                        if (!vec(blk(l, bn[i]), rows[i], bd[i])) return 0;
+                        *bln[i] = rows[i];
+                    }
+                }
+            } else {
+                GgufMat m;
+                if (!mat(blk(l, "attn_qkv.weight"), &m)) return 0;
+                const int64_t rb = row_bytes_of((int)m.type, m.cols);
+                if (rb <= 0 || m.rows != (int64_t)rows[0] + rows[1] + rows[2]) {
+                    gguf_note(path, "attn_qkv rows do not split into q/k/v");
+                    return 0;
+                }
+                const float *qkv_b = nullptr;
+                const bool has_b = G.find(blk(l, "attn_qkv.bias")) != nullptr;
+                if (has_b && !vec(blk(l, "attn_qkv.bias"), (size_t)m.rows, &qkv_b)) return 0;
+                int64_t r0 = 0;
+                const float **bd[3] = {&d.bq, &d.bk, &d.bv};
+                uint32_t *bln[3] = {&d.bq_len, &d.bk_len, &d.bv_len};
+                for (int i = 0; i < 3; i++) {
+                    d.w[i] = m.p + r0 * rb;
+                    d.w_len[i] = (uintptr_t)(rows[i] * rb);
+                    d.w_rows[i] = rows[i];
+                    d.w_dt[i] = m.type;
+                    if (has_b) {
+                        *bd[i] = qkv_b + r0;
+                        *bln[i] = rows[i];
+                    }
+                    r0 += rows[i];
+                }
+            }
+            const char *on[4] = {"attn_output.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+            for (int i = 0; i < 4; i++) {
+                GgufMat m;
+                if (!mat(blk(l, on[i]), &m)) return 0;
+                d.w[3 + i] = m.p;
+                d.w_len[3 + i] = (uintptr_t)m.len;
+                d.w_rows[3 + i] = (uint32_t)m.rows;
+                d.w_dt[3 + i] = m.type;
+            }
+            if (!vec(blk(l, "attn_norm.weight"), c.dim, &d.attn_norm) ||
+                !vec(blk(l, "ffn_norm.weight"), c.dim, &d.ffn_norm))
+                return 0;
+            if (!rusty_hip_resident_set_layer(l, &d)) return 0;
+            keep.clear();
+        }
+        if (G.find("output.weight")) {
+            if (!mat("output.weight", &outw)) return 0;
+        } else {
+            outw = emb;  // output tied to the embedding (src/model.rs:3653-3667)
+        }
+    }
+    std::vector<float> inv = rope_table(c, c.arch == "gpt-oss", &conc);
+    if (!rusty_hip_resident_set_output(out_norm.data(), outw.p, (uintptr_t)outw.len, (uint32_t)outw.rows, outw.type,
+                                       inv.data(), (uint32_t)inv.size()))
+        return 0;
+    if (!rusty_hip_resident_set_embedding(emb.p, (uintptr_t)emb.len, emb.type)) return 0;
+    return 1;
 }
 
 }  // extern "C"

@@ -33,7 +33,8 @@ SYMBOLS = [
     "rusty_hip_debug_f16", "rusty_hip_weight_cache_clear", "rusty_hip_attention_mode", "rusty_hip_debug_expf",
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
     "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
-    "rusty_hip_bench_attention", "rusty_hip_attention_noalloc",
+    "rusty_hip_bench_attention", "rusty_hip_attention_noalloc", "rusty_hip_gguf_summary",
+    "rusty_hip_resident_load_gguf",
 ]
 
 
@@ -99,6 +100,31 @@ _sig("rusty_hip_bench_matvec", _i, _u32, _p, _u, _p, _u, _u, _u32, _u32, _p)
 _sig("rusty_hip_bench_attention", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _i, _p)
 _sig("rusty_hip_moe_ffn", _i, _p, _u, _p, _u, _u32, _p, _u32, _u32, _p, _u, _p, _u, _p, _u, _u32, _u, _p, _p, _p, _p,
      _p, _p)
+
+
+
+class GgufSummary(C.Structure):
+    _fields_ = [("arch", C.c_char * 32), ("version", C.c_uint32), ("n_tensors", C.c_uint32),
+                ("data_offset", C.c_uint64), ("n_layers", C.c_uint32), ("dim", C.c_uint32), ("n_heads", C.c_uint32),
+                ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("value_dim", C.c_uint32),
+                ("hidden_dim", C.c_uint32), ("vocab", C.c_uint32), ("context_length", C.c_uint32),
+                ("sliding_window", C.c_uint32), ("n_experts", C.c_uint32), ("top_k", C.c_uint32),
+                ("rope_orig_ctx", C.c_uint32), ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+                ("rope_scaling", C.c_float), ("tied_output", C.c_uint32), ("fused_qkv", C.c_uint32),
+                ("qkv_bias", C.c_uint32)]
+
+
+_sig("rusty_hip_gguf_summary", _i, C.c_char_p, C.POINTER(GgufSummary))
+_sig("rusty_hip_resident_load_gguf", _i, C.c_char_p, _u32)
+
+
+def gguf_summary(path: str):
+    """The library's native parse of a GGUF file (host only), or None."""
+    s = GgufSummary()
+    if lib.rusty_hip_gguf_summary(os.fsencode(path), C.byref(s)) != 1:
+        return None
+    return s
+
 
 Q8_0, Q4_K, Q6_K, MXFP4 = 8, 12, 14, 39
 
@@ -442,6 +468,24 @@ class ResidentGptOss(Resident):
                 raise RuntimeError(f"rusty_hip_resident_set_moe_layer({l}) failed")
         self._set_output(model)
         self._keep = []
+
+
+class ResidentGguf(Resident):
+    """The resident decoder configured straight from a GGUF file by the
+    library (rusty_hip_resident_load_gguf): mapped, parsed and uploaded
+    natively, no host model in between."""
+
+    def __init__(self, path: str, max_len: int):
+        s = gguf_summary(path)
+        if s is None:
+            raise RuntimeError(f"{path}: not a readable GGUF file")
+        if lib.rusty_hip_resident_load_gguf(os.fsencode(path), max_len) != 1:
+            raise RuntimeError(f"rusty_hip_resident_load_gguf({path}) failed")
+        self.summary = s
+        self.cfg = {"n_kv_heads": s.n_kv_heads, "head_dim": s.head_dim, "value_dim": s.value_dim,
+                    "n_layers": s.n_layers, "dim": s.dim}
+        self.storage_len = max_len
+        self.vocab = s.vocab
 
 
 # ---- profiling -------------------------------------------------------------------------
