@@ -204,6 +204,20 @@ int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);
 int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in);
 
+/* KVCache::enable_bf16 (src/model.rs:1406-1421) for the standard resident
+ * decoder (no reference GPU counterpart; the reference's bf16 cache is a CPU
+ * path): on = 1 switches the cache to bf16 elements, narrowed as
+ * KVCache::write_k / write_v do (f32_to_bf16, round to nearest even), and
+ * attention becomes attention_over_kv_heads_bf16 (src/model.rs:6205-6580):
+ * the same recurrence over widened rows, with every head's scores in
+ * dot_bf16_f32's single-accumulator order.  Call after configure; the cache
+ * is cleared by the switch.  kv_read / kv_write then move uint16 elements
+ * (n_slots * width * 2 bytes).  Split-K attention has no bf16 form: with a
+ * bf16 cache the reference order runs in both attention modes.  Returns 0
+ * in gpt-oss mode (the reference keeps bf16 KV to the standard
+ * architecture). */
+int rusty_hip_resident_enable_bf16(int on);
+
 /* gpt-oss mode of the resident decoder: the whole forward_gpt_oss_into step
  * (src/model.rs:6733-6908) on the device, one graph per token.  The reference
  * runs this model on the CPU with per-op GPU hooks; this path has no Metal
@@ -253,8 +267,8 @@ int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *desc);
  * exact order's scores, coefficients and masks, or the split-K partials) is
  * one fixed 16 MiB device array per GPU, held until the process ends.
  * Returns 0, with a message on stderr, when a call needs more than that
- * (exact order: about 12 bytes per query head per attended position, so
- * heads x positions up to ~1.3 M, e.g. 40 heads over 32768 positions).  Calls
+ * (exact order: about 8.2 bytes per query head per attended position, so
+ * heads x positions up to ~2 M, e.g. 40 heads over 49152 positions).  Calls
  * that overlap on one GPU share the array and race.  Synchronous. */
 int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
                                 const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,

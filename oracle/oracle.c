@@ -839,6 +839,163 @@ void orc_attention_over_kv_heads(const float *q, const float *keys, const float 
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* bf16 KV cache (KVCache::enable_bf16, model.rs:1406-1421; attention,
+ * model.rs:6205-6580).  bf16_to_f32 is exact (simd.rs:82-85), so the
+ * reference's widened-row kernels axpy_bf16_f32, scale_add_bf16_f32 and
+ * affine_add_bf16x4_f32 (simd.rs:7314-7440) are the f32 kernels above on the
+ * widened row, element for element; dot_bf16x4_f32 is dot_f32x4 on the
+ * widened key.  dot_bf16_f32 (simd.rs:7292-7311) has an order of its own:
+ * one 8-wide accumulator, hsum_avx, then the scalar tail. */
+uint16_t orc_f32_to_bf16(float x) {
+    /* simd.rs:88-96: round to nearest even; NaN keeps its payload, quiet */
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    if (isnan(x)) return (uint16_t)((bits >> 16) | 0x0040);
+    uint32_t rounded = bits + 0x7fffu + ((bits >> 16) & 1u);
+    return (uint16_t)(rounded >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t b = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+static void bf16_widen(const uint16_t *src, float *dst, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = orc_bf16_to_f32(src[i]);
+}
+
+/* dot_bf16_f32_avx2, simd.rs:7292-7311 (on the widened key row) */
+__attribute__((target("avx2,fma")))
+float orc_dot_bf16_f32_avx2(const float *a, const float *bw, int64_t n) {
+    int64_t main_ = n / 8;
+    __m256 acc = _mm256_setzero_ps();
+    for (int64_t i = 0; i < main_; i++)
+        acc = _mm256_fmadd_ps(_mm256_loadu_ps(a + 8 * i), _mm256_loadu_ps(bw + 8 * i), acc);
+    float sum = hsum_avx(acc);
+    for (int64_t i = main_ * 8; i < n; i++) sum += a[i] * bw[i];
+    return sum;
+}
+
+#define BF16_MAX_DIM 512
+/* online_attention_bf16, model.rs:6219-6276 */
+static void online_attention_bf16(const float *q, const uint16_t *keys, const uint16_t *values, int64_t ks,
+                                  int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t start_t, int64_t end_t,
+                                  float scale, float *out) {
+    if (slots == 0 || start_t > end_t) return;
+    float kw[BF16_MAX_DIM], vw[BF16_MAX_DIM];
+    float max_score = -INFINITY, denom = 0.0f;
+    int64_t slot = linear_slots(start_t, end_t, slots) ? start_t : start_t % slots;
+    for (int64_t t = start_t; t <= end_t; t++) {
+        bf16_widen(keys + slot * ks, kw, hd);
+        bf16_widen(values + slot * vs, vw, vd);
+        float score = orc_dot_bf16_f32_avx2(q, kw, hd) * scale;
+        if (score > max_score) {
+            float old_scale = isfinite(max_score) ? expf(max_score - score) : 0.0f;
+            scale_add_f32_avx2(out, old_scale, vw, vd);
+            denom = denom * old_scale + 1.0f;
+            max_score = score;
+        } else {
+            float weight = expf(score - max_score);
+            axpy_f32_avx2(out, weight, vw, vd);
+            denom += weight;
+        }
+        slot++;
+        if (slot == slots) slot = 0;
+    }
+    if (denom > 0.0f) scale_f32_avx2(out, 1.0f / denom, vd);
+}
+
+/* online_attention_grouped_bf16, model.rs:6278-6437 */
+void orc_online_attention_grouped_bf16(const float *queries, const uint16_t *keys, const uint16_t *values, int64_t ks,
+                                       int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t kv_mul,
+                                       int64_t start_t, int64_t end_t, float scale, float *out) {
+    if (slots == 0 || start_t > end_t) return;
+    if (kv_mul == 1) {
+        online_attention_bf16(queries, keys, values, ks, vs, slots, hd, vd, start_t, end_t, scale, out);
+        return;
+    }
+    if (kv_mul > MAX_KV_MUL) kv_mul = MAX_KV_MUL;
+    float kw[BF16_MAX_DIM], vw[BF16_MAX_DIM];
+    float max_score[MAX_KV_MUL], denom[MAX_KV_MUL];
+    for (int g = 0; g < MAX_KV_MUL; g++) {
+        max_score[g] = -INFINITY;
+        denom[g] = 0.0f;
+    }
+    int64_t slot = linear_slots(start_t, end_t, slots) ? start_t : start_t % slots;
+    for (int64_t t = start_t; t <= end_t; t++) {
+        bf16_widen(keys + slot * ks, kw, hd);
+        bf16_widen(values + slot * vs, vw, vd);
+        if (kv_mul == 4 || kv_mul == 6) {
+            float scores[4];
+            dot_f32x4_avx2(queries, queries + hd, queries + 2 * hd, queries + 3 * hd, kw, hd, scores);
+            float multiplier[4] = {1.0f, 1.0f, 1.0f, 1.0f}, alpha[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int g = 0; g < 4; g++) {
+                float score = scores[g] * scale;
+                if (score > max_score[g]) {
+                    float old_scale = isfinite(max_score[g]) ? expf(max_score[g] - score) : 0.0f;
+                    multiplier[g] = old_scale;
+                    alpha[g] = 1.0f;
+                    denom[g] = denom[g] * old_scale + 1.0f;
+                    max_score[g] = score;
+                } else {
+                    alpha[g] = expf(score - max_score[g]);
+                    denom[g] += alpha[g];
+                }
+            }
+            affine_add_f32x4_avx2(out, out + vd, out + 2 * vd, out + 3 * vd, multiplier, alpha, vw, vd);
+            for (int64_t g = 4; g < kv_mul; g++) {
+                float score = orc_dot_bf16_f32_avx2(queries + g * hd, kw, hd) * scale;
+                float *o = out + g * vd;
+                if (score > max_score[g]) {
+                    float old_scale = isfinite(max_score[g]) ? expf(max_score[g] - score) : 0.0f;
+                    scale_add_f32_avx2(o, old_scale, vw, vd);
+                    denom[g] = denom[g] * old_scale + 1.0f;
+                    max_score[g] = score;
+                } else {
+                    float weight = expf(score - max_score[g]);
+                    axpy_f32_avx2(o, weight, vw, vd);
+                    denom[g] += weight;
+                }
+            }
+        } else {
+            for (int64_t g = 0; g < kv_mul; g++) {
+                float score = orc_dot_bf16_f32_avx2(queries + g * hd, kw, hd) * scale;
+                float *o = out + g * vd;
+                if (score > max_score[g]) {
+                    float old_scale = isfinite(max_score[g]) ? expf(max_score[g] - score) : 0.0f;
+                    scale_add_f32_avx2(o, old_scale, vw, vd);
+                    denom[g] = denom[g] * old_scale + 1.0f;
+                    max_score[g] = score;
+                } else {
+                    float weight = expf(score - max_score[g]);
+                    axpy_f32_avx2(o, weight, vw, vd);
+                    denom[g] += weight;
+                }
+            }
+        }
+        slot++;
+        if (slot == slots) slot = 0;
+    }
+    for (int64_t g = 0; g < kv_mul; g++)
+        if (denom[g] > 0.0f) scale_f32_avx2(out + g * vd, 1.0f / denom[g], vd);
+}
+
+/* attention_over_kv_heads_bf16, model.rs:6508-6580 */
+void orc_attention_over_kv_heads_bf16(const float *q, const uint16_t *keys, const uint16_t *values, int64_t ks,
+                                      int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t n_kv,
+                                      int64_t kv_mul, int64_t start_t, int64_t end_t, float scale, float *out) {
+    int nt = g_threads < (int)n_kv ? g_threads : (int)n_kv;
+    int64_t work = (end_t >= start_t ? end_t - start_t + 1 : 0) * n_kv;
+#pragma omp parallel for schedule(static) num_threads(nt > 0 ? nt : 1) if (n_kv > 1 && nt > 1 && work >= 4096)
+    for (int64_t h = 0; h < n_kv; h++) {
+        orc_online_attention_grouped_bf16(q + h * kv_mul * hd, keys + h * hd, values + h * vd, ks, vs, slots, hd, vd,
+                                          kv_mul, start_t, end_t, scale, out + h * kv_mul * vd);
+    }
+}
+
 /* per-head sink attention loop, model.rs:6812-6833 (output zeroed first) */
 void orc_attention_sink_heads(const float *q, const float *keys, const float *values, const float *sinks,
                               int64_t ks, int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t n_heads,
@@ -1120,9 +1277,11 @@ orc_model *orc_model_create(const orc_config *cfg) {
     m->layers = (orc_layer *)calloc((size_t)cfg->n_layers, sizeof(orc_layer));
     m->k = (float **)calloc((size_t)cfg->n_layers, sizeof(float *));
     m->v = (float **)calloc((size_t)cfg->n_layers, sizeof(float *));
+    /* bf16 storage holds uint16 elements in the same buffers (enable_bf16) */
+    const size_t esz = cfg->kv_bf16 ? 2 : 4;
     for (int l = 0; l < cfg->n_layers; l++) {
-        m->k[l] = (float *)calloc((size_t)(cfg->storage_len * kdim), 4);
-        m->v[l] = (float *)calloc((size_t)(cfg->storage_len * vdim), 4);
+        m->k[l] = (float *)calloc((size_t)(cfg->storage_len * kdim), esz);
+        m->v[l] = (float *)calloc((size_t)(cfg->storage_len * vdim), esz);
     }
     int64_t dim = cfg->dim;
     m->x = (float *)calloc((size_t)dim, 4);
@@ -1202,12 +1361,22 @@ void orc_model_forward_from(orc_model *m, uint32_t token, int64_t pos, int64_t s
             orc_rope_qk_neox(m->q, m->kk, pos, hd, c->n_heads, c->n_kv_heads, m->inv_freq);
         else
             orc_rope_qk(m->q, m->kk, pos, hd, c->n_heads, c->n_kv_heads, m->inv_freq);
-        memcpy(m->k[l] + slot * kdim, m->kk, (size_t)kdim * 4);
-        memcpy(m->v[l] + slot * vdim, m->vv, (size_t)vdim * 4);
         float scale = 1.0f / sqrtf((float)hd);
         int64_t start = start_t >= 0 ? start_t : orc_attention_start_pos(pos, window);
-        orc_attention_over_kv_heads(m->q, m->k[l], m->v[l], kdim, vdim, c->storage_len, hd, vd, c->n_kv_heads,
-                                    kv_mul, start, pos, scale, m->attn);
+        if (c->kv_bf16) {
+            /* KVCache::write_k / write_v narrow to bf16 (model.rs:1478-1502);
+             * forward_into then takes attention_over_kv_heads_bf16 (:7245-7261) */
+            uint16_t *kc = (uint16_t *)m->k[l] + slot * kdim, *vc = (uint16_t *)m->v[l] + slot * vdim;
+            for (int64_t i = 0; i < kdim; i++) kc[i] = orc_f32_to_bf16(m->kk[i]);
+            for (int64_t i = 0; i < vdim; i++) vc[i] = orc_f32_to_bf16(m->vv[i]);
+            orc_attention_over_kv_heads_bf16(m->q, (const uint16_t *)m->k[l], (const uint16_t *)m->v[l], kdim, vdim,
+                                             c->storage_len, hd, vd, c->n_kv_heads, kv_mul, start, pos, scale, m->attn);
+        } else {
+            memcpy(m->k[l] + slot * kdim, m->kk, (size_t)kdim * 4);
+            memcpy(m->v[l] + slot * vdim, m->vv, (size_t)vdim * 4);
+            orc_attention_over_kv_heads(m->q, m->k[l], m->v[l], kdim, vdim, c->storage_len, hd, vd, c->n_kv_heads,
+                                        kv_mul, start, pos, scale, m->attn);
+        }
         orc_matvec((int)L->w_type[3], L->w[3], m->attn, L->w_rows[3], (int64_t)c->n_heads * vd, m->proj, th);
         for (int64_t i = 0; i < dim; i++) m->x[i] += m->proj[i];
         orc_rms_norm(m->x, L->ffn_norm, c->eps, dim, m->xn);

@@ -117,6 +117,7 @@ typedef struct {
     int32_t sliding_window;   /* 0 = none */
     int32_t neox;             /* 1 = rotate-half RoPE (qwen2/qwen3) */
     float eps;
+    int32_t kv_bf16;          /* 1 = bf16 KV cache (KVCache::enable_bf16) */
 } orc_config;
 
 /* weight order: wq, wk, wv, wo, gate(w1), up(w3), down(w2); types are GGML ids */
@@ -142,7 +143,17 @@ int orc_model_set_output(orc_model *m, const float *output_norm, const uint8_t *
 void orc_model_forward_from(orc_model *m, uint32_t token, int64_t pos, int64_t start_t, float *logits,
                             int want_logits);
 void orc_model_forward(orc_model *m, uint32_t token, int64_t pos, float *logits, int want_logits);
+/* the layer's K (which = 0) or V cache: float, or uint16 bf16 with kv_bf16 */
 float *orc_model_kv(orc_model *m, int32_t layer, int32_t which);
+uint16_t orc_f32_to_bf16(float x);
+float orc_bf16_to_f32(uint16_t h);
+float orc_dot_bf16_f32_avx2(const float *a, const float *bw, int64_t n);
+void orc_online_attention_grouped_bf16(const float *queries, const uint16_t *keys, const uint16_t *values, int64_t ks,
+                                       int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t kv_mul,
+                                       int64_t start_t, int64_t end_t, float scale, float *out);
+void orc_attention_over_kv_heads_bf16(const float *q, const uint16_t *keys, const uint16_t *values, int64_t ks,
+                                      int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t n_kv,
+                                      int64_t kv_mul, int64_t start_t, int64_t end_t, float scale, float *out);
 /* prefill prompt (per token) then greedy-decode n_gen tokens. Returns count. */
 int64_t orc_model_generate(orc_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t start_pos,
                            int64_t n_gen, float penalty, uint32_t *out_tokens, float *last_logits);

@@ -69,6 +69,11 @@ _sig("orc_online_attention_grouped", None, _p, _p, _p, _i64, _i64, _i64, _i64, _
 _sig("orc_attention_over_kv_heads", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
 _sig("orc_attention_sink_heads", None, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
 _sig("orc_attention_start_pos", _i64, _i64, _i64)
+_sig("orc_f32_to_bf16", C.c_uint16, _f)
+_sig("orc_bf16_to_f32", _f, C.c_uint16)
+_sig("orc_dot_bf16_f32_avx2", _f, _p, _p, _i64)
+_sig("orc_attention_over_kv_heads_bf16", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f,
+     _p)
 _sig("orc_rms_norm", None, _p, _p, _f, _i64, _p)
 _sig("orc_build_rope_inv_freq", None, _f, _i64, _f, _p)
 _sig("orc_rope_qk", None, _p, _p, _i64, _i64, _i64, _i64, _p)
@@ -181,6 +186,23 @@ def attention(q, k, v, n_heads, n_kv, hd, vd, key_stride, value_stride, slot_cou
         s = f32(sinks)
         lib.orc_attention_sink_heads(ptr(q), ptr(k), ptr(v), ptr(s), key_stride, value_stride, slot_count, hd, vd,
                                      n_heads, kv_mul, start_t, end_t, scale, ptr(out))
+    return out
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    """f32_to_bf16 (simd.rs:88-96) per element: uint16 bit patterns."""
+    x = f32(x).reshape(-1)
+    return np.array([lib.orc_f32_to_bf16(float(v)) for v in x], np.uint16)
+
+
+def attention_bf16(q, k16, v16, n_heads, n_kv, hd, vd, key_stride, value_stride, slot_count, start_t, end_t,
+                   scale) -> np.ndarray:
+    """attention_over_kv_heads_bf16 (model.rs:6508-6580) over uint16 bf16 K/V."""
+    q = f32(q)
+    k16, v16 = np.ascontiguousarray(k16, np.uint16), np.ascontiguousarray(v16, np.uint16)
+    out = np.zeros(n_heads * vd, np.float32)
+    lib.orc_attention_over_kv_heads_bf16(ptr(q), ptr(k16), ptr(v16), key_stride, value_stride, slot_count, hd, vd,
+                                         n_kv, n_heads // n_kv, start_t, end_t, scale, ptr(out))
     return out
 
 
@@ -401,7 +423,8 @@ def mxfp4_test_activation(n):
 class OrcConfig(C.Structure):
     _fields_ = [("n_layers", C.c_int32), ("dim", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
                 ("head_dim", C.c_int32), ("value_dim", C.c_int32), ("hidden_dim", C.c_int32), ("vocab", C.c_int32),
-                ("storage_len", C.c_int32), ("sliding_window", C.c_int32), ("neox", C.c_int32), ("eps", C.c_float)]
+                ("storage_len", C.c_int32), ("sliding_window", C.c_int32), ("neox", C.c_int32), ("eps", C.c_float),
+                ("kv_bf16", C.c_int32)]
 
 
 class OrcLayer(C.Structure):
@@ -415,14 +438,15 @@ class OracleModel:
     """Oracle forward_into (model.rs:7177-7358) over a model dict produced by
     rustyllm_amd.synth (the same bytes the HIP decoder consumes)."""
 
-    def __init__(self, model, storage_len: int, threads: int = 0):
+    def __init__(self, model, storage_len: int, threads: int = 0, kv_bf16: bool = False):
         cfg = model["config"]
         self.model = model
         self.cfg = cfg
         self.vocab = cfg["vocab"]
+        self.kv_bf16 = kv_bf16
         c = OrcConfig(cfg["n_layers"], cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
                       cfg["value_dim"], cfg["hidden_dim"], cfg["vocab"], storage_len, cfg.get("sliding_window", 0),
-                      1 if cfg.get("neox") else 0, cfg["eps"])
+                      1 if cfg.get("neox") else 0, cfg["eps"], 1 if kv_bf16 else 0)
         if threads:
             lib.orc_set_threads(threads)
         self.h = lib.orc_model_create(C.byref(c))
@@ -460,6 +484,11 @@ class OracleModel:
         vd = cfg["n_kv_heads"] * cfg["value_dim"]
         kp = lib.orc_model_kv(self.h, layer, 0)
         vp = lib.orc_model_kv(self.h, layer, 1)
+        if self.kv_bf16:  # uint16 bf16 elements
+            u16 = C.POINTER(C.c_uint16)
+            k = np.ctypeslib.as_array(C.cast(kp, u16), shape=(storage_len * kd,))
+            v = np.ctypeslib.as_array(C.cast(vp, u16), shape=(storage_len * vd,))
+            return k, v
         k = np.ctypeslib.as_array(kp, shape=(storage_len * kd,))
         v = np.ctypeslib.as_array(vp, shape=(storage_len * vd,))
         return k, v

@@ -17,9 +17,10 @@
 //      before every step from the tile maxima and an in-tile prefix max, so
 //      each step's branch and expf argument are known up front; expf is
 //      glibc's (restated below, checked against glibc on all 2^32 inputs).
-//      Each step gets a coefficient a and a multiplier m: (a, m) = (w, 1) on
-//      an ordinary step and (1, old) on a new maximum, so the grouped form
-//      is o = fma(a, v, o*m) on every step (o*1 is exact).
+//      Each step gets one coefficient: the weight w = expf(s - max) on an
+//      ordinary step, the old-output multiplier old = expf(max - s) on a new
+//      maximum (flagged in a bit mask).  The grouped form is then
+//      o = fma(a, v, o*m) with (a, m) = (w, 1) or (1, old) (o*1 is exact).
 //   C  attn_exact_chain:   the FMA recurrences, one lane per (head, dim),
 //      V streamed into LDS by direct global->LDS loads; the denominators run
 //      as the same recurrence with v = 1.
@@ -83,8 +84,7 @@ struct AttnExactArgs {
     const float *v;
     const float *sinks;  // [n_heads] or null
     float *scores;       // [n_heads][cap]   q.k * scale per position
-    float *e;            // [n_heads][cap]   the step's coefficient a: expf(s - max), or 1 on a new max
-    float *mul;          // [n_heads][cap]   the step's multiplier m: 1, or expf(old max - s) on a new max
+    float *e;            // [n_heads][cap]   expf(s - max), or on a new max expf(old max - s) (0 from -inf)
     float *tmax;         // [n_heads][cap/64] max score of each 64-position tile
     uint32_t *newmask;   // [n_heads][cap/32] bit t%32 set when step t sets a new max
     float *den;          // [n_heads]         final denominators
@@ -101,10 +101,11 @@ struct AttnExactArgs {
     // n_tok = 0: one token, ranges from st or start_t/end_t.
     int32_t n_tok, pos0;
     int64_t q_tok, o_tok, tok_scratch;
-    // Optional transposed V copy [n_kv*vd][vt_stride] (position fastest):
-    // with a range starting on a multiple of 4 positions and not wrapping,
-    // the chain kernel streams V from it so that one 16-byte LDS read gives a
-    // lane four steps of its value dim.  null: V only.
+    // Optional tiled transposed V copy (vt4_off layout, vt_stride slots per
+    // column): with a range starting on a multiple of 4 positions and not
+    // wrapping, the chain kernel streams V from it, a 16-dim slice's tile in
+    // one contiguous 4 KB block, so that one 16-byte LDS read gives a lane
+    // four steps of its value dim.  null: V only.
     const float *vt;
     int32_t vt_stride;
     // Decode only (n_tok = 0): the lane-sliced scores kernel also does the
@@ -112,6 +113,11 @@ struct AttnExactArgs {
     // the raw q/k/v in rope, so that launch is not needed.
     RopeArgs rope;
     int32_t fuse_rope;
+    // 1: the K and V caches hold bf16 (attention_over_kv_heads_bf16,
+    // src/model.rs:6205-6580): rows widened on load, every head's scores in
+    // dot_bf16_f32's single-accumulator order, V from the f32 tiled copy
+    // (widened bf16 values) or, without it, widened from the rows
+    int32_t kv_bf16;
 };
 
 // Element e of a head vector x after RoPE with the row's cos/sin, exactly as
@@ -144,7 +150,6 @@ __device__ __forceinline__ AttnExactArgs tok_view(const AttnExactArgs &A0) {
     A.out += (int64_t)z * A0.o_tok;
     A.scores += sc;
     A.e += sc;
-    A.mul += sc;
     A.tmax += sc;
     A.newmask += sc;
     A.den += sc;
@@ -200,8 +205,16 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     const int nt = min(EX_TILE, ctx - t_base);
     for (int i = tid; i < kvm * hd; i += 256) s_q[i] = A.q[(size_t)h * kvm * hd + i];
     const float *kh = A.k + (size_t)h * hd;
+    const uint16_t *kh16 = (const uint16_t *)A.k + (size_t)h * hd;
     const int h4 = hd >> 2;
-    if (A.kvec && (256 % h4) == 0 && A.slot_count >= EX_TILE) {
+    if (A.kv_bf16) {
+#pragma unroll 4
+        for (int i = tid; i < nt * hd; i += 256) {
+            int tt = i / hd, c = i - tt * hd;
+            int slot = (s0 + t_base + tt) % A.slot_count;
+            s_k[tt * ldk + c] = bf16_to_f32(kh16[(size_t)slot * A.key_stride + c]);
+        }
+    } else if (A.kvec && (256 % h4) == 0 && A.slot_count >= EX_TILE) {
         // thread -> (row r0 + k*rstep, float4 column c): one division, and the
         // ring wrap as a compare (a tile spans fewer rows than the ring)
         const int r0 = tid / h4, c = (tid - r0 * h4) * 4, rstep = 256 / h4;
@@ -223,7 +236,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
     __syncthreads();
     // x4 heads: 8 lanes per (head, position), one accumulator per lane,
     // chained over the hd/8 chunks, then hsum_avx.
-    const int nx4 = (A.sinks == nullptr && (kvm == 4 || kvm == 6)) ? 4 : 0;
+    const int nx4 = A.kv_bf16 ? kvm : ((A.sinks == nullptr && (kvm == 4 || kvm == 6)) ? 4 : 0);
     // (head g, row tt) pairs are numbered g*EX_TILE + tt, rows past nt idle
     {
         const int pairs = nx4 * EX_TILE;
@@ -324,6 +337,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, kvm = A.kv_mul;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float *kh = A.k + (size_t)h * HD;
+    const uint16_t *kh16 = (const uint16_t *)A.k + (size_t)h * HD;
     // the K tile's loads first (registers), so their latency overlaps the q
     // staging below; element 4*c4 + i of a row goes to lane slice
     // (4*c4 + i) % 8, position (4*c4 + i) / 8
@@ -336,7 +350,8 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         for (int i = 0; i < NKR; i++) {
             int slot = base + min(r0 + i * RSTEP, rows - 1);
             if (slot >= A.slot_count) slot -= A.slot_count;
-            kreg[i] = *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
+            kreg[i] = A.kv_bf16 ? bf16x4_load(kh16 + (size_t)slot * A.key_stride + 4 * c4)
+                                : *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
         }
     };
     // Without a window the range starts at start_t, which the host passes as
@@ -387,19 +402,33 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         const int slot = RA.ring ? e0 % RA.slots : e0;
         const int kvd = RA.n_kv * HD, vvd = RA.n_kv * RA.vd;
         for (int e = tid; e < HD; e += 256) {
-            const float kr = rope_elem(RA.k + (size_t)h * HD, e, half, RA.neox != 0, ct, stb);
+            float kr = rope_elem(RA.k + (size_t)h * HD, e, half, RA.neox != 0, ct, stb);
+            if (RA.kv_bf16) {
+                const uint16_t kb = f32_to_bf16(kr);
+                ((uint16_t *)RA.kcache)[(size_t)slot * kvd + h * HD + e] = kb;
+                kr = bf16_to_f32(kb);  // the score reads the stored (bf16) key
+            } else {
+                RA.kcache[(size_t)slot * kvd + h * HD + e] = kr;
+            }
             s_k[tt_cur * RS + (e & 7) * LS + (e >> 3)] = kr;
-            RA.kcache[(size_t)slot * kvd + h * HD + e] = kr;
         }
         for (int e = tid; e < RA.vd; e += 256) {
-            const float v = RA.v[(size_t)h * RA.vd + e];
-            RA.vcache[(size_t)slot * vvd + h * RA.vd + e] = v;
-            if (RA.vtcache) RA.vtcache[(size_t)(h * RA.vd + e) * RA.vt_stride + slot] = v;
+            float v = RA.v[(size_t)h * RA.vd + e];
+            if (RA.kv_bf16) {
+                const uint16_t vb = f32_to_bf16(v);
+                ((uint16_t *)RA.vcache)[(size_t)slot * vvd + h * RA.vd + e] = vb;
+                v = bf16_to_f32(vb);
+            } else {
+                RA.vcache[(size_t)slot * vvd + h * RA.vd + e] = v;
+            }
+            if (RA.vtcache) RA.vtcache[vt4_off(h * RA.vd + e, slot, RA.vt_stride)] = v;
         }
     }
     __syncthreads();
     for (int g = wave; g < kvm; g += 4) {
-        const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4;
+        // dot_f32x4 / dot_bf16x4 / dot_bf16_f32: one accumulator per lane;
+        // dot_f32_avx2: four
+        const bool x4 = A.kv_bf16 || (A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4);
         float q[M];
         {
             const float *qr = s_q + g * RS + l * LS;
@@ -463,10 +492,10 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
 // B: one wave per (tile of 64 positions, query head), four tiles per workgroup.  The running max before
 // each step is max(initial, maxima of the earlier tiles, prefix max inside the
 // tile), so every step's branch and expf argument are known without a serial
-// scan.  On a new max the multiplier is isfinite(run) ? expf(run - s) : 0
-// (the factor the old output and denominator are scaled by) and the
-// coefficient 1; otherwise the coefficient is expf(s - run) and the
-// multiplier 1.  The new-max steps are also marked in newmask.
+// scan.  On a new max the step's coefficient is isfinite(run) ? expf(run -
+// s) : 0 (the factor the old output and denominator are scaled by; its own
+// weight is 1), otherwise expf(s - run); the new-max steps are marked in
+// newmask.
 __global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     int s0, e0;
@@ -501,16 +530,14 @@ __global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) 
         float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, p), __builtin_bit_cast(int, p), 0x138, 0xF, 0xF, false));
     const float run = lane == 0 ? m : fmaxf(m, prev);
     const bool flag = valid && s > run;
-    float e = 0.0f, mlt = 1.0f;
+    float e = 0.0f;
     if (flag) {
-        mlt = __builtin_isfinite(run) ? expf_glibc(run - s) : 0.0f;
-        e = 1.0f;
+        e = __builtin_isfinite(run) ? expf_glibc(run - s) : 0.0f;
     } else if (valid) {
         e = expf_glibc(s - run);
     }
     const int kvm = A.kv_mul, g = head % kvm;
     A.e[e_index(A, head / kvm, g, t)] = e;
-    A.mul[e_index(A, head / kvm, g, t)] = mlt;
     const unsigned long long bits = __ballot(flag);
     if (lane < 2) A.newmask[(size_t)head * (A.cap / 32) + 2 * tile + lane] = (uint32_t)(bits >> (32 * lane));
 }
@@ -539,6 +566,8 @@ __device__ __forceinline__ void dma4(const void *src, void *lds) {
 #define RH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
 // lgkmcnt(0) only
 #define RH_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14))
+// lgkmcnt(N) only (N <= 15)
+#define RH_WAIT_LGKM(N) __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | ((N) << 8) | (3 << 14))
 
 // Workgroup barrier without the memory-model waits of __syncthreads (which
 // would drain the producers' loads); the asm statements keep the compiler
@@ -609,39 +638,55 @@ __device__ __forceinline__ void cons_affine16_dpp(float a16, float m16, const fl
 
 // 16 recurrence steps with per-step new-max flags `bits`: the update forms
 // selected per step (rare: only chunks holding a new maximum come here).
+// e[j] is the weight of an ordinary step and the old-output factor of a
+// flagged one.
 template <bool DEN, bool X4>
-__device__ __forceinline__ void chain_steps16_flags(const float *e, const float *m, const float *v, float &o,
-                                                    uint32_t bits) {
+__device__ __forceinline__ void chain_steps16_flags(const float *e, const float *v, float &o, uint32_t bits) {
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const float vj = DEN ? 1.0f : v[j];
         const float on = fmaf(e[j], vj, o);
-        const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * m[j]) : fmaf(o, m[j], vj);
+        const float ox = (DEN || X4) ? fmaf(vj, 1.0f, o * e[j]) : fmaf(o, e[j], vj);
         o = ((bits >> j) & 1u) ? ox : on;
     }
+}
+
+// The grouped form's per-step pair for lane j of a 16-lane row from the
+// step's coefficient and new-max bit (bit j of bits16): (a, m) = (e, 1) on
+// an ordinary step, (1, e) on a new maximum.
+__device__ __forceinline__ void aff_pair16(float e16, uint32_t bits16, int lane, float &a16, float &m16) {
+    const bool nm = ((bits16 >> (lane & 15)) & 1u) != 0u;
+    a16 = nm ? 1.0f : e16;
+    m16 = nm ? e16 : 1.0f;
 }
 
 // C, four query heads per wave: chain workgroups, one per (kv head, group of
 // four query heads, 16 value dims).  The consumer wave's four 16-lane rows
 // are the four heads and lane % 16 the value dim, so all four rows read the
-// same V element (one LDS broadcast) and each row takes its own head's e
-// through row_newbcast.  V of a kv head is then streamed from HBM once per
-// layer, 64 B per position per workgroup.  What bounds the chain is how fast
-// a workgroup's value stream arrives (bytes in flight / load latency), not
-// the FMAs: one wave's direct loads complete at a fixed rate however many are
-// in flight (about 75 ns per contiguous KB), so a tile (4 KB of V, 1 KB of
-// e) is split over four producer waves, and the ring keeps C4_P tiles in
-// flight.  The denominators run in a second recurrence wave as the same DPP
-// chain with v = 1.
+// same V element (one LDS broadcast) and each row takes its own head's
+// coefficient through row_newbcast.  V of a kv head is then streamed from HBM
+// once per layer, 64 B per position per workgroup.  A wave's direct loads
+// complete at a fixed rate however many are in flight (about 75 ns per 64-lane
+// 16-byte load of contiguous memory, about 130 ns when it touches sixteen
+// separate 64-byte pieces), so the tile's loads are spread over five producer
+// waves: four each load a quarter of the tile's V (16 positions x 16 dims, one
+// contiguous KB of the tiled transposed copy), the fifth the four heads'
+// coefficients and new-max words.  The ring keeps C4_P tiles in flight; the
+// consumer meets the producers at one barrier per C4_PER tiles.  The
+// denominators run in a second kind of workgroup as the same DPP chain with
+// v = 1.
 #define C4_NT 16
-#define C4_P 10
-#define C4_PER 2
+#ifndef C4_P
+#define C4_P 12
+#endif
+#ifndef C4_PER
+#define C4_PER 4
+#endif
 
 struct Chain4Lds {
-    float v[C4_NT][EX_TILE * 16];       // [slot][position][16 dims]
-    float e[C4_NT][CH_MAXG * EX_TILE];  // [slot][head][position] coefficients
-    float mu[C4_NT][CH_MAXG * EX_TILE]; // [slot][head][position] multipliers
-    uint32_t m[C4_NT][2 * CH_MAXG];     // [slot][head][2 words]
+    float v[C4_NT][EX_TILE * 16];  // [slot][position][16 dims] (tiled copy: [position/4][16 dims][4])
+    float e[C4_NT][4 * EX_TILE];   // [slot][row (head g0 + row)][position] coefficients
+    uint32_t m[C4_NT][8];          // [slot][2 * row + word] new-max words
 };
 
 template <int IPT>
@@ -659,15 +704,17 @@ __device__ __forceinline__ void c4_wait_tiles_after(int n_after) {
         default: RH_WAIT_VM(0); break;
     }
 }
-static_assert(C4_P - 1 <= 9, "c4_wait_tiles_after covers at most 9 tiles");
-static_assert(3 * 9 <= 63, "vmcnt is 6 bits (up to three loads per producer per tile)");
+static_assert(C4_P - C4_PER <= 9, "c4_wait_tiles_after covers at most 9 tiles");
+static_assert(2 * 9 <= 63, "vmcnt is 6 bits (up to two loads per producer per tile)");
 static_assert(C4_NT >= C4_P + C4_PER, "ring too small");
 
-// Same protocol as chain_producer_loop on the C4 ring; after(j) runs once
-// group j's tiles are published (and before the barrier that lets their
-// slots be refilled, three groups later).
-template <int IPT, class Issue, class After>
-__device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue, After &after) {
+// Producer protocol on the C4 ring: C4_P tiles are issued up front; at group
+// j the producer waits until the group's tiles have landed, meets the
+// consumer at the group's barrier (after which the consumer reads them), then
+// issues the next C4_PER tiles, whose slots were last read in an earlier
+// group.  issue(i) loads tile i into slot i % C4_NT.
+template <int IPT, class Issue>
+__device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue) {
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
     for (int i = 0; i < min(C4_P, ntiles); i++) issue(i);
     for (int j = 0; j < ngroups; j++) {
@@ -679,73 +726,55 @@ __device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue, After
             const int i = C4_P + C4_PER * j + t;
             if (i < ntiles) issue(i);
         }
-        after(j);
     }
 }
 
-// Producer P (0..3) of a chain workgroup, per tile: the direct load of V
-// positions 16P..16P+15 (lane -> position 16P + lane/4, dims 4*(lane%4)..+3);
-// P = 0 also loads e (lane -> head g0 + lane/16, positions 4*(lane%16)..+3),
-// P = 1 the heads' new-max words.  A position's 16 dims are 64 bytes of a
-// 4 KB cache row, and a wave's direct loads cost about 8 ns per such piece,
-// so a tile's V is split four ways.
+// V producer P (0..3): per tile, positions 16P..16P+15 of the 16-dim slice.
+// VT: one contiguous KB of the tiled copy, lane -> positions 16P + 4*(lane/16)
+// ..+3 of dim lane%16, which is the consumer's LDS layout as it stands.
+// Rows: lane -> position 16P + lane/4, dims 4*(lane%4)..+3 of the cache row
+// (ring slots wrap).
 template <int P, bool VT>
-__device__ void c4_producer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int g0, int slice) {
-    constexpr int IPT = P < 3 ? 2 : 1;
-    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+__device__ void c4_vproducer(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int slice) {
+    const int lane = threadIdx.x & 63;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const char *v_base = (const char *)(A.v + (size_t)h * A.vd + slice * 16) + (lane & 3) * 16;
-    // VT: lane -> dim lane%16 of the slice, positions 16P + 4*(lane/16) ..+3
-    // of the tile (the range starts on a multiple of 4 and does not wrap)
-    const char *vt_base = VT ? (const char *)(A.vt + (size_t)(h * A.vd + slice * 16 + (lane & 15)) * A.vt_stride +
-                                              s0 + 16 * P + 4 * (lane >> 4))
-                             : nullptr;
+    const char *vt_base =
+        VT ? (const char *)(A.vt + vt4_off((int64_t)h * A.vd + slice * 16, s0 + 16 * P, A.vt_stride)) + lane * 16
+           : nullptr;
     const uint32_t row_bytes = (uint32_t)A.value_stride * 4u;
     const uint32_t wrap = (uint32_t)A.slot_count * row_bytes;
     const uint32_t step = 64u * row_bytes;
     uint32_t roff = (uint32_t)((s0 + 16 * P + (lane >> 2)) % A.slot_count) * row_bytes;
-    const int re = min(g0 + (lane >> 4), kvm - 1);
-    const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
-    const char *mu_base = (const char *)(A.mul + e_index(A, h, re, 0)) + (lane & 15) * 16;
-    const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
-    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
     auto issue = [&](int i) {
         const int sl = i & (C4_NT - 1);
         if (VT) {
-            dma16(vt_base + (uint32_t)i * 256u, &L.v[sl][P * 256]);
+            dma16(vt_base + (size_t)i * 4096u, &L.v[sl][P * 256]);
         } else {
             dma16(v_base + roff, &L.v[sl][P * 256]);
             roff += step;
             if (roff >= wrap) roff -= wrap;
         }
-        if (P == 0) dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
-        if (P == 1)
-            if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
-        if (P == 2) dma16(mu_base + (uint32_t)i * 256u, &L.mu[sl][0]);
     };
-    auto none = [](int) {};
-    c4_producer_loop<IPT>(ntiles, issue, none);
+    c4_producer_loop<1>(ntiles, issue);
 }
 
-// Producer of a denominator workgroup: e of the four heads and their
-// new-max words, the same slots as a chain workgroup's.
-__device__ void c4_den_producer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
-    constexpr int IPT = 3;
+// Coefficient producer: per tile the four heads' coefficients (lane -> head
+// g0 + lane/16, positions 4*(lane%16)..+3) and their new-max words (lanes
+// 0-7: head g0 + lane/2, word lane%2).
+__device__ void c4_eproducer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
     const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const int re = min(g0 + (lane >> 4), kvm - 1);
     const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
-    const char *mu_base = (const char *)(A.mul + e_index(A, h, re, 0)) + (lane & 15) * 16;
     const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
     const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
     auto issue = [&](int i) {
         const int sl = i & (C4_NT - 1);
         dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
-        dma16(mu_base + (uint32_t)i * 256u, &L.mu[sl][0]);
         if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
     };
-    auto none = [](int) {};
-    c4_producer_loop<IPT>(ntiles, issue, none);
+    c4_producer_loop<2>(ntiles, issue);
 }
 
 // A wave with nothing to load still takes part in every barrier.
@@ -755,9 +784,9 @@ __device__ void c4_idle(int ctx) {
     for (int j = 0; j < ngroups; j++) tile_barrier();
 }
 
-// 16 steps of a 16-dim row: e16 = e of step (lane % 16) of this row's head,
-// v[j] = V of step j at this lane's dim (broadcast across the four rows), or
-// 1 for the denominators.
+// 16 steps of a 16-dim row: e16 = coefficient of step (lane % 16) of this
+// row's head, v[j] = V of step j at this lane's dim (broadcast across the
+// four rows), or 1 for the denominators.
 // V tile layouts in LDS: VT = false [position][16 dims] (vt = &v[dcol], one
 // value per read); VT = true [position/4][16 dims][4 positions] (vt =
 // &v[4*dcol], four steps of the lane's dim per 16-byte read).
@@ -778,45 +807,108 @@ __device__ __forceinline__ void c4_load16(const float *et, const float *vt, int 
         for (int j = 0; j < 16; j++) v[j] = DEN ? 1.0f : vt[(k * 16 + j) * 16];
     }
 }
-template <bool DEN, bool VT>
-__device__ __forceinline__ void c4_load16m(const float *et, const float *mt, const float *vt, int k, int lane,
-                                           float &e16, float &m16, float *v) {
-    m16 = mt[k * 16 + (lane & 15)];
-    c4_load16<DEN, VT>(et, vt, k, lane, e16, v);
-}
 
-// Consumer chunk: all rows' flags clear -> the DPP FMA run; else every step
-// in the per-lane update forms (each row its own head's flags).  Branching
-// per step instead measured slower.
-// slow: wave-uniform (an SGPR bit of the group's chunk mask), so the common
-// case costs one scalar test and branch; a vector compare feeding the branch
-// (VCC from a VALU, right after the flag words arrive from LDS) measured
-// about 115 clocks per 16-step chunk on its own.
+// One 16-step chunk holding a new maximum, per step in its own form (rows
+// whose flags are clear take the ordinary form throughout).
 template <bool X4>
-__device__ __forceinline__ void c4_steps16(float e16, float m16, const float *v, float &o, uint32_t bits, bool slow) {
-    if (!slow) {
-        cons_fma16_dpp(e16, v, o);
-    } else {
-        float e[16], m[16];
-        bcast16_all(e16, e);
-        bcast16_all(m16, m);
-        chain_steps16_flags<false, X4>(e, m, v, o, bits);
-    }
+__device__ __forceinline__ void c4_steps16_slow(float e16, const float *v, float &o, uint32_t bits) {
+    float e[16];
+    bcast16_all(e16, e);
+    chain_steps16_flags<false, X4>(e, v, o, bits);
 }
 
-// New-max summary of a two-tile group for the wave's four rows.  w: lane
-// l < 16 holds new-max word l & 1 of head (l >> 1) & 3 in tile l >> 3 of the
-// group (0 in the other lanes); bit l of lo (hi) is set when that word has a
-// new maximum in its low (high) 16 positions.  Chunk c of the group (16
-// positions) is tile c >> 2, word (c >> 1) & 1, half c & 1, so its bits are
-// c4_chunk_slow's four-head mask of the ballot of that half.
+// New-max summary of a group for the wave's four rows.  w: lane l < 8*C4_PER
+// holds new-max word l & 1 of row (l >> 1) & 3 in tile l >> 3 of the group
+// (0 in the other lanes); bit l of lo (hi) is set when that word has a new
+// maximum in its low (high) 16 positions.  Chunk k of tile t (16 positions)
+// is word k >> 1, half k & 1: its bits are 0x55 << (8t + (k >> 1)) of lo or
+// hi.
 __device__ __forceinline__ void c4_group_ballots(uint32_t w, uint32_t &lo, uint32_t &hi) {
     lo = (uint32_t)__builtin_amdgcn_ballot_w64((w & 0xFFFFu) != 0u);
     hi = (uint32_t)__builtin_amdgcn_ballot_w64((w >> 16) != 0u);
 }
-template <int C>
-__device__ __forceinline__ bool c4_chunk_slow(uint32_t lo, uint32_t hi) {
-    return (((C & 1) ? hi : lo) & (0x55u << (8 * (C >> 2) + ((C >> 1) & 1)))) != 0u;
+
+// One tile (four 16-step chunks) of a consumer group in one of three forms:
+// FAST 16 DPP FMAs per chunk; AFF the grouped form o = fma(a, v, o*m) on
+// every step, (a, m) from the coefficient and the row's new-max bit; FLAGS
+// (scale_add heads) per chunk the fast run unless the chunk holds a new
+// maximum, then each step in its own form.  Chunk k computes from register
+// set k & 1 while chunk k + 1 (or chunk 0 of the group's next tile) loads
+// into the other.
+enum { C4_FAST = 0, C4_AFF = 1, C4_FLAGS = 2 };
+template <bool X4, bool DEN, bool VT, int MODE>
+__device__ __forceinline__ void c4_tile(const Chain4Lds &L, int i, int row, int dcol, int lane, bool has_next,
+                                        uint32_t glo, uint32_t ghi, int t, float (&a)[2], float (&v)[2][16],
+                                        float &o) {
+    const int sl = i & (C4_NT - 1), sn = (i + 1) & (C4_NT - 1);
+    const float *et = &L.e[sl][row * EX_TILE], *vt = &L.v[sl][VT ? 4 * dcol : dcol];
+    const float *en = &L.e[sn][row * EX_TILE], *vn = &L.v[sn][VT ? 4 * dcol : dcol];
+    uint32_t w0 = 0, w1 = 0;
+    if (MODE != C4_FAST) {
+        w0 = L.m[sl][2 * row];
+        w1 = L.m[sl][2 * row + 1];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = k & 1, n = c ^ 1;
+        RH_WAIT_LGKM0();
+        if (k < 3) c4_load16<DEN, VT>(et, vt, k + 1, lane, a[n], v[n]);
+        else if (has_next) c4_load16<DEN, VT>(en, vn, 0, lane, a[n], v[n]);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t wk = (k >> 1) ? w1 : w0;
+        const uint32_t bits = (k & 1) ? (wk >> 16) : (wk & 0xFFFFu);
+        if (MODE == C4_FAST) {
+            cons_fma16_dpp(a[c], v[c], o);
+        } else if (MODE == C4_AFF) {
+            float a16, m16;
+            aff_pair16(a[c], bits, lane, a16, m16);
+            cons_affine16_dpp(a16, m16, v[c], o);
+        } else {
+            const uint32_t half = (k & 1) ? ghi : glo;
+            if (half & (0x55u << (8 * t + (k >> 1)))) c4_steps16_slow<X4>(a[c], v[c], o, bits);
+            else cons_fma16_dpp(a[c], v[c], o);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// One full group (C4_PER tiles) of a consumer wave, each tile in the form its
+// new-max summary calls for.
+template <bool X4, bool DEN, bool VT>
+__device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, int dcol, int lane, float &o) {
+    // the group's new-max words first, then chunk 0, so the summary is ready
+    // while chunk 0 is still in flight
+    const uint32_t wraw = lane < 8 * C4_PER ? L.m[(i0 + (lane >> 3)) & (C4_NT - 1)][lane & 7] : 0u;
+    const int s0 = i0 & (C4_NT - 1);
+    float a[2], v[2][16];
+    c4_load16<DEN, VT>(&L.e[s0][row * EX_TILE], &L.v[s0][VT ? 4 * dcol : dcol], 0, lane, a[0], v[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t glo, ghi;
+    c4_group_ballots(wraw, glo, ghi);
+    const uint32_t any = glo | ghi;  // bits 8t..8t+7: tile t of the group
+    if (any == 0u) {
+        // no new maximum in any of the group's steps (the common case past
+        // the first tiles): straight-line FMA runs
+#pragma unroll
+        for (int t = 0; t < C4_PER; t++)
+            c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+    } else if (X4 || DEN) {
+        // grouped form: a tile holding a new maximum for any of the four rows
+        // runs o = fma(a, v, o*m) on every step
+#pragma unroll
+        for (int t = 0; t < C4_PER; t++) {
+            if ((any >> (8 * t)) & 0xFFu)
+                c4_tile<X4, DEN, VT, C4_AFF>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+            else
+                c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+        }
+    } else {
+        // scale_add heads: each 16-step chunk holding a new maximum runs
+        // every step in its own form
+#pragma unroll
+        for (int t = 0; t < C4_PER; t++)
+            c4_tile<X4, DEN, VT, C4_FLAGS>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+    }
 }
 
 // The recurrence of one wave: DEN = false the outputs (lane = value dim of
@@ -834,117 +926,20 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
         const int i0 = C4_PER * j;
         const bool full = i0 + C4_PER <= ntiles && ctx >= (i0 + C4_PER) * EX_TILE;
         if (full) {
-            const int sa = i0 & (C4_NT - 1), sb = (i0 + 1) & (C4_NT - 1);
-            const float *va = &L.v[sa][VT ? 4 * dcol : dcol], *vb = &L.v[sb][VT ? 4 * dcol : dcol];
-            const float *ea = &L.e[sa][row * EX_TILE], *eb = &L.e[sb][row * EX_TILE];
-            // the group's new-max words first, then chunk 0, so the mask
-            // is ready while chunk 0 is still in flight
-            const uint32_t wraw = L.m[(lane & 8) ? sb : sa][lane & 7];
-            float a0, a1, v0[16], v1[16];
-            c4_load16<DEN, VT>(ea, va, 0, lane, a0, v0);
-            __builtin_amdgcn_sched_barrier(0);
-            uint32_t glo, ghi;
-            c4_group_ballots(lane < 16 ? wraw : 0u, glo, ghi);
-            if ((glo | ghi) == 0u) {
-                // no new maximum in any of the group's 128 steps (the common
-                // case past the first tiles): straight-line FMA runs
-#define C4_FAST(ET, VP, K, NA, NV, CA, CV)   \
-    RH_WAIT_LGKM0();                         \
-    c4_load16<DEN, VT>(ET, VP, K, lane, NA, NV); \
-    __builtin_amdgcn_sched_barrier(0);       \
-    cons_fma16_dpp(CA, CV, o);               \
-    __builtin_amdgcn_sched_barrier(0);
-                C4_FAST(ea, va, 1, a1, v1, a0, v0)
-                C4_FAST(ea, va, 2, a0, v0, a1, v1)
-                C4_FAST(ea, va, 3, a1, v1, a0, v0)
-                C4_FAST(eb, vb, 0, a0, v0, a1, v1)
-                C4_FAST(eb, vb, 1, a1, v1, a0, v0)
-                C4_FAST(eb, vb, 2, a0, v0, a1, v1)
-                C4_FAST(eb, vb, 3, a1, v1, a0, v0)
-#undef C4_FAST
-                RH_WAIT_LGKM0();
-                cons_fma16_dpp(a1, v1, o);
-            } else if (X4 || DEN) {
-                const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
-                float u0 = 1.0f, u1 = 1.0f;
-#define C4_FAST(ET, VP, K, NA, NV, CA, CV)       \
-    RH_WAIT_LGKM0();                             \
-    c4_load16<DEN, VT>(ET, VP, K, lane, NA, NV); \
-    __builtin_amdgcn_sched_barrier(0);           \
-    cons_fma16_dpp(CA, CV, o);                   \
-    __builtin_amdgcn_sched_barrier(0);
-#define C4_AFF(ET, MT, VP, K, NA, NU, NV, CA, CU, CV)     \
-    RH_WAIT_LGKM0();                                      \
-    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV); \
-    __builtin_amdgcn_sched_barrier(0);                    \
-    cons_affine16_dpp(CA, CU, CV, o);                     \
-    __builtin_amdgcn_sched_barrier(0);
-                if (((glo | ghi) & 0xFFu) == 0u) {
-                    C4_FAST(ea, va, 1, a1, v1, a0, v0)
-                    C4_FAST(ea, va, 2, a0, v0, a1, v1)
-                    C4_FAST(ea, va, 3, a1, v1, a0, v0)
-                    C4_FAST(eb, vb, 0, a0, v0, a1, v1)
-                } else {
-                    u0 = ma[lane & 15];
-                    C4_AFF(ea, ma, va, 1, a1, u1, v1, a0, u0, v0)
-                    C4_AFF(ea, ma, va, 2, a0, u0, v0, a1, u1, v1)
-                    C4_AFF(ea, ma, va, 3, a1, u1, v1, a0, u0, v0)
-                    C4_AFF(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1)
-                }
-                if (((glo | ghi) & 0xFF00u) == 0u) {
-                    C4_FAST(eb, vb, 1, a1, v1, a0, v0)
-                    C4_FAST(eb, vb, 2, a0, v0, a1, v1)
-                    C4_FAST(eb, vb, 3, a1, v1, a0, v0)
-                    RH_WAIT_LGKM0();
-                    cons_fma16_dpp(a1, v1, o);
-                } else {
-                    u0 = mb[lane & 15];
-                    C4_AFF(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0)
-                    C4_AFF(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1)
-                    C4_AFF(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0)
-                    RH_WAIT_LGKM0();
-                    cons_affine16_dpp(a1, u1, v1, o);
-                }
-#undef C4_FAST
-#undef C4_AFF
-            } else {
-                // scale_add heads: each step in its own form, chunk by chunk
-                const float *ma = &L.mu[sa][row * EX_TILE], *mb = &L.mu[sb][row * EX_TILE];
-                const uint32_t m0 = L.m[sa][2 * row], m1 = L.m[sa][2 * row + 1];
-                const uint32_t m2 = L.m[sb][2 * row], m3 = L.m[sb][2 * row + 1];
-                float u0, u1;
-                u0 = ma[lane & 15];
-#define C4_STEP(ET, MT, VP, K, NA, NU, NV, CA, CU, CV, BITS, C) \
-    RH_WAIT_LGKM0();                                            \
-    c4_load16m<DEN, VT>(ET, MT, VP, K, lane, NA, NU, NV);           \
-    __builtin_amdgcn_sched_barrier(0);                          \
-    c4_steps16<X4>(CA, CU, CV, o, BITS, c4_chunk_slow<C>(glo, ghi)); \
-    __builtin_amdgcn_sched_barrier(0);
-                C4_STEP(ea, ma, va, 1, a1, u1, v1, a0, u0, v0, m0 & 0xFFFFu, 0)
-                C4_STEP(ea, ma, va, 2, a0, u0, v0, a1, u1, v1, m0 >> 16, 1)
-                C4_STEP(ea, ma, va, 3, a1, u1, v1, a0, u0, v0, m1 & 0xFFFFu, 2)
-                C4_STEP(eb, mb, vb, 0, a0, u0, v0, a1, u1, v1, m1 >> 16, 3)
-                C4_STEP(eb, mb, vb, 1, a1, u1, v1, a0, u0, v0, m2 & 0xFFFFu, 4)
-                C4_STEP(eb, mb, vb, 2, a0, u0, v0, a1, u1, v1, m2 >> 16, 5)
-                C4_STEP(eb, mb, vb, 3, a1, u1, v1, a0, u0, v0, m3 & 0xFFFFu, 6)
-#undef C4_STEP
-                RH_WAIT_LGKM0();
-                c4_steps16<X4>(a1, u1, v1, o, m3 >> 16, c4_chunk_slow<7>(glo, ghi));
-            }
+            c4_group<X4, DEN, VT>(L, i0, row, dcol, lane, o);
         } else {
             for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
                 const int sl = i & (C4_NT - 1);
                 const int ntok = min(EX_TILE, ctx - i * EX_TILE);
                 const float *vt = &L.v[sl][dcol];
                 const float *et = &L.e[sl][row * EX_TILE];
-                const float *mt = &L.mu[sl][row * EX_TILE];
                 const uint32_t mw0 = L.m[sl][2 * row], mw1 = L.m[sl][2 * row + 1];
                 for (int t = 0; t < ntok; t++) {
                     const uint32_t mw = t < 32 ? mw0 : mw1;
-                    const float e = et[t], mlt = mt[t];
+                    const float e = et[t];
                     const float v = DEN ? 1.0f : (VT ? L.v[sl][(t >> 2) * 64 + 4 * dcol + (t & 3)] : vt[t * 16]);
                     const float on = fmaf(e, v, o);
-                    const float ox = X4 ? fmaf(v, 1.0f, o * mlt) : fmaf(o, mlt, v);
+                    const float ox = X4 ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
                     o = ((mw >> (t & 31)) & 1u) ? ox : on;
                 }
             }
@@ -954,12 +949,46 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
     if (dst) *dst = o;
 }
 
+// The output recurrence with V widened from bf16 cache rows in global memory
+// (a bf16 cache whose range the tiled f32 copy cannot serve: an unaligned
+// start or a wrapped ring), step by step, coefficients and new-max words
+// from the ring as in c4_consumer.  Rare and slow; the V producers idle.
+template <bool X4>
+__device__ void c4_consumer_vg(const AttnExactArgs &A, Chain4Lds &L, int s0, int ctx, int h, int slice,
+                               float *dst) {
+    const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
+    const uint16_t *vcol = (const uint16_t *)A.v + (size_t)h * A.vd + slice * 16 + dcol;
+    float o = 0.0f;
+    for (int j = 0; j < ngroups; j++) {
+        tile_barrier();
+        for (int i = C4_PER * j; i < min(C4_PER * j + C4_PER, ntiles); i++) {
+            const int sl = i & (C4_NT - 1);
+            const int ntok = min(EX_TILE, ctx - i * EX_TILE);
+            const float *et = &L.e[sl][row * EX_TILE];
+            const uint32_t mw0 = L.m[sl][2 * row], mw1 = L.m[sl][2 * row + 1];
+            for (int t = 0; t < ntok; t++) {
+                const uint32_t mw = t < 32 ? mw0 : mw1;
+                const float e = et[t];
+                const int slot = (s0 + i * EX_TILE + t) % A.slot_count;
+                const float v = bf16_to_f32(vcol[(size_t)slot * A.value_stride]);
+                const float on = fmaf(e, v, o);
+                const float ox = X4 ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
+                o = ((mw >> (t & 31)) & 1u) ? ox : on;
+            }
+        }
+        RH_WAIT_LGKM0();
+    }
+    if (dst) *dst = o;
+}
+
 // grid: n_kv * ceil(kv_mul/4) * (vd/16) chain workgroups (wave 0 the
-// outputs, waves 1-4 the producers), then n_kv * ceil(kv_mul/4) denominator
-// workgroups (wave 0 the four heads' denominators as the same DPP recurrence
-// with v = 1, wave 1 their producer, the rest idle); block b serves kv head
-// b % n_kv.
-#define C4_WAVES 5
+// outputs, waves 1-4 the V producers, wave 5 the coefficient producer), then
+// n_kv * ceil(kv_mul/4) denominator workgroups (wave 0 the four heads'
+// denominators as the same DPP recurrence with v = 1, wave 1 their
+// coefficient producer, the rest idle); block b serves kv head b % n_kv.
+#define C4_WAVES 6
 __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     __shared__ Chain4Lds L;
@@ -971,33 +1000,41 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
     const int h = blockIdx.x % A.n_kv, r = blockIdx.x / A.n_kv;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    // V from the transposed copy when the range starts on a multiple of 4
-    // positions, does not wrap, and its tiles stay inside the copy's rows
+    // V from the tiled transposed copy when the range starts on a multiple
+    // of 4 positions, does not wrap, and its tiles stay inside the copy
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const bool vt_ok = A.vt != nullptr && (s0 & 3) == 0 && e0 < A.slot_count && s0 + ntiles * EX_TILE <= A.vt_stride;
+    const bool vg = A.kv_bf16 && !vt_ok;  // bf16 rows cannot be streamed into the f32 ring as they are
     if (r < ngrp * nsl) {
         const int g0 = 4 * (r / nsl), slice = r % nsl;
         const int g = g0 + (lane >> 4);
         if (wave == 0) {
             float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
             const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
-            if (vt_ok) {
+            if (vg) {
+                if (x4) c4_consumer_vg<true>(A, L, s0, ctx, h, slice, dst);
+                else c4_consumer_vg<false>(A, L, s0, ctx, h, slice, dst);
+            } else if (vt_ok) {
                 if (x4) c4_consumer<true, false, true>(A, L, ctx, dst);
                 else c4_consumer<false, false, true>(A, L, ctx, dst);
             } else {
                 if (x4) c4_consumer<true, false, false>(A, L, ctx, dst);
                 else c4_consumer<false, false, false>(A, L, ctx, dst);
             }
+        } else if (wave == 5) {
+            c4_eproducer(A, L, ctx, h, g0);
+        } else if (vg) {
+            c4_idle(ctx);
         } else if (vt_ok) {
-            if (wave == 1) c4_producer<0, true>(A, L, s0, ctx, h, g0, slice);
-            else if (wave == 2) c4_producer<1, true>(A, L, s0, ctx, h, g0, slice);
-            else if (wave == 3) c4_producer<2, true>(A, L, s0, ctx, h, g0, slice);
-            else c4_producer<3, true>(A, L, s0, ctx, h, g0, slice);
+            if (wave == 1) c4_vproducer<0, true>(A, L, s0, ctx, h, slice);
+            else if (wave == 2) c4_vproducer<1, true>(A, L, s0, ctx, h, slice);
+            else if (wave == 3) c4_vproducer<2, true>(A, L, s0, ctx, h, slice);
+            else c4_vproducer<3, true>(A, L, s0, ctx, h, slice);
         } else {
-            if (wave == 1) c4_producer<0, false>(A, L, s0, ctx, h, g0, slice);
-            else if (wave == 2) c4_producer<1, false>(A, L, s0, ctx, h, g0, slice);
-            else if (wave == 3) c4_producer<2, false>(A, L, s0, ctx, h, g0, slice);
-            else c4_producer<3, false>(A, L, s0, ctx, h, g0, slice);
+            if (wave == 1) c4_vproducer<0, false>(A, L, s0, ctx, h, slice);
+            else if (wave == 2) c4_vproducer<1, false>(A, L, s0, ctx, h, slice);
+            else if (wave == 3) c4_vproducer<2, false>(A, L, s0, ctx, h, slice);
+            else c4_vproducer<3, false>(A, L, s0, ctx, h, slice);
         }
     } else {
         const int g0 = 4 * (r - ngrp * nsl);
@@ -1005,7 +1042,7 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
         if (wave == 0) {
             c4_consumer<true, true, false>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
         } else if (wave == 1) {
-            c4_den_producer(A, L, ctx, h, g0);
+            c4_eproducer(A, L, ctx, h, g0);
         } else {
             c4_idle(ctx);
         }
@@ -1018,7 +1055,7 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
 // (token, kv head, group of four query heads, 16 value dims) or the group's
 // denominators, with no LDS ring: V comes straight from the cache (the
 // transposed copy gives four steps of a lane's dim per 16-byte load), the
-// coefficients, multipliers and new-max words from global memory, and many
+// coefficients and new-max words from global memory, and many
 // waves per SIMD hide the latency.  The update forms are the chain4
 // consumer's, step for step.
 __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs A0) {
@@ -1037,16 +1074,16 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
     const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
     const int g = g0 + row, gr = min(g, kvm - 1);
     const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
-    const float *ef = A.e + e_index(A, h, gr, 0), *mf = A.mul + e_index(A, h, gr, 0);
+    const float *ef = A.e + e_index(A, h, gr, 0);
     const uint32_t *mk = A.newmask + (size_t)(h * kvm + gr) * (A.cap / 32);
     const int dim = h * A.vd + slice * 16 + dcol;
     const bool vt = A.vt != nullptr && (s0 & 3) == 0 && e0 < A.slot_count &&
                     s0 + (ctx + EX_TILE - 1) / EX_TILE * EX_TILE <= A.vt_stride;
-    const float *vtr = vt ? A.vt + (size_t)dim * A.vt_stride + s0 : nullptr;
+    const float *vtr = vt ? A.vt + vt4_off(dim, s0, A.vt_stride) : nullptr;
     float o = (den && A.sinks) ? 1.0f : 0.0f;
     for (int k = 0; 16 * k < ctx; k++) {
         const int n = min(16, ctx - 16 * k);
-        const float e16 = ef[16 * k + dcol], m16 = mf[16 * k + dcol];
+        const float e16 = ef[16 * k + dcol];
         const uint32_t bits = (mk[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
         float v[16];
         if (den) {
@@ -1055,7 +1092,8 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
         } else if (vt) {
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float4 f = *(const float4 *)(vtr + 16 * k + 4 * q);
+                // four consecutive slots of the lane's dim: 64 floats per slot group
+                const float4 f = *(const float4 *)(vtr + (size_t)(4 * k + q) * 64);
                 v[4 * q] = f.x;
                 v[4 * q + 1] = f.y;
                 v[4 * q + 2] = f.z;
@@ -1065,7 +1103,8 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 const int slot = (s0 + 16 * k + min(j, n - 1)) % A.slot_count;
-                v[j] = A.v[(size_t)slot * A.value_stride + dim];
+                v[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[(size_t)slot * A.value_stride + dim])
+                                 : A.v[(size_t)slot * A.value_stride + dim];
             }
         }
         if (n == 16) {
@@ -1075,20 +1114,19 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
             if (any == 0u) {
                 cons_fma16_dpp(e16, v, o);
             } else if (x4 || den) {
-                cons_affine16_dpp(e16, m16, v, o);
+                float a16, m16;
+                aff_pair16(e16, bits, lane, a16, m16);
+                cons_affine16_dpp(a16, m16, v, o);
             } else {
-                float ee[16], mm[16];
-                bcast16_all(e16, ee);
-                bcast16_all(m16, mm);
-                chain_steps16_flags<false, false>(ee, mm, v, o, bits);
+                c4_steps16_slow<false>(e16, v, o, bits);
             }
         } else {
             // the last, partial chunk: step by step in its own form
             for (int j = 0; j < n; j++) {
-                const float e = ef[16 * k + j], mlt = mf[16 * k + j];
+                const float e = ef[16 * k + j];
                 const float vj = v[j];
                 const float on = fmaf(e, vj, o);
-                const float ox = (x4 || den) ? fmaf(vj, 1.0f, o * mlt) : fmaf(o, mlt, vj);
+                const float ox = (x4 || den) ? fmaf(vj, 1.0f, o * e) : fmaf(o, e, vj);
                 o = ((bits >> j) & 1u) ? ox : on;
             }
         }
@@ -1117,21 +1155,21 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) 
     const bool dim_ok = dim < A.vd;
     const bool x4 = is_x4(A, g);
     const float *ef = A.e + e_index(A, h, g, 0);
-    const float *mf = A.mul + e_index(A, h, g, 0);
     const uint32_t *mk = A.newmask + (size_t)head * (A.cap / 32);
     const float *vbase = A.v + (size_t)h * A.vd + (dim_ok ? dim : 0);
     float o = 0.0f;
     float d = A.sinks ? 1.0f : 0.0f;
     for (int t0 = 0; t0 < ctx; t0 += 32) {
         const int n = min(32, ctx - t0);
-        float vb[32], eb[32], mb[32];
+        float vb[32], eb[32];
 #pragma unroll
         for (int j = 0; j < 32; j++) {
             int t = t0 + j < ctx ? t0 + j : ctx - 1;
             int slot = (s0 + t) % A.slot_count;
-            vb[j] = vbase[(size_t)slot * A.value_stride];
+            vb[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[(size_t)h * A.vd + (dim_ok ? dim : 0) +
+                                                                     (size_t)slot * A.value_stride])
+                              : vbase[(size_t)slot * A.value_stride];
             eb[j] = ef[t];
-            mb[j] = mf[t];
         }
         const uint32_t bits = mk[t0 >> 5];
         if (bits == 0 && n == 32) {
@@ -1146,10 +1184,10 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) 
                 if (j < n) {
                     if ((bits >> j) & 1u) {
                         if (x4)
-                            o = fmaf(vb[j], 1.0f, o * mb[j]);  // affine_add: fma(value, 1, out*old)
+                            o = fmaf(vb[j], 1.0f, o * eb[j]);  // affine_add: fma(value, 1, out*old)
                         else
-                            o = fmaf(o, mb[j], vb[j]);         // scale_add: fma(out, old, value)
-                        float p = d * mb[j];
+                            o = fmaf(o, eb[j], vb[j]);         // scale_add: fma(out, old, value)
+                        float p = d * eb[j];
                         d = p + 1.0f;
                     } else {
                         o = fmaf(eb[j], vb[j], o);             // axpy / affine_add with mul 1

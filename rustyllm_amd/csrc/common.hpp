@@ -38,6 +38,26 @@ __device__ __forceinline__ uint16_t ld2(const uint8_t *p) {
 
 // IEEE half -> float (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// bf16 <-> f32 as the reference's f32_to_bf16 / bf16_to_f32 (src/simd.rs:
+// 82-96): widening is exact; narrowing rounds to nearest even, a NaN keeps
+// its payload with the quiet bit set.
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    if (x != x) return (uint16_t)((b >> 16) | 0x0040u);
+    return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+// f32 with the value a bf16 store keeps
+__host__ __device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// four consecutive bf16 (8 bytes) widened
+__device__ __forceinline__ float4 bf16x4_load(const uint16_t *p) {
+    const uint2 u = *(const uint2 *)p;
+    return make_float4(__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xFFFF0000u),
+                       __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xFFFF0000u));
+}
 __device__ __forceinline__ float ldh(const uint8_t *p) { return h2f(ld2(p)); }
 
 // v_dot4_i32_i8: c + sum_k a.byte[k] * b.byte[k] (signed bytes, exact).
@@ -186,6 +206,15 @@ struct XQ {
 
 // Decode step state kept on the device so a captured graph can replay every
 // token without host updates.
+// Float offset of value column j (kv head * vd + dim) at slot p in the tiled
+// transposed V copy, layout [j / 16][p / 4][j % 16][p % 4] with vt_stride
+// slots per column (a multiple of 4): the 16 dims of a slice over 64
+// consecutive slots are one contiguous 4 KB block, and 16 bytes hold four
+// consecutive slots of one dim.
+__host__ __device__ __forceinline__ size_t vt4_off(int64_t j, int64_t p, int64_t vt_stride) {
+    return (size_t)(((j >> 4) * (vt_stride >> 2) + (p >> 2)) * 64 + (j & 15) * 4 + (p & 3));
+}
+
 struct StepState {
     int32_t pos;       // position being written / attended to (end_t)
     int32_t start_t;   // first attended position

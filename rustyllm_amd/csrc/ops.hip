@@ -83,8 +83,10 @@ struct RopeArgs {
     int32_t max_pos;      // rows of the cos/sin table
     int32_t n_heads, n_kv, hd, vd, slots, ring, neox;
     int32_t q_tok, k_tok, v_tok;  // per-token row strides of q/k/v (prefill: token blockIdx.y at pos + y)
-    float *vtcache;       // optional transposed V copy [n_kv*vd][vt_stride] (slot fastest), or null
+    float *vtcache;       // optional tiled transposed V copy (vt4_off layout), or null
     int32_t vt_stride;
+    int32_t kv_bf16;      // 1: kcache / vcache hold bf16 (uint16), narrowed as KVCache::write_k/v do;
+                          // the f32 V copy then holds the widened bf16 values
 };
 
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
@@ -121,6 +123,10 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
             if (isq) {
                 A.q[i0] = r0;
                 A.q[i1] = r1;
+            } else if (A.kv_bf16) {
+                uint16_t *kc = (uint16_t *)A.kcache + (size_t)slot * kvd;
+                kc[i0] = f32_to_bf16(r0);
+                kc[i1] = f32_to_bf16(r1);
             } else {
                 float *kc = A.kcache + (size_t)slot * kvd;
                 kc[i0] = r0;
@@ -128,9 +134,15 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
             }
         } else {
             int j = i - nq - nk;
-            const float v = A.v[j];
-            A.vcache[(size_t)slot * vvd + j] = v;
-            if (A.vtcache) A.vtcache[(size_t)j * A.vt_stride + slot] = v;
+            float v = A.v[j];
+            if (A.kv_bf16) {
+                const uint16_t h = f32_to_bf16(v);
+                ((uint16_t *)A.vcache)[(size_t)slot * vvd + j] = h;
+                v = bf16_to_f32(h);
+            } else {
+                A.vcache[(size_t)slot * vvd + j] = v;
+            }
+            if (A.vtcache) A.vtcache[vt4_off(j, slot, A.vt_stride)] = v;
         }
     }
 }

@@ -888,7 +888,7 @@ static size_t exact_e_floats(int n_kv, int kv_mul, int cap) { return (size_t)n_k
 
 static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
     size_t n = (size_t)n_kv * kv_mul;
-    return n * cap + 2 * exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
+    return n * cap + exact_e_floats(n_kv, kv_mul, cap) + n * (cap / 64) + n * (cap / 32) + (n + 63) / 64 * 64;
 }
 
 // Launches the exact attention kernels; cap = positions reserved per head
@@ -909,8 +909,7 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     A.scores = scratch;
     A.e = scratch + nh * cap;
-    A.mul = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
-    A.tmax = A.mul + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
+    A.tmax = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
     A.newmask = (uint32_t *)(A.tmax + nh * (cap / 64));
     A.den = (float *)(A.newmask + nh * (cap / 32));
     A.kvec = (A.key_stride % 4 == 0 && A.hd % 4 == 0 && ((uintptr_t)A.k & 15) == 0) ? 1 : 0;
@@ -1806,6 +1805,8 @@ struct Resident {
     // slot_for_pos, src/model.rs:1450-1464).
     uint32_t storage = 0, max_pos = 0;
     bool ring = false;
+    // KV cache elements in bf16 (KVCache::enable_bf16, src/model.rs:1406-1421)
+    bool kv_bf16 = false;
     uint32_t neox = 0;
     uint32_t vt_stride = 0;  // positions per row of the transposed V copies (storage rounded up to 64)
     float eps = 1e-5f;
@@ -1885,6 +1886,7 @@ static void r_reset() {
     R.has_embd = false;
     R.tok_cap = 0;
     R.moe = false;
+    R.kv_bf16 = false;
     R.n_exp = R.top_k = R.window = 0;
     R.rope_conc = 1.0f;
     R.moebuf = nullptr;
@@ -1922,13 +1924,25 @@ static ActSpec r_act_norm(const float *norm_w) {
     return a;
 }
 
-// V rows [slot][w] of slots slot0..slot0+n-1 into the transposed copy
-// vt[j][slot] (row length vt_stride).
+// V rows [slot][w] of slots slot0..slot0+n-1 into the tiled transposed copy
+// (vt4_off layout, vt_stride slots per column).
 __global__ void kv_transpose_kernel(const float *v, int w, int slot0, int n, float *vt, int vt_stride) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)n * w) return;
     const int t = (int)(i / w), j = (int)(i % w);
-    vt[(int64_t)j * vt_stride + slot0 + t] = v[(int64_t)(slot0 + t) * w + j];
+    vt[vt4_off(j, slot0 + t, vt_stride)] = v[(int64_t)(slot0 + t) * w + j];
+}
+
+// Split-K attention for this decoder: the mode switch, except with a bf16
+// KV cache, which only the reference-order kernels read.
+static bool r_fast() { return attn_fast_mode() && !R.kv_bf16; }
+
+// bf16 V rows of slots slot0..slot0+n-1, widened, into the tiled f32 copy.
+__global__ void kv_transpose16_kernel(const uint16_t *v, int w, int slot0, int n, float *vt, int vt_stride) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * w) return;
+    const int t = (int)(i / w), j = (int)(i % w);
+    vt[vt4_off(j, slot0 + t, vt_stride)] = bf16_to_f32(v[(int64_t)(slot0 + t) * w + j]);
 }
 
 // One token through the layer stack (and head / greedy by mode) on stream s.
@@ -1969,8 +1983,9 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             A.slots = R.storage;
             A.ring = 0;
             A.neox = R.neox;
+            A.kv_bf16 = R.kv_bf16 ? 1 : 0;
             r_rope = A;
-            if (attn_fast_mode()) {
+            if (r_fast()) {
                 int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
                 ProfScope ps("rope_kv", s);
                 rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
@@ -1979,7 +1994,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
         }
         ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
         act_o.xq = attn_cols % 256 == 0 ? R.xq_attn : XQ{};
-        if (attn_fast_mode()) {
+        if (r_fast()) {
             AttnArgs A;
             memset(&A, 0, sizeof(A));
             A.q = R.q;
@@ -2025,6 +2040,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.scale = 1.0f / sqrtf((float)R.hd);
             E.rope = r_rope;  // RoPE + KV store inside the scores launch
             E.fuse_rope = 1;
+            E.kv_bf16 = R.kv_bf16 ? 1 : 0;
             E.start_t = R.st_host ? R.st_host->start_t : 0;  // the range's start as of this enqueue (a hint)
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
@@ -2341,6 +2357,7 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
             A.slots = R.storage;
             A.ring = 0;
             A.neox = R.neox;
+            A.kv_bf16 = R.kv_bf16 ? 1 : 0;
             A.q_tok = qd;
             A.k_tok = kd;
             A.v_tok = vdim;
@@ -2373,6 +2390,7 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
             E.n_tok = T;
             E.pos0 = pos0;
             E.q_tok = qd;
+            E.kv_bf16 = R.kv_bf16 ? 1 : 0;
             E.o_tok = attn_cols;
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.pex, XQ{}, s, false, &den)) return 0;
@@ -2780,30 +2798,55 @@ int rusty_hip_resident_time_decode(uint32_t n_tokens, float penalty, double *ms)
     return 1;
 }
 
+// KV elements are f32, or bf16 (uint16) after rusty_hip_resident_enable_bf16.
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (!R.configured || l >= R.n_layers || !host_out || (uint64_t)slot0 + n_slots > R.storage) return 0;
-    size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd;
-    float *src = which ? R.L[l].v : R.L[l].k;
+    const size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd, es = R.kv_bf16 ? 2 : 4;
+    const char *src = (const char *)(which ? R.L[l].v : R.L[l].k);
     if (!src) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
-    RH_CHECK(hipMemcpy(host_out, src + (size_t)slot0 * w, (size_t)n_slots * w * 4, hipMemcpyDeviceToHost));
+    RH_CHECK(hipMemcpy(host_out, src + (size_t)slot0 * w * es, (size_t)n_slots * w * es, hipMemcpyDeviceToHost));
     return 1;
 }
 
 int rusty_hip_resident_kv_write(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, const float *host_in) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (!R.configured || l >= R.n_layers || !host_in || (uint64_t)slot0 + n_slots > R.storage) return 0;
-    size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd;
-    float *dst = which ? R.L[l].v : R.L[l].k;
+    const size_t w = which ? (size_t)R.n_kv * R.vd : (size_t)R.n_kv * R.hd, es = R.kv_bf16 ? 2 : 4;
+    char *dst = (char *)(which ? R.L[l].v : R.L[l].k);
     if (!dst) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
-    RH_CHECK(hipMemcpy(dst + (size_t)slot0 * w, host_in, (size_t)n_slots * w * 4, hipMemcpyHostToDevice));
+    RH_CHECK(hipMemcpy(dst + (size_t)slot0 * w * es, host_in, (size_t)n_slots * w * es, hipMemcpyHostToDevice));
     if (which && R.L[l].vt && n_slots > 0) {
-        rh_launch(kv_transpose_kernel, dim3((n_slots * w + 255) / 256), dim3(256), 0, g.s, (const float *)dst, (int)w,
-                  (int)slot0, (int)n_slots, R.L[l].vt, (int)R.vt_stride);
+        if (R.kv_bf16)
+            rh_launch(kv_transpose16_kernel, dim3((n_slots * w + 255) / 256), dim3(256), 0, g.s, (const uint16_t *)dst,
+                      (int)w, (int)slot0, (int)n_slots, R.L[l].vt, (int)R.vt_stride);
+        else
+            rh_launch(kv_transpose_kernel, dim3((n_slots * w + 255) / 256), dim3(256), 0, g.s, (const float *)dst,
+                      (int)w, (int)slot0, (int)n_slots, R.L[l].vt, (int)R.vt_stride);
         RH_LAUNCH_OK();
         RH_CHECK(hipStreamSynchronize(g.s));
+    }
+    return 1;
+}
+
+// KVCache::enable_bf16 (src/model.rs:1406-1421) for the resident decoder.
+int rusty_hip_resident_enable_bf16(int on) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.configured || R.moe) return 0;  // the reference keeps bf16 KV to the standard architecture
+    const bool want = on != 0;
+    if (want != R.kv_bf16) {
+        R.kv_bf16 = want;
+        // a fresh cache of the new element type (the buffers hold f32 either way)
+        RH_CHECK(hipStreamSynchronize(g.s));
+        const size_t kd = (size_t)R.n_kv * R.hd, vdim = (size_t)R.n_kv * R.vd;
+        for (RLayer &Ly : R.L) {
+            if (Ly.k) RH_CHECK(hipMemset(Ly.k, 0, (size_t)R.storage * kd * 4));
+            if (Ly.v) RH_CHECK(hipMemset(Ly.v, 0, (size_t)R.storage * vdim * 4));
+            if (Ly.vt) RH_CHECK(hipMemset(Ly.vt, 0, (size_t)R.vt_stride * vdim * 4));
+        }
+        r_invalidate_graphs();
     }
     return 1;
 }

@@ -34,7 +34,7 @@ SYMBOLS = [
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
     "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
     "rusty_hip_bench_attention", "rusty_hip_attention_noalloc", "rusty_hip_gguf_summary",
-    "rusty_hip_resident_load_gguf",
+    "rusty_hip_resident_load_gguf", "rusty_hip_resident_enable_bf16",
 ]
 
 
@@ -116,6 +116,7 @@ class GgufSummary(C.Structure):
 
 _sig("rusty_hip_gguf_summary", _i, C.c_char_p, C.POINTER(GgufSummary))
 _sig("rusty_hip_resident_load_gguf", _i, C.c_char_p, _u32)
+_sig("rusty_hip_resident_enable_bf16", _i, _i)
 
 
 def gguf_summary(path: str):
@@ -319,7 +320,9 @@ class ResidentLayerDesc(C.Structure):
 class Resident:
     """Whole-token-on-device decoder over a model dict from rustyllm_amd.synth."""
 
-    def __init__(self, model, storage_len: int):
+    kv_bf16 = False
+
+    def __init__(self, model, storage_len: int, kv_bf16: bool = False):
         cfg = model["config"]
         self.cfg = cfg
         self.storage_len = storage_len
@@ -354,6 +357,15 @@ class Resident:
                 raise RuntimeError(f"rusty_hip_resident_set_layer({l}) failed")
         self._set_output(model)
         self._keep = []
+        if kv_bf16:
+            self.enable_bf16(True)
+
+    def enable_bf16(self, on: bool = True):
+        """KVCache::enable_bf16: a fresh bf16 KV cache (kv_read/kv_write then
+        move uint16 elements)."""
+        if lib.rusty_hip_resident_enable_bf16(1 if on else 0) != 1:
+            raise RuntimeError("rusty_hip_resident_enable_bf16 failed")
+        self.kv_bf16 = bool(on)
 
     def _set_output(self, model):
         cfg = self.cfg
@@ -396,7 +408,7 @@ class Resident:
     def kv_read(self, layer, which, slot0, n_slots):
         cfg = self.cfg
         w = cfg["n_kv_heads"] * (cfg["value_dim"] if which else cfg["head_dim"])
-        out = np.zeros(n_slots * w, np.float32)
+        out = np.zeros(n_slots * w, np.uint16 if self.kv_bf16 else np.float32)
         if lib.rusty_hip_resident_kv_read(layer, which, slot0, n_slots, _ptr(out)) != 1:
             raise RuntimeError("kv_read failed")
         return out
@@ -404,7 +416,7 @@ class Resident:
     def kv_write(self, layer, which, slot0, data):
         cfg = self.cfg
         w = cfg["n_kv_heads"] * (cfg["value_dim"] if which else cfg["head_dim"])
-        d = _f32(data)
+        d = np.ascontiguousarray(data, np.uint16) if self.kv_bf16 else _f32(data)
         n_slots = d.size // w
         if lib.rusty_hip_resident_kv_write(layer, which, slot0, n_slots, _ptr(d)) != 1:
             raise RuntimeError("kv_write failed")

@@ -129,9 +129,18 @@ def matvec_ref(w, t, rows, cols, x):
     return W @ xv
 
 
-def forward_model(model, tokens, start_pos=0):
+def bf16_round(x):
+    """x through a bf16 store: f32, round to nearest even on the top 16 bits."""
+    b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (((b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFFFFFF) >> 16 << 16).astype(np.uint32)
+    return r.view(np.float32).astype(np.float64)
+
+
+def forward_model(model, tokens, start_pos=0, kv_bf16=False):
     """float64 restatement of forward_into (src/model.rs:7177-7358) for a
-    rustyllm_amd.synth model; returns the logits of every position."""
+    rustyllm_amd.synth model; returns the logits of every position.  kv_bf16:
+    the cache keeps each K/V element as its bf16 rounding (KVCache::write_k /
+    write_v with enable_bf16)."""
     c = model["config"]
     dim, hd, vd = c["dim"], c["head_dim"], c.get("value_dim", c["head_dim"])
     nh, nkv = c["n_heads"], c["n_kv_heads"]
@@ -182,8 +191,8 @@ def forward_model(model, tokens, start_pos=0):
             if L.get("bq") is not None:
                 q, k, v = q + L["bq"], k + L["bk"], v + L["bv"]
             q, k = rope(q, nh, pos), rope(k, nkv, pos)
-            K[l].append(k)
-            V[l].append(v)
+            K[l].append(bf16_round(k) if kv_bf16 else k)
+            V[l].append(bf16_round(v) if kv_bf16 else v)
             Kc, Vc = np.array(K[l]), np.array(V[l])
             att = attention_f64(q, Kc, Vc, nh, nkv, hd, vd, np.float32(1.0) / np.sqrt(np.float32(hd)))
             x = x + mv(W[3], 3, att, l, nh * vd)

@@ -118,3 +118,19 @@ def test_yarn_table(theta, hd, scaling, orig):
     assert np.array_equal(inv[lo_pairs], (f(1.0) / base[lo_pairs]).astype(np.float32))
     assert np.array_equal(inv[hi_pairs], (f(1.0) / (f(scaling) * base[hi_pairs])).astype(np.float32))
     assert np.all(np.diff(inv) < 0)
+
+
+@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-qwen"])
+def test_forward_bf16_kv_vs_f64(name):
+    """forward_into with KVCache::enable_bf16 (the oracle's bf16 cache and
+    attention_over_kv_heads_bf16) against the float64 forward whose cache
+    holds bf16-rounded K/V; the same bound as the f32 cache."""
+    model = synth.make_model(name, seed=3)
+    toks = [int(t) for t in synth.token_ids(5, 6, model["config"]["vocab"])]
+    om = O.OracleModel(model, storage_len=32, threads=4, kv_bf16=True)
+    got = np.array([om.forward(t, p) for p, t in enumerate(toks)])
+    ref = npref.forward_model(model, toks, kv_bf16=True)
+    scale = np.abs(ref).max()
+    assert np.max(np.abs(got - ref)) < 5e-4 * scale, (np.max(np.abs(got - ref)), scale)
+    k, v = om.kv(0, 32)
+    assert k.dtype == np.uint16 and np.any(k[: 6 * model["config"]["n_kv_heads"] * 64] != 0)

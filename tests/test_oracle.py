@@ -487,3 +487,75 @@ def test_greedy_duplicates_compound_and_first_max_wins():
     assert tok == 2
     tok, _ = O.greedy(np.array([np.nan, np.nan], np.float32), [], 1.0)
     assert tok == 0
+
+
+# ---- bf16 KV cache (KVCache::enable_bf16, model.rs:1406-1421, 6205-6580) ----------
+def _bf16_np(x):
+    """f32_to_bf16 from the bit layout (round to nearest even, NaN quieted)."""
+    b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFFFFFF) >> 16
+    q = (b >> 16) | 0x40
+    return np.where(np.isnan(np.asarray(x, np.float32)), q, r).astype(np.uint16)
+
+
+def test_f32_to_bf16_closed_form():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(2000).astype(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1.0, -1.5], np.float32),
+                        np.array([0x3F808000, 0x3F818000, 0x3F80C000, 0x7F7FFFFF, 0x00000001, 0x7FC00001,
+                                  0xFF800001, 0x007FFFFF], np.uint32).view(np.float32)])
+    got = O.f32_to_bf16(x)
+    assert np.array_equal(got, _bf16_np(x))
+    # ties go to even: 1 + 2^-8 exactly between 0x3F80 and 0x3F81 -> 0x3F80; 0x3F818000 -> 0x3F82
+    assert got[-8] == 0x3F80 and got[-7] == 0x3F82
+    assert got[-5] == 0x7F80  # the largest finite float rounds to +inf
+    assert got[-3] & 0x7FC0 == 0x7FC0 and got[-2] & 0xFFC0 == 0xFFC0  # NaNs stay NaN (quiet bit)
+    w = np.array([O.lib.orc_bf16_to_f32(int(h)) for h in got[:2000]], np.float32)
+    assert np.array_equal(w.view(np.uint32), (got[:2000].astype(np.uint32) << 16))
+
+
+def test_dot_bf16_single_accumulator_vs_f64():
+    rng = np.random.default_rng(6)
+    for n in (64, 128, 136, 7):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        got = O.lib.orc_dot_bf16_f32_avx2(O.ptr(a), O.ptr(b), n)
+        ref = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+        assert abs(got - ref) <= 1e-5 * np.sum(np.abs(a * b)) + 1e-7
+
+
+def _kv_bf16(rng, slots, w):
+    k = rng.standard_normal(slots * w).astype(np.float32)
+    v = rng.standard_normal(slots * w).astype(np.float32)
+    k16, v16 = _bf16_np(k), _bf16_np(v)
+    return k16, v16, (k16.astype(np.uint32) << 16).view(np.float32), (v16.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_bf16_attention_equals_f32_on_widened_rows_x4():
+    """kv_mul 4: dot_bf16x4 / affine_add_bf16x4 are the f32 x4 kernels on the
+    widened rows, so bf16 attention over bf16 K/V equals f32 attention over
+    the widened values bit for bit (ring ranges included)."""
+    rng = np.random.default_rng(7)
+    nh, nkv, hd = 8, 2, 128
+    slots = 300
+    k16, v16, kw, vw = _kv_bf16(rng, slots, nkv * hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    for st, en, sl in ((0, 299, 300), (17, 250, 300), (0, 700, 256)):
+        got = O.attention_bf16(q, k16, v16, nh, nkv, hd, hd, nkv * hd, nkv * hd, sl, st, en, np.float32(0.088))
+        ref = O.attention(q, kw, vw, nh, nkv, hd, hd, nkv * hd, nkv * hd, sl, st, en, np.float32(0.088))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("nh,nkv", [(4, 4), (10, 2), (16, 2), (12, 2)])
+def test_bf16_attention_vs_f64(nh, nkv):
+    """Other group sizes (single-accumulator dots for every head) against the
+    textbook softmax in float64 over the widened values."""
+    rng = np.random.default_rng(nh * 10 + nkv)
+    hd, ctx = 64, 333
+    k16, v16, kw, vw = _kv_bf16(rng, ctx, nkv * hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    scale = np.float32(0.125)
+    got = O.attention_bf16(q, k16, v16, nh, nkv, hd, hd, nkv * hd, nkv * hd, ctx, 0, ctx - 1, scale)
+    ref = npref.attention_f64(q, kw.reshape(ctx, -1), vw.reshape(ctx, -1), nh, nkv, hd, hd, scale)
+    r = ref.reshape(nh, hd)
+    assert np.all(np.abs(got.reshape(nh, hd) - r).max(axis=1) <= 1e-5 * np.linalg.norm(r, axis=1) + 1e-6)
