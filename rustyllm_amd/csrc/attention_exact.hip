@@ -552,22 +552,6 @@ __global__ __launch_bounds__(256) void attn_exact_coef_kernel(AttnExactArgs A0) 
 // their LDS reads: e enters each FMA through its DPP row_newbcast operand
 // (lane j of a 16-lane row holds step j), V comes from LDS, and producer
 // waves stream both into a ring by direct global->LDS loads.
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ void dma16(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void *src, void *lds) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 4, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
-// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
-#define RH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
-// lgkmcnt(0) only
-#define RH_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14))
-// lgkmcnt(N) only (N <= 15)
-#define RH_WAIT_LGKM(N) __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | ((N) << 8) | (3 << 14))
 
 // Workgroup barrier without the memory-model waits of __syncthreads (which
 // would drain the producers' loads); the asm statements keep the compiler

@@ -36,6 +36,24 @@ __device__ __forceinline__ uint16_t ld2(const uint8_t *p) {
     return v;
 }
 
+// Direct global -> LDS loads: lane l's 16 (or 4) bytes from its own address
+// land at lds + 16 l (4 l); completion is counted by vmcnt.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ __forceinline__ void dma16(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+#define RH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
+// lgkmcnt(0) only
+#define RH_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (0 << 8) | (3 << 14))
+// lgkmcnt(N) only (N <= 15)
+#define RH_WAIT_LGKM(N) __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | ((N) << 8) | (3 << 14))
+
 // IEEE half -> float (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 

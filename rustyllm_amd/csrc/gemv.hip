@@ -752,6 +752,27 @@ __global__ __launch_bounds__(256) void gemv_kq2_kernel(GemvArgs A, GemvArgs B, i
 __constant__ float kMxfp4Lut[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
                                     -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
 
+// Both FP4 values of byte u of w (low nibble first), each times scale:
+// gfx950's v_cvt_scalef32_pk_f32_fp4.
+typedef float fp4x2_f32 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ fp4x2_f32 fp4x2_scaled(uint32_t w, float scale, int u) {
+    switch (u) {
+    case 0: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
+    case 1: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
+    case 2: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
+    default: return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
+    }
+}
+
+// kMxfp4Lut[n] without a memory access: magnitudes 0 and 0.5 for n & 7 < 2,
+// else exponent 126 + (n & 7) / 2 with the low bit as the one mantissa bit;
+// bit 3 is the sign (n = 8 gives -0).
+__device__ __forceinline__ float mxfp4_nibble(uint32_t n) {
+    const uint32_t v = n & 7u;
+    const float mag = v < 2u ? (float)v * 0.5f : __builtin_bit_cast(float, (v << 22) + 0x3F000000u);
+    return (n & 8u) ? -mag : mag;
+}
+
 __device__ __forceinline__ float mxfp4_scale(uint32_t e) {
     // 2^(e-127) as an exact power of two (e = 0 is the subnormal 2^-127).
     if (e == 0) return __builtin_bit_cast(float, 0x00400000u);
@@ -843,21 +864,15 @@ __global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
     }
 }
 
-// f32-activation GEMVs, bit-identical to the reference rows:
-//   Q8_0  (dot_q8_0_f32_avx2, src/simd.rs:6671-6692): eight accumulators per
-//         row, acc_j = fma(d*q, x, acc_j) over elements 32b + 8i + j (block b
-//         outer, group i inner), then hsum_avx ((a0+a4)+(a1+a5)) +
-//         ((a2+a6)+(a3+a7)); eight lanes per row, eight rows per wave;
-//   MXFP4 (dot_mxfp4_f32_scalar, src/simd.rs:5886-5902): one running sum per
-//         row, sum += (lut*scale)*x element by element; one lane per row.
-// A workgroup is one wave over tiles of 8 (Q8_0) or 64 (MXFP4) rows; the
-// activation (the matrix's own, else the launch's) is staged in LDS.
-template <int FMT>
-__global__ __launch_bounds__(64) void gemv_f32x_kernel(GemvArgs A) {
+// Q8_0 rows with f32 activations (dot_q8_0_f32_avx2, src/simd.rs:6671-6692),
+// bit-identical: eight accumulators per row, acc_j = fma(d*q, x, acc_j) over
+// elements 32b + 8i + j (block b outer, group i inner), then hsum_avx
+// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)); eight lanes per row, eight rows per
+// wave.  A workgroup is one wave over tiles of 8 rows; the activation (the
+// matrix's own, else the launch's) is staged in LDS.
+__global__ __launch_bounds__(64) void gemv_q8_0_f32x_kernel(GemvArgs A) {
     extern __shared__ float s_x[];  // [K]
-    __shared__ float s_lut[16];
     const int K = A.K, nb = K >> 5, lane = threadIdx.x;
-    if (FMT == F_MXFP4 && lane < 16) s_lut[lane] = kMxfp4Lut[lane];
     const float *staged = nullptr;
     for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
         int mi = 0;
@@ -879,56 +894,30 @@ __global__ __launch_bounds__(64) void gemv_f32x_kernel(GemvArgs A) {
             w += e * M.sel_w;
             if (bias) bias += e * M.sel_b;
         }
-        float out;
-        int row;
-        bool store;
-        if (FMT == F_MXFP4) {
-            row = (tile - M.tile_begin) * 64 + lane;
-            store = row < M.rows;
-            const uint8_t *rp = w + (int64_t)(store ? row : 0) * M.row_stride;
-            float sum = 0.0f;
-            for (int b = 0; b < nb; b++) {
-                const uint4 q = ld16(rp + b * 17);
-                const float sc = mxfp4_scale(rp[b * 17 + 16]);
-                const float *xb = s_x + b * 32;
-                const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        const int j = lane & 7;
+        const int row = (tile - M.tile_begin) * 8 + (lane >> 3);
+        const bool ok = row < M.rows;
+        const uint8_t *rp = w + (int64_t)(ok ? row : 0) * M.row_stride;
+        const uint32_t sh = 8u * (uint32_t)(j & 3);
+        const bool hi = j >= 4;
+        float acc = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            const uint8_t *blk = rp + b * 34;
+            const float d = ldh(blk);
+            const uint4 q0 = ld16(blk + 2), q1 = ld16(blk + 18);
+            // byte 8i + j of the 32 quants: dword 2i + j/4, bits 8*(j%4)
+            const uint32_t dw[4] = {hi ? q0.y : q0.x, hi ? q0.w : q0.z, hi ? q1.y : q1.x, hi ? q1.w : q1.z};
+            const float *xb = s_x + b * 32 + j;
 #pragma unroll
-                for (int k = 0; k < 4; k++)
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        const uint32_t byte = (wd[k] >> (8 * t)) & 0xFFu;
-                        sum += s_lut[byte & 0xFu] * sc * xb[8 * k + 2 * t];
-                        sum += s_lut[byte >> 4] * sc * xb[8 * k + 2 * t + 1];
-                    }
+            for (int i = 0; i < 4; i++) {
+                const float q = (float)(int)__builtin_amdgcn_sbfe((int)dw[i], sh, 8u);
+                acc = fmaf(d * q, xb[8 * i], acc);
             }
-            out = sum;
-        } else {
-            const int j = lane & 7;
-            row = (tile - M.tile_begin) * 8 + (lane >> 3);
-            const bool ok = row < M.rows;
-            const uint8_t *rp = w + (int64_t)(ok ? row : 0) * M.row_stride;
-            const uint32_t sh = 8u * (uint32_t)(j & 3);
-            const bool hi = j >= 4;
-            float acc = 0.0f;
-            for (int b = 0; b < nb; b++) {
-                const uint8_t *blk = rp + b * 34;
-                const float d = ldh(blk);
-                const uint4 q0 = ld16(blk + 2), q1 = ld16(blk + 18);
-                // byte 8i + j of the 32 quants: dword 2i + j/4, bits 8*(j%4)
-                const uint32_t dw[4] = {hi ? q0.y : q0.x, hi ? q0.w : q0.z, hi ? q1.y : q1.x, hi ? q1.w : q1.z};
-                const float *xb = s_x + b * 32 + j;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float q = (float)(int)__builtin_amdgcn_sbfe((int)dw[i], sh, 8u);
-                    acc = fmaf(d * q, xb[8 * i], acc);
-                }
-            }
-            const float t = acc + __shfl_xor(acc, 4, 64);
-            const float u = t + __shfl_xor(t, 1, 64);
-            out = u + __shfl_xor(u, 2, 64);
-            store = ok && j == 0;
         }
-        if (store) {
+        const float t = acc + __shfl_xor(acc, 4, 64);
+        const float u = t + __shfl_xor(t, 1, 64);
+        float out = u + __shfl_xor(u, 2, 64);
+        if (ok && j == 0) {
             if (bias) out += bias[row];
             if (A.epi == EPI_ADD)
                 M.y[row] += out;
@@ -941,28 +930,33 @@ __global__ __launch_bounds__(64) void gemv_f32x_kernel(GemvArgs A) {
 // MXFP4 rows in dot_mxfp4_f32_scalar's order (src/simd.rs:5886-5902): one
 // running sum per row over the elements in order, each term
 // (lut[nibble] * scale) * x.  The sum is a dependent chain of K adds, so a
-// row is one lane's work; the terms are independent.  A workgroup of five
-// waves serves 64 rows of one matrix: waves 1-4 compute the terms of one
-// 32-element block each (lane = row) into an LDS ring, wave 0 adds them in
-// order (lane = row), eight LDS reads and 32 adds per block.  One barrier per
-// four blocks: the adder reads blocks 4j..4j+3 while the producers write
-// 4j+4..4j+7 into the ring's other half.
+// row is one lane's work; the terms are independent.  A workgroup of
+// 1 + MXP waves serves 64 rows of one matrix: waves 1..MXP compute the terms
+// of one 32-element block each (lane = row) into an LDS ring, wave 0 adds
+// them in order (lane = row), eight LDS reads and 32 adds per block.  One
+// barrier per group of MXP blocks: the adder reads group j while the
+// producers write group j + 1 into the ring's other half.
+#define MXP 4   // producer waves
+#define MX_D 4  // groups of block loads in flight per producer
+typedef const __attribute__((address_space(4))) float *const_f32_ptr;
 // Barrier that waits only for this wave's LDS operations (global loads stay in
-// flight across it); the asm statements keep the compiler from moving memory
-// accesses across the barrier.
+// flight across it); the compiler fences keep memory accesses from moving
+// across the barrier.
 __device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt/expcnt unrestricted
     __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Ring layout: slot, row r, then the row's eight 4-term groups with group g
-// stored at g ^ (r % 8), so the adder's 16-byte reads of one group by eight
-// consecutive rows fall in 32 distinct banks.
-__global__ __launch_bounds__(320) void gemv_mxfp4_serial_kernel(GemvArgs A) {
-    extern __shared__ float s_x[];                   // [K]
-    __shared__ __align__(16) float s_t[8][64 * 32];  // [slot][row][8 groups of 4 terms]
+// Ring layout: slot (block % 2P), 4-term group g (0..7) of the block, row r:
+// one 16-byte read or write of a group by the wave's 64 rows covers 1 KB of
+// consecutive LDS, every bank four times, the conflict-free minimum.
+template <int P>
+__global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
+    GemvArgs A) {
+    constexpr int NT = 64 * (P + 1), SLOTS = 2 * P;
+    __shared__ __align__(16) float s_t[SLOTS][64 * 32];  // [slot][8 groups][row][4 terms]
     __shared__ float s_lut[16];
     const int K = A.K, nb = K >> 5, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -974,7 +968,6 @@ __global__ __launch_bounds__(320) void gemv_mxfp4_serial_kernel(GemvArgs A) {
     const GemvMat M = mat_sel(A, mi);
     const float *xs = M.x ? M.x : A.x;
     if (tid < 16) s_lut[tid] = kMxfp4Lut[tid];
-    for (int i = 4 * tid; i < K; i += 4 * 320) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
     const uint8_t *w = M.w;
     const float *bias = M.bias;
     if (M.sel) {
@@ -985,68 +978,273 @@ __global__ __launch_bounds__(320) void gemv_mxfp4_serial_kernel(GemvArgs A) {
     const int row = (tile - M.tile_begin) * 64 + lane;
     const bool live = row < M.rows;
     const uint8_t *rp = w + (int64_t)(live ? row : 0) * M.row_stride;
-    const int ngroups = (nb + 3) / 4;
-    // producer wave p = wave - 1 handles blocks 4j + p; each block's bytes
-    // are loaded a group ahead, and the barriers wait only for LDS, so that
-    // load stays in flight across them
+    const int ngroups = (nb + P - 1) / P;
+    // producer wave pw = wave - 1 handles blocks P j + pw
     const int pw = wave - 1;
-    auto load_blk = [&](int b, uint4 &q, uint32_t &e) {
+    // the scale byte (offset 16) is loaded as the top byte of the dword at
+    // offset 13 and extracted where it is used: a byte load's zero-extension
+    // is placed by the compiler right after the load, which waits for it
+    auto load_blk = [&](int b, uint4 &q, uint32_t &e4) {
         const int bb = min(b, nb - 1);  // past the end: a clamped, unused load
         q = ld16(rp + bb * 17);
-        e = rp[bb * 17 + 16];
+        e4 = ld4(rp + bb * 17 + 13);
     };
-    auto produce = [&](int b, const uint4 &q, uint32_t e) {
+    // the 32 x values of one block, loaded a group ahead of their use
+    struct XBlk {
+        float v[32];
+    };
+    auto load_x = [&](int b, XBlk &xr) {
+        // x is the same for every row: scalar loads (the block index is
+        // wave-uniform), an SGPR operand per multiply, no LDS traffic
+        const const_f32_ptr p = (const_f32_ptr)xs + min(b, nb - 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xr.v[i] = p[i];
+        // pin the loads here, ahead of the barrier that follows (its
+        // lgkmcnt(0) covers them), instead of next to their first use
+#pragma unroll
+        for (int i = 0; i < 32; i++) asm volatile("" ::"s"(xr.v[i]));
+    };
+    auto produce = [&](int b, const uint4 &q, uint32_t e4, const XBlk &xr) {
         if (b >= nb) return;
+        const uint32_t e = e4 >> 24;
         const float sc = mxfp4_scale(e);
-        const float *xb = s_x + b * 32;
-        float *dst = &s_t[b & 7][lane * 32];
-        const int sw = lane & 7;
+        float *dst = &s_t[b % SLOTS][lane * 4];
         const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        // lut[nibble] * scale is exact (two significant bits times a power of
+        // two), which the hardware FP4 conversion computes for both nibbles of
+        // a byte at once; a subnormal (e = 0) or infinite (e = 255) scale takes
+        // the table.  The choice is made once per wave and block, so the
+        // common case runs without divergent branches.
+        auto store = [&](int k, const float (&t)[8]) {
+            *(float4 *)(dst + 256 * (2 * k)) = make_float4(t[0], t[1], t[2], t[3]);
+            *(float4 *)(dst + 256 * (2 * k + 1)) = make_float4(t[4], t[5], t[6], t[7]);
+        };
+        if (__builtin_amdgcn_ballot_w64(e == 0u || e == 255u) == 0) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float t[8];
+            for (int k = 0; k < 4; k++) {
+                float t[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t byte = (wd[k] >> (8 * u)) & 0xFFu;
-                t[2 * u] = s_lut[byte & 0xFu] * sc * xb[8 * k + 2 * u];
-                t[2 * u + 1] = s_lut[byte >> 4] * sc * xb[8 * k + 2 * u + 1];
+                for (int u = 0; u < 4; u++) {
+                    const fp4x2_f32 p = fp4x2_scaled(wd[k], sc, u);
+                    t[2 * u] = p.x * xr.v[8 * k + 2 * u];
+                    t[2 * u + 1] = p.y * xr.v[8 * k + 2 * u + 1];
+                }
+                store(k, t);
             }
-            *(float4 *)(dst + 4 * ((2 * k) ^ sw)) = make_float4(t[0], t[1], t[2], t[3]);
-            *(float4 *)(dst + 4 * ((2 * k + 1) ^ sw)) = make_float4(t[4], t[5], t[6], t[7]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float t[8];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t byte = (wd[k] >> (8 * u)) & 0xFFu;
+                    t[2 * u] = s_lut[byte & 0xFu] * sc * xr.v[8 * k + 2 * u];
+                    t[2 * u + 1] = s_lut[byte >> 4] * sc * xr.v[8 * k + 2 * u + 1];
+                }
+                store(k, t);
+            }
         }
     };
-    uint4 qc = make_uint4(0, 0, 0, 0), qn = make_uint4(0, 0, 0, 0);
-    uint32_t ec = 0, en = 0;
+    // MX_D groups of block loads in flight per producer: a group's worth of
+    // the adder's work is far shorter than one load's latency.  Group g's
+    // bytes live in ring entry g % MX_D; every index below is a constant
+    // after unrolling, so the ring stays in registers.  The adder and the
+    // producers run separate loops with the same barrier count (1 + npad),
+    // the group count rounded up to MX_D: groups past the end add nothing,
+    // produce nothing and load a clamped block, so the producer loop body is
+    // straight-line and its loads retire in issue order.
+    const int npad = (ngroups + MX_D - 1) / MX_D * MX_D;
+    uint4 q[MX_D];
+    uint32_t e[MX_D];
     if (wave > 0) {
-        load_blk(pw, qc, ec);
-        load_blk(4 + pw, qn, en);
-    }
-    __syncthreads();  // x and the LUT staged
-    if (wave > 0) produce(pw, qc, ec);
-    lds_barrier();
-    float sum = 0.0f;
-    for (int j = 0; j < ngroups; j++) {
-        if (wave == 0) {
-            for (int b = 4 * j; b < min(4 * j + 4, nb); b++) {
-                const float *src = &s_t[b & 7][lane * 32];
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float4 v = *(const float4 *)(src + 4 * (k ^ (lane & 7)));
-                    sum += v.x;
-                    sum += v.y;
-                    sum += v.z;
-                    sum += v.w;
+        for (int u = 0; u < MX_D; u++) load_blk(P * u + pw, q[u], e[u]);
+    }
+    __syncthreads();  // the LUT staged
+    if (wave == 0) {
+        lds_barrier();  // group 0 produced
+        float sum = 0.0f;
+        for (int j = 0; j < npad; j++) {
+            const int b0 = P * j;
+            // the next block's eight reads are in flight while this block's
+            // 32 adds run
+            float4 v[2][8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[0][k] = *(const float4 *)(&s_t[b0 % SLOTS][lane * 4] + 256 * k);
+#pragma unroll
+            for (int i = 0; i < P; i++) {
+                if (i + 1 < P) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++)
+                        v[(i + 1) & 1][k] = *(const float4 *)(&s_t[(b0 + i + 1) % SLOTS][lane * 4] + 256 * k);
+                }
+                if (b0 + i < nb) {
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        sum += v[i & 1][k].x;
+                        sum += v[i & 1][k].y;
+                        sum += v[i & 1][k].z;
+                        sum += v[i & 1][k].w;
+                    }
                 }
             }
-        } else if (j + 1 < ngroups) {
-            qc = qn;
-            ec = en;
-            load_blk(4 * (j + 2) + pw, qn, en);
-            produce(4 * (j + 1) + pw, qc, ec);
+            lds_barrier();
         }
-        lds_barrier();
+        if (live) {
+            float out = sum;
+            if (bias) out += bias[row];
+            if (A.epi == EPI_ADD)
+                M.y[row] += out;
+            else
+                M.y[row] = out;
+        }
+        return;
     }
-    if (wave == 0 && live) {
+    XBlk xr;
+    load_x(pw, xr);
+    produce(pw, q[0], e[0], xr);
+    load_blk(P * MX_D + pw, q[0], e[0]);
+    load_x(P + pw, xr);
+    lds_barrier();
+    for (int j0 = 0; j0 < npad; j0 += MX_D) {
+#pragma unroll
+        for (int u = 0; u < MX_D; u++) {
+            // group j0 + u + 1 from ring entry (u + 1) % MX_D, which then
+            // takes the loads of group j0 + u + 1 + MX_D
+            const int r = (u + 1) % MX_D, b = P * (j0 + u + 1) + pw;
+            produce(b, q[r], e[r], xr);
+            load_blk(P * (j0 + u + 1 + MX_D) + pw, q[r], e[r]);
+            load_x(b + P, xr);
+            lds_barrier();
+        }
+    }
+}
+
+// MXFP4 rows in the same order, one wave per 64-row tile that computes the
+// terms and the running sums itself (lane = row).  Per block that is 16 FP4
+// conversions, 32 multiplies and the 32 dependent adds on one wave: slower per
+// tile than the producer/adder workgroup above, but with 64 threads per
+// workgroup every SIMD holds a tile, the choice for launches with more tiles
+// than CUs.  The weights arrive in chunks of 16 blocks: 64 rows x 272 bytes =
+// 1088 aligned 16-byte pieces, piece f = row * 17 + p, moved by 17 coalesced
+// direct global->LDS loads (instruction i carries pieces 64 i .. 64 i + 63,
+// about four rows' contiguous bytes) into a 17 KB LDS chunk; each lane then
+// reads its row's 272 bytes into registers (17 reads; the 17-piece row stride
+// keeps them conflict-free), the next chunk's loads start, and the 17-byte
+// blocks are funnel-shifted out of the registers.  A row-per-lane global load
+// would touch 64 cache lines per instruction.
+#define MXF_C 16  // blocks per chunk
+__global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
+    __shared__ __align__(16) uint4 s_b[64 * 17];
+    const int K = A.K, nb = K >> 5, lane = threadIdx.x;
+    const int tile = blockIdx.x;
+    int mi = 0;
+#pragma unroll
+    for (int t = 1; t < GEMV_MAX_MATS; t++)
+        if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+    const GemvMat M = mat_sel(A, mi);
+    const float *xs = M.x ? M.x : A.x;
+    const uint8_t *w = M.w;
+    const float *bias = M.bias;
+    if (M.sel) {
+        const int64_t e = *M.sel;
+        w += e * M.sel_w;
+        if (bias) bias += e * M.sel_b;
+    }
+    const int row0 = (tile - M.tile_begin) * 64, row = row0 + lane;
+    const bool live = row < M.rows;
+    const int64_t stride = M.row_stride;  // a multiple of 16 that holds nb * 17 bytes
+    const int nch = (nb + MXF_C - 1) / MXF_C;
+    // the 17 pieces this lane moves per chunk: piece f = 64 i + lane of the
+    // tile is row f / 17, bytes 16 (f % 17) of the chunk; rows past the
+    // matrix read its last row and bytes past the row's end its last piece
+    auto issue_chunk = [&](int c) {
+        int r = lane / 17, p = lane - 17 * (lane / 17);
+#pragma unroll
+        for (int i = 0; i < 17; i++) {
+            const int rr = min(row0 + r, M.rows - 1);
+            const int64_t off = min((int64_t)(MXF_C * 17 * c + 16 * p), stride - 16);
+            dma16(w + (int64_t)rr * stride + off, &s_b[64 * i]);
+            r += 3;  // 64 = 3 * 17 + 13
+            p += 13;
+            if (p >= 17) {
+                p -= 17;
+                r += 1;
+            }
+        }
+    };
+    struct XBlk {
+        float v[32];
+    };
+    auto load_x = [&](int b, XBlk &xr) {
+        const const_f32_ptr p = (const_f32_ptr)xs + min(b, nb - 1) * 32;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xr.v[i] = p[i];
+    };
+    // one block's 32 terms added to sum in element order; fast: every lane's
+    // scale is normal, so the hardware conversion applies (lut * scale exact)
+    auto add_block = [&](float sum, const uint32_t (&wd)[4], uint32_t e, const XBlk &xr) {
+        const float sc = mxfp4_scale(e);
+        if (__builtin_amdgcn_ballot_w64(e == 0u || e == 255u) == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const fp4x2_f32 p = fp4x2_scaled(wd[k], sc, u);
+                    sum += p.x * xr.v[8 * k + 2 * u];
+                    sum += p.y * xr.v[8 * k + 2 * u + 1];
+                }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t byte = (wd[k] >> (8 * u)) & 0xFFu;
+                    sum += mxfp4_nibble(byte & 0xFu) * sc * xr.v[8 * k + 2 * u];
+                    sum += mxfp4_nibble(byte >> 4) * sc * xr.v[8 * k + 2 * u + 1];
+                }
+        }
+        return sum;
+    };
+    // block j of this lane's chunk: bytes 17 j .. 17 j + 16 of the 68 dwords
+    auto block_of = [&](const uint32_t (&dw)[68], int j, uint32_t (&wd)[4], uint32_t &e) {
+        const int d = (17 * j) >> 2, o = (17 * j) & 3;
+#pragma unroll
+        for (int k = 0; k < 4; k++) wd[k] = o ? __builtin_amdgcn_alignbyte(dw[d + k + 1], dw[d + k], o) : dw[d + k];
+        e = (dw[d + 4] >> (8 * o)) & 0xFFu;
+    };
+    float sum = 0.0f;
+    XBlk xr[2];
+    load_x(0, xr[0]);
+    issue_chunk(0);
+    for (int c = 0; c < nch; c++) {
+        // chunk c: from LDS into registers, then chunk c + 1 into the freed
+        // LDS while this one is summed
+        RH_WAIT_VM(0);
+        uint32_t dw[68];
+        const uint4 *src = &s_b[17 * lane];
+#pragma unroll
+        for (int p = 0; p < 17; p++) {
+            const uint4 v = src[p];
+            dw[4 * p] = v.x;
+            dw[4 * p + 1] = v.y;
+            dw[4 * p + 2] = v.z;
+            dw[4 * p + 3] = v.w;
+        }
+        RH_WAIT_LGKM0();
+        if (c + 1 < nch) issue_chunk(c + 1);  // uniform
+        const int b0 = MXF_C * c;
+#pragma unroll
+        for (int j = 0; j < MXF_C; j++) {
+            if (b0 + j < nb) {  // uniform; false only in a last, partial chunk
+                load_x(b0 + j + 1, xr[(j + 1) & 1]);
+                uint32_t wd[4], e;
+                block_of(dw, j, wd, e);
+                sum = add_block(sum, wd, e, xr[j & 1]);
+            }
+        }
+    }
+    if (live) {
         float out = sum;
         if (bias) out += bias[row];
         if (A.epi == EPI_ADD)

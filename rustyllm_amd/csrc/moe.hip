@@ -1,9 +1,9 @@
 // moe.hip — the routed mixture-of-experts feed-forward block of gpt-oss
 // decode (forward_gpt_oss_into, src/model.rs:6846-6898): router selection,
 // the gpt-oss SwiGLU with expert biases, and the weighted combine.  The
-// expert matrix-vector products are gemv_f32x_kernel launches whose expert
-// is read on the device (GemvMat::sel), so a whole block runs without a host
-// round trip.
+// expert matrix-vector products are f32-activation GEMV launches (MXFP4 or
+// Q8_0) whose expert is read on the device (GemvMat::sel), so a whole block
+// runs without a host round trip.
 #pragma once
 #include "attention_exact.hip"  // expf_glibc
 #include "common.hpp"

@@ -493,20 +493,27 @@ static int launch_q8i(const GemvArgs &A, hipStream_t s) {
 }
 template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
-    if (FMT == F_MXFP4 && A.K % 4 == 0 && A.K <= 16384) {
-        // one workgroup per 64-row tile: the serial row sums are spread over
-        // a summing wave and four term-producing waves
+    if constexpr (FMT == F_MXFP4) {
         ProfScope ps("gemv_mxfp4", s);
-        rh_launch(gemv_mxfp4_serial_kernel, dim3(A.n_tiles), dim3(320), (uint32_t)(A.K * sizeof(float)), s, A);
+        if (A.n_tiles > g.n_cu) {
+            // more tiles than CUs: one wave per tile computes its own terms,
+            // several tiles per SIMD
+            rh_launch(gemv_mxfp4_fused_kernel, dim3(A.n_tiles), dim3(64), 0, s, A);
+        } else {
+            // one workgroup per tile: the serial row sums are spread over a
+            // summing wave and MXP term-producing waves
+            rh_launch(gemv_mxfp4_serial_kernel<MXP>, dim3(A.n_tiles), dim3(64 * (MXP + 1)), 0, s, A);
+        }
+        RH_LAUNCH_OK();
+        return 1;
+    } else {
+        static_assert(FMT == F_Q8_0, "f32-activation formats: Q8_0 and MXFP4");
+        int grid = std::min(A.n_tiles, g.n_cu * 8);
+        ProfScope ps("gemv_f32x", s);
+        rh_launch(gemv_q8_0_f32x_kernel, dim3(grid), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
         RH_LAUNCH_OK();
         return 1;
     }
-    auto kern = gemv_f32x_kernel<FMT>;
-    int grid = std::min(A.n_tiles, g.n_cu * 8);
-    ProfScope ps("gemv_f32x", s);
-    rh_launch(kern, dim3(grid), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
-    RH_LAUNCH_OK();
-    return 1;
 }
 // K-quant tiles: it = units per lane (a wave tile is 64*it quarter-block
 // units of r whole rows; SWIGLU tiles hold r gate + r up rows).  Small

@@ -348,3 +348,50 @@ def test_bench_attention_exact_and_split_k_agree(hip, ctx):
     assert np.all(np.isfinite(ex)) and np.all(np.isfinite(fa))
     err = np.abs(ex - fa).max(axis=1)
     assert np.all(err <= 1e-4 * np.linalg.norm(ex, axis=1) + 1e-7), err.max()
+
+
+def test_mxfp4_gemv_every_scale_byte(hip):
+    """MXFP4 rows over random nibbles with every scale byte 0..255 (the
+    hardware FP4 conversion for normal scales, the table for the subnormal
+    2^-127 and the infinite 2^128), bit-identical to dot_mxfp4_f32_scalar
+    (NaN where the reference's arithmetic makes one)."""
+    rng = np.random.default_rng(39)
+    rows, cols = 256, 2048
+    raw = rng.integers(0, 256, (rows, cols // 32, 17), dtype=np.uint8)
+    raw[:, :, 16] = (np.arange(rows * (cols // 32)).reshape(rows, -1) * 7) % 256
+    w = raw.reshape(-1)
+    x = (rng.standard_normal(cols) * 1e-3).astype(np.float32)
+    out = np.zeros(rows, np.float32)
+    assert hip.matvec_into(39, w, x, rows, cols, out)
+    ref = O.matvec(39, w, x, rows, cols, threads=8)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    # rows whose scales avoid 0 and 255 carry finite sums
+    assert (~nan).sum() > 0
+
+
+@pytest.mark.parametrize("rows,cols,scales", [
+    (19237, 2880, "normal"),   # > 256 tiles: the one-wave-per-tile kernel; ragged last tile
+    (19200, 352, "every"),     # 11 blocks: one partial 16-block chunk; every scale byte
+])
+def test_mxfp4_gemv_many_tiles(hip, rows, cols, scales):
+    """Launches with more 64-row tiles than CUs take the kernel that stages
+    16-block chunks through LDS with coalesced loads; its sums stay
+    bit-identical to dot_mxfp4_f32_scalar."""
+    rng = np.random.default_rng(rows + cols)
+    nb = cols // 32
+    raw = rng.integers(0, 256, (rows, nb, 17), dtype=np.uint8)
+    if scales == "every":
+        raw[:, :, 16] = (np.arange(rows * nb).reshape(rows, nb) * 7) % 256
+    else:
+        raw[:, :, 16] = rng.integers(100, 140, (rows, nb))
+    w = raw.reshape(-1)
+    x = rng.standard_normal(cols).astype(np.float32)
+    out = np.zeros(rows, np.float32)
+    assert hip.matvec_into(39, w, x, rows, cols, out)
+    ref = O.matvec(39, w, x, rows, cols, threads=8)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert (~nan).sum() > rows // 2
