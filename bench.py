@@ -10,9 +10,13 @@ reference's repeat penalty 1.1.  A "step" is one decode token: embedding ->
 32 layers -> logits -> on-device greedy pick, replayed as one HIP graph.
 
 Also measured in the same run:
-- roofline: the fused gate/up Q4_K GEMV (SwiGLU epilogue), the largest
-  per-launch weight stream, timed per launch with HIP events on the library
-  stream during a profiling pass of the same decode;
+- roofline: the dominant kernel family, exact decode attention (the scores,
+  coefficient and recurrence launches of one layer): the K and V bytes it
+  must read at the profiled positions over the sum of the three launches'
+  average durations, timed with HIP events on the library stream during a
+  profiling pass of the same decode;
+- roofline_gemv: the fused gate/up Q4_K GEMV (SwiGLU epilogue), the largest
+  per-launch weight stream, timed the same way;
 - cpu_baseline: the CPU oracle (C restatement of the reference's AVX2 path,
   oracle/) continuing the same decode from the GPU's KV cache on the host's
   cores, for a bounded sample of tokens;
@@ -160,9 +164,35 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(model, res, storage, args, log)
 
+    # exact attention of one layer: K and V rows of every attended position
+    # (the profiling pass decodes positions p0 .. p0 + profile_tokens - 1,
+    # each attending p + 1 positions) plus q and the outputs
     roofline = None
-    if cnt:
+    attn_parts = {f: prof[f][0] / prof[f][1] for f in ATTN_FAMS if f in prof and prof[f][1]}
+    if len(attn_parts) == len(ATTN_FAMS):
+        p0 = args.ctx - 1 + args.warmup + args.steps
+        n_att = p0 + 1 + (args.profile_tokens - 1) / 2
+        hd = cfg["head_dim"]
+        attn_bytes = int(n_att * cfg["n_kv_heads"] * 2 * hd * 4 + cfg["n_heads"] * 2 * hd * 4)
+        attn_ms = sum(attn_parts.values())
+        attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {
+            "kernel": "exact attention per layer: attn_exact_scores + attn_exact_coef + attn_exact_chain "
+                      "(%d q / %d kv heads, head_dim %d, %.1f positions)" % (cfg["n_heads"], cfg["n_kv_heads"], hd, n_att),
+            "bound": "hbm",
+            "achieved": round(attn_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": recorded_traffic(args, ATTN_TRAFFIC_FILE),
+            "bytes_per_launch": attn_bytes,
+            "avg_launch_us": round(attn_ms * 1e3, 3),
+            "avg_launch_us_parts": {f: round(v * 1e3, 3) for f, v in attn_parts.items()},
+            "launches": prof[ATTN_FAMS[2]][1],
+        }
+    roofline_gemv = None
+    if cnt:
+        roofline_gemv = {
             "kernel": "gemv_kquant_swiglu (Q4_K gate+up %dx%d x2, SwiGLU epilogue)" % (hid, dim),
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -196,6 +226,7 @@ def main():
             "repeat_penalty": args.penalty, "seed": args.seed,
         },
         "roofline": roofline,
+        "roofline_gemv": roofline_gemv,
         "token_bytes": token_bytes,
         "effective_GBps": round(eff_gbs, 1),
         "effective_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
@@ -315,6 +346,8 @@ def measure_prefill(hip, res, toks, cfg, log):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_kquant_swiglu_llama3-8b-q4km_traffic.json")
+ATTN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_exact_llama3-8b-q4km_ctx4096_traffic.json")
+ATTN_FAMS = ("attn_exact_scores", "attn_exact_coef", "attn_exact_chain")
 
 
 # (block elements, block bytes) per GGML type, and the kernel family that
@@ -392,13 +425,13 @@ def kernel_sweep(args):
           flush=True)
 
 
-def recorded_traffic(args):
-    """HBM bytes per launch of the roofline kernel, from the two rocprofv3
+def recorded_traffic(args, path=TRAFFIC_FILE):
+    """HBM bytes per launch of a roofline kernel, from the two rocprofv3
     --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded for this workload, each
     scaled by the same counter's reading on a copy kernel of known size."""
-    if args.config != "llama3-8b-q4km" or not os.path.exists(TRAFFIC_FILE):
+    if args.config != "llama3-8b-q4km" or args.ctx != 4096 or not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         rec = json.load(f)
     return rec.get("traffic_bytes_per_launch")
 
