@@ -257,11 +257,19 @@ def bench_gptoss(args):
     cfg = model["config"]
     log(f"model {args.config} generated in {time.time() - t0:.1f}s")
     storage = args.ctx + args.warmup + args.steps + args.profile_tokens + 8
-    res = hip.ResidentGptOss(model, storage_len=storage)
+    res = hip.ResidentGptOss(model, max(storage, args.prefill_tokens + 1))
+    prefill = None
+    if args.prefill_tokens:
+        # BASELINE configs[4]'s prompt: batched prefill of prefill_tokens ids
+        prompt_pf = synth.token_ids(args.seed + 2, args.prefill_tokens, cfg["vocab"]).astype(np.int32)
+        prefill = measure_prefill_gptoss(hip, res, prompt_pf, log)
     kd = cfg["n_kv_heads"] * cfg["head_dim"]
+    # the cache is the reference's ring of min(window, max_len) slots: random
+    # rows in every slot stand for the last positions before ctx - 1
+    n_fill = min(args.ctx - 1, res.slots)
     for layer in range(cfg["n_layers"]):
         for which in (0, 1):
-            res.kv_write(layer, which, 0, synth.normal_f32(args.seed + 7 * layer + which, args.ctx - 1, kd, 1.0))
+            res.kv_write(layer, which, 0, synth.normal_f32(args.seed + 7 * layer + which, n_fill, kd, 1.0))
     prompt = synth.token_ids(args.seed + 1, 4, cfg["vocab"]).astype(np.int32)
     res.generate(prompt[-1:], args.warmup, penalty=args.penalty, start_pos=args.ctx - 1, want_logits=False)
     ms = res.time_decode(args.steps, penalty=args.penalty)
@@ -296,8 +304,32 @@ def bench_gptoss(args):
         "effective_frac": round(eff / HBM_PEAK_GBS, 4),
         "profile_ms_per_token": {kk: round(v[0] / args.profile_tokens, 4) for kk, v in fam},
         "cpu_baseline": None,
+        "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
+
+
+def measure_prefill_gptoss(hip, res, toks, log):
+    """Batched gpt-oss prefill (rusty_hip_resident_prefill in MoE mode) of
+    `toks` from position 0: whole-call wall time on the host clock around the
+    synchronous call, then a profiling pass for per-launch times.  The
+    reference prefills gpt-oss one decode step per token."""
+    n = int(toks.size)
+    if not res.prefill(toks, 0):  # warm-up (allocates the chunk buffers)
+        log("prefill: model not batchable")
+        return None
+    t0 = time.perf_counter()
+    res.prefill(toks, 0)
+    sec = time.perf_counter() - t0
+    hip.profile_enable(True)
+    res.prefill(toks, 0)
+    prof = hip.profile_results()
+    hip.profile_enable(False)
+    log(f"prefill {n} tokens: {sec * 1e3:.1f} ms -> {n / sec:.1f} tok/s")
+    fam = sorted(((k, v) for k, v in prof.items() if v[1] > 0), key=lambda kv: -kv[1][0])
+    log("prefill profile: " + ", ".join(f"{k}={v[0]:.2f}ms/{v[1]}" for k, v in fam[:12]))
+    return {"tokens": n, "tok_s": round(n / sec, 1), "ms": round(sec * 1e3, 2),
+            "profile_ms": {k: round(v[0], 3) for k, v in fam}}
 
 
 def measure_prefill(hip, res, toks, cfg, log):

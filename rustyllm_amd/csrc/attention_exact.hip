@@ -118,6 +118,13 @@ struct AttnExactArgs {
     // dot_bf16_f32's single-accumulator order, V from the f32 tiled copy
     // (widened bf16 values) or, without it, widened from the rows
     int32_t kv_bf16;
+    // Ring layers in a multi-token launch (lin = 1): k and v are a linear
+    // buffer whose row r holds position lin_pos0 + r (the ring's positions
+    // before the chunk, then the chunk's own), and every token reads the ring
+    // as it stood at its own step: slot s (of slot_count) holds the latest
+    // position <= the token's that is congruent to s.  tok_view sets lin_b
+    // and lin_c for the token; kv_row maps a slot to its buffer row.
+    int32_t lin, lin_pos0, lin_b, lin_c;
 };
 
 // Element e of a head vector x after RoPE with the row's cos/sin, exactly as
@@ -156,7 +163,19 @@ __device__ __forceinline__ AttnExactArgs tok_view(const AttnExactArgs &A0) {
     A.st = nullptr;
     A.end_t = A0.pos0 + z;
     A.start_t = A0.window > 0 ? max(0, A.end_t + 1 - A0.window) : A0.start_t;
+    if (A0.lin) {
+        A.lin_c = A.end_t % A0.slot_count;
+        A.lin_b = A.end_t - A0.lin_pos0 - A.lin_c;
+    }
     return A;
+}
+
+// The K/V row that holds ring slot `slot` (the slot itself unless lin).  A
+// slot past the token's own position (read only by the scores kernels'
+// speculative full-tile loads, whose rows are never used) has no row yet:
+// it maps to row 0, so every load stays inside the buffer.
+__device__ __forceinline__ int kv_row(const AttnExactArgs &A, int slot) {
+    return A.lin ? max(0, slot + A.lin_b - (slot > A.lin_c ? A.slot_count : 0)) : slot;
 }
 
 __device__ __forceinline__ void exact_range(const AttnExactArgs &A, int &s, int &e) {
@@ -212,7 +231,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
         for (int i = tid; i < nt * hd; i += 256) {
             int tt = i / hd, c = i - tt * hd;
             int slot = (s0 + t_base + tt) % A.slot_count;
-            s_k[tt * ldk + c] = bf16_to_f32(kh16[(size_t)slot * A.key_stride + c]);
+            s_k[tt * ldk + c] = bf16_to_f32(kh16[(size_t)kv_row(A, slot) * A.key_stride + c]);
         }
     } else if (A.kvec && (256 % h4) == 0 && A.slot_count >= EX_TILE) {
         // thread -> (row r0 + k*rstep, float4 column c): one division, and the
@@ -223,14 +242,14 @@ __global__ __launch_bounds__(256) void attn_exact_scores_kernel(AttnExactArgs A0
         for (int tt = r0; tt < nt; tt += rstep) {
             int slot = base + tt;
             if (slot >= A.slot_count) slot -= A.slot_count;
-            *(float4 *)(s_k + tt * ldk + c) = *(const float4 *)(kh + (size_t)slot * A.key_stride + c);
+            *(float4 *)(s_k + tt * ldk + c) = *(const float4 *)(kh + (size_t)kv_row(A, slot) * A.key_stride + c);
         }
     } else {
 #pragma unroll 4
         for (int i = tid; i < nt * hd; i += 256) {
             int tt = i / hd, c = i - tt * hd;
             int slot = (s0 + t_base + tt) % A.slot_count;
-            s_k[tt * ldk + c] = kh[(size_t)slot * A.key_stride + c];
+            s_k[tt * ldk + c] = kh[(size_t)kv_row(A, slot) * A.key_stride + c];
         }
     }
     __syncthreads();
@@ -350,8 +369,8 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         for (int i = 0; i < NKR; i++) {
             int slot = base + min(r0 + i * RSTEP, rows - 1);
             if (slot >= A.slot_count) slot -= A.slot_count;
-            kreg[i] = A.kv_bf16 ? bf16x4_load(kh16 + (size_t)slot * A.key_stride + 4 * c4)
-                                : *(const float4 *)(kh + (size_t)slot * A.key_stride + 4 * c4);
+            const size_t kr = (size_t)kv_row(A, slot) * A.key_stride + 4 * c4;
+            kreg[i] = A.kv_bf16 ? bf16x4_load(kh16 + kr) : *(const float4 *)(kh + kr);
         }
     };
     // Without a window the range starts at start_t, which the host passes as
@@ -399,7 +418,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
         // k rotated into the tile (over the cache row staged above) and both
         // cache rows of the current position stored, as rope_kv_kernel does
         __syncthreads();
-        const int slot = RA.ring ? e0 % RA.slots : e0;
+        const int slot = RA.ring ? e0 % RA.slots : e0 - RA.slot_off;
         const int kvd = RA.n_kv * HD, vvd = RA.n_kv * RA.vd;
         for (int e = tid; e < HD; e += 256) {
             float kr = rope_elem(RA.k + (size_t)h * HD, e, half, RA.neox != 0, ct, stb);
@@ -956,7 +975,7 @@ __device__ void c4_consumer_vg(const AttnExactArgs &A, Chain4Lds &L, int s0, int
                 const uint32_t mw = t < 32 ? mw0 : mw1;
                 const float e = et[t];
                 const int slot = (s0 + i * EX_TILE + t) % A.slot_count;
-                const float v = bf16_to_f32(vcol[(size_t)slot * A.value_stride]);
+                const float v = bf16_to_f32(vcol[(size_t)kv_row(A, slot) * A.value_stride]);
                 const float on = fmaf(e, v, o);
                 const float ox = X4 ? fmaf(v, 1.0f, o * e) : fmaf(o, e, v);
                 o = ((mw >> (t & 31)) & 1u) ? ox : on;
@@ -1087,8 +1106,8 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 const int slot = (s0 + 16 * k + min(j, n - 1)) % A.slot_count;
-                v[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[(size_t)slot * A.value_stride + dim])
-                                 : A.v[(size_t)slot * A.value_stride + dim];
+                const size_t vr = (size_t)kv_row(A, slot) * A.value_stride + dim;
+                v[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[vr]) : A.v[vr];
             }
         }
         if (n == 16) {
@@ -1150,9 +1169,9 @@ __global__ __launch_bounds__(64) void attn_exact_chain_kernel(AttnExactArgs A0) 
         for (int j = 0; j < 32; j++) {
             int t = t0 + j < ctx ? t0 + j : ctx - 1;
             int slot = (s0 + t) % A.slot_count;
-            vb[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[(size_t)h * A.vd + (dim_ok ? dim : 0) +
-                                                                     (size_t)slot * A.value_stride])
-                              : vbase[(size_t)slot * A.value_stride];
+            const size_t vr = (size_t)kv_row(A, slot) * A.value_stride;
+            vb[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[(size_t)h * A.vd + (dim_ok ? dim : 0) + vr])
+                              : vbase[vr];
             eb[j] = ef[t];
         }
         const uint32_t bits = mk[t0 >> 5];

@@ -23,7 +23,7 @@ __device__ __forceinline__ int32_t total_key(float v) {
 // index first among equal ones; that is each logit's rank here.  Then
 // softmax_selected_into (:6639-6656): m = max, e_r = exp(v_r - m), sum in
 // slot order, e_r /= sum.  One wave; n <= 64 experts, k <= 8.
-__global__ __launch_bounds__(64) void moe_topk_kernel(const float *logits, int n, int k, int32_t *sel, float *prob) {
+__device__ __forceinline__ void moe_topk_row(const float *logits, int n, int k, int32_t *sel, float *prob) {
     __shared__ float s_v[8];
     __shared__ int32_t s_i[8];
     const int lane = threadIdx.x;
@@ -52,6 +52,10 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float *logits, int n
             prob[r] = sum > 0.0f ? e[r] / sum : e[r];
         }
     }
+}
+
+__global__ __launch_bounds__(64) void moe_topk_kernel(const float *logits, int n, int k, int32_t *sel, float *prob) {
+    moe_topk_row(logits, n, k, sel, prob);
 }
 
 // swiglu_gpt_oss (src/model.rs:6596-6600): min(g, 7) (a NaN g gives 7),

@@ -37,8 +37,9 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *x, int n
 // bit).  x is first staged in LDS by all threads at once (dynamic LDS of n
 // floats).  Each block then writes its 256 outputs and, when xq.qs != null
 // and n % 256 == 0, their Q8_K quantization.
-__global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *x, const float *w, float eps, int n,
-                                                          float *xn, XQ xq) {
+// One row's RMSNorm (element blockIdx.x * 256 + threadIdx.x) and its Q8_K
+// block; every workgroup of the row computes the row's sum.
+__device__ __forceinline__ void rmsnorm_row(const float *x, const float *w, float eps, int n, float *xn, XQ xq) {
     extern __shared__ float s_x[];
     __shared__ float red[40];
     {
@@ -65,6 +66,11 @@ __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *x, const 
     if (xq.qs) q8k_block_store(o, blockIdx.x, e, xq, red);
 }
 
+__global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *x, const float *w, float eps, int n,
+                                                          float *xn, XQ xq) {
+    rmsnorm_row(x, w, eps, n, xn, xq);
+}
+
 // RoPE + KV store (apply_rope_qk / apply_rope_qk_neox, src/model.rs:
 // 5562-5647; KVCache::write_k/v :1478-1502).  cos/sin come from a table the
 // host built with libm sinf/cosf of (float)pos * inv_freq[i], exactly the
@@ -87,6 +93,7 @@ struct RopeArgs {
     int32_t vt_stride;
     int32_t kv_bf16;      // 1: kcache / vcache hold bf16 (uint16), narrowed as KVCache::write_k/v do;
                           // the f32 V copy then holds the widened bf16 values
+    int32_t slot_off;     // with ring = 0: the row is pos - slot_off (a linear buffer starting there)
 };
 
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
@@ -97,7 +104,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeArgs A) {
     A.v += (int64_t)z * A.v_tok;
     if (pos < 0 || pos >= A.max_pos) return;
     const int half = A.hd / 2;
-    const int slot = A.ring ? pos % A.slots : pos;
+    const int slot = A.ring ? pos % A.slots : pos - A.slot_off;
     const float *ct = A.cos_t + (size_t)pos * half;
     const float *stb = A.sin_t + (size_t)pos * half;
     const int nq = A.n_heads * half, nk = A.n_kv * half;

@@ -1,0 +1,304 @@
+// prefill_moe.hip — batched prefill for the gpt-oss resident decoder.  The
+// reference prefills gpt-oss token by token (forward_prefill_gpt_oss,
+// src/model.rs:10286, i.e. forward_hidden_gpt_oss_impl without the final
+// norm); here a chunk of T prompt tokens goes through each layer together, so
+// each dense matrix is read once per token group and each expert matrix once
+// per group of the tokens routed to it, while every token's arithmetic is its
+// decode step's: the same dot orders, RMSNorm, RoPE, attention, SwiGLU and
+// slot-ordered combine.  The kernels here add a token dimension to the decode
+// step's kernels; the host side (r_prefill_chunk_moe) strings them together.
+#pragma once
+#include "attention_exact.hip"
+#include "common.hpp"
+#include "gemv.hip"
+#include "moe.hip"
+#include "ops.hip"
+
+namespace rh {
+
+// rms_norm_into of T rows, f32 out: rmsnorm_q8k_kernel's arithmetic per row.
+// grid (ceil(n/256), T), dynamic LDS n floats; n % 4 == 0.
+__global__ __launch_bounds__(256) void rmsnorm_f32_batch_kernel(const float *x, const float *w, float eps, int n,
+                                                                float *xn) {
+    const int64_t t = blockIdx.y;
+    rmsnorm_row(x + t * n, w, eps, n, xn + t * n, XQ{});
+}
+
+// Q8_0 rows for T tokens; each (row, token) is exactly the single-token
+// kernel's value: F32, dot_q8_0_f32_avx2 as gemv_q8_0_f32x_kernel (eight
+// lane accumulators acc_j = fma(d*q, x[32b + 8i + j], acc_j)); otherwise
+// dot_q8_0_q8k_avx2 as gemv_q8_0_int_kernel (acc_j = fma(dx*d, s_j, acc_j),
+// s_j the exact dot of bytes 4j..4j+3); then hsum_avx, bias, store or add.
+// A workgroup is 32 rows (4 waves x 8 rows x 8 lanes, lane j accumulator j)
+// by TG tokens whose activations are staged in LDS: F32 float [TG][K]; Q8_K
+// int8 [TG][K] then the scales float [TG][K/256].  grid (ceil(rows/32),
+// ceil(T/TG)).
+struct Q80BatchArgs {
+    const uint8_t *w;
+    int64_t row_stride;
+    int32_t rows, K, T, epi;
+    const float *x;    // F32: [T][K]
+    const int8_t *qs;  // Q8_K: quants [T][K], scales [K/256][ldx] (token-minor)
+    const float *dx;
+    int32_t ldx;
+    const float *bias;
+    float *y;  // [T][ldy]
+    int32_t ldy;
+};
+
+template <bool F32, int TG>
+__global__ __launch_bounds__(256) void gemv_q8_0_batch_kernel(Q80BatchArgs A) {
+    extern __shared__ __align__(16) uint8_t s_act[];
+    const int K = A.K, nb = K >> 5, tid = threadIdx.x;
+    const int t0 = blockIdx.y * TG, tn = min(TG, A.T - t0);
+    if (F32) {
+        float4 *sx = (float4 *)s_act;
+        const int k4 = K / 4;
+        for (int i = tid; i < TG * k4; i += 256) {
+            const int z = i / k4, c = i - z * k4;
+            sx[i] = z < tn ? ((const float4 *)(A.x + (int64_t)(t0 + z) * K))[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    } else {
+        int4 *sq = (int4 *)s_act;
+        float *sd = (float *)(s_act + (size_t)TG * K);
+        const int k16 = K / 16, nsb = K / 256;
+        for (int i = tid; i < TG * k16; i += 256) {
+            const int z = i / k16, c = i - z * k16;
+            sq[i] = z < tn ? ((const int4 *)(A.qs + (int64_t)(t0 + z) * K))[c] : make_int4(0, 0, 0, 0);
+        }
+        for (int i = tid; i < TG * nsb; i += 256) {
+            const int z = i / nsb, b = i - z * nsb;
+            sd[i] = z < tn ? A.dx[(int64_t)b * A.ldx + t0 + z] : 0.0f;
+        }
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, j = lane & 7;
+    const int row = blockIdx.x * 32 + wave * 8 + (lane >> 3);
+    const bool ok = row < A.rows;
+    const uint8_t *rp = A.w + (int64_t)(ok ? row : 0) * A.row_stride;
+    float acc[TG];
+#pragma unroll
+    for (int z = 0; z < TG; z++) acc[z] = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *blk = rp + b * 34;
+        const float d = ldh(blk);
+        const uint4 q0 = ld16(blk + 2), q1 = ld16(blk + 18);
+        if (F32) {
+            // byte 8i + j of the 32 quants: dword 2i + j/4, bits 8*(j%4)
+            const uint32_t sh = 8u * (uint32_t)(j & 3);
+            const bool hi = j >= 4;
+            const uint32_t dw[4] = {hi ? q0.y : q0.x, hi ? q0.w : q0.z, hi ? q1.y : q1.x, hi ? q1.w : q1.z};
+            float dq[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) dq[i] = d * (float)(int)__builtin_amdgcn_sbfe((int)dw[i], sh, 8u);
+            const float *sx = (const float *)s_act + b * 32 + j;
+#pragma unroll
+            for (int z = 0; z < TG; z++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[z] = fmaf(dq[i], sx[(size_t)z * K + 8 * i], acc[z]);
+        } else {
+            const uint32_t wsel[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            uint32_t wj = wsel[0];
+#pragma unroll
+            for (int i = 1; i < 8; i++) wj = j == i ? wsel[i] : wj;
+            const int32_t *sq = (const int32_t *)s_act;
+            const float *sd = (const float *)(s_act + (size_t)TG * K);
+#pragma unroll
+            for (int z = 0; z < TG; z++) {
+                const float sc = sd[z * (K / 256) + (b >> 3)] * d;
+                const int s = sdot4(wj, sq[(size_t)z * (K / 4) + b * 8 + j], 0);
+                acc[z] = fmaf(sc, (float)s, acc[z]);
+            }
+        }
+    }
+#pragma unroll
+    for (int z = 0; z < TG; z++) {
+        // hsum_avx: t_i = a_i + a_{i+4}; ((t0+t1) + (t2+t3))
+        const float t = acc[z] + __shfl_xor(acc[z], 4, 64);
+        const float u = t + __shfl_xor(t, 1, 64);
+        float v = u + __shfl_xor(u, 2, 64);
+        if (z < tn && ok && j == 0) {
+            if (A.bias) v += A.bias[row];
+            float *y = A.y + (int64_t)(t0 + z) * A.ldy + row;
+            if (A.epi == EPI_ADD)
+                *y += v;
+            else
+                *y = v;
+        }
+    }
+}
+
+// Router selection of T tokens (moe_topk_kernel per token): logits [T][ldl],
+// sel / prob [T][k].  grid T.
+__global__ __launch_bounds__(64) void moe_topk_batch_kernel(const float *logits, int ldl, int n, int k, int32_t *sel,
+                                                            float *prob) {
+    const int64_t t = blockIdx.x;
+    moe_topk_row(logits + t * ldl, n, k, sel + t * k, prob + t * k);
+}
+
+// x[t] += sum over slots r in order of (proj[t k + r] + db[e_r]) * p_r, per
+// token (moe_combine_kernel).  grid (ceil(dim/256), T).
+__global__ __launch_bounds__(256) void moe_combine_batch_kernel(const float *proj, int dim, int k, const int32_t *sel,
+                                                                const float *prob, const float *db, int db_stride,
+                                                                float *x) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int64_t t = blockIdx.y;
+    if (i >= dim) return;
+    float acc = 0.0f;
+    for (int r = 0; r < k; r++) {
+        const int64_t p = t * k + r;
+        float v = proj[p * dim + i];
+        if (db) v = v + db[(size_t)sel[p] * db_stride + i];
+        acc += v * prob[p];
+    }
+    x[t * dim + i] += acc;
+}
+
+// MXFP4 expert rows for the (token, slot) pairs routed to each expert, every
+// sum dot_mxfp4_f32_scalar's running sum (as the single-token kernels).  One
+// wave per (64-row tile, expert, matrix): it lists the pairs p = t k + r with
+// sel[p] == expert, then for groups of MXE_G pairs streams the expert's rows
+// once per group in 16-block chunks (coalesced direct loads into LDS, then
+// each lane's row into registers, as gemv_mxfp4_fused_kernel) and runs the
+// group's MXE_G sums per lane side by side; x comes through scalar loads.
+// y[mat] row p gets the sum of pair p.  grid (ceil(rows/64), n_exp, n_mats).
+#define MXE_G 4
+#define MXE_MAX_PAIRS 2048  // a token routes to an expert at most once: pairs per expert <= T
+struct MxExpArgs {
+    const uint8_t *w[2];  // expert tensors: expert e's row r at w + e*exp_stride + r*row_stride
+    float *y[2];          // [T*k][ldy]
+    int64_t row_stride, exp_stride;
+    int32_t rows, K, n_pairs, k;
+    const float *x;  // the activation of pair p: x + (x_pair ? p : p / k) * ldx
+    int64_t ldx, ldy;
+    int32_t x_pair;
+    const int32_t *sel;  // [n_pairs]
+};
+
+__global__ __launch_bounds__(64) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
+    __shared__ __align__(16) uint4 s_b[64 * 17];
+    __shared__ int32_t s_list[MXE_MAX_PAIRS];
+    const int lane = threadIdx.x, e = blockIdx.y, mat = blockIdx.z;
+    const int K = A.K, nb = K >> 5;
+    // the pairs routed to expert e, in pair order
+    int n = 0;
+    for (int base = 0; base < A.n_pairs; base += 64) {
+        const int p = base + lane;
+        const bool hit = p < A.n_pairs && A.sel[p] == e;
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
+        if (hit) s_list[n + __builtin_popcountll(m & ((1ull << lane) - 1ull))] = p;
+        n += __builtin_popcountll(m);
+    }
+    if (n == 0) return;
+    __syncthreads();
+    const uint8_t *w = A.w[mat] + (int64_t)e * A.exp_stride;
+    const int row0 = blockIdx.x * 64, row = row0 + lane;
+    const bool live = row < A.rows;
+    const int64_t stride = A.row_stride;
+    const int nch = (nb + MXF_C - 1) / MXF_C;
+    auto issue_chunk = [&](int c) {
+        int r = lane / 17, p = lane - 17 * (lane / 17);
+#pragma unroll
+        for (int i = 0; i < 17; i++) {
+            const int rr = min(row0 + r, A.rows - 1);
+            const int64_t off = min((int64_t)(MXF_C * 17 * c + 16 * p), stride - 16);
+            dma16(w + (int64_t)rr * stride + off, &s_b[64 * i]);
+            r += 3;  // 64 = 3 * 17 + 13
+            p += 13;
+            if (p >= 17) {
+                p -= 17;
+                r += 1;
+            }
+        }
+    };
+    for (int g0 = 0; g0 < n; g0 += MXE_G) {
+        const float *xp[MXE_G];
+#pragma unroll
+        for (int i = 0; i < MXE_G; i++) {
+            // uniform, so that x arrives through scalar loads
+            const int p = __builtin_amdgcn_readfirstlane(s_list[min(g0 + i, n - 1)]);
+            xp[i] = A.x + (A.x_pair ? (int64_t)p : (int64_t)(p / A.k)) * A.ldx;
+        }
+        float sum[MXE_G];
+#pragma unroll
+        for (int i = 0; i < MXE_G; i++) sum[i] = 0.0f;
+        issue_chunk(0);
+        for (int c = 0; c < nch; c++) {
+            RH_WAIT_VM(0);
+            uint32_t dw[68];
+            const uint4 *src = &s_b[17 * lane];
+#pragma unroll
+            for (int p = 0; p < 17; p++) {
+                const uint4 v = src[p];
+                dw[4 * p] = v.x;
+                dw[4 * p + 1] = v.y;
+                dw[4 * p + 2] = v.z;
+                dw[4 * p + 3] = v.w;
+            }
+            RH_WAIT_LGKM0();
+            if (c + 1 < nch) issue_chunk(c + 1);  // uniform
+#pragma unroll
+            for (int j = 0; j < MXF_C; j++) {
+                const int b = MXF_C * c + j;
+                if (b < nb) {  // uniform
+                    const int d = (17 * j) >> 2, o = (17 * j) & 3;
+                    uint32_t wd[4];
+#pragma unroll
+                    for (int k4 = 0; k4 < 4; k4++)
+                        wd[k4] = o ? __builtin_amdgcn_alignbyte(dw[d + k4 + 1], dw[d + k4], o) : dw[d + k4];
+                    const uint32_t ex = (dw[d + 4] >> (8 * o)) & 0xFFu;
+                    const float sc = mxfp4_scale(ex);
+                    // the block's 32 weights lut * scale, exact either way
+                    float wv[32];
+                    if (__builtin_amdgcn_ballot_w64(ex == 0u || ex == 255u) == 0) {
+#pragma unroll
+                        for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+                            for (int u = 0; u < 4; u++) {
+                                const fp4x2_f32 pr = fp4x2_scaled(wd[k4], sc, u);
+                                wv[8 * k4 + 2 * u] = pr.x;
+                                wv[8 * k4 + 2 * u + 1] = pr.y;
+                            }
+                    } else {
+#pragma unroll
+                        for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+                            for (int u = 0; u < 4; u++) {
+                                const uint32_t byte = (wd[k4] >> (8 * u)) & 0xFFu;
+                                wv[8 * k4 + 2 * u] = mxfp4_nibble(byte & 0xFu) * sc;
+                                wv[8 * k4 + 2 * u + 1] = mxfp4_nibble(byte >> 4) * sc;
+                            }
+                    }
+#pragma unroll
+                    for (int i = 0; i < MXE_G; i++) {
+                        const const_f32_ptr xb = (const_f32_ptr)xp[i] + b * 32;
+#pragma unroll
+                        for (int q = 0; q < 32; q++) sum[i] += wv[q] * xb[q];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MXE_G; i++)
+            if (g0 + i < n && live) A.y[mat][(int64_t)s_list[g0 + i] * A.ldy + row] = sum[i];
+    }
+}
+
+// K/V rows between a ring cache and the linear buffer of a batched ring
+// prefill: gather lin[r] = ring[(p0 + r) % S] for r < n rows; scatter
+// ring[(p0 + r) % S] = lin[off + r].  grid (ceil(width/256), n, 2 (K, V)).
+__global__ __launch_bounds__(256) void kv_ring_copy_kernel(float *kring, float *vring, float *klin, float *vlin,
+                                                           int kw, int vw, int p0, int S, int off, int to_ring) {
+    const int r = blockIdx.y, which = blockIdx.z, c = blockIdx.x * 256 + threadIdx.x;
+    const int w = which ? vw : kw;
+    if (c >= w) return;
+    float *ring = which ? vring : kring;
+    float *lin = which ? vlin : klin;
+    const int64_t slot = (p0 + r) % S;
+    if (to_ring)
+        ring[slot * w + c] = lin[(int64_t)(off + r) * w + c];
+    else
+        lin[(int64_t)r * w + c] = ring[slot * w + c];
+}
+
+}  // namespace rh

@@ -11,6 +11,7 @@
 #include "moe.hip"
 #include "gemm_mfma.hip"
 #include "prefill.hip"
+#include "prefill_moe.hip"
 #include "gguf.hpp"
 
 #include <hip/hip_ext.h>
@@ -914,6 +915,7 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         if (finish) return 0;
         A.tok_scratch = (int64_t)exact_scratch_floats(A.n_kv, A.kv_mul, A.cap);
     }
+    if (A.lin && (A.n_tok <= 0 || A.vt)) return 0;  // the linear ring view is per token, rows only
     A.scores = scratch;
     A.e = scratch + nh * cap;
     A.tmax = A.e + exact_e_floats(A.n_kv, A.kv_mul, A.cap);
@@ -1848,6 +1850,11 @@ struct Resident {
     float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pattn = nullptr, *ptg = nullptr,
           *ptu = nullptr, *pex = nullptr;
     int8_t *pbq = nullptr;
+    // batched gpt-oss prefill, on top of the above: normalized rows, the
+    // linear K/V buffers of the ring layers, router and expert rows
+    float *pxn = nullptr, *plk = nullptr, *plv = nullptr, *plog = nullptr, *pprob = nullptr, *pgate = nullptr,
+          *pup = nullptr, *pproj = nullptr;
+    int32_t *psel = nullptr;
     std::map<std::pair<int, uint32_t>, hipGraphExec_t> graphs;  // by (mode, penalty bits)
     std::vector<void *> allocs;
     std::vector<std::pair<const void *, DevW>> wown;  // weight copies owned by the decoder
@@ -1898,6 +1905,7 @@ static void r_reset() {
     R.rope_conc = 1.0f;
     R.moebuf = nullptr;
     R.pf_cap = 0;
+    R.pxn = nullptr;  // with the other batched-prefill buffers, freed through allocs
 }
 
 static void r_invalidate_graphs() {
@@ -2425,8 +2433,285 @@ static int r_prefill_chunk(const int32_t *tok, int T, int pos0, hipStream_t s) {
     return 1;
 }
 
+// ---- batched gpt-oss prefill (forward_prefill_gpt_oss token by token,
+// src/model.rs:10286) ----------------------------------------------------------
+// The gpt-oss resident decoder batches when its attention projections and
+// router are Q8_0, its experts MXFP4 and its KV f32.
+static bool r_prefill_moe_batchable() {
+    if (!R.ready || !R.moe || !R.has_embd || R.kv_bf16) return false;
+    const int dim = (int)R.dim, attn_cols = (int)(R.n_heads * R.vd);
+    if (dim % 32 != 0 || attn_cols % 256 != 0 || !cat_of(8, dim) || !cat_of(8, attn_cols)) return false;
+    for (const RLayer &Ly : R.L) {
+        for (int i = 0; i < 4; i++)
+            if (Ly.w[i].fmt != 8) return false;
+        const MoeDev &M = Ly.moe;
+        if (M.router.fmt != 8 || M.gate.fmt != 39 || M.up.fmt != 39 || M.down.fmt != 39) return false;
+        if (M.dim != dim || M.hidden % 32 != 0 || M.k < 1 || M.k > 8 || M.n_exp > 64) return false;
+    }
+    return true;
+}
+
+static int r_prefill_moe_alloc() {
+    if (R.pxn) return 1;
+    if (!r_prefill_alloc()) return 0;
+    const size_t C = R.pf_cap, k = R.top_k, kd = (size_t)R.n_kv * R.hd, vdim = (size_t)R.n_kv * R.vd;
+    const size_t hid = R.L.empty() ? 0 : (size_t)R.L[0].moe.hidden, rows = R.storage + C;
+    if (!r_alloc((void **)&R.plk, rows * kd * 4) || !r_alloc((void **)&R.plv, rows * vdim * 4) ||
+        !r_alloc((void **)&R.plog, C * 64 * 4) || !r_alloc((void **)&R.psel, C * k * 4) ||
+        !r_alloc((void **)&R.pprob, C * k * 4) || !r_alloc((void **)&R.pgate, C * k * hid * 4) ||
+        !r_alloc((void **)&R.pup, C * k * hid * 4) || !r_alloc((void **)&R.pproj, C * k * R.dim * 4) ||
+        !r_alloc((void **)&R.pxn, C * R.dim * 4))
+        return 0;
+    return 1;
+}
+
+// y[t][r] (=, or += with EPI_ADD) Q8_0 row r of W times token t (+ bias):
+// f32 activations x [T][K] or the batched Q8_K in bq, as cat_of picks for K.
+static int q80_batch_enqueue(const DevW &W, int rows, int K, int T, const float *x, const BatchXq *bq,
+                             const float *bias, float *y, int ldy, int epi, const char *name, hipStream_t s) {
+    if (W.fmt != 8 || T <= 0) return 0;
+    Q80BatchArgs A;
+    memset(&A, 0, sizeof(A));
+    A.w = W.p;
+    A.row_stride = W.stride;
+    A.rows = rows;
+    A.K = K;
+    A.T = T;
+    A.epi = epi;
+    A.bias = bias;
+    A.y = y;
+    A.ldy = ldy;
+    const int cat = cat_of(8, K);
+    ProfScope ps(name, s);
+    const dim3 rg((unsigned)((rows + 31) / 32));
+    if (cat == CAT_F32) {
+        if (!x || K % 4 != 0) return 0;
+        A.x = x;
+        if (K <= 4096)
+            rh_launch((gemv_q8_0_batch_kernel<true, 4>), dim3(rg.x, (unsigned)((T + 3) / 4)), dim3(256),
+                      (size_t)4 * K * 4, s, A);
+        else
+            rh_launch((gemv_q8_0_batch_kernel<true, 1>), dim3(rg.x, (unsigned)T), dim3(256), (size_t)K * 4, s, A);
+    } else if (cat == CAT_Q8I) {
+        if (!bq) return 0;
+        A.qs = bq->qs;
+        A.dx = bq->dx;
+        A.ldx = bq->ldx;
+        if (K <= 8192)
+            rh_launch((gemv_q8_0_batch_kernel<false, 8>), dim3(rg.x, (unsigned)((T + 7) / 8)), dim3(256),
+                      (size_t)8 * K + 8 * (K / 256) * 4, s, A);
+        else
+            rh_launch((gemv_q8_0_batch_kernel<false, 2>), dim3(rg.x, (unsigned)((T + 1) / 2)), dim3(256),
+                      (size_t)2 * K + 2 * (K / 256) * 4, s, A);
+    } else {
+        return 0;
+    }
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// RMSNorm of the chunk's rows into R.pxn (f32), plus their Q8_K in b when
+// the width takes the integer Q8_0 path.
+static int r_norm_batch_moe(const float *norm_w, int T, const BatchXq &b, hipStream_t s) {
+    const int dim = (int)R.dim;
+    {
+        ProfScope ps("rmsnorm_batch", s);
+        rh_launch(rmsnorm_f32_batch_kernel, dim3((unsigned)((dim + 255) / 256), (unsigned)T), dim3(256),
+                  (size_t)dim * 4, s, (const float *)R.px, norm_w, R.eps, dim, R.pxn);
+        RH_LAUNCH_OK();
+    }
+    if (cat_of(8, dim) == CAT_Q8I && !quantize_batch_enqueue(R.pxn, dim, T, dim, b, s)) return 0;
+    return 1;
+}
+
+static int kv_ring_copy(RLayer &Ly, int p0, int n, int off, int to_ring, hipStream_t s) {
+    if (n <= 0) return 1;
+    const int kd = (int)(R.n_kv * R.hd), vdim = (int)(R.n_kv * R.vd);
+    ProfScope ps("kv_ring_copy", s);
+    rh_launch(kv_ring_copy_kernel, dim3((unsigned)((std::max(kd, vdim) + 255) / 256), (unsigned)n, 2), dim3(256), 0, s,
+              Ly.k, Ly.v, R.plk, R.plv, kd, vdim, p0, (int)R.storage, off, to_ring);
+    RH_LAUNCH_OK();
+    return 1;
+}
+
+// T (<= pf_cap) tokens of a gpt-oss model at positions pos0.. .  Each layer:
+// RMSNorm, q/k/v (+ bias), RoPE with the K/V rows stored into a linear buffer
+// that also holds the ring's rows of the S - 1 positions before the chunk,
+// exact attention with sinks (window on even layers) where each token reads
+// the ring as it stood at its own step, the chunk's last S rows written back
+// to the ring, wo (+ bias, residual), RMSNorm, router, top-k, the experts'
+// gate/up, SwiGLU, down, and the slot-ordered combine into the residual.
+static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t s) {
+    const int dim = (int)R.dim, qd = (int)(R.n_heads * R.hd), kd = (int)(R.n_kv * R.hd), vdim = (int)(R.n_kv * R.vd);
+    const int attn_cols = (int)(R.n_heads * R.vd), kvm = (int)(R.n_heads / R.n_kv), S = (int)R.storage;
+    if (T <= 0 || (uint32_t)T > R.pf_cap || T > MXE_MAX_PAIRS) return 0;
+    const int P0 = std::max(0, pos0 - S + 1), npre = pos0 - P0;
+    {
+        ProfScope ps("embed_batch", s);
+        rh_launch(embed_batch_kernel, dim3((dim + 255) / 256, (unsigned)T), dim3(256), 0, s, R.embd.p, R.embd.stride,
+                  R.embd.fmt, dim, tok, R.px);
+        RH_LAUNCH_OK();
+    }
+    const BatchXq bd = batch_xq_at(R.pbq, T, dim), ba = batch_xq_at(R.pbq, T, attn_cols);
+    const int cap = (pos0 + T + 63) / 64 * 64;
+    const int last0 = std::max(pos0, pos0 + T - S);  // the chunk's positions the ring keeps
+    for (uint32_t l = 0; l < R.n_layers; l++) {
+        RLayer &Ly = R.L[l];
+        const MoeDev &M = Ly.moe;
+        if (!r_norm_batch_moe(Ly.attn_norm, T, bd, s)) return 0;
+        if (!q80_batch_enqueue(Ly.w[0], qd, dim, T, R.pxn, &bd, Ly.bias[0], R.pq, qd, EPI_STORE, "pf_q80_q", s) ||
+            !q80_batch_enqueue(Ly.w[1], kd, dim, T, R.pxn, &bd, Ly.bias[1], R.pk, kd, EPI_STORE, "pf_q80_k", s) ||
+            !q80_batch_enqueue(Ly.w[2], vdim, dim, T, R.pxn, &bd, Ly.bias[2], R.pv, vdim, EPI_STORE, "pf_q80_v", s))
+            return 0;
+        if (!kv_ring_copy(Ly, P0, npre, 0, 0, s)) return 0;
+        {
+            RopeArgs A;
+            memset(&A, 0, sizeof(A));
+            A.q = R.pq;
+            A.k = R.pk;
+            A.v = R.pv;
+            A.kcache = R.plk;
+            A.vcache = R.plv;
+            A.cos_t = R.cos_t;
+            A.sin_t = R.sin_t;
+            A.pos = pos0;
+            A.max_pos = R.max_pos;
+            A.n_heads = R.n_heads;
+            A.n_kv = R.n_kv;
+            A.hd = R.hd;
+            A.vd = R.vd;
+            A.slots = S;
+            A.ring = 0;
+            A.slot_off = P0;  // row = pos - P0 of the linear buffer
+            A.neox = 0;
+            A.q_tok = qd;
+            A.k_tok = kd;
+            A.v_tok = vdim;
+            const int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+            ProfScope ps("rope_kv_batch", s);
+            rh_launch(rope_kv_kernel, dim3((work + 255) / 256, (unsigned)T), dim3(256), 0, s, A);
+            RH_LAUNCH_OK();
+        }
+        {
+            AttnExactArgs E;
+            memset(&E, 0, sizeof(E));
+            E.q = R.pq;
+            E.k = R.plk;
+            E.v = R.plv;
+            E.sinks = Ly.sinks;
+            E.out = R.pattn;
+            E.n_heads = R.n_heads;
+            E.n_kv = R.n_kv;
+            E.kv_mul = kvm;
+            E.hd = R.hd;
+            E.vd = R.vd;
+            E.key_stride = kd;
+            E.value_stride = vdim;
+            E.slot_count = S;
+            E.start_t = 0;
+            E.window = (l % 2 == 0) ? (int)R.window : 0;  // attention_start_pos, src/model.rs:6788-6792
+            E.cap = cap;
+            E.scale = 1.0f / sqrtf((float)R.hd);
+            E.n_tok = T;
+            E.pos0 = pos0;
+            E.q_tok = qd;
+            E.o_tok = attn_cols;
+            E.lin = 1;
+            E.lin_pos0 = P0;
+            const float *den = nullptr;
+            if (!attn_exact_launch(E, R.pex, XQ{}, s, false, &den)) return 0;
+            ProfScope ps("attn_finish_batch", s);
+            rh_launch(attn_finish_q8k_batch_kernel, dim3(attn_cols / 256, (unsigned)T), dim3(256), 0, s,
+                      (const float *)R.pattn, den, (int64_t)exact_scratch_floats(R.n_kv, kvm, cap), (int)R.vd,
+                      attn_cols, ba.qs, ba.dx, ba.ldx);
+            RH_LAUNCH_OK();
+        }
+        if (!kv_ring_copy(Ly, last0, pos0 + T - last0, last0 - P0, 1, s)) return 0;
+        // x += wo attn + bo (src/model.rs:6837-6840)
+        if (!q80_batch_enqueue(Ly.w[3], dim, attn_cols, T, nullptr, &ba, Ly.bo, R.px, dim, EPI_ADD, "pf_q80_o", s))
+            return 0;
+        // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2) (src/model.rs:6846-6898)
+        if (!r_norm_batch_moe(Ly.ffn_norm, T, bd, s)) return 0;
+        const int k = M.k, hid = M.hidden, np = T * k;
+        if (!q80_batch_enqueue(M.router, M.n_exp, dim, T, R.pxn, &bd, M.router_bias, R.plog, 64, EPI_STORE,
+                               "pf_router", s))
+            return 0;
+        {
+            ProfScope ps("moe_topk_batch", s);
+            rh_launch(moe_topk_batch_kernel, dim3((unsigned)T), dim3(64), 0, s, (const float *)R.plog, 64, M.n_exp, k,
+                      R.psel, R.pprob);
+            RH_LAUNCH_OK();
+        }
+        {
+            MxExpArgs A;
+            memset(&A, 0, sizeof(A));
+            A.w[0] = M.gate.p;
+            A.w[1] = M.up.p;
+            A.y[0] = R.pgate;
+            A.y[1] = R.pup;
+            A.row_stride = M.gate.stride;
+            A.exp_stride = (int64_t)hid * M.gate.stride;
+            A.rows = hid;
+            A.K = dim;
+            A.n_pairs = np;
+            A.k = k;
+            A.x = R.pxn;
+            A.ldx = dim;
+            A.ldy = hid;
+            A.x_pair = 0;
+            A.sel = R.psel;
+            if (M.up.stride != M.gate.stride) return 0;
+            ProfScope ps("pf_mxfp4_gate_up", s);
+            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((hid + 63) / 64), (unsigned)M.n_exp, 2), dim3(64), 0,
+                      s, A);
+            RH_LAUNCH_OK();
+        }
+        {
+            ProfScope ps("moe_swiglu_batch", s);
+            rh_launch(moe_swiglu_kernel, dim3((unsigned)((hid + 255) / 256), (unsigned)np), dim3(256), 0, s, R.pgate,
+                      (const float *)R.pup, hid, np, (const int32_t *)R.psel, M.gb, M.gb_stride, M.ub, M.ub_stride);
+            RH_LAUNCH_OK();
+        }
+        {
+            MxExpArgs A;
+            memset(&A, 0, sizeof(A));
+            A.w[0] = M.down.p;
+            A.y[0] = R.pproj;
+            A.row_stride = M.down.stride;
+            A.exp_stride = (int64_t)dim * M.down.stride;
+            A.rows = dim;
+            A.K = hid;
+            A.n_pairs = np;
+            A.k = k;
+            A.x = R.pgate;
+            A.ldx = hid;
+            A.ldy = dim;
+            A.x_pair = 1;
+            A.sel = R.psel;
+            ProfScope ps("pf_mxfp4_down", s);
+            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((dim + 63) / 64), (unsigned)M.n_exp, 1), dim3(64), 0,
+                      s, A);
+            RH_LAUNCH_OK();
+        }
+        {
+            ProfScope ps("moe_combine_batch", s);
+            rh_launch(moe_combine_batch_kernel, dim3((unsigned)((dim + 255) / 256), (unsigned)T), dim3(256), 0, s,
+                      (const float *)R.pproj, dim, k, (const int32_t *)R.psel, (const float *)R.pprob, M.db,
+                      M.db_stride, R.px);
+            RH_LAUNCH_OK();
+        }
+    }
+    return 1;
+}
+
 // n tokens already in R.tokens[0..n) at positions pos0.. in chunks.
 static int r_prefill_tokens(int n, int pos0) {
+    if (R.moe) {
+        if (!r_prefill_moe_alloc()) return 0;
+        for (int c = 0; c < n; c += (int)R.pf_cap)
+            if (!r_prefill_chunk_moe(R.tokens + c, std::min<int>((int)R.pf_cap, n - c), pos0 + c, g.s)) return 0;
+        return 1;
+    }
     if (!r_prefill_alloc()) return 0;
     for (int c = 0; c < n; c += (int)R.pf_cap)
         if (!r_prefill_chunk(R.tokens + c, std::min<int>((int)R.pf_cap, n - c), pos0 + c, g.s)) return 0;
@@ -2727,7 +3012,8 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
     // prefill_prompt_tokens (src/runtime.rs:3368-3420): every prompt token but
     // the last in batched chunks when the model allows it, then the last one
     // through the decode step for its logits.
-    const bool batched = n_prompt > 2 && r_prefill_enabled() && r_prefill_batchable();
+    const bool batched =
+        n_prompt > 2 && r_prefill_enabled() && (r_prefill_batchable() || r_prefill_moe_batchable());
     if (batched && !r_prefill_tokens((int)n_prompt - 1, (int)start_pos)) return 0;
     // recent window = last <= 64 prompt tokens (recent_token_tail, src/runtime.rs:508-512)
     uint32_t tail = n_prompt > 64 ? n_prompt - 64 : 0;
@@ -2757,8 +3043,9 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
 
 int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos) {
     std::lock_guard<std::mutex> lk(g.mu);
-    if (!tokens || n_tokens == 0 || !r_prefill_batchable()) return 0;
-    if ((uint64_t)start_pos + n_tokens > (uint64_t)R.storage) return 0;
+    if (!tokens || n_tokens == 0 || !(r_prefill_batchable() || r_prefill_moe_batchable())) return 0;
+    // positions: the cache's slots, or the decoder's range for a ring cache
+    if ((uint64_t)start_pos + n_tokens > (uint64_t)(R.moe ? R.max_pos : R.storage)) return 0;
     for (uint32_t i = 0; i < n_tokens; i++)
         if (tokens[i] < 0 || (uint32_t)tokens[i] >= R.vocab) return 0;
     if (!r_ensure_tokens(n_tokens + 1)) return 0;

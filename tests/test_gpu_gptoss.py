@@ -64,3 +64,58 @@ def test_gptoss_greedy_stream(hip, exact, name, max_len, n_prompt, n_gen):
     o_toks, o_logits = orc.generate(prompt, n_gen, penalty=1.1)
     assert list(g_toks) == list(o_toks)
     assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))
+
+
+@pytest.mark.parametrize("name,max_len,pieces", [
+    ("tiny-gptoss", 80, [(0, 30), (30, 61)]),           # ring of 8: every chunk wraps it many times
+    ("tiny-gptoss-w128", 512, [(0, 200), (200, 390)]),  # ring of 128: chunks longer than the ring
+])
+def test_gptoss_prefill_kv_and_next_logits_bit_exact(hip, exact, name, max_len, pieces):
+    """Batched gpt-oss prefill (the reference prefills gpt-oss token by token,
+    forward_prefill_gpt_oss): after prefilling the prompt in pieces, the ring
+    K/V of every layer and the next decode step's logits equal the oracle's
+    sequential forward bit for bit.  Each token attends the ring as it stood
+    at its own step, also across the pieces."""
+    model = synth.make_gptoss(name, seed=13)
+    cfg = model["config"]
+    res = hip.ResidentGptOss(model, max_len)
+    orc = O.OracleGptOss(model, max_len)
+    n = pieces[-1][1]
+    toks = synth.token_ids(21, n + 1, cfg["vocab"])
+    for a, b in pieces:
+        assert res.prefill(toks[a:b], a)
+    for pos in range(n):
+        orc.forward(int(toks[pos]), pos)
+    S = orc.storage
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(res.kv_read(layer, 0, 0, S).view(np.uint32), orc.kc[layer].view(np.uint32)), layer
+        assert np.array_equal(res.kv_read(layer, 1, 0, S).view(np.uint32), orc.vc[layer].view(np.uint32)), layer
+    emb, et = model["token_embd"]
+    x = O.dequant_row(et, emb[int(toks[n]) * O.row_bytes(et, cfg["dim"]):], cfg["dim"])
+    g = res.decode(x, n, 0, True)
+    r = orc.forward(int(toks[n]), n)
+    assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), np.max(np.abs(g - r))
+
+
+def test_gptoss_prefill_after_decoded_positions(hip, exact):
+    """Prefill that continues a ring the decode step started, then decode."""
+    model = synth.make_gptoss("tiny-gptoss", seed=5)
+    cfg = model["config"]
+    res = hip.ResidentGptOss(model, 64)
+    orc = O.OracleGptOss(model, 64)
+    toks = synth.token_ids(8, 40, cfg["vocab"])
+    emb, et = model["token_embd"]
+    dim = cfg["dim"]
+
+    def x_of(t):
+        return O.dequant_row(et, emb[int(t) * O.row_bytes(et, dim):], dim)
+
+    for pos in range(5):
+        res.decode(x_of(toks[pos]), pos, 0, False)
+    assert res.prefill(toks[5:33], 5)
+    for pos in range(33):
+        orc.forward(int(toks[pos]), pos)
+    for pos in range(33, 40):
+        g = res.decode(x_of(toks[pos]), pos, 0, True)
+        r = orc.forward(int(toks[pos]), pos)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), pos
