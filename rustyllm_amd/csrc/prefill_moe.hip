@@ -155,15 +155,18 @@ __global__ __launch_bounds__(256) void moe_combine_batch_kernel(const float *pro
 }
 
 // MXFP4 expert rows for the (token, slot) pairs routed to each expert, every
-// sum dot_mxfp4_f32_scalar's running sum (as the single-token kernels).  One
-// wave per (64-row tile, expert, matrix): it lists the pairs p = t k + r with
-// sel[p] == expert, then for groups of MXE_G pairs streams the expert's rows
-// once per group in 16-block chunks (coalesced direct loads into LDS, then
-// each lane's row into registers, as gemv_mxfp4_fused_kernel) and runs the
-// group's MXE_G sums per lane side by side; x comes through scalar loads.
-// y[mat] row p gets the sum of pair p.  grid (ceil(rows/64), n_exp, n_mats).
-#define MXE_G 4
-#define MXE_MAX_PAIRS 2048  // a token routes to an expert at most once: pairs per expert <= T
+// sum dot_mxfp4_f32_scalar's running sum (as the single-token kernels).  A
+// workgroup of four waves serves one (64-row tile, expert, matrix): it lists
+// the pairs p = t k + r with sel[p] == expert, then in passes of 4 x MXE_G
+// pairs (wave w takes MXE_G of them, one running sum per pair and lane = row)
+// streams the tile's rows once per pass in 16-block chunks: coalesced direct
+// loads into a double-buffered LDS chunk (64 rows x 272 bytes, 17 loads of 1
+// KB shared among the waves), from which every lane reads its row's 17-byte
+// blocks.  A block's 32 weights are decoded once per wave and used for all
+// of its pairs; x comes through scalar loads.  y[mat] row p gets pair p's
+// sum.  grid (ceil(rows/64), n_exp, n_mats).
+#define MXE_G 8
+#define MXE_MAX_PAIRS 1024  // a token routes to an expert at most once: pairs per expert <= T
 struct MxExpArgs {
     const uint8_t *w[2];  // expert tensors: expert e's row r at w + e*exp_stride + r*row_stride
     float *y[2];          // [T*k][ldy]
@@ -175,112 +178,122 @@ struct MxExpArgs {
     const int32_t *sel;  // [n_pairs]
 };
 
-__global__ __launch_bounds__(64) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
-    __shared__ __align__(16) uint4 s_b[64 * 17];
+__global__ __launch_bounds__(256) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
+    __shared__ __align__(16) uint4 s_b[2][64 * 17];
     __shared__ int32_t s_list[MXE_MAX_PAIRS];
-    const int lane = threadIdx.x, e = blockIdx.y, mat = blockIdx.z;
+    __shared__ int32_t s_cnt[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int e = blockIdx.y, mat = blockIdx.z;
     const int K = A.K, nb = K >> 5;
-    // the pairs routed to expert e, in pair order
-    int n = 0;
-    for (int base = 0; base < A.n_pairs; base += 64) {
+    // the pairs routed to expert e, in pair order: each wave counts a quarter
+    // of the pairs, then writes its hits after the earlier waves'
+    const int per = (A.n_pairs + 3) / 4, pa = wave * per, pb = min(A.n_pairs, pa + per);
+    int cnt = 0;
+    for (int base = pa; base < pb; base += 64) {
         const int p = base + lane;
-        const bool hit = p < A.n_pairs && A.sel[p] == e;
-        const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
-        if (hit) s_list[n + __builtin_popcountll(m & ((1ull << lane) - 1ull))] = p;
-        n += __builtin_popcountll(m);
+        cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(p < pb && A.sel[p] == e));
     }
-    if (n == 0) return;
+    if (lane == 0) s_cnt[wave] = cnt;
+    __syncthreads();
+    int off = 0, n = 0;
+    for (int i = 0; i < 4; i++) {
+        off += i < wave ? s_cnt[i] : 0;
+        n += s_cnt[i];
+    }
+    for (int base = pa; base < pb; base += 64) {
+        const int p = base + lane;
+        const bool hit = p < pb && A.sel[p] == e;
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
+        if (hit) s_list[off + __builtin_popcountll(m & ((1ull << lane) - 1ull))] = p;
+        off += __builtin_popcountll(m);
+    }
+    if (n == 0) return;  // uniform over the workgroup
     __syncthreads();
     const uint8_t *w = A.w[mat] + (int64_t)e * A.exp_stride;
     const int row0 = blockIdx.x * 64, row = row0 + lane;
     const bool live = row < A.rows;
     const int64_t stride = A.row_stride;
     const int nch = (nb + MXF_C - 1) / MXF_C;
-    auto issue_chunk = [&](int c) {
-        int r = lane / 17, p = lane - 17 * (lane / 17);
-#pragma unroll
-        for (int i = 0; i < 17; i++) {
+    // piece f = 64 i + lane of a chunk is row f / 17, bytes 16 (f % 17); wave
+    // w issues pieces i = w, w + 4, ...
+    auto issue_chunk = [&](int c, int buf) {
+        for (int i = wave; i < 17; i += 4) {
+            const int f = 64 * i + lane, r = f / 17, p = f - 17 * r;
             const int rr = min(row0 + r, A.rows - 1);
-            const int64_t off = min((int64_t)(MXF_C * 17 * c + 16 * p), stride - 16);
-            dma16(w + (int64_t)rr * stride + off, &s_b[64 * i]);
-            r += 3;  // 64 = 3 * 17 + 13
-            p += 13;
-            if (p >= 17) {
-                p -= 17;
-                r += 1;
-            }
+            const int64_t o = min((int64_t)(MXF_C * 17 * c + 16 * p), stride - 16);
+            dma16(w + (int64_t)rr * stride + o, &s_b[buf][64 * i]);
         }
     };
-    for (int g0 = 0; g0 < n; g0 += MXE_G) {
+    for (int g0 = 0; g0 < n; g0 += 4 * MXE_G) {
+        const int q0 = g0 + wave * MXE_G;  // this wave's first pair of the pass
         const float *xp[MXE_G];
 #pragma unroll
         for (int i = 0; i < MXE_G; i++) {
             // uniform, so that x arrives through scalar loads
-            const int p = __builtin_amdgcn_readfirstlane(s_list[min(g0 + i, n - 1)]);
+            const int p = __builtin_amdgcn_readfirstlane(s_list[min(q0 + i, n - 1)]);
             xp[i] = A.x + (A.x_pair ? (int64_t)p : (int64_t)(p / A.k)) * A.ldx;
         }
         float sum[MXE_G];
 #pragma unroll
         for (int i = 0; i < MXE_G; i++) sum[i] = 0.0f;
-        issue_chunk(0);
+        issue_chunk(0, 0);
         for (int c = 0; c < nch; c++) {
             RH_WAIT_VM(0);
-            uint32_t dw[68];
-            const uint4 *src = &s_b[17 * lane];
+            __syncthreads();  // chunk c landed from every wave; chunk c - 1's reads are done
+            if (c + 1 < nch) issue_chunk(c + 1, (c + 1) & 1);
+            const uint8_t *rowb = (const uint8_t *)&s_b[c & 1][17 * lane];
+            for (int jj = 0; jj < MXF_C / 4; jj++) {
 #pragma unroll
-            for (int p = 0; p < 17; p++) {
-                const uint4 v = src[p];
-                dw[4 * p] = v.x;
-                dw[4 * p + 1] = v.y;
-                dw[4 * p + 2] = v.z;
-                dw[4 * p + 3] = v.w;
-            }
-            RH_WAIT_LGKM0();
-            if (c + 1 < nch) issue_chunk(c + 1);  // uniform
+            for (int o = 0; o < 4; o++) {
+                const int j = 4 * jj + o, b = MXF_C * c + j;
+                if (b >= nb) break;  // uniform
+                // block j's 17 bytes start at byte 17 j = 68 jj + 16 o + o of
+                // the row: five dwords from the aligned 68 jj + 16 o, shifted
+                // by o bytes
+                const uint32_t *wp = (const uint32_t *)(rowb + 68 * jj + 16 * o);
+                uint32_t dw[5];
 #pragma unroll
-            for (int j = 0; j < MXF_C; j++) {
-                const int b = MXF_C * c + j;
-                if (b < nb) {  // uniform
-                    const int d = (17 * j) >> 2, o = (17 * j) & 3;
-                    uint32_t wd[4];
+                for (int i = 0; i < 5; i++) dw[i] = wp[i];
+                uint32_t wd[4];
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++) wd[k4] = o ? __builtin_amdgcn_alignbyte(dw[k4 + 1], dw[k4], o) : dw[k4];
+                const uint32_t e4 = dw[4] >> (8 * o);
+                const uint32_t ex = e4 & 0xFFu;
+                const float sc = mxfp4_scale(ex);
+                // the block's 32 weights lut * scale, exact either way
+                float wv[32];
+                if (__builtin_amdgcn_ballot_w64(ex == 0u || ex == 255u) == 0) {
 #pragma unroll
                     for (int k4 = 0; k4 < 4; k4++)
-                        wd[k4] = o ? __builtin_amdgcn_alignbyte(dw[d + k4 + 1], dw[d + k4], o) : dw[d + k4];
-                    const uint32_t ex = (dw[d + 4] >> (8 * o)) & 0xFFu;
-                    const float sc = mxfp4_scale(ex);
-                    // the block's 32 weights lut * scale, exact either way
-                    float wv[32];
-                    if (__builtin_amdgcn_ballot_w64(ex == 0u || ex == 255u) == 0) {
 #pragma unroll
-                        for (int k4 = 0; k4 < 4; k4++)
+                        for (int u = 0; u < 4; u++) {
+                            const fp4x2_f32 pr = fp4x2_scaled(wd[k4], sc, u);
+                            wv[8 * k4 + 2 * u] = pr.x;
+                            wv[8 * k4 + 2 * u + 1] = pr.y;
+                        }
+                } else {
 #pragma unroll
-                            for (int u = 0; u < 4; u++) {
-                                const fp4x2_f32 pr = fp4x2_scaled(wd[k4], sc, u);
-                                wv[8 * k4 + 2 * u] = pr.x;
-                                wv[8 * k4 + 2 * u + 1] = pr.y;
-                            }
-                    } else {
+                    for (int k4 = 0; k4 < 4; k4++)
 #pragma unroll
-                        for (int k4 = 0; k4 < 4; k4++)
+                        for (int u = 0; u < 4; u++) {
+                            const uint32_t byte = (wd[k4] >> (8 * u)) & 0xFFu;
+                            wv[8 * k4 + 2 * u] = mxfp4_nibble(byte & 0xFu) * sc;
+                            wv[8 * k4 + 2 * u + 1] = mxfp4_nibble(byte >> 4) * sc;
+                        }
+                }
 #pragma unroll
-                            for (int u = 0; u < 4; u++) {
-                                const uint32_t byte = (wd[k4] >> (8 * u)) & 0xFFu;
-                                wv[8 * k4 + 2 * u] = mxfp4_nibble(byte & 0xFu) * sc;
-                                wv[8 * k4 + 2 * u + 1] = mxfp4_nibble(byte >> 4) * sc;
-                            }
-                    }
+                for (int i = 0; i < MXE_G; i++) {
+                    const const_f32_ptr xb = (const_f32_ptr)xp[i] + b * 32;
 #pragma unroll
-                    for (int i = 0; i < MXE_G; i++) {
-                        const const_f32_ptr xb = (const_f32_ptr)xp[i] + b * 32;
-#pragma unroll
-                        for (int q = 0; q < 32; q++) sum[i] += wv[q] * xb[q];
-                    }
+                    for (int q = 0; q < 32; q++) sum[i] += wv[q] * xb[q];
                 }
             }
+            }
         }
+        __syncthreads();  // the last chunk's reads are done before the next pass restages
 #pragma unroll
         for (int i = 0; i < MXE_G; i++)
-            if (g0 + i < n && live) A.y[mat][(int64_t)s_list[g0 + i] * A.ldy + row] = sum[i];
+            if (q0 + i < n && live) A.y[mat][(int64_t)s_list[q0 + i] * A.ldy + row] = sum[i];
     }
 }
 

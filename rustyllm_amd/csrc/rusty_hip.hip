@@ -2662,7 +2662,7 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
             A.sel = R.psel;
             if (M.up.stride != M.gate.stride) return 0;
             ProfScope ps("pf_mxfp4_gate_up", s);
-            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((hid + 63) / 64), (unsigned)M.n_exp, 2), dim3(64), 0,
+            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((hid + 63) / 64), (unsigned)M.n_exp, 2), dim3(256), 0,
                       s, A);
             RH_LAUNCH_OK();
         }
@@ -2689,7 +2689,7 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
             A.x_pair = 1;
             A.sel = R.psel;
             ProfScope ps("pf_mxfp4_down", s);
-            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((dim + 63) / 64), (unsigned)M.n_exp, 1), dim3(64), 0,
+            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((dim + 63) / 64), (unsigned)M.n_exp, 1), dim3(256), 0,
                       s, A);
             RH_LAUNCH_OK();
         }
@@ -2708,8 +2708,9 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
 static int r_prefill_tokens(int n, int pos0) {
     if (R.moe) {
         if (!r_prefill_moe_alloc()) return 0;
-        for (int c = 0; c < n; c += (int)R.pf_cap)
-            if (!r_prefill_chunk_moe(R.tokens + c, std::min<int>((int)R.pf_cap, n - c), pos0 + c, g.s)) return 0;
+        const int cap = std::min<int>((int)R.pf_cap, MXE_MAX_PAIRS);  // the experts' pair lists hold one chunk
+        for (int c = 0; c < n; c += cap)
+            if (!r_prefill_chunk_moe(R.tokens + c, std::min<int>(cap, n - c), pos0 + c, g.s)) return 0;
         return 1;
     }
     if (!r_prefill_alloc()) return 0;
