@@ -867,63 +867,77 @@ __global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
 // Q8_0 rows with f32 activations (dot_q8_0_f32_avx2, src/simd.rs:6671-6692),
 // bit-identical: eight accumulators per row, acc_j = fma(d*q, x, acc_j) over
 // elements 32b + 8i + j (block b outer, group i inner), then hsum_avx
-// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)); eight lanes per row, eight rows per
-// wave.  A workgroup is one wave over tiles of 8 rows; the activation (the
-// matrix's own, else the launch's) is staged in LDS.
+// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)); eight lanes per row (lane j is
+// accumulator j), eight rows per wave.  A workgroup is one wave and one tile
+// of 8 rows; the activation (the matrix's own, else the launch's) is staged
+// in LDS.  The tile's bytes arrive in chunks of 32 blocks (8 rows x 1088
+// bytes = 544 aligned 16-byte pieces, piece f = row * 68 + p) by 9 coalesced
+// direct global->LDS loads into a double-buffered chunk, the next chunk's
+// loads in flight while this one is summed; each lane then reads its
+// block's scale (2 bytes) and its four quants (bytes 8i + j) from LDS.
+#define Q8F_C 32  // blocks per chunk
 __global__ __launch_bounds__(64) void gemv_q8_0_f32x_kernel(GemvArgs A) {
     extern __shared__ float s_x[];  // [K]
+    __shared__ __align__(16) uint4 s_w[2][9 * 64];
     const int K = A.K, nb = K >> 5, lane = threadIdx.x;
-    const float *staged = nullptr;
-    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
-        int mi = 0;
+    const int tile = blockIdx.x;
+    int mi = 0;
 #pragma unroll
-        for (int t = 1; t < GEMV_MAX_MATS; t++)
-            if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        const GemvMat M = mat_sel(A, mi);
-        const float *xs = M.x ? M.x : A.x;
-        if (xs != staged) {
-            __syncthreads();
-            for (int i = 4 * lane; i < K; i += 256) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
-            __syncthreads();
-            staged = xs;
+    for (int t = 1; t < GEMV_MAX_MATS; t++)
+        if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+    const GemvMat M = mat_sel(A, mi);
+    const float *xs = M.x ? M.x : A.x;
+    const uint8_t *w = M.w;
+    const float *bias = M.bias;
+    if (M.sel) {
+        const int64_t e = *M.sel;
+        w += e * M.sel_w;
+        if (bias) bias += e * M.sel_b;
+    }
+    const int row0 = (tile - M.tile_begin) * 8;
+    const int64_t stride = M.row_stride;  // a multiple of 16 that holds nb * 34 bytes
+    const int nch = (nb + Q8F_C - 1) / Q8F_C;
+    auto issue_chunk = [&](int c, int buf) {
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            const int f = min(64 * i + lane, 8 * 68 - 1), r = f / 68, p = f - 68 * r;
+            const int rr = min(row0 + r, M.rows - 1);
+            const int64_t o = min((int64_t)(Q8F_C * 34 * c + 16 * p), stride - 16);
+            dma16(w + (int64_t)rr * stride + o, &s_w[buf][64 * i]);
         }
-        const uint8_t *w = M.w;
-        const float *bias = M.bias;
-        if (M.sel) {
-            const int64_t e = *M.sel;
-            w += e * M.sel_w;
-            if (bias) bias += e * M.sel_b;
-        }
-        const int j = lane & 7;
-        const int row = (tile - M.tile_begin) * 8 + (lane >> 3);
-        const bool ok = row < M.rows;
-        const uint8_t *rp = w + (int64_t)(ok ? row : 0) * M.row_stride;
-        const uint32_t sh = 8u * (uint32_t)(j & 3);
-        const bool hi = j >= 4;
-        float acc = 0.0f;
-        for (int b = 0; b < nb; b++) {
-            const uint8_t *blk = rp + b * 34;
-            const float d = ldh(blk);
-            const uint4 q0 = ld16(blk + 2), q1 = ld16(blk + 18);
-            // byte 8i + j of the 32 quants: dword 2i + j/4, bits 8*(j%4)
-            const uint32_t dw[4] = {hi ? q0.y : q0.x, hi ? q0.w : q0.z, hi ? q1.y : q1.x, hi ? q1.w : q1.z};
-            const float *xb = s_x + b * 32 + j;
+    };
+    issue_chunk(0, 0);
+    for (int i = 4 * lane; i < K; i += 256) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
+    const int j = lane & 7, rr = lane >> 3;
+    const int row = row0 + rr;
+    const bool ok = row < M.rows;
+    float acc = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        RH_WAIT_VM(0);
+        __syncthreads();  // chunk c (and x) in LDS; every read of chunk c - 1 done
+        if (c + 1 < nch) issue_chunk(c + 1, (c + 1) & 1);
+        const uint8_t *rb = (const uint8_t *)&s_w[c & 1][0] + rr * (Q8F_C * 34);
+        const int nbc = min(Q8F_C, nb - Q8F_C * c);
+        for (int lb = 0; lb < nbc; lb++) {
+            const uint8_t *blk = rb + 34 * lb;
+            const float d = h2f(*(const uint16_t *)blk);
+            const float *xb = s_x + (Q8F_C * c + lb) * 32 + j;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float q = (float)(int)__builtin_amdgcn_sbfe((int)dw[i], sh, 8u);
+                const float q = (float)(int)(int8_t)blk[2 + 8 * i + j];
                 acc = fmaf(d * q, xb[8 * i], acc);
             }
         }
-        const float t = acc + __shfl_xor(acc, 4, 64);
-        const float u = t + __shfl_xor(t, 1, 64);
-        float out = u + __shfl_xor(u, 2, 64);
-        if (ok && j == 0) {
-            if (bias) out += bias[row];
-            if (A.epi == EPI_ADD)
-                M.y[row] += out;
-            else
-                M.y[row] = out;
-        }
+    }
+    const float t = acc + __shfl_xor(acc, 4, 64);
+    const float u = t + __shfl_xor(t, 1, 64);
+    float out = u + __shfl_xor(u, 2, 64);
+    if (ok && j == 0) {
+        if (bias) out += bias[row];
+        if (A.epi == EPI_ADD)
+            M.y[row] += out;
+        else
+            M.y[row] = out;
     }
 }
 

@@ -509,9 +509,9 @@ static int launch_f32x(const GemvArgs &A, hipStream_t s) {
         return 1;
     } else {
         static_assert(FMT == F_Q8_0, "f32-activation formats: Q8_0 and MXFP4");
-        int grid = std::min(A.n_tiles, g.n_cu * 8);
+        // one workgroup per 8-row tile
         ProfScope ps("gemv_f32x", s);
-        rh_launch(gemv_q8_0_f32x_kernel, dim3(grid), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
+        rh_launch(gemv_q8_0_f32x_kernel, dim3(A.n_tiles), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
         RH_LAUNCH_OK();
         return 1;
     }
