@@ -50,9 +50,12 @@ struct GemvMat {
 // the standalone kernel (and its launch) that would otherwise produce it:
 //   KQ_ACT_NORM: RMSNorm of act_x with act_w (rms_norm_into), then Q8_K;
 //   KQ_ACT_DEN:  attention normalisation act_x[e] * (1/act_den[e/act_group])
-//                where the denominator is positive, then Q8_K.
-enum KqAct : int { KQ_ACT_XQ = 0, KQ_ACT_NORM = 1, KQ_ACT_DEN = 2 };
-#define KQ_ACT_KMAX 4096  // widest activation a prologue builds: one 16-element chunk per thread
+//                where the denominator is positive, then Q8_K;
+//   KQ_ACT_QUANT: Q8_K of act_x as is (quantize_row_q8k), up to four chunks
+//                per thread.
+enum KqAct : int { KQ_ACT_XQ = 0, KQ_ACT_NORM = 1, KQ_ACT_DEN = 2, KQ_ACT_QUANT = 3 };
+#define KQ_ACT_KMAX 4096        // widest activation NORM / DEN build: one 16-element chunk per thread
+#define KQ_ACT_QUANT_KMAX 16384  // QUANT: four chunks per thread
 
 struct GemvArgs {
     GemvMat m[GEMV_MAX_MATS];
@@ -598,6 +601,7 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
     float dxr;
     float4 xf[ACT == KQ_ACT_NORM ? 8 : 1];  // this thread's 16-element chunk of x, then of w (NORM)
     float4 xd[ACT == KQ_ACT_DEN ? 4 : 1];  // this thread's 16-element chunk (DEN)
+    float4 xq4[ACT == KQ_ACT_QUANT ? 16 : 1];  // chunks tid + 256 r, r < 4 (QUANT)
     float dd = 0.0f;
     if (ACT == KQ_ACT_XQ) {
         const int4 *src = (const int4 *)A.xq.qs;
@@ -614,11 +618,18 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         for (int i = 0; i < 4; i++) xf[i] = ((const float4 *)A.act_x)[4 * c + i];
 #pragma unroll
         for (int i = 0; i < 4; i++) xf[4 + i] = ((const float4 *)A.act_w)[4 * c + i];
-    } else {
+    } else if (ACT == KQ_ACT_DEN) {
         const int c = min(tid, n16 - 1);
 #pragma unroll
         for (int i = 0; i < 4; i++) xd[i] = ((const float4 *)A.act_x)[4 * c + i];
         dd = A.act_den[(16 * c) / A.act_group];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int c = min(tid + 256 * r, n16 - 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) xq4[4 * r + i] = ((const float4 *)A.act_x)[4 * c + i];
+        }
     }
 
     // the activation's loads are issued before the tile geometry's arithmetic
@@ -685,6 +696,20 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         }
         __syncthreads();  // every read of the f32 staging precedes the quant stores over it
         kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
+    } else if (ACT == KQ_ACT_QUANT) {
+        // the standalone quantize_q8k_kernel's values, chunk by chunk
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[4 * i + 0] = xq4[4 * r + i].x;
+                v[4 * i + 1] = xq4[4 * r + i].y;
+                v[4 * i + 2] = xq4[4 * r + i].z;
+                v[4 * i + 3] = xq4[4 * r + i].w;
+            }
+            kq_quant_chunk(v, tid + 256 * r, tid + 256 * r < n16, s_xq, s_dx, s_bs, s_s16);
+        }
     } else {
         // attention normalisation (out *= 1/den where den > 0, as the
         // reference's final scale) and Q8_K

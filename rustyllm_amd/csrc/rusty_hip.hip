@@ -481,6 +481,7 @@ template <int FMT, bool SW, int U>
 static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
     if (act == KQ_ACT_NORM) return launch_kq_act<FMT, SW, U, KQ_ACT_NORM>(A, s);
     if (act == KQ_ACT_DEN) return launch_kq_act<FMT, SW, U, KQ_ACT_DEN>(A, s);
+    if (act == KQ_ACT_QUANT) return launch_kq_act<FMT, SW, U, KQ_ACT_QUANT>(A, s);
     return launch_kq_act<FMT, SW, U, KQ_ACT_XQ>(A, s);
 }
 template <int IT, int R>
@@ -575,7 +576,9 @@ static int kq_prologue_act(const ActSpec &a, int K) {
         off = (e && atoi(e) == 0) ? 1 : 0;
     }
     if (a.mode == ACT_XQ) return KQ_ACT_XQ;
-    if (off || K % 256 != 0 || K > KQ_ACT_KMAX) return -1;
+    if (off || K % 256 != 0) return -1;
+    if (a.mode == ACT_QUANT && K <= KQ_ACT_QUANT_KMAX && ((uintptr_t)a.x & 15) == 0) return KQ_ACT_QUANT;
+    if (K > KQ_ACT_KMAX) return -1;
     if (a.mode == ACT_RMSNORM && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.norm_w & 15) == 0) return KQ_ACT_NORM;
     if (a.mode == ACT_DEN && a.group > 0 && a.group % 16 == 0 && ((uintptr_t)a.x & 15) == 0) return KQ_ACT_DEN;
     return -1;
