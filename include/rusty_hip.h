@@ -194,10 +194,15 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
  * chunks (512 tokens; RUSTY_HIP_PREFILL_CHUNK, 64..2048) that run each weight matrix once per chunk on
  * the matrix cores.  Needs the device embedding (set_embedding) and a model
  * that standard_prefill_batchable (:9869-9887) accepts: every projection
- * Q4_K or Q6_K, widths multiples of 256, no MoE; returns 0 otherwise (the
- * caller then decodes token by token).  start_pos + n_tokens <= storage_len.
- * Every cached K/V value is bit-identical to decoding the tokens in turn
- * with the reference-order attention. */
+ * Q4_K or Q6_K, widths multiples of 256; start_pos + n_tokens <= storage_len.
+ * A gpt-oss decoder (resident_configure_moe) with Q8_0 attention and router,
+ * MXFP4 experts and f32 KV is batched too (the reference prefills gpt-oss one
+ * forward_prefill_gpt_oss step per token, src/model.rs:10286): each token's
+ * arithmetic is its decode step's, every ring layer's token reads the ring as
+ * it stood at its own step, and start_pos + n_tokens <= max_len.  Returns 0
+ * for other models (the caller then decodes token by token).  Every cached
+ * K/V value is bit-identical to decoding the tokens in turn with the
+ * reference-order attention. */
 int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos);
 /* Copies slots [slot0, slot0+n_slots) of layer l's K (which = 0) or V
  * (which = 1) cache to / from host memory. */
