@@ -1125,8 +1125,11 @@ struct MoeDev {
     int gb_stride, ub_stride, db_stride;      // floats between expert bias rows
     int n_exp, k, dim, hidden;
 };
-static int moe_ffn_enqueue(const MoeDev &M, const float *xn, float *moe_out, float *x_add, float *buf, hipStream_t s,
-                           int32_t **sel_out = nullptr, float **prob_out = nullptr) {
+// xq: the Q8_K form of xn for the router's integer path when dim is a whole
+// number of 256-blocks; an empty XQ quantizes xn here into a buffer this call
+// may allocate (so not under graph capture).
+static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float *moe_out, float *x_add, float *buf,
+                           hipStream_t s, int32_t **sel_out = nullptr, float **prob_out = nullptr) {
     const int k = M.k, dim = M.dim, hidden = M.hidden;
     if (k < 1 || k > 8 || M.n_exp > 64 || k > M.n_exp) return 0;
     if (cat_of(M.gate.fmt, dim) != CAT_F32 || M.up.fmt != M.gate.fmt || cat_of(M.down.fmt, hidden) != CAT_F32)
@@ -1144,11 +1147,10 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, float *moe_out, flo
         MatSpec mr = {M.router, logits, M.router_bias};
         ActSpec a;
         memset(&a, 0, sizeof(a));
-        a.mode = dim % 256 == 0 ? ACT_QUANT : ACT_XQ;
+        a.mode = (dim % 256 == 0 && !xq.qs) ? ACT_QUANT : ACT_XQ;
         a.x = (float *)xn;
-        a.xq = g.xq;
         if (a.mode == ACT_QUANT && !ensure_xq(&g.xq, &g.xq_cap, dim)) return 0;
-        a.xq = g.xq;
+        a.xq = a.mode == ACT_QUANT ? g.xq : (dim % 256 == 0 ? xq : XQ{});
         if (!gemv_multi_act(&mr, 1, dim, EPI_STORE, a, s)) return 0;
     }
     {
@@ -1600,7 +1602,7 @@ int rusty_hip_moe_ffn(const float *x, uintptr_t dim, const uint8_t *router_w, ui
     RH_CHECK(hipMemcpyAsync(g.x, x, dim * 4, hipMemcpyHostToDevice, g.s));
     int32_t *sel = nullptr;
     float *prob = nullptr;
-    if (!moe_ffn_enqueue(M, g.x, g.y, nullptr, g.moe, g.s, &sel, &prob)) return 0;
+    if (!moe_ffn_enqueue(M, g.x, XQ{}, g.y, nullptr, g.moe, g.s, &sel, &prob)) return 0;
     RH_CHECK(hipMemcpyAsync(out, g.y, dim * 4, hipMemcpyDeviceToHost, g.s));
     if (selected) RH_CHECK(hipMemcpyAsync(selected, sel, top_k * 4, hipMemcpyDeviceToHost, g.s));
     if (probs) RH_CHECK(hipMemcpyAsync(probs, prob, top_k * 4, hipMemcpyDeviceToHost, g.s));
@@ -2199,7 +2201,7 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
         // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2)
         ActSpec use;
         if (!act_materialize(r_act_norm(Ly.ffn_norm), dim, &use, s)) return 0;
-        if (!moe_ffn_enqueue(Ly.moe, R.xn, nullptr, R.x, R.moebuf, s)) return 0;
+        if (!moe_ffn_enqueue(Ly.moe, R.xn, use.xq, nullptr, R.x, R.moebuf, s)) return 0;
     }
     if (mode & (MODE_LOGITS | MODE_GREEDY)) {
         MatSpec mh = {R.out_w, R.logits, nullptr};

@@ -119,3 +119,27 @@ def test_gptoss_prefill_after_decoded_positions(hip, exact):
         g = res.decode(x_of(toks[pos]), pos, 0, True)
         r = orc.forward(int(toks[pos]), pos)
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), pos
+
+
+def test_gptoss_prefill_q8k_widths(hip, exact):
+    """A gpt-oss shape whose d_model is a multiple of 256: the attention
+    projections and the router then take the Q8_K integer path (the decode
+    step's Q8_0 x Q8_K kernels), batched over the chunk's tokens."""
+    cfg = dict(synth.GPTOSS_CONFIGS["tiny-gptoss-w128"], dim=256, n_heads=4, head_dim=64, window=16)
+    model = synth.make_gptoss(cfg, seed=17)
+    res = hip.ResidentGptOss(model, 96)
+    orc = O.OracleGptOss(model, 96)
+    n = 70
+    toks = synth.token_ids(3, n + 1, cfg["vocab"])
+    assert res.prefill(toks[:40], 0) and res.prefill(toks[40:n], 40)
+    for pos in range(n):
+        orc.forward(int(toks[pos]), pos)
+    S = orc.storage
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(res.kv_read(layer, 0, 0, S).view(np.uint32), orc.kc[layer].view(np.uint32)), layer
+        assert np.array_equal(res.kv_read(layer, 1, 0, S).view(np.uint32), orc.vc[layer].view(np.uint32)), layer
+    emb, et = model["token_embd"]
+    x = O.dequant_row(et, emb[int(toks[n]) * O.row_bytes(et, cfg["dim"]):], cfg["dim"])
+    g = res.decode(x, n, 0, True)
+    r = orc.forward(int(toks[n]), n)
+    assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), np.max(np.abs(g - r))
