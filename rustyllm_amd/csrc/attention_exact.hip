@@ -51,15 +51,12 @@ __constant__ uint64_t kExp2fTab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float expf_glibc(float x) {
-    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
-    const uint32_t abstop = (ux >> 20) & 0x7ff;
-    if (abstop >= (0x42b00000u >> 20)) {  // |x| >= 88 or nan
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= (0x7f800000u >> 20)) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7f800000u);
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
+// tab: the 2^(k/N) table (kExp2fTab, or a copy of it in LDS).  Branch-free:
+// the main path runs for every input (its table index is always in range)
+// and the special cases of glibc's |x| >= 88 branch are selected after it:
+// -inf -> 0, NaN -> x + x, +inf and x > 0x1.62e42ep6 -> inf, x <
+// -0x1.9fe368p6 -> 0; the rest of that range takes the main path there too.
+__device__ __forceinline__ float expf_glibc_tab(float x, const uint64_t *tab) {
     const double invln2n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32768.0, c1 = 0x1.ebfce50fac4f3p-3 / 1024.0,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
@@ -68,15 +65,20 @@ __device__ __forceinline__ float expf_glibc(float x) {
     uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     double r = __builtin_fma(invln2n, xd, -kd);
-    uint64_t t = kExp2fTab[ki % 32] + (ki << 47);
+    uint64_t t = tab[ki % 32] + (ki << 47);
     double s = __builtin_bit_cast(double, t);
     double z = __builtin_fma(c0, r, c1);
     double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    float res = (float)y;
+    asm volatile("" : "+v"(res));  // the main path runs on every lane: no branch around it
+    res = x > 0x1.62e42ep6f ? __builtin_bit_cast(float, 0x7f800000u) : res;
+    res = x < -0x1.9fe368p6f ? 0.0f : res;
+    return __builtin_isnan(x) ? x + x : res;
 }
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_tab(x, kExp2fTab); }
 
 struct AttnExactArgs {
     const float *q;      // [n_heads * hd]
@@ -674,10 +676,12 @@ __device__ __forceinline__ void aff_pair16(float e16, uint32_t bits16, int lane,
 // separate 64-byte pieces), so the tile's loads are spread over five producer
 // waves: four each load a quarter of the tile's V (16 positions x 16 dims, one
 // contiguous KB of the tiled transposed copy), the fifth the four heads'
-// coefficients and new-max words.  The ring keeps C4_P tiles in flight; the
-// consumer meets the producers at one barrier per C4_PER tiles.  The
-// denominators run in a second kind of workgroup as the same DPP chain with
-// v = 1.
+// scores.  Four coefficient waves, one per row, turn the scores into the
+// steps' coefficients and new-max words in the ring (the coefficient stage,
+// B, done here one group ahead of the recurrence instead of in a launch of
+// its own).  The ring keeps C4_P tiles in flight; every wave meets at one
+// barrier per C4_PER tiles.  The denominators run in a second kind of
+// workgroup as the same DPP chain with v = 1.
 #define C4_NT 16
 #ifndef C4_P
 #define C4_P 12
@@ -690,6 +694,8 @@ struct Chain4Lds {
     float v[C4_NT][EX_TILE * 16];  // [slot][position][16 dims] (tiled copy: [position/4][16 dims][4])
     float e[C4_NT][4 * EX_TILE];   // [slot][row (head g0 + row)][position] coefficients
     uint32_t m[C4_NT][8];          // [slot][2 * row + word] new-max words
+    float s[C4_NT][4 * EX_TILE];   // [slot][row][position] scores, for the coefficient waves
+    uint64_t exp2tab[32];          // kExp2fTab for the coefficient waves' expf
 };
 
 template <int IPT>
@@ -711,17 +717,23 @@ static_assert(C4_P - C4_PER <= 9, "c4_wait_tiles_after covers at most 9 tiles");
 static_assert(2 * 9 <= 63, "vmcnt is 6 bits (up to two loads per producer per tile)");
 static_assert(C4_NT >= C4_P + C4_PER, "ring too small");
 
-// Producer protocol on the C4 ring: C4_P tiles are issued up front; at group
-// j the producer waits until the group's tiles have landed, meets the
-// consumer at the group's barrier (after which the consumer reads them), then
-// issues the next C4_PER tiles, whose slots were last read in an earlier
-// group.  issue(i) loads tile i into slot i % C4_NT.
-template <int IPT, class Issue>
+// Producer protocol on the C4 ring: C4_P tiles are issued up front and every
+// wave of the workgroup meets at a first barrier, then at one barrier per
+// group.  Before group j's barrier the producer waits until the tiles of
+// group j + LEAD have landed; after it, it issues the next C4_PER tiles,
+// whose slots were last read in an earlier group.  LEAD = 0 feeds the
+// recurrence wave (it reads group j after barrier j); LEAD = 1 feeds the
+// coefficient waves, which work one group ahead (group j + 1 between barriers
+// j and j + 1, group 0 between the first barrier and barrier 0).  issue(i)
+// loads tile i into slot i % C4_NT.
+template <int IPT, int LEAD, class Issue>
 __device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue) {
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
     for (int i = 0; i < min(C4_P, ntiles); i++) issue(i);
+    if (LEAD) c4_wait_tiles_after<IPT>(min(C4_P, ntiles) - 1 - min(C4_PER - 1, ntiles - 1));
+    tile_barrier();
     for (int j = 0; j < ngroups; j++) {
-        const int last = min(C4_PER * j + C4_PER - 1, ntiles - 1);
+        const int last = min(C4_PER * (j + LEAD) + C4_PER - 1, ntiles - 1);
         const int issued = min(C4_P + C4_PER * j, ntiles);
         c4_wait_tiles_after<IPT>(issued - 1 - last);
         tile_barrier();
@@ -759,31 +771,110 @@ __device__ void c4_vproducer(const AttnExactArgs &A, Chain4Lds &L, int s0, int c
             if (roff >= wrap) roff -= wrap;
         }
     };
-    c4_producer_loop<1>(ntiles, issue);
+    c4_producer_loop<1, 0>(ntiles, issue);
 }
 
-// Coefficient producer: per tile the four heads' coefficients (lane -> head
-// g0 + lane/16, positions 4*(lane%16)..+3) and their new-max words (lanes
-// 0-7: head g0 + lane/2, word lane%2).
-__device__ void c4_eproducer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
+// Scores producer: per tile the four heads' scores (lane -> head g0 +
+// lane/16, positions 4*(lane%16)..+3; rows past kv_mul repeat the last head).
+__device__ void c4_sproducer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0) {
     const int lane = threadIdx.x & 63, kvm = A.kv_mul;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
-    const int re = min(g0 + (lane >> 4), kvm - 1);
-    const char *e_base = (const char *)(A.e + e_index(A, h, re, 0)) + (lane & 15) * 16;
-    const int rm = min(g0 + ((lane >> 1) & 3), kvm - 1);
-    const char *m_base = (const char *)(A.newmask + (size_t)(h * kvm + rm) * (A.cap / 32)) + (lane & 1) * 4;
-    auto issue = [&](int i) {
-        const int sl = i & (C4_NT - 1);
-        dma16(e_base + (uint32_t)i * 256u, &L.e[sl][0]);
-        if (lane < 8) dma4(m_base + (uint32_t)i * 8u, &L.m[sl][0]);
-    };
-    c4_producer_loop<2>(ntiles, issue);
+    const int r = min(g0 + (lane >> 4), kvm - 1);
+    const char *base = (const char *)(A.scores + (size_t)(h * kvm + r) * A.cap) + (lane & 15) * 16;
+    auto issue = [&](int i) { dma16(base + (uint32_t)i * 256u, &L.s[i & (C4_NT - 1)][0]); };
+    c4_producer_loop<1, 1>(ntiles, issue);
 }
 
-// A wave with nothing to load still takes part in every barrier.
+// Coefficient wave k: row k of the ring (head g0 + k, or the last head of
+// the group past kv_mul), the work of attn_exact_coef_kernel in position
+// order, so the running max of the earlier tiles is carried instead of
+// gathered: lane = position; the running max before each step is max(sink,
+// earlier tiles, in-tile prefix), the step's coefficient and new-max bit as
+// there.  (max is exact in any order and ignores NaN, so the values are the
+// same; the sign of a zero maximum cannot change any comparison or
+// coefficient.)  A group's four tiles are worked together (only the carried
+// maximum is serial), group j + 1 between barriers j and j + 1, group 0
+// before barrier 0; expf reads its table from LDS.
+__device__ __forceinline__ void c4_egroup(const AttnExactArgs &A, Chain4Lds &L, int ctx, int ntiles, int i0, int k,
+                                          float sink, float &mt) {
+    const int lane = threadIdx.x & 63;
+    float sc[C4_PER], p[C4_PER], run[C4_PER];
+    bool valid[C4_PER];
+#pragma unroll
+    for (int t = 0; t < C4_PER; t++) {
+        // tiles past the range read a slot they never write (no effect)
+        sc[t] = L.s[(i0 + t) & (C4_NT - 1)][k * EX_TILE + lane];
+        valid[t] = (i0 + t) * EX_TILE + lane < ctx;
+    }
+#pragma unroll
+    for (int t = 0; t < C4_PER; t++) {
+        // inclusive prefix max over lanes, the steps of dpp_max as single
+        // v_max_f32_dpp instructions (a lane without a source keeps its value)
+        float q = valid[t] ? sc[t] : -INFINITY;
+        asm("s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+            "s_nop 1\n\t"
+            "v_max_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf"
+            : "+v"(q));
+        p[t] = q;
+    }
+#pragma unroll
+    for (int t = 0; t < C4_PER; t++) {
+        // each lane's exclusive prefix from lane - 1 (wave_shr:1), after the
+        // running max of the tiles before
+        const float prev = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, p[t]),
+                                                                                 __builtin_bit_cast(int, p[t]), 0x138,
+                                                                                 0xF, 0xF, false));
+        const float m = A.sinks ? fmaxf(sink, mt) : mt;
+        run[t] = lane == 0 ? m : fmaxf(m, prev);
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[t]), 63)));
+    }
+#pragma unroll
+    for (int t = 0; t < C4_PER; t++) {
+        const bool flag = valid[t] && sc[t] > run[t];
+        const float x = flag ? run[t] - sc[t] : sc[t] - run[t];
+        const float ex = expf_glibc_tab(x, L.exp2tab);
+        const bool zero = (flag && !__builtin_isfinite(run[t])) || (!flag && !valid[t]);
+        const float e = zero ? 0.0f : ex;
+        const unsigned long long bits = __ballot(flag);
+        if (i0 + t < ntiles) {
+            const int sl = (i0 + t) & (C4_NT - 1);
+            L.e[sl][k * EX_TILE + lane] = e;
+            if (lane < 2) L.m[sl][2 * k + lane] = (uint32_t)(bits >> (32 * lane));
+        }
+    }
+}
+__device__ void c4_ewave(const AttnExactArgs &A, Chain4Lds &L, int ctx, int h, int g0, int k) {
+    const int lane = threadIdx.x & 63, kvm = A.kv_mul;
+    const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
+    const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
+    const int head = h * kvm + min(g0 + k, kvm - 1);
+    const float sink = A.sinks ? A.sinks[head] : 0.0f;
+    if (k == 0 && lane < 32) L.exp2tab[lane] = kExp2fTab[lane];
+    float mt = -INFINITY;  // max score of the tiles before
+    RH_WAIT_LGKM0();
+    tile_barrier();  // group 0's scores have landed; the table is in LDS
+    c4_egroup(A, L, ctx, ntiles, 0, k, sink, mt);
+    for (int j = 0; j < ngroups; j++) {
+        RH_WAIT_LGKM0();  // this group's coefficients are in LDS before its barrier
+        tile_barrier();
+        if (C4_PER * (j + 1) < ntiles) c4_egroup(A, L, ctx, ntiles, C4_PER * (j + 1), k, sink, mt);
+    }
+}
+
+// A wave with nothing to do still takes part in every barrier.
 __device__ void c4_idle(int ctx) {
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
+    tile_barrier();
     for (int j = 0; j < ngroups; j++) tile_barrier();
 }
 
@@ -924,6 +1015,7 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
     float o = (DEN && A.sinks) ? 1.0f : 0.0f;
+    tile_barrier();
     for (int j = 0; j < ngroups; j++) {
         tile_barrier();
         const int i0 = C4_PER * j;
@@ -964,6 +1056,7 @@ __device__ void c4_consumer_vg(const AttnExactArgs &A, Chain4Lds &L, int s0, int
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
     const uint16_t *vcol = (const uint16_t *)A.v + (size_t)h * A.vd + slice * 16 + dcol;
     float o = 0.0f;
+    tile_barrier();
     for (int j = 0; j < ngroups; j++) {
         tile_barrier();
         for (int i = C4_PER * j; i < min(C4_PER * j + C4_PER, ntiles); i++) {
@@ -986,12 +1079,21 @@ __device__ void c4_consumer_vg(const AttnExactArgs &A, Chain4Lds &L, int s0, int
     if (dst) *dst = o;
 }
 
-// grid: n_kv * ceil(kv_mul/4) * (vd/16) chain workgroups (wave 0 the
-// outputs, waves 1-4 the V producers, wave 5 the coefficient producer), then
-// n_kv * ceil(kv_mul/4) denominator workgroups (wave 0 the four heads'
-// denominators as the same DPP recurrence with v = 1, wave 1 their
-// coefficient producer, the rest idle); block b serves kv head b % n_kv.
-#define C4_WAVES 6
+// grid: n_kv * ceil(kv_mul/4) * (vd/16) chain workgroups, then n_kv *
+// ceil(kv_mul/4) denominator workgroups (the four heads' denominators as the
+// same DPP recurrence with v = 1, no V); block b serves kv head b % n_kv.
+// Waves: 0 the recurrence; 1, 2, 3, 5 the coefficient waves of rows 0-3; 9
+// the scores producer; 4, 8, 6, 7 the V producers 0-3 (idle in denominator
+// workgroups).  A workgroup's waves go to its four SIMDs in turn, so the
+// recurrence wave shares its SIMD only with two V producers, which issue
+// loads and hardly any VALU work.
+#define C4_WAVES 10
+__device__ __forceinline__ int c4_ewave_row(int wave) {
+    return wave == 1 ? 0 : wave == 2 ? 1 : wave == 3 ? 2 : wave == 5 ? 3 : -1;
+}
+__device__ __forceinline__ int c4_vwave_part(int wave) {
+    return wave == 4 ? 0 : wave == 8 ? 1 : wave == 6 ? 2 : wave == 7 ? 3 : -1;
+}
 __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     __shared__ Chain4Lds L;
@@ -1008,47 +1110,42 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const bool vt_ok = A.vt != nullptr && (s0 & 3) == 0 && e0 < A.slot_count && s0 + ntiles * EX_TILE <= A.vt_stride;
     const bool vg = A.kv_bf16 && !vt_ok;  // bf16 rows cannot be streamed into the f32 ring as they are
-    if (r < ngrp * nsl) {
-        const int g0 = 4 * (r / nsl), slice = r % nsl;
-        const int g = g0 + (lane >> 4);
-        if (wave == 0) {
-            float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
-            const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
-            if (vg) {
-                if (x4) c4_consumer_vg<true>(A, L, s0, ctx, h, slice, dst);
-                else c4_consumer_vg<false>(A, L, s0, ctx, h, slice, dst);
-            } else if (vt_ok) {
-                if (x4) c4_consumer<true, false, true>(A, L, ctx, dst);
-                else c4_consumer<false, false, true>(A, L, ctx, dst);
-            } else {
-                if (x4) c4_consumer<true, false, false>(A, L, ctx, dst);
-                else c4_consumer<false, false, false>(A, L, ctx, dst);
-            }
-        } else if (wave == 5) {
-            c4_eproducer(A, L, ctx, h, g0);
-        } else if (vg) {
-            c4_idle(ctx);
+    const bool den = r >= ngrp * nsl;
+    const int g0 = den ? 4 * (r - ngrp * nsl) : 4 * (r / nsl), slice = den ? 0 : r % nsl;
+    const int g = g0 + (lane >> 4);
+    const int erow = c4_ewave_row(wave), vpart = c4_vwave_part(wave);
+    if (erow >= 0) {
+        c4_ewave(A, L, ctx, h, g0, erow);
+    } else if (wave == 9) {
+        c4_sproducer(A, L, ctx, h, g0);
+    } else if (den) {
+        if (wave == 0) c4_consumer<true, true, false>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
+        else c4_idle(ctx);
+    } else if (wave == 0) {
+        float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
+        const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
+        if (vg) {
+            if (x4) c4_consumer_vg<true>(A, L, s0, ctx, h, slice, dst);
+            else c4_consumer_vg<false>(A, L, s0, ctx, h, slice, dst);
         } else if (vt_ok) {
-            if (wave == 1) c4_vproducer<0, true>(A, L, s0, ctx, h, slice);
-            else if (wave == 2) c4_vproducer<1, true>(A, L, s0, ctx, h, slice);
-            else if (wave == 3) c4_vproducer<2, true>(A, L, s0, ctx, h, slice);
-            else c4_vproducer<3, true>(A, L, s0, ctx, h, slice);
+            if (x4) c4_consumer<true, false, true>(A, L, ctx, dst);
+            else c4_consumer<false, false, true>(A, L, ctx, dst);
         } else {
-            if (wave == 1) c4_vproducer<0, false>(A, L, s0, ctx, h, slice);
-            else if (wave == 2) c4_vproducer<1, false>(A, L, s0, ctx, h, slice);
-            else if (wave == 3) c4_vproducer<2, false>(A, L, s0, ctx, h, slice);
-            else c4_vproducer<3, false>(A, L, s0, ctx, h, slice);
+            if (x4) c4_consumer<true, false, false>(A, L, ctx, dst);
+            else c4_consumer<false, false, false>(A, L, ctx, dst);
         }
+    } else if (vg) {
+        c4_idle(ctx);
+    } else if (vt_ok) {
+        if (vpart == 0) c4_vproducer<0, true>(A, L, s0, ctx, h, slice);
+        else if (vpart == 1) c4_vproducer<1, true>(A, L, s0, ctx, h, slice);
+        else if (vpart == 2) c4_vproducer<2, true>(A, L, s0, ctx, h, slice);
+        else c4_vproducer<3, true>(A, L, s0, ctx, h, slice);
     } else {
-        const int g0 = 4 * (r - ngrp * nsl);
-        const int g = g0 + (lane >> 4);
-        if (wave == 0) {
-            c4_consumer<true, true, false>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
-        } else if (wave == 1) {
-            c4_eproducer(A, L, ctx, h, g0);
-        } else {
-            c4_idle(ctx);
-        }
+        if (vpart == 0) c4_vproducer<0, false>(A, L, s0, ctx, h, slice);
+        else if (vpart == 1) c4_vproducer<1, false>(A, L, s0, ctx, h, slice);
+        else if (vpart == 2) c4_vproducer<2, false>(A, L, s0, ctx, h, slice);
+        else c4_vproducer<3, false>(A, L, s0, ctx, h, slice);
     }
 }
 

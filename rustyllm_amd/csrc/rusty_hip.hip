@@ -950,18 +950,19 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         }
         RH_LAUNCH_OK();
     }
-    {
+    // the LDS-fed chain kernel needs 16-byte rows of 16-dim slices and a
+    // ring that fits the cache (its row offsets are 32-bit); it computes the
+    // coefficients itself
+    const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
+                    A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
+                    (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
+    if (!c4 || A.n_tok > 0) {
         ProfScope ps("attn_exact_coef", s);
         rh_launch(attn_exact_coef_kernel, dim3((ntl + 3) / 4, A.n_heads, nz), dim3(256), 0, s, A);
         RH_LAUNCH_OK();
     }
     {
         ProfScope ps("attn_exact_chain", s);
-        // the LDS-fed kernel needs 16-byte rows of 16-dim slices and a ring
-        // that fits the cache (its row offsets are 32-bit)
-        const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
-                        A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
-                        (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
         if (c4 && A.n_tok > 0) {
             // many query tokens: one independent wave per task, no LDS ring
             const int tasks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
