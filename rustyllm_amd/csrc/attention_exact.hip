@@ -127,6 +127,12 @@ struct AttnExactArgs {
     // position <= the token's that is congruent to s.  tok_view sets lin_b
     // and lin_c for the token; kv_row maps a slot to its buffer row.
     int32_t lin, lin_pos0, lin_b, lin_c;
+    // Streamed decode launch (attn_exact_stream_kernel): scores and chain
+    // workgroups in one grid; sync = [epoch, ticket, timeouts, flags
+    // [n_kv][cap/64]] (zeroed once when allocated), ep = the epoch the
+    // launch reads at its start.  null: separate launches.
+    uint32_t *sync;
+    uint32_t ep;
 };
 
 // Element e of a head vector x after RoPE with the row's cos/sin, exactly as
@@ -178,6 +184,67 @@ __device__ __forceinline__ AttnExactArgs tok_view(const AttnExactArgs &A0) {
 // it maps to row 0, so every load stays inside the buffer.
 __device__ __forceinline__ int kv_row(const AttnExactArgs &A, int slot) {
     return A.lin ? max(0, slot + A.lin_b - (slot > A.lin_c ? A.slot_count : 0)) : slot;
+}
+
+// ---- streamed decode launch: flags between scores and chain workgroups -------
+// A scores workgroup publishes tile `tile` of kv head h by storing epoch + 1
+// in its flag after the scores (and the current position's K/V rows) are
+// written back; chain workgroups wait for it before loading them, by loads
+// coherent across the XCDs' L2 caches.  The scores workgroups never wait, and
+// the chain workgroups take far fewer CUs than the device has, so every
+// awaited flag is set within microseconds.  The wait is bounded all the same
+// (about 20 ms): a wait that runs out marks the launch in sync[2] (epoch + 1)
+// and every later wait of that launch returns at once, so a broken launch
+// ends with wrong values, never a hang.
+#define STREAM_SPIN_MAX (1 << 14)
+__device__ __forceinline__ uint32_t *stream_flag(const AttnExactArgs &A, int h, int tile) {
+    return A.sync + 3 + (size_t)h * (A.cap / 64) + tile;
+}
+// Waits until tiles 0..tile of kv head h are published; ready counts the
+// tiles known to be (a prefix), and one poll reads the flags of the next 64
+// tiles at once (one load per lane), so a run of published tiles costs one
+// round trip, not one per tile.
+__device__ __forceinline__ void stream_wait_prefix(const AttnExactArgs &A, int h, int tile, int ntiles, int &ready) {
+    if (tile < ready) return;
+    const int lane = threadIdx.x & 63;
+    for (int it = 0; it < STREAM_SPIN_MAX; it++) {
+        const int t = ready + lane;
+        const uint32_t v = t < ntiles ? __hip_atomic_load(stream_flag(A, h, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                      : A.ep + 1;
+        const unsigned long long ok = __ballot(v == A.ep + 1);
+        ready += ~ok == 0ull ? 64 : (int)__builtin_ctzll(~ok);  // the published run from `ready` on
+        if (tile < ready) return;
+        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(bad) == A.ep + 1) {
+            ready = ntiles;
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __hip_atomic_store(A.sync + 2, A.ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ready = ntiles;
+}
+__device__ __forceinline__ void stream_wait(const AttnExactArgs &A, int h, int tile) {
+    const uint32_t *f = stream_flag(A, h, tile);
+    for (int it = 0; it < STREAM_SPIN_MAX; it++) {
+        const uint32_t v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(v) == A.ep + 1) return;
+        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(bad) == A.ep + 1) return;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __hip_atomic_store(A.sync + 2, A.ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A store the streamed launch's other workgroups may read: device scope
+// (sc1, written through the non-coherent L2), so no L2 write-back is needed
+// before the flag that publishes it.
+__device__ __forceinline__ void st_pub(float *p, float v, bool coherent) {
+    if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+// A 16-byte direct global->LDS load that bypasses the non-coherent L2 (sc1).
+__device__ __forceinline__ void dma16_coherent(const void *src, void *lds) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds, 16, 0, 16);
 }
 
 __device__ __forceinline__ void exact_range(const AttnExactArgs &A, int &s, int &e) {
@@ -345,17 +412,18 @@ __device__ __forceinline__ float row_shl(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x100 + N, 0xF, 0xF, false));
 }
 
+// Tile `tile` of kv head h by threads 0-255 of the workgroup; returns false
+// when the tile lies past the range (nothing written).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A0) {
+__device__ __forceinline__ bool scores8_tile(const AttnExactArgs &A, int tile, int h) {
     constexpr int M = HD / 8;        // elements per lane
     constexpr int LS = M + 4;        // LDS floats per lane slice (padded: a row's 8 slices hit distinct banks)
     constexpr int RS = 8 * LS;       // LDS floats per K row
-    const AttnExactArgs A = tok_view(A0);
     __shared__ __align__(16) float s_k[EX_TILE * RS];
     __shared__ __align__(16) float s_q[CH_MAXG * RS];  // the heads' q, lane-sliced like a K row
     __shared__ float s_sc[CH_MAXG * EX_TILE];
-    const int t_base = blockIdx.x * EX_TILE;
-    const int h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, kvm = A.kv_mul;
+    const int t_base = tile * EX_TILE;
+    const int tid = threadIdx.x, lane = tid & 63, kvm = A.kv_mul;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float *kh = A.k + (size_t)h * HD;
     const uint16_t *kh16 = (const uint16_t *)A.k + (size_t)h * HD;
@@ -385,7 +453,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
-    if (ctx <= 0 || t_base >= ctx) return;
+    if (ctx <= 0 || t_base >= ctx) return false;
     const int nt = min(EX_TILE, ctx - t_base);
     if (!spec || s0 != A.start_t) load_k(s0, nt);
     // fused RoPE: the current position e0 and its cos/sin row
@@ -429,7 +497,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
                 ((uint16_t *)RA.kcache)[(size_t)slot * kvd + h * HD + e] = kb;
                 kr = bf16_to_f32(kb);  // the score reads the stored (bf16) key
             } else {
-                RA.kcache[(size_t)slot * kvd + h * HD + e] = kr;
+                st_pub(RA.kcache + (size_t)slot * kvd + h * HD + e, kr, A.sync != nullptr);
             }
             s_k[tt_cur * RS + (e & 7) * LS + (e >> 3)] = kr;
         }
@@ -440,9 +508,9 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
                 ((uint16_t *)RA.vcache)[(size_t)slot * vvd + h * RA.vd + e] = vb;
                 v = bf16_to_f32(vb);
             } else {
-                RA.vcache[(size_t)slot * vvd + h * RA.vd + e] = v;
+                st_pub(RA.vcache + (size_t)slot * vvd + h * RA.vd + e, v, A.sync != nullptr);
             }
-            if (RA.vtcache) RA.vtcache[vt4_off(h * RA.vd + e, slot, RA.vt_stride)] = v;
+            if (RA.vtcache) st_pub(RA.vtcache + vt4_off(h * RA.vd + e, slot, RA.vt_stride), v, A.sync != nullptr);
         }
     }
     __syncthreads();
@@ -504,10 +572,16 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     for (int g = wave; g < kvm; g += 4) {
         const int head = h * kvm + g;
         float v = lane < nt ? s_sc[g * EX_TILE + lane] : -INFINITY;
-        if (lane < nt) A.scores[(size_t)head * A.cap + t_base + lane] = v;
+        if (lane < nt) st_pub(A.scores + (size_t)head * A.cap + t_base + lane, v, A.sync != nullptr);
         const float mx = wave_max(v);
-        if (lane == 0) A.tmax[(size_t)head * ntl + blockIdx.x] = mx;
+        if (lane == 0) A.tmax[(size_t)head * ntl + tile] = mx;
     }
+    return true;
+}
+template <int HD>
+__global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
+    scores8_tile<HD>(A, blockIdx.x, blockIdx.y);
 }
 
 // B: one wave per (tile of 64 positions, query head), four tiles per workgroup.  The running max before
@@ -763,10 +837,14 @@ __device__ void c4_vproducer(const AttnExactArgs &A, Chain4Lds &L, int s0, int c
     uint32_t roff = (uint32_t)((s0 + 16 * P + (lane >> 2)) % A.slot_count) * row_bytes;
     auto issue = [&](int i) {
         const int sl = i & (C4_NT - 1);
-        if (VT) {
-            dma16(vt_base + (size_t)i * 4096u, &L.v[sl][P * 256]);
-        } else {
-            dma16(v_base + roff, &L.v[sl][P * 256]);
+        // streamed: the last tile holds the current position's V, stored by
+        // a scores workgroup of this launch
+        const bool fresh = A.sync != nullptr && i == ntiles - 1;
+        if (fresh) stream_wait(A, h, i);
+        const char *src = VT ? vt_base + (size_t)i * 4096u : v_base + roff;
+        if (fresh) dma16_coherent(src, &L.v[sl][P * 256]);
+        else dma16(src, &L.v[sl][P * 256]);
+        if (!VT) {
             roff += step;
             if (roff >= wrap) roff -= wrap;
         }
@@ -781,7 +859,15 @@ __device__ void c4_sproducer(const AttnExactArgs &A, Chain4Lds &L, int ctx, int 
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
     const int r = min(g0 + (lane >> 4), kvm - 1);
     const char *base = (const char *)(A.scores + (size_t)(h * kvm + r) * A.cap) + (lane & 15) * 16;
-    auto issue = [&](int i) { dma16(base + (uint32_t)i * 256u, &L.s[i & (C4_NT - 1)][0]); };
+    int ready = 0;  // tiles known to be published (streamed launch)
+    auto issue = [&](int i) {
+        if (A.sync) {
+            stream_wait_prefix(A, h, i, ntiles, ready);
+            dma16_coherent(base + (uint32_t)i * 256u, &L.s[i & (C4_NT - 1)][0]);
+        } else {
+            dma16(base + (uint32_t)i * 256u, &L.s[i & (C4_NT - 1)][0]);
+        }
+    };
     c4_producer_loop<1, 1>(ntiles, issue);
 }
 
@@ -1062,6 +1148,11 @@ __device__ void c4_consumer_vg(const AttnExactArgs &A, Chain4Lds &L, int s0, int
         for (int i = C4_PER * j; i < min(C4_PER * j + C4_PER, ntiles); i++) {
             const int sl = i & (C4_NT - 1);
             const int ntok = min(EX_TILE, ctx - i * EX_TILE);
+            if (A.sync && i == ntiles - 1) {
+                // streamed: the current position's V row is stored in this launch
+                stream_wait(A, h, i);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
             const float *et = &L.e[sl][row * EX_TILE];
             const uint32_t mw0 = L.m[sl][2 * row], mw1 = L.m[sl][2 * row + 1];
             for (int t = 0; t < ntok; t++) {
@@ -1094,15 +1185,17 @@ __device__ __forceinline__ int c4_ewave_row(int wave) {
 __device__ __forceinline__ int c4_vwave_part(int wave) {
     return wave == 4 ? 0 : wave == 8 ? 1 : wave == 6 ? 2 : wave == 7 ? 3 : -1;
 }
-__global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
-    const AttnExactArgs A = tok_view(A0);
+__device__ __forceinline__ int chain4_blocks(const AttnExactArgs &A) {
+    return A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
+}
+__device__ __forceinline__ void chain4_block(const AttnExactArgs &A, int block) {
     __shared__ Chain4Lds L;
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
     if (ctx <= 0) return;
     const int kvm = A.kv_mul, ngrp = (kvm + 3) / 4, nsl = A.vd / 16;
-    const int h = blockIdx.x % A.n_kv, r = blockIdx.x / A.n_kv;
+    const int h = block % A.n_kv, r = block / A.n_kv;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     // V from the tiled transposed copy when the range starts on a multiple
@@ -1146,6 +1239,54 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnEx
         else if (vpart == 1) c4_vproducer<1, false>(A, L, s0, ctx, h, slice);
         else if (vpart == 2) c4_vproducer<2, false>(A, L, s0, ctx, h, slice);
         else c4_vproducer<3, false>(A, L, s0, ctx, h, slice);
+    }
+}
+
+__global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
+    const AttnExactArgs A = tok_view(A0);
+    chain4_block(A, blockIdx.x);
+}
+
+// A, B and C of one decode step in one launch, sized so every workgroup is
+// resident at once: blocks 0..ns-1 are the scores workgroups, J = ns / n_kv
+// per kv head, workgroup j scoring tiles j, j + J, j + 2J, ... in order, so
+// the early tiles come first; the chain workgroups come last and compute
+// while the later tiles are still being scored.  Only chain workgroups wait,
+// each for a flag (see stream_wait), and the scores workgroups never do.
+// The last workgroup to finish advances the epoch and resets the ticket for
+// the next launch.
+template <int HD>
+__global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_stream_kernel(AttnExactArgs A0) {
+    AttnExactArgs A = A0;
+    A.ep = __hip_atomic_load(A0.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int ns = (int)gridDim.x - chain4_blocks(A);
+    if ((int)blockIdx.x >= ns) {
+        chain4_block(A, (int)blockIdx.x - ns);
+        __syncthreads();
+    } else {
+        if (threadIdx.x >= 256) return;  // the scores work takes four waves
+        const int J = ns / A.n_kv, j = (int)blockIdx.x / A.n_kv, h = (int)blockIdx.x - j * A.n_kv;
+        for (int tile = j; tile < A.cap / EX_TILE; tile += J) {
+            const bool wrote = scores8_tile<HD>(A, tile, h);
+            if (!wrote) break;  // past the range (uniform)
+            // this wave's device-scope stores (scores, f32 K/V rows)
+            // complete; a bf16 cache's rows are plain stores and need the L2
+            // written back
+            if (A.kv_bf16) __threadfence();
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();  // also: the tile's LDS is free for the next
+            if (threadIdx.x == 0)
+                __hip_atomic_store(stream_flag(A, h, tile), A.ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (threadIdx.x == 0) {
+        // (nothing of this launch is read after the ticket but the epoch,
+        // which the next launch reads)
+        const uint32_t t = atomicAdd(A.sync + 1, 1u);
+        if (t == gridDim.x - 1) {
+            __hip_atomic_store(A.sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(A.sync, A.ep + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 

@@ -909,8 +909,21 @@ static size_t exact_scratch_floats(int n_kv, int kv_mul, int cap) {
 // With A.n_tok > 0 the launch covers that many query tokens (grid z), each
 // with its own scratch block of exact_scratch_floats; finish must then be
 // false (the caller normalises the rows).
+// RUSTY_HIP_STREAM=0: the resident decoder's exact attention as separate
+// launches instead of the streamed one
+static bool stream_enabled() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("RUSTY_HIP_STREAM");
+        on = (e && e[0] == '0') ? 0 : 1;
+    }
+    return on == 1;
+}
+
+// sync: the resident decoder's flag block for the streamed launch (null:
+// separate scores, coefficient and chain launches).
 static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s, bool finish = true,
-                             const float **den_out = nullptr) {
+                             const float **den_out = nullptr, uint32_t *sync = nullptr) {
     const size_t nh = (size_t)A.n_heads, cap = (size_t)A.cap;
     const int ntl = A.cap / EX_TILE;
     const unsigned nz = A.n_tok > 0 ? (unsigned)A.n_tok : 1u;
@@ -937,6 +950,36 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         RH_LAUNCH_OK();
         A.fuse_rope = 0;
     }
+    // the LDS-fed chain kernel needs 16-byte rows of 16-dim slices and a
+    // ring that fits the cache (its row offsets are 32-bit); it computes the
+    // coefficients itself
+    const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
+                    A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
+                    (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
+    A.sync = nullptr;
+    // The streamed launch: the scores workgroups (as many per kv head, J, as
+    // the CUs the chain workgroups leave, each scoring every J-th tile), then
+    // the chain workgroups.  A scores workgroup takes about 4.5 us per tile
+    // and the recurrence about 0.27 us, so with J >= 17 (or one tile each)
+    // the scores stay ahead of it; otherwise separate launches.
+    const int nc = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
+    const int J = std::max(1, std::min(ntl, (g.n_cu - nc) / A.n_kv));
+    if (sync && s8 && c4 && A.n_tok == 0 && !A.lin && stream_enabled() && nc + 32 <= g.n_cu &&
+        (J >= 17 || J >= ntl)) {
+        A.sync = sync;
+        const int blocks = J * A.n_kv + nc;
+        ProfScope ps("attn_exact_stream", s);
+        if (A.hd == 128) rh_launch(attn_exact_stream_kernel<128>, dim3(blocks), dim3(64 * C4_WAVES), 0, s, A);
+        else rh_launch(attn_exact_stream_kernel<64>, dim3(blocks), dim3(64 * C4_WAVES), 0, s, A);
+        RH_LAUNCH_OK();
+        if (den_out) *den_out = A.den;
+        if (finish) {
+            ProfScope ps2("attn_exact_finish", s);
+            rh_launch(attn_exact_finish_kernel, dim3((n_out + 255) / 256), dim3(256), 0, s, A.out, A.den, A.vd, n_out, xq);
+            RH_LAUNCH_OK();
+        }
+        return 1;
+    }
     {
         ProfScope ps("attn_exact_scores", s);
         if (s8 && A.hd == 128) {
@@ -950,12 +993,6 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         }
         RH_LAUNCH_OK();
     }
-    // the LDS-fed chain kernel needs 16-byte rows of 16-dim slices and a
-    // ring that fits the cache (its row offsets are 32-bit); it computes the
-    // coefficients itself
-    const bool c4 = A.vd % 16 == 0 && A.value_stride % 4 == 0 && ((uintptr_t)A.v & 15) == 0 &&
-                    A.kv_mul <= CH_MAXG && A.slot_count >= 64 &&
-                    (int64_t)A.slot_count * A.value_stride * 4 < ((int64_t)1 << 31);
     if (!c4 || A.n_tok > 0) {
         ProfScope ps("attn_exact_coef", s);
         rh_launch(attn_exact_coef_kernel, dim3((ntl + 3) / 4, A.n_heads, nz), dim3(256), 0, s, A);
@@ -1839,6 +1876,7 @@ struct Resident {
     int n_chunks = 1;
     float *ex = nullptr;  // exact-attention scratch
     int ex_cap = 0;
+    uint32_t *sync = nullptr;  // streamed exact attention: epoch, ticket, timeouts, flags [n_kv][ex_cap/64]
     float *am_v = nullptr;
     int32_t *am_i = nullptr;
     uint32_t *ticket = nullptr;
@@ -2064,7 +2102,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.kv_bf16 = R.kv_bf16 ? 1 : 0;
             E.start_t = R.st_host ? R.st_host->start_t : 0;  // the range's start as of this enqueue (a hint)
             const float *den = nullptr;
-            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
+            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den, R.sync)) return 0;
             act_o.mode = ACT_DEN;
             act_o.den = den;
             act_o.group = R.vd;
@@ -2191,7 +2229,7 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
             E.cap = R.ex_cap;
             E.scale = 1.0f / sqrtf((float)R.hd);
             const float *den = nullptr;
-            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den)) return 0;
+            if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den, R.sync)) return 0;
             act_o.mode = ACT_DEN;
             act_o.den = den;
             act_o.group = R.vd;
@@ -2795,6 +2833,9 @@ static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n
         return 0;
     R.ex_cap = (int)((max_pos + 63) / 64 * 64);  // a range is at most max_pos positions
     if (!r_alloc((void **)&R.ex, exact_scratch_floats((int)n_kv_heads, (int)(n_heads / n_kv_heads), R.ex_cap) * 4)) return 0;
+    const size_t sync_words = 3 + (size_t)n_kv_heads * (R.ex_cap / 64);
+    if (!r_alloc((void **)&R.sync, sync_words * 4)) return 0;
+    RH_CHECK(hipMemset(R.sync, 0, sync_words * 4));
     R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
     if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
         !r_alloc((void **)&R.ticket, 64) || !r_alloc((void **)&R.st, sizeof(StepState)) ||
