@@ -10,11 +10,12 @@ reference's repeat penalty 1.1.  A "step" is one decode token: embedding ->
 32 layers -> logits -> on-device greedy pick, replayed as one HIP graph.
 
 Also measured in the same run:
-- roofline: the dominant kernel family, exact decode attention (the scores,
-  coefficient and recurrence launches of one layer): the K and V bytes it
-  must read at the profiled positions over the sum of the three launches'
-  average durations, timed with HIP events on the library stream during a
-  profiling pass of the same decode;
+- roofline: the dominant kernel, exact decode attention of one layer (the
+  streamed launch: scores, coefficients and recurrence in one grid; or the
+  separate launches where a shape takes those): the K and V bytes it must
+  read at the profiled positions over the launch's (launches') average
+  duration, timed with HIP events on the library stream during a profiling
+  pass of the same decode;
 - roofline_gemv: the fused gate/up Q4_K GEMV (SwiGLU epilogue), the largest
   per-launch weight stream, timed the same way;
 - cpu_baseline: the CPU oracle (C restatement of the reference's AVX2 path,
@@ -168,8 +169,9 @@ def main():
     # (the profiling pass decodes positions p0 .. p0 + profile_tokens - 1,
     # each attending p + 1 positions) plus q and the outputs
     roofline = None
-    attn_parts = {f: prof[f][0] / prof[f][1] for f in ATTN_FAMS if f in prof and prof[f][1]}
-    if len(attn_parts) == len(ATTN_FAMS):
+    fams = ATTN_STREAM_FAMS if ATTN_STREAM_FAMS[0] in prof else ATTN_FAMS
+    attn_parts = {f: prof[f][0] / prof[f][1] for f in fams if f in prof and prof[f][1]}
+    if len(attn_parts) == len(fams):
         p0 = args.ctx - 1 + args.warmup + args.steps
         n_att = p0 + 1 + (args.profile_tokens - 1) / 2
         hd = cfg["head_dim"]
@@ -177,8 +179,8 @@ def main():
         attn_ms = sum(attn_parts.values())
         attn_gbs = attn_bytes / (attn_ms * 1e-3) / 1e9
         roofline = {
-            "kernel": "exact attention per layer: attn_exact_scores + attn_exact_coef + attn_exact_chain "
-                      "(%d q / %d kv heads, head_dim %d, %.1f positions)" % (cfg["n_heads"], cfg["n_kv_heads"], hd, n_att),
+            "kernel": "exact attention per layer: %s (%d q / %d kv heads, head_dim %d, %.1f positions)"
+                      % (" + ".join(fams), cfg["n_heads"], cfg["n_kv_heads"], hd, n_att),
             "bound": "hbm",
             "achieved": round(attn_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -188,7 +190,7 @@ def main():
             "bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_ms * 1e3, 3),
             "avg_launch_us_parts": {f: round(v * 1e3, 3) for f, v in attn_parts.items()},
-            "launches": prof[ATTN_FAMS[2]][1],
+            "launches": prof[fams[-1]][1],
         }
     roofline_gemv = None
     if cnt:
@@ -380,6 +382,7 @@ def measure_prefill(hip, res, toks, cfg, log):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_kquant_swiglu_llama3-8b-q4km_traffic.json")
 ATTN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_exact_llama3-8b-q4km_ctx4096_traffic.json")
 ATTN_FAMS = ("attn_exact_scores", "attn_exact_coef", "attn_exact_chain")
+ATTN_STREAM_FAMS = ("attn_exact_stream",)
 
 
 # (block elements, block bytes) per GGML type, and the kernel family that
