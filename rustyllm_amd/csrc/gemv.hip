@@ -441,6 +441,23 @@ __device__ __forceinline__ KqGeo<KQ_U> kq_geo(int tr, int nb, int nbp, int64_t s
     return G;
 }
 
+// Row-split tiles (KQ_SPLIT): a tile is one row whose nb blocks are shared by
+// the workgroup's four waves, bw = ceil(nb / 4) consecutive blocks each (one
+// unit per lane), so a wide row (K = 14336: 56 blocks) runs with the
+// one-unit geometry instead of four units per lane.
+template <int FMT>
+__device__ __forceinline__ KqGeo<1> kq_geo_split(int nb, int wave, int lane) {
+    KqGeo<1> G;
+    const int bw = (nb + 3) >> 2, b = wave * bw + (lane >> 2);
+    G.up[0] = false;
+    G.rrow[0] = 0;
+    G.in[0] = (lane >> 2) < bw && b < nb;
+    G.blk[0] = G.in[0] ? b : 0;
+    G.vidx[0] = G.blk[0];
+    G.roff[0] = (int64_t)G.blk[0] * (FMT == F_Q4_K ? 144 : 210);
+    return G;
+}
+
 template <int FMT, bool SWIGLU, int KQ_U>
 __device__ __forceinline__ void kq_load_tile(const GemvArgs &A, const KqTile &T, const KqGeo<KQ_U> &G,
                                              UnitLoad (&L)[KQ_U]) {
@@ -547,6 +564,32 @@ __device__ __forceinline__ void kq_compute_tile(const GemvArgs &A, const KqTile 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A row-split tile: every wave stores its blocks' values in the workgroup's
+// row buffer (parity: the tile's, so the next tile's values go to the other
+// half while this one is summed), then lane 0 of wave 0 sums the row serially
+// in block order.  Every wave of the workgroup runs the same tiles, so the
+// barrier is uniform.
+template <int FMT>
+__device__ __forceinline__ void kq_compute_split(const GemvArgs &A, const KqTile &T, const KqEpi &E,
+                                                 const KqGeo<1> &G, const Q4KScaleSel &S, int nb, int wave, int lane,
+                                                 int parity, const UnitLoad (&L)[1], const int32_t *s_xq,
+                                                 const float *s_dx, const int16_t *s_bs, const int16_t *s_s16,
+                                                 float *s_row) {
+    const int q = lane & 3;
+    const bool ok = G.in[0];
+    const int bb = G.blk[0];
+    const float v = unit_block_value<FMT>(L[0], q, S, ok, s_xq + bb * KQ_XQ_STRIDE, s_bs + bb * 8, s_s16 + bb * 16,
+                                          s_dx[bb]);
+    float *row = s_row + parity * 64;
+    if (ok && q == 0) row[bb] = v;
+    __syncthreads();
+    if (wave == 0 && lane == 0 && T.row0 < T.M.rows) {
+        float acc = kq_row_sum(row, nb);
+        if (T.M.bias) acc += E.bias;
+        T.M.y[T.row0] = A.epi == EPI_ADD ? E.y + acc : acc;
+    }
+}
+
 template <bool SWIGLU, int KOFF = 0>
 __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int tr) {
     KqTile T;
@@ -570,13 +613,15 @@ struct KqShared {
     float dx[NB256_MAX];
     int16_t bs[NB32_MAX];
     int16_t s16[KMAX / 16];
-    __align__(16) float v[4][64];
+    __align__(16) float v[4][64];  // per wave: the tile's block values (row-split tiles: v[0..1] is the
+                                   // workgroup's row buffer, two halves by tile parity)
 };
 
 // One workgroup's share of a launch: workgroup blk of the nblk that serve
 // A's tiles (the whole grid for a one-group launch).
-template <int FMT, bool SWIGLU, int KQ_U, int ACT, int KOFF>
+template <int FMT, bool SWIGLU, int KQ_U, int ACT, int KOFF, bool SPLIT = false>
 __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqShared &SH) {
+    static_assert(!SPLIT || (KQ_U == 1 && !SWIGLU), "row-split tiles: one unit per lane, plain rows");
     int32_t *s_xq = SH.xq;
     float *s_red = SH.red;
     float *s_dx = SH.dx;
@@ -634,9 +679,12 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
 
     // the activation's loads are issued before the tile geometry's arithmetic
     __builtin_amdgcn_sched_barrier(0);
-    const int step = nblk * 4;
-    int tile = blk * 4 + wave;
-    const KqGeo<KQ_U> G = kq_geo<FMT, SWIGLU, KQ_U>(tr, nb, nbp, A.m[0].row_stride, lane);
+    // row-split: the workgroup's waves share each tile (one row)
+    const int step = SPLIT ? nblk : nblk * 4;
+    int tile = SPLIT ? blk : blk * 4 + wave;
+    KqGeo<KQ_U> G;
+    if constexpr (SPLIT) G = kq_geo_split<FMT>(nb, wave, lane);
+    else G = kq_geo<FMT, SWIGLU, KQ_U>(tr, nb, nbp, A.m[0].row_stride, lane);
     const Q4KScaleSel S = q4k_scale_sel(lane & 3);
 
     UnitLoad L0[KQ_U], L1[KQ_U];
@@ -734,6 +782,23 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         if (tid < nb) A.xq.d[tid] = s_dx[tid];
     }
 
+    if constexpr (SPLIT) {
+        while (T0.valid) {
+            kq_compute_split<FMT>(A, T0, E0, G, S, nb, wave, lane, 0, L0, s_xq, s_dx, s_bs, s_s16, s_v[0]);
+            tile += step;
+            if (!T1.valid) break;
+            T0 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
+            kq_load_tile<FMT, SWIGLU, KQ_U>(A, T0, G, L0);
+            E0 = kq_epi_load<SWIGLU>(T0, lane);
+            kq_compute_split<FMT>(A, T1, E1, G, S, nb, wave, lane, 1, L1, s_xq, s_dx, s_bs, s_s16, s_v[0]);
+            tile += step;
+            if (!T0.valid) break;
+            T1 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
+            kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
+            E1 = kq_epi_load<SWIGLU>(T1, lane);
+        }
+        return;
+    }
     while (T0.valid) {
         kq_compute_tile<FMT, SWIGLU, KQ_U>(A, T0, E0, G, S, tr, nb, nbp, lane, L0, s_xq, s_dx, s_bs, s_s16,
                                            s_v[wave]);
@@ -752,10 +817,10 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
     }
 }
 
-template <int FMT, bool SWIGLU, int KQ_U, int ACT>
+template <int FMT, bool SWIGLU, int KQ_U, int ACT, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
     __shared__ KqShared sh;
-    kq_run<FMT, SWIGLU, KQ_U, ACT, 0>(A, blockIdx.x, gridDim.x, sh);
+    kq_run<FMT, SWIGLU, KQ_U, ACT, 0, SPLIT>(A, blockIdx.x, gridDim.x, sh);
 }
 
 // Two launch groups of different formats that build the same activation in

@@ -477,6 +477,22 @@ static int launch_kq_act(const GemvArgs &A, hipStream_t s) {
     RH_LAUNCH_OK();
     return 1;
 }
+template <int FMT, int ACT>
+static int launch_kq_split_act(const GemvArgs &A, hipStream_t s) {
+    auto kern = gemv_kq_kernel<FMT, false, 1, ACT, true>;
+    int grid = persistent_grid(kern, A.n_tiles * 4, 4, ACT != KQ_ACT_XQ);  // four waves per tile
+    ProfScope ps("gemv_kquant", s);
+    rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
+    RH_LAUNCH_OK();
+    return 1;
+}
+template <int FMT>
+static int launch_kq_split(const GemvArgs &A, int act, hipStream_t s) {
+    if (act == KQ_ACT_NORM) return launch_kq_split_act<FMT, KQ_ACT_NORM>(A, s);
+    if (act == KQ_ACT_DEN) return launch_kq_split_act<FMT, KQ_ACT_DEN>(A, s);
+    if (act == KQ_ACT_QUANT) return launch_kq_split_act<FMT, KQ_ACT_QUANT>(A, s);
+    return launch_kq_split_act<FMT, KQ_ACT_XQ>(A, s);
+}
 template <int FMT, bool SW, int U>
 static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
     if (act == KQ_ACT_NORM) return launch_kq_act<FMT, SW, U, KQ_ACT_NORM>(A, s);
@@ -581,6 +597,17 @@ static int kq_prologue_act(const ActSpec &a, int K) {
 
 // The launch arguments for y_i = W_i x over matrices of one category: the
 // category, units per lane (it) and activation mode (kact) of the launch.
+// Row-split K-quant tiles (KQ_SPLIT): plain rows of at least 32 blocks are
+// shared by a workgroup's four waves, one unit per lane.
+static bool kq_split(int K, int epi) {
+    static int off = -1;
+    if (off < 0) {
+        const char *e = getenv("RUSTY_HIP_KQ_SPLIT");  // 0: rows of one wave
+        off = (e && atoi(e) == 0) ? 1 : 0;
+    }
+    return !off && epi != EPI_SWIGLU && K / 256 >= 32;
+}
+
 static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec &act, GemvArgs &A, int &cat_out,
                          int &it_out, int &kact_out) {
     if (n <= 0 || n > GEMV_MAX_MATS) return 0;
@@ -595,6 +622,7 @@ static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec
         for (int i = 0; i < n; i++) rows += ms[i].w.rows;
         it = kq_units_per_lane(K, rows, epi == EPI_SWIGLU);
         r = kq_tile_rows(K, it, epi == EPI_SWIGLU);
+        if (kq_split(K, epi)) it = 1, r = 1;  // one row per workgroup tile
     }
     const int kact = cat == CAT_KQ ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
     if (kact < 0) return 0;
@@ -646,6 +674,8 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
     GemvArgs A;
     int cat, it, kact;
     if (!gemv_cat_args(ms, n, K, epi, act, A, cat, it, kact)) return 0;
+    if (cat == CAT_KQ && kq_split(K, epi))
+        return A.m[0].fmt == 12 ? launch_kq_split<F_Q4_K>(A, kact, s) : launch_kq_split<F_Q6_K>(A, kact, s);
     if (cat == CAT_KQ) {
         const bool q4 = A.m[0].fmt == 12;
 #define RH_KQ_U(U)                                                                                     \
@@ -728,7 +758,7 @@ static int gemv_kq2(const MatSpec *ga, int na, const MatSpec *gb, int nb, int K,
     }
     if (off) return 0;
     if (ga[0].w.fmt == 14) std::swap(ga, gb), std::swap(na, nb);
-    if (ga[0].w.fmt != 12 || gb[0].w.fmt != 14) return 0;
+    if (ga[0].w.fmt != 12 || gb[0].w.fmt != 14 || kq_split(K, EPI_STORE)) return 0;
     GemvArgs A, B;
     int ca, ia, ka, cb, ib, kb;
     if (!gemv_cat_args(ga, na, K, EPI_STORE, act, A, ca, ia, ka)) return 0;
