@@ -35,6 +35,9 @@ CONFIGS = {
                       vocab=1024, theta=10000.0, eps=1e-5, quant="q4k_m"),
     "tiny-q8": dict(arch="llama", n_layers=2, dim=256, n_heads=4, n_kv_heads=1, head_dim=64, hidden_dim=512,
                     vocab=1024, theta=10000.0, eps=1e-5, quant="q8_0"),
+    # ffn_down rows of 32 blocks (the row-split K-quant tiles) at a test's size
+    "tiny-q4km-wide": dict(arch="llama", n_layers=2, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, hidden_dim=8192,
+                           vocab=1024, theta=10000.0, eps=1e-5, quant="q4k_m"),
     "tiny-qwen": dict(arch="qwen2", n_layers=2, dim=512, n_heads=4, n_kv_heads=1, head_dim=128, hidden_dim=768,
                       vocab=1024, theta=1000000.0, eps=1e-6, quant="q4k_m", qkv_bias=True),
     # config 1: TinyLlama-1.1B shape, all Q8_0

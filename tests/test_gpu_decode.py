@@ -41,7 +41,7 @@ def fast(hip):
     hip.attention_mode(prev)
 
 
-@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8", "tiny-qwen"])
+@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8", "tiny-qwen", "tiny-q4km-wide"])
 def test_host_embedding_decode_bit_exact(hip, exact, name):
     """rusty_hip_resident_decode with the embedding row from the host, as the
     reference's resident path calls it (src/model.rs:7193-7199)."""
@@ -78,7 +78,8 @@ def test_fast_attention_decode_logits(hip, fast, name):
         assert np.max(np.abs(g - r)) < 5e-2, (pos, np.max(np.abs(g - r)))
 
 
-@pytest.mark.parametrize("name,penalty", [("tiny-q4km", 1.1), ("tiny-q8", 1.1), ("tiny-qwen", 1.0)])
+@pytest.mark.parametrize("name,penalty", [("tiny-q4km", 1.1), ("tiny-q8", 1.1), ("tiny-qwen", 1.0),
+                                          ("tiny-q4km-wide", 1.1)])
 def test_greedy_stream_64_tokens(hip, exact, name, penalty):
     model, res, orc = _pair(name, 160)
     prompt = synth.token_ids(21, 32, model["config"]["vocab"])
