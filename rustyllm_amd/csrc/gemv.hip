@@ -872,85 +872,151 @@ __device__ __forceinline__ float mxfp4_scale(uint32_t e) {
 // Q8_0, K % 256 == 0: reproduces dot_q8_0_q8k_avx2 (src/simd.rs:7184-7210):
 // eight lane accumulators acc_j = fma(dx*d_b, s_{b,j}, acc_j) over blocks in
 // order, s_{b,j} = exact int dot of bytes 4j..4j+3, then the hsum_avx tree.
-template <int ITERS, int R>
-__global__ __launch_bounds__(256) void gemv_q8_0_int_kernel(GemvArgs A) {
+// A persistent grid of independent waves.  A wave tile is 8 rows; the wave
+// walks its tiles' rows in chunks of Q8P_CH blocks (items), the next item's
+// weights in flight while it works on the current one:
+//   owner step: lane (r, j) holds blocks 8j..8j+7 of the chunk of row r
+//     (272 bytes = 17 aligned 16-byte loads; one Q8_K block of x, one dx)
+//     and computes c_b = dx * d_b and s_{b,i} (i < 8) for them;
+//   chain step: through a wave-private LDS transpose, lane (r, j) runs
+//     accumulator j of row r over the chunk's blocks in order,
+//     acc = fma(c_b, s_{b,j}, acc);
+// after a row's last chunk, hsum_avx over the eight lanes.
+#define Q8P_CH 64   // blocks of a row per item: 8 lanes x 272 bytes
+#define Q8P_PAD 68  // floats per (row, accumulator) line of the transpose
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) {
     __shared__ int32_t s_xq[KMAX / 4];
     __shared__ float s_dx[NB256_MAX];
-    extern __shared__ float s_part[];  // [4R][nb32][9]: scale, s_0..s_7
-    const int K = A.K, nb = K >> 5;
+    __shared__ __align__(16) float s_s[WAVES][8][8][Q8P_PAD];  // [wave][row][accumulator][block]: s
+    __shared__ __align__(16) float s_c[WAVES][8][Q8P_CH];      // [wave][row][block]: c
+    const int K = A.K, nb = K >> 5, nch = (nb + Q8P_CH - 1) / Q8P_CH;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps tile math scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     {
         const int4 *src = (const int4 *)A.xq.qs;
         int4 *dst = (int4 *)s_xq;
-        for (int i = tid; i < K / 16; i += 256) dst[i] = src[i];
-        for (int i = tid; i < (K >> 8); i += 256) s_dx[i] = A.xq.d[i];
+        for (int i = tid; i < K / 16; i += 64 * WAVES) dst[i] = src[i];
+        for (int i = tid; i < (K >> 8); i += 64 * WAVES) s_dx[i] = A.xq.d[i];
     }
     __syncthreads();
-    for (int tile = blockIdx.x; tile < A.n_tiles; tile += gridDim.x) {
+    const int r = lane >> 3, j = lane & 7;
+    const int gw = blockIdx.x * WAVES + wave, nw = gridDim.x * WAVES;
+    const int my_tiles = gw < A.n_tiles ? (A.n_tiles - 1 - gw) / nw + 1 : 0;
+    const int n_items = my_tiles * nch;
+    auto mat_of = [&](int tile) {
         int mi = 0;
 #pragma unroll
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
-        const GemvMat M = mat_sel(A, mi);
-        int row0 = (tile - M.tile_begin) * (4 * R);
-        uint4 wa[R][ITERS], wb[R][ITERS];
-        uint32_t dd[R][ITERS];
+        return mat_sel(A, mi);
+    };
+    // item i: tile gw + (i / nch) * nw, chunk i % nch; loads are clamped in
+    // bounds and unconditional, so the vmcnt bookkeeping stays exact
+    auto load = [&](int i, uint4 (&w)[17]) {
+        const int ii = min(i, n_items - 1);
+        const int tile = gw + (ii / nch) * nw, ch = ii % nch;
+        const GemvMat M = mat_of(tile);
+        const int row = min((tile - M.tile_begin) * 8 + r, M.rows - 1);
+        const int b0 = min(ch * Q8P_CH + 8 * j, nb - 8);
+        const uint4 *p = (const uint4 *)(M.w + (int64_t)row * M.row_stride + (int64_t)b0 * 34);
 #pragma unroll
-        for (int r = 0; r < R; r++)
+        for (int q = 0; q < 17; q++) w[q] = p[q];
+    };
+    float acc = 0.0f;
+    auto process = [&](int i, const uint4 (&w)[17]) {
+        const int tile = gw + (i / nch) * nw, ch = i % nch;
+        const GemvMat M = mat_of(tile);
+        const int row = (tile - M.tile_begin) * 8 + r;
+        const int b0 = ch * Q8P_CH + 8 * j;
+        uint32_t wd[68];
+        __builtin_memcpy(wd, w, sizeof(wd));
+        const int bx = min(b0, nb - 8);
+        const float dx = s_dx[bx >> 3];
+        float sv[8][8];  // [accumulator][block]
+        float cv[8];
 #pragma unroll
-            for (int i = 0; i < ITERS; i++) {
-                int b = lane + 64 * i, row = row0 + wave * R + r;
-                if (b < nb && row < M.rows) {
-                    const uint8_t *blk = M.w + (int64_t)row * M.row_stride + b * 34;
-                    dd[r][i] = ld2(blk);
-                    wa[r][i] = ld16(blk + 2);
-                    wb[r][i] = ld16(blk + 18);
-                }
+        for (int k = 0; k < 8; k++) {
+            // block k at byte 34k: even k start dword-aligned (d, then quants 2
+            // bytes off), odd k start 2 bytes in (quants aligned)
+            const int m = 17 * (k >> 1);
+            uint32_t q[8];
+            uint16_t d;
+            if ((k & 1) == 0) {
+                d = (uint16_t)(wd[m] & 0xFFFFu);
+#pragma unroll
+                for (int t = 0; t < 8; t++) q[t] = __builtin_amdgcn_alignbyte(wd[m + t + 1], wd[m + t], 2);
+            } else {
+                d = (uint16_t)(wd[m + 8] >> 16);
+#pragma unroll
+                for (int t = 0; t < 8; t++) q[t] = wd[m + 9 + t];
             }
+            const int4 *xp = (const int4 *)(s_xq + (bx + k) * 8);
+            const int4 x0 = xp[0], x1 = xp[1];
+            sv[0][k] = (float)sdot4(q[0], x0.x, 0);
+            sv[1][k] = (float)sdot4(q[1], x0.y, 0);
+            sv[2][k] = (float)sdot4(q[2], x0.z, 0);
+            sv[3][k] = (float)sdot4(q[3], x0.w, 0);
+            sv[4][k] = (float)sdot4(q[4], x1.x, 0);
+            sv[5][k] = (float)sdot4(q[5], x1.y, 0);
+            sv[6][k] = (float)sdot4(q[6], x1.z, 0);
+            sv[7][k] = (float)sdot4(q[7], x1.w, 0);
+            cv[k] = dx * h2f(d);
+        }
+        float *ss = &s_s[wave][r][0][8 * j];
 #pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int i = 0; i < ITERS; i++) {
-                int b = lane + 64 * i, row = row0 + wave * R + r;
-                if (b < nb && row < M.rows) {
-                    const int4 *xp = (const int4 *)(s_xq + b * 8);
-                    int4 x0 = xp[0], x1 = xp[1];
-                    float *dst = s_part + ((size_t)(wave * R + r) * nb + b) * 9;
-                    dst[0] = s_dx[b >> 3] * h2f(dd[r][i]);
-                    dst[1] = (float)sdot4(wa[r][i].x, x0.x, 0);
-                    dst[2] = (float)sdot4(wa[r][i].y, x0.y, 0);
-                    dst[3] = (float)sdot4(wa[r][i].z, x0.z, 0);
-                    dst[4] = (float)sdot4(wa[r][i].w, x0.w, 0);
-                    dst[5] = (float)sdot4(wb[r][i].x, x1.x, 0);
-                    dst[6] = (float)sdot4(wb[r][i].y, x1.y, 0);
-                    dst[7] = (float)sdot4(wb[r][i].z, x1.z, 0);
-                    dst[8] = (float)sdot4(wb[r][i].w, x1.w, 0);
-                }
-            }
-        __syncthreads();
-        // 8 threads per row run the lane chains; 4R rows need 32R threads.
-        {
-            int rr = tid >> 3, j = tid & 7;
-            float acc = 0.0f;
-            int row = row0 + rr;
-            if (rr < 4 * R && row < M.rows) {
-                const float *p = s_part + (size_t)rr * nb * 9;
-                for (int b = 0; b < nb; b++) acc = fmaf(p[b * 9], p[b * 9 + 1 + j], acc);
-            }
+        for (int t = 0; t < 8; t++) {
+            *(float4 *)(ss + t * Q8P_PAD) = make_float4(sv[t][0], sv[t][1], sv[t][2], sv[t][3]);
+            *(float4 *)(ss + t * Q8P_PAD + 4) = make_float4(sv[t][4], sv[t][5], sv[t][6], sv[t][7]);
+        }
+        float *sc = &s_c[wave][r][8 * j];
+        *(float4 *)sc = make_float4(cv[0], cv[1], cv[2], cv[3]);
+        *(float4 *)(sc + 4) = make_float4(cv[4], cv[5], cv[6], cv[7]);
+        // the wave's transpose writes are complete before any lane reads them
+        RH_WAIT_LGKM0();
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+        const int nbc = min(Q8P_CH, nb - ch * Q8P_CH);  // a multiple of 8
+        const float *ps = &s_s[wave][r][j][0], *pc = &s_c[wave][r][0];
+        for (int b = 0; b < nbc; b += 8) {
+            const float4 s0 = *(const float4 *)(ps + b), s1 = *(const float4 *)(ps + b + 4);
+            const float4 c0 = *(const float4 *)(pc + b), c1 = *(const float4 *)(pc + b + 4);
+            acc = fmaf(c0.x, s0.x, acc);
+            acc = fmaf(c0.y, s0.y, acc);
+            acc = fmaf(c0.z, s0.z, acc);
+            acc = fmaf(c0.w, s0.w, acc);
+            acc = fmaf(c1.x, s1.x, acc);
+            acc = fmaf(c1.y, s1.y, acc);
+            acc = fmaf(c1.z, s1.z, acc);
+            acc = fmaf(c1.w, s1.w, acc);
+        }
+        // the chain's reads are done before the next item's writes
+        RH_WAIT_LGKM0();
+        asm volatile("" ::: "memory");
+        if (ch == nch - 1) {
             // hsum_avx: t_i = a_i + a_{i+4}; ((t0+t1) + (t2+t3))
-            float t = acc + __shfl_xor(acc, 4, 64);
-            float u = t + __shfl_xor(t, 1, 64);
+            const float t = acc + __shfl_xor(acc, 4, 64);
+            const float u = t + __shfl_xor(t, 1, 64);
             float v = u + __shfl_xor(u, 2, 64);
-            if (rr < 4 * R && j == 0 && row < M.rows) {
+            if (j == 0 && row < M.rows) {
                 if (M.bias) v += M.bias[row];
                 if (A.epi == EPI_ADD)
                     M.y[row] += v;
                 else
                     M.y[row] = v;
             }
+            acc = 0.0f;
         }
-        __syncthreads();
+    };
+    if (n_items <= 0) return;
+    uint4 w0[17], w1[17];
+    load(0, w0);
+    for (int i = 0; i < n_items; i += 2) {
+        load(i + 1, w1);
+        process(i, w0);
+        if (i + 1 >= n_items) break;
+        load(i + 2, w0);
+        process(i + 1, w1);
     }
 }
 

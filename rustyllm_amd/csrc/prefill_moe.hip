@@ -27,7 +27,7 @@ __global__ __launch_bounds__(256) void rmsnorm_f32_batch_kernel(const float *x, 
 // Q8_0 rows for T tokens; each (row, token) is exactly the single-token
 // kernel's value: F32, dot_q8_0_f32_avx2 as gemv_q8_0_f32x_kernel (eight
 // lane accumulators acc_j = fma(d*q, x[32b + 8i + j], acc_j)); otherwise
-// dot_q8_0_q8k_avx2 as gemv_q8_0_int_kernel (acc_j = fma(dx*d, s_j, acc_j),
+// dot_q8_0_q8k_avx2 as gemv_q8_0_pipe_kernel (acc_j = fma(dx*d, s_j, acc_j),
 // s_j the exact dot of bytes 4j..4j+3); then hsum_avx, bias, store or add.
 // A workgroup is 32 rows (4 waves x 8 rows x 8 lanes, lane j accumulator j)
 // by TG tokens whose activations are staged in LDS: F32 float [TG][K]; Q8_K

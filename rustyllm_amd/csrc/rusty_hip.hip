@@ -500,14 +500,39 @@ static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
     if (act == KQ_ACT_QUANT) return launch_kq_act<FMT, SW, U, KQ_ACT_QUANT>(A, s);
     return launch_kq_act<FMT, SW, U, KQ_ACT_XQ>(A, s);
 }
-template <int IT, int R>
-static int launch_q8i(const GemvArgs &A, hipStream_t s) {
-    int grid = std::min(A.n_tiles, grid_cap());
-    size_t lds = (size_t)4 * R * (A.K / 32) * 9 * sizeof(float);
+template <int W>
+static int launch_q8p(const GemvArgs &A, hipStream_t s) {
+    // one workgroup per CU (the wave-private transposes take most of the LDS)
+    const int grid = std::max(1, std::min((A.n_tiles + W - 1) / W, g.n_cu));
     ProfScope ps("gemv_q8_0_int", s);
-    rh_launch((gemv_q8_0_int_kernel<IT, R>), dim3(grid), dim3(256), lds, s, A);
+    rh_launch((gemv_q8_0_pipe_kernel<W>), dim3(grid), dim3(64 * W), 0, s, A);
     RH_LAUNCH_OK();
     return 1;
+}
+// Waves per workgroup W: the fewest tiles on the busiest CU,
+// W * ceil(tiles / (W * CUs)), ties to the larger W (more loads in flight);
+// RUSTY_HIP_Q8P_WAVES=1/2/4/7 forces one (sweeps).
+static int launch_q8p_any(const GemvArgs &A, hipStream_t s) {
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("RUSTY_HIP_Q8P_WAVES");
+        forced = e ? atoi(e) : 0;
+    }
+    int w = forced;
+    if (w != 1 && w != 2 && w != 4 && w != 7) {
+        const int cands[4] = {1, 2, 4, 7};
+        long best = -1;
+        for (int c : cands) {
+            const long f = (long)c * ((A.n_tiles + (long)c * g.n_cu - 1) / ((long)c * g.n_cu));
+            if (best < 0 || f <= best) best = f, w = c;
+        }
+    }
+    switch (w) {
+    case 1: return launch_q8p<1>(A, s);
+    case 2: return launch_q8p<2>(A, s);
+    case 4: return launch_q8p<4>(A, s);
+    default: return launch_q8p<7>(A, s);
+    }
 }
 template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
@@ -560,22 +585,13 @@ static int kq_tile_rows(int K, int units_per_lane, bool swiglu) {
     return std::max(1, std::min(16 * units_per_lane / nb, 64 / nbp) / m);
 }
 
-// rows per tile for each (category, ITERS)
+// rows per wave tile of a category's kernel
 static void pick_iters(int cat, int K, int *it, int *r) {
-    int units = (cat == CAT_KQ) ? (K / 256) * 4 : K / 32;
-    int iters = (units + 63) / 64;
-    if (cat == CAT_KQ) {
-        // wave tile = r rows x all blocks in 64*it units (it = units per lane)
-        *it = 1;
-        *r = 1;
-    } else {
-        if (iters <= 1) { *it = 1; *r = 4; }
-        else if (iters == 2) { *it = 2; *r = 2; }
-        else if (iters <= 3) { *it = 3; *r = 1; }
-        else if (iters <= 4) { *it = 4; *r = 1; }
-        else if (iters <= 6) { *it = 6; *r = 1; }
-        else { *it = 8; *r = 1; }
-    }
+    (void)K;
+    // K-quant: one row per wave tile (units per lane chosen by the caller);
+    // Q8_0 int: gemv_q8_0_pipe_kernel's 8-row wave tiles
+    *it = cat == CAT_Q8I ? 0 : 1;
+    *r = cat == CAT_Q8I ? 2 : 1;
 }
 
 // The prologue mode a K-quant launch uses to build act itself, or -1 when a
@@ -688,17 +704,7 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
 #undef RH_KQ_U
         return 0;
     }
-    if (cat == CAT_Q8I) {
-        switch (it) {
-        case 1: return launch_q8i<1, 4>(A, s);
-        case 2: return launch_q8i<2, 2>(A, s);
-        case 3: return launch_q8i<3, 1>(A, s);
-        case 4: return launch_q8i<4, 1>(A, s);
-        case 6: return launch_q8i<6, 1>(A, s);
-        case 8: return launch_q8i<8, 1>(A, s);
-        default: return 0;
-        }
-    }
+    if (cat == CAT_Q8I) return launch_q8p_any(A, s);
     return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
 }
 
