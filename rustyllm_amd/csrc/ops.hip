@@ -250,11 +250,19 @@ __global__ __launch_bounds__(256) void argmax_greedy_kernel(ArgmaxArgs A) {
     const int nrec = s_nrec;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    // the window in registers (uniform: scalar loads); each occurrence of a
+    // token applies the penalty once more, and all apply the same map, so an
+    // element needs only its occurrence count
+    int rec[64];
+#pragma unroll
+    for (int r = 0; r < 64; r++) rec[r] = s_rec[r];
     for (int i = blockIdx.x * 256 + tid; i < A.n; i += gridDim.x * 256) {
         float v = A.logits[i];
         if (A.penalty != 1.0f) {
-            for (int r = 0; r < nrec; r++)
-                if (s_rec[r] == i) v = !isfinite(v) ? -INFINITY : (v > 0.0f ? v / A.penalty : v * A.penalty);
+            int k = 0;
+#pragma unroll
+            for (int r = 0; r < 64; r++) k += (r < nrec && rec[r] == i) ? 1 : 0;
+            for (int r = 0; r < k; r++) v = !isfinite(v) ? -INFINITY : (v > 0.0f ? v / A.penalty : v * A.penalty);
         }
         if (!isfinite(v)) v = -INFINITY;
         if (better(v, i, bv, bi)) {
@@ -273,15 +281,16 @@ __global__ __launch_bounds__(256) void argmax_greedy_kernel(ArgmaxArgs A) {
         __syncthreads();
     }
     if (tid == 0) {
-        A.part_v[blockIdx.x] = s_v[0];
-        A.part_i[blockIdx.x] = s_i[0];
-        __threadfence();
+        // the partial by device-scope stores (through the XCD's non-coherent
+        // L2), complete before the ticket, instead of a cache write-back fence
+        __hip_atomic_store(A.part_v + blockIdx.x, s_v[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(A.part_i + blockIdx.x, s_i[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
         uint32_t t = atomicAdd(A.ticket, 1u);
         s_last = (t == gridDim.x - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     bv = -INFINITY;
     bi = 0x7fffffff;
     for (int b = tid; b < (int)gridDim.x; b += 256) {
@@ -302,25 +311,27 @@ __global__ __launch_bounds__(256) void argmax_greedy_kernel(ArgmaxArgs A) {
         }
         __syncthreads();
     }
+    int tok = s_i[0];
+    if (tok == 0x7fffffff) tok = 0;  // all logits non-finite: token 0, as the reference
     if (tid == 0) {
-        int tok = s_i[0];
-        if (tok == 0x7fffffff) tok = 0;  // all logits non-finite: token 0, as the reference
         *A.ticket = 0;
         if (A.out_tokens) {
             int k = *A.out_index;
             A.out_tokens[k] = tok;
             *A.out_index = k + 1;
         }
-        if (A.st && A.advance) {
-            StepState *st = A.st;
-            int nr = st->n_recent;
-            if (nr == 64) {
-                for (int r = 0; r < 63; r++) st->recent[r] = st->recent[r + 1];
-                st->recent[63] = tok;
-            } else {
-                st->recent[nr] = tok;
-                st->n_recent = nr + 1;
-            }
+    }
+    if (A.st && A.advance) {
+        // the window as read at the start (s_rec, s_nrec: nothing else writes
+        // it during the launch), shifted by 64 threads at once when full
+        StepState *st = A.st;
+        if (nrec == 64) {
+            if (tid < 64) st->recent[tid] = tid < 63 ? s_rec[tid + 1] : tok;
+        } else if (tid == 0) {
+            st->recent[nrec] = tok;
+            st->n_recent = nrec + 1;
+        }
+        if (tid == 0) {
             st->token = tok;
             st->pos = st->pos + 1;
         }
