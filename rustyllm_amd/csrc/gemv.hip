@@ -882,44 +882,111 @@ __device__ __forceinline__ float mxfp4_scale(uint32_t e) {
 //     accumulator j of row r over the chunk's blocks in order,
 //     acc = fma(c_b, s_{b,j}, acc);
 // after a row's last chunk, hsum_avx over the eight lanes.
+// ACT: the Q8_K activation from memory (KQ_ACT_XQ) or built in the prologue
+// as in the K-quant kernel (RMSNorm, attention normalisation or plain Q8_K,
+// the same arithmetic), staged in the K-quant kernel's padded layout.
+// SWIGLU: a tile is rows row0..row0+3 of the gate matrix (lanes r < 4) and of
+// the up matrix (r >= 4); y = silu(gate) * up.
 #define Q8P_CH 64   // blocks of a row per item: 8 lanes x 272 bytes
 #define Q8P_PAD 68  // floats per (row, accumulator) line of the transpose
-template <int WAVES>
+template <int ACT>
+__device__ __forceinline__ void q8p_build_act(const GemvArgs &A, KqShared &sh, int nt) {
+    const int K = A.K, n16 = K >> 4, tid = threadIdx.x;
+    if (ACT == KQ_ACT_XQ) {
+        const int4 *src = (const int4 *)A.xq.qs;
+        int4 *dst = (int4 *)sh.xq;
+        for (int c = tid; c < n16; c += nt) dst[(c >> 4) * (KQ_XQ_STRIDE / 4) + (c & 15)] = src[c];
+        for (int b = tid; b < (K >> 8); b += nt) sh.dx[b] = A.xq.d[b];
+        return;
+    }
+    float scale = 1.0f;
+    if (ACT == KQ_ACT_NORM) {
+        // rms_norm_into (src/model.rs:5429-5437): the sum of squares in the
+        // reference's AVX2 order from x staged transposed (element 32c + L
+        // at L*ld + c), then (x * scale) * w per element
+        float *s_xt = (float *)sh.xq;
+        const int ld = (K >> 5) + 4;
+        for (int c = tid; c < n16; c += nt) {
+            const int cc = c >> 1, l0 = 16 * (c & 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 xv = ((const float4 *)A.act_x)[4 * c + i];
+                s_xt[(l0 + 4 * i + 0) * ld + cc] = xv.x;
+                s_xt[(l0 + 4 * i + 1) * ld + cc] = xv.y;
+                s_xt[(l0 + 4 * i + 2) * ld + cc] = xv.z;
+                s_xt[(l0 + 4 * i + 3) * ld + cc] = xv.w;
+            }
+        }
+        __syncthreads();
+        const float ss = kq_sumsq_t(s_xt, ld, K, sh.red);  // ends with a barrier after its reads
+        scale = 1.0f / sqrtf(ss / (float)K + A.act_eps);
+    }
+    // chunk c = 16 elements; a 256-block's 16 chunks sit in 16 consecutive
+    // lanes (nt is a multiple of 64), every lane takes part in each pass
+    for (int base = 0; base < n16; base += nt) {
+        const int c = base + tid, cl = min(c, n16 - 1);
+        float v[16];
+        float dd = 0.0f;
+        if (ACT == KQ_ACT_DEN) dd = A.act_den[(16 * cl) / A.act_group];
+        const float inv = dd > 0.0f ? 1.0f / dd : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 xv = ((const float4 *)A.act_x)[4 * cl + i];
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+            float4 wv = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            if (ACT == KQ_ACT_NORM) wv = ((const float4 *)A.act_w)[4 * cl + i];
+            const float ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (ACT == KQ_ACT_NORM) v[4 * i + e] = xs[e] * scale * ws[e];
+                else if (ACT == KQ_ACT_DEN) v[4 * i + e] = dd > 0.0f ? xs[e] * inv : xs[e];
+                else v[4 * i + e] = xs[e];
+            }
+        }
+        // (NORM: the staging's last reads precede kq_sumsq_t's barrier, so the
+        // quant stores may overwrite it)
+        kq_quant_chunk(v, c, c < n16, sh.xq, sh.dx, sh.bs, sh.s16);
+    }
+}
+
+template <int WAVES, int ACT, bool SWIGLU>
 __global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) {
-    __shared__ int32_t s_xq[KMAX / 4];
-    __shared__ float s_dx[NB256_MAX];
+    __shared__ KqShared sh;
     __shared__ __align__(16) float s_s[WAVES][8][8][Q8P_PAD];  // [wave][row][accumulator][block]: s
     __shared__ __align__(16) float s_c[WAVES][8][Q8P_CH];      // [wave][row][block]: c
     const int K = A.K, nb = K >> 5, nch = (nb + Q8P_CH - 1) / Q8P_CH;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    {
-        const int4 *src = (const int4 *)A.xq.qs;
-        int4 *dst = (int4 *)s_xq;
-        for (int i = tid; i < K / 16; i += 64 * WAVES) dst[i] = src[i];
-        for (int i = tid; i < (K >> 8); i += 64 * WAVES) s_dx[i] = A.xq.d[i];
-    }
+    q8p_build_act<ACT>(A, sh, 64 * WAVES);
     __syncthreads();
     const int r = lane >> 3, j = lane & 7;
+    // the tile's rows: 8 of one matrix, or (SWIGLU) 4 of the gate and the
+    // same 4 of the up matrix
+    constexpr int TR = SWIGLU ? 4 : 8;
+    const int rr = SWIGLU ? (r & 3) : r;
     const int gw = blockIdx.x * WAVES + wave, nw = gridDim.x * WAVES;
     const int my_tiles = gw < A.n_tiles ? (A.n_tiles - 1 - gw) / nw + 1 : 0;
     const int n_items = my_tiles * nch;
     auto mat_of = [&](int tile) {
+        if (SWIGLU) return mat_sel(A, 0);
         int mi = 0;
 #pragma unroll
         for (int t = 1; t < GEMV_MAX_MATS; t++)
             if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
         return mat_sel(A, mi);
     };
+    // (SWIGLU) the up matrix's bytes for lanes r >= 4; both share rows and stride
+    const uint8_t *w_up = SWIGLU ? A.m[1].w : nullptr;
     // item i: tile gw + (i / nch) * nw, chunk i % nch; loads are clamped in
     // bounds and unconditional, so the vmcnt bookkeeping stays exact
     auto load = [&](int i, uint4 (&w)[17]) {
         const int ii = min(i, n_items - 1);
         const int tile = gw + (ii / nch) * nw, ch = ii % nch;
         const GemvMat M = mat_of(tile);
-        const int row = min((tile - M.tile_begin) * 8 + r, M.rows - 1);
+        const int row = min((tile - M.tile_begin) * TR + rr, M.rows - 1);
         const int b0 = min(ch * Q8P_CH + 8 * j, nb - 8);
-        const uint4 *p = (const uint4 *)(M.w + (int64_t)row * M.row_stride + (int64_t)b0 * 34);
+        const uint8_t *wm = (SWIGLU && r >= 4) ? w_up : M.w;
+        const uint4 *p = (const uint4 *)(wm + (int64_t)row * M.row_stride + (int64_t)b0 * 34);
 #pragma unroll
         for (int q = 0; q < 17; q++) w[q] = p[q];
     };
@@ -927,12 +994,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) 
     auto process = [&](int i, const uint4 (&w)[17]) {
         const int tile = gw + (i / nch) * nw, ch = i % nch;
         const GemvMat M = mat_of(tile);
-        const int row = (tile - M.tile_begin) * 8 + r;
+        const int row = (tile - M.tile_begin) * TR + rr;
         const int b0 = ch * Q8P_CH + 8 * j;
         uint32_t wd[68];
         __builtin_memcpy(wd, w, sizeof(wd));
         const int bx = min(b0, nb - 8);
-        const float dx = s_dx[bx >> 3];
+        const float dx = sh.dx[bx >> 3];
+        // x of this lane's 256-block in the padded staging
+        const int32_t *xb = sh.xq + (bx >> 3) * KQ_XQ_STRIDE;
         float sv[8][8];  // [accumulator][block]
         float cv[8];
 #pragma unroll
@@ -951,7 +1020,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) 
 #pragma unroll
                 for (int t = 0; t < 8; t++) q[t] = wd[m + 9 + t];
             }
-            const int4 *xp = (const int4 *)(s_xq + (bx + k) * 8);
+            const int4 *xp = (const int4 *)(xb + k * 8);
             const int4 x0 = xp[0], x1 = xp[1];
             sv[0][k] = (float)sdot4(q[0], x0.x, 0);
             sv[1][k] = (float)sdot4(q[1], x0.y, 0);
@@ -998,7 +1067,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) 
             const float t = acc + __shfl_xor(acc, 4, 64);
             const float u = t + __shfl_xor(t, 1, 64);
             float v = u + __shfl_xor(u, 2, 64);
-            if (j == 0 && row < M.rows) {
+            if (SWIGLU) {
+                // the up row's value from the lane four rows on
+                const float up = __shfl(v, lane + 32, 64);
+                if (j == 0 && r < 4 && row < M.rows) M.y[row] = silu_mul_ref(v, up);
+            } else if (j == 0 && row < M.rows) {
                 if (M.bias) v += M.bias[row];
                 if (A.epi == EPI_ADD)
                     M.y[row] += v;

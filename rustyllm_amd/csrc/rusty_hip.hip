@@ -500,19 +500,30 @@ static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
     if (act == KQ_ACT_QUANT) return launch_kq_act<FMT, SW, U, KQ_ACT_QUANT>(A, s);
     return launch_kq_act<FMT, SW, U, KQ_ACT_XQ>(A, s);
 }
-template <int W>
+template <int W, int ACT, bool SW>
 static int launch_q8p(const GemvArgs &A, hipStream_t s) {
     // one workgroup per CU (the wave-private transposes take most of the LDS)
     const int grid = std::max(1, std::min((A.n_tiles + W - 1) / W, g.n_cu));
     ProfScope ps("gemv_q8_0_int", s);
-    rh_launch((gemv_q8_0_pipe_kernel<W>), dim3(grid), dim3(64 * W), 0, s, A);
+    rh_launch((gemv_q8_0_pipe_kernel<W, ACT, SW>), dim3(grid), dim3(64 * W), 0, s, A);
     RH_LAUNCH_OK();
     return 1;
+}
+template <int W>
+static int launch_q8p_w(const GemvArgs &A, int act, bool sw, hipStream_t s) {
+    if (sw) return act == KQ_ACT_NORM ? launch_q8p<W, KQ_ACT_NORM, true>(A, s) : launch_q8p<W, KQ_ACT_XQ, true>(A, s);
+    switch (act) {
+    case KQ_ACT_NORM: return launch_q8p<W, KQ_ACT_NORM, false>(A, s);
+    case KQ_ACT_DEN: return launch_q8p<W, KQ_ACT_DEN, false>(A, s);
+    case KQ_ACT_QUANT: return launch_q8p<W, KQ_ACT_QUANT, false>(A, s);
+    default: return launch_q8p<W, KQ_ACT_XQ, false>(A, s);
+    }
 }
 // Waves per workgroup W: the fewest tiles on the busiest CU,
 // W * ceil(tiles / (W * CUs)), ties to the larger W (more loads in flight);
 // RUSTY_HIP_Q8P_WAVES=1/2/4/7 forces one (sweeps).
-static int launch_q8p_any(const GemvArgs &A, hipStream_t s) {
+static int launch_q8p_any(const GemvArgs &A, int act, bool sw, hipStream_t s) {
+    if (sw && act != KQ_ACT_NORM && act != KQ_ACT_XQ) return 0;
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("RUSTY_HIP_Q8P_WAVES");
@@ -528,10 +539,10 @@ static int launch_q8p_any(const GemvArgs &A, hipStream_t s) {
         }
     }
     switch (w) {
-    case 1: return launch_q8p<1>(A, s);
-    case 2: return launch_q8p<2>(A, s);
-    case 4: return launch_q8p<4>(A, s);
-    default: return launch_q8p<7>(A, s);
+    case 1: return launch_q8p_w<1>(A, act, sw, s);
+    case 2: return launch_q8p_w<2>(A, act, sw, s);
+    case 4: return launch_q8p_w<4>(A, act, sw, s);
+    default: return launch_q8p_w<7>(A, act, sw, s);
     }
 }
 template <int FMT>
@@ -640,7 +651,7 @@ static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec
         r = kq_tile_rows(K, it, epi == EPI_SWIGLU);
         if (kq_split(K, epi)) it = 1, r = 1;  // one row per workgroup tile
     }
-    const int kact = cat == CAT_KQ ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
+    const int kact = (cat == CAT_KQ || cat == CAT_Q8I) ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
     if (kact < 0) return 0;
     memset(&A, 0, sizeof(A));
     A.K = K;
@@ -656,6 +667,7 @@ static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec
     A.act_store = (kact > 0 && act.xq.qs) ? 1 : 0;
     int tiles = 0;
     int rows_per_tile = (cat == CAT_KQ) ? r : (cat == CAT_F32) ? (ms[0].w.fmt == 8 ? 8 : 64) : 4 * r;
+    if (cat == CAT_Q8I && epi == EPI_SWIGLU) rows_per_tile = 4;  // 4 gate + the same 4 up rows per wave tile
     if (cat == CAT_F32)
         for (int i = 1; i < n; i++)
             if (ms[i].w.fmt != ms[0].w.fmt) return 0;  // one format per launch
@@ -671,7 +683,9 @@ static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec
         if (epi != EPI_SWIGLU) tiles += (m.rows + rows_per_tile - 1) / rows_per_tile;
     }
     if (epi == EPI_SWIGLU) {
-        if (n != 2 || cat != CAT_KQ || A.m[0].rows != A.m[1].rows) return 0;
+        if (n != 2 || (cat != CAT_KQ && cat != CAT_Q8I) || A.m[0].rows != A.m[1].rows ||
+            A.m[0].row_stride != A.m[1].row_stride || ms[0].bias || ms[1].bias)
+            return 0;
         tiles = (A.m[0].rows + rows_per_tile - 1) / rows_per_tile;
     }
     A.n_tiles = tiles;
@@ -704,7 +718,7 @@ static int gemv_cat(const MatSpec *ms, int n, int K, int epi, const ActSpec &act
 #undef RH_KQ_U
         return 0;
     }
-    if (cat == CAT_Q8I) return launch_q8p_any(A, s);
+    if (cat == CAT_Q8I) return launch_q8p_any(A, kact, epi == EPI_SWIGLU, s);
     return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
 }
 
@@ -789,6 +803,12 @@ static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpe
     // standalone activation kernel
     bool prologue = kq_prologue_act(act, K) > 0;
     for (int i = 0; i < n && prologue; i++) prologue = cat_of(ms[i].w.fmt, K) == CAT_KQ;
+    if (kq_prologue_act(act, K) > 0 && !prologue) {
+        // Q8_0 matrices build the same activation in their prologue (one
+        // launch group: all Q8_0)
+        prologue = true;
+        for (int i = 0; i < n && prologue; i++) prologue = cat_of(ms[i].w.fmt, K) == CAT_Q8I;
+    }
     ActSpec use = act;
     if (!prologue && !act_materialize(act, K, &use, s)) return 0;
     // with a prologue, the first launch group publishes the Q8_K vector it
@@ -857,7 +877,9 @@ static int launch_silu(const float *g_, const float *u, int n, float *out, hipSt
 // fused epilogue, other formats two GEMVs plus the SiLU kernel.
 static int gemv_swiglu_act(const DevW &gate, const DevW &up, int K, const ActSpec &act, float *hidden,
                            float *tmp_g, float *tmp_u, hipStream_t s) {
-    if (cat_of(gate.fmt, K) == CAT_KQ && gate.fmt == up.fmt && gate.rows == up.rows && K / 256 <= 32) {
+    const int gc = cat_of(gate.fmt, K);
+    if ((gc == CAT_KQ || gc == CAT_Q8I) && gate.fmt == up.fmt && gate.rows == up.rows && gate.stride == up.stride &&
+        (gc == CAT_Q8I || K / 256 <= 32)) {
         MatSpec ms[2] = {{gate, hidden, nullptr}, {up, hidden, nullptr}};
         ActSpec use = act;
         if (kq_prologue_act(act, K) < 0 && !act_materialize(act, K, &use, s)) return 0;
