@@ -2210,6 +2210,13 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
         RLayer &Ly = R.L[l];
         MatSpec qkv[3] = {{Ly.w[0], R.q, Ly.bias[0]}, {Ly.w[1], R.k, Ly.bias[1]}, {Ly.w[2], R.v, Ly.bias[2]}};
         if (!gemv_multi_act(qkv, 3, dim, EPI_STORE, r_act_norm(Ly.attn_norm), s)) return 0;
+        // The exact path stores the current position's K/V inside its scores
+        // launch, unless another position of the range shares its ring slot
+        // (a full-range layer past the ring's length reads that slot as the
+        // reference does after the store: the store must come first).
+        const int window = (l % 2 == 0) ? (int)R.window : 0;
+        const bool rope_in_scores = !attn_fast_mode() && (!R.ring || window > 0);
+        RopeArgs r_rope;
         {
             RopeArgs A;
             memset(&A, 0, sizeof(A));
@@ -2229,14 +2236,16 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
             A.slots = R.storage;
             A.ring = R.ring ? 1 : 0;  // KVCache::k_offset(pos) (src/model.rs:6778-6783)
             A.neox = 0;
-            int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
-            ProfScope ps("rope_kv", s);
-            rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
-            RH_LAUNCH_OK();
+            r_rope = A;
+            if (!rope_in_scores) {
+                int work = R.n_heads * (R.hd / 2) + R.n_kv * (R.hd / 2) + vdim;
+                ProfScope ps("rope_kv", s);
+                rh_launch(rope_kv_kernel, dim3((work + 255) / 256), dim3(256), 0, s, A);
+                RH_LAUNCH_OK();
+            }
         }
         // attention with sinks; even layers see the sliding window only
         // (attention_start_pos, src/model.rs:6788-6792)
-        const int window = (l % 2 == 0) ? (int)R.window : 0;
         ActSpec act_o = act_xq(attn_cols % 256 == 0 ? R.xq_attn : XQ{}, R.attn);
         if (attn_fast_mode()) {
             AttnArgs A;
@@ -2281,6 +2290,8 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
             E.window = window;
             E.cap = R.ex_cap;
             E.scale = 1.0f / sqrtf((float)R.hd);
+            E.rope = r_rope;  // RoPE + KV store inside the scores launch (or a rope_kv launch it makes)
+            E.fuse_rope = rope_in_scores ? 1 : 0;
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den, R.sync)) return 0;
             act_o.mode = ACT_DEN;
