@@ -17,6 +17,8 @@
 #pragma once
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace rh {
 
 enum Fmt : int { F_Q8_0 = 8, F_Q4_K = 12, F_Q6_K = 14, F_MXFP4 = 39 };
@@ -53,8 +55,11 @@ struct GemvMat {
 //                where the denominator is positive, then Q8_K;
 //   KQ_ACT_QUANT: Q8_K of act_x as is (quantize_row_q8k), up to four chunks
 //                per thread.
-enum KqAct : int { KQ_ACT_XQ = 0, KQ_ACT_NORM = 1, KQ_ACT_DEN = 2, KQ_ACT_QUANT = 3 };
+//   KQ_ACT_NORM2 / KQ_ACT_DEN2: the same for 4096 < K < 8192, two 16-element
+//                chunks per thread.
+enum KqAct : int { KQ_ACT_XQ = 0, KQ_ACT_NORM = 1, KQ_ACT_DEN = 2, KQ_ACT_QUANT = 3, KQ_ACT_NORM2 = 4, KQ_ACT_DEN2 = 5 };
 #define KQ_ACT_KMAX 4096        // widest activation NORM / DEN build: one 16-element chunk per thread
+#define KQ_ACT_KMAX2 8191       // NORM2 / DEN2: two chunks per thread (rows of fewer than 32 blocks)
 #define KQ_ACT_QUANT_KMAX 16384  // QUANT: four chunks per thread
 
 struct GemvArgs {
@@ -607,8 +612,10 @@ __device__ __forceinline__ KqTile kq_tile_info(const GemvArgs &A, int tile, int 
 
 // FMT: every matrix of the launch has this format (Q4_K or Q6_K).  KQ_U:
 // units per lane (a wave tile is 64*KQ_U quarter-block units).
-struct KqShared {
-    __align__(16) int32_t xq[KQ_XQ_WORDS];
+// XQW: words of the activation staging (NORM2 stages K + 128 floats of x)
+template <int XQW>
+struct KqSharedT {
+    __align__(16) int32_t xq[XQW];
     float red[40];
     float dx[NB256_MAX];
     int16_t bs[NB32_MAX];
@@ -616,11 +623,18 @@ struct KqShared {
     __align__(16) float v[4][64];  // per wave: the tile's block values (row-split tiles: v[0..1] is the
                                    // workgroup's row buffer, two halves by tile parity)
 };
+using KqShared = KqSharedT<KQ_XQ_WORDS>;
+template <int ACT>
+using KqSharedFor = typename std::conditional<ACT == KQ_ACT_NORM2, KqSharedT<8192 + 128>, KqShared>::type;
 
 // One workgroup's share of a launch: workgroup blk of the nblk that serve
 // A's tiles (the whole grid for a one-group launch).
-template <int FMT, bool SWIGLU, int KQ_U, int ACT, int KOFF, bool SPLIT = false>
-__device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqShared &SH) {
+template <int FMT, bool SWIGLU, int KQ_U, int ACT, int KOFF, bool SPLIT = false, class SHT = KqShared>
+__device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, SHT &SH) {
+    static_assert(ACT != KQ_ACT_NORM2 || sizeof(SH.xq) >= (8192 + 128) * 4, "NORM2 stages up to 8320 floats");
+    constexpr bool NORMA = ACT == KQ_ACT_NORM || ACT == KQ_ACT_NORM2;
+    constexpr bool DENA = ACT == KQ_ACT_DEN || ACT == KQ_ACT_DEN2;
+    constexpr int CH = (ACT == KQ_ACT_NORM2 || ACT == KQ_ACT_DEN2) ? 2 : 1;  // 16-element chunks per thread
     static_assert(!SPLIT || (KQ_U == 1 && !SWIGLU), "row-split tiles: one unit per lane, plain rows");
     int32_t *s_xq = SH.xq;
     float *s_red = SH.red;
@@ -644,10 +658,10 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
     const int ns16 = K >> 7;  // int4 chunks of sums16 (16 per 256)
     int4 x0, x1, x2, x3, bsr, s16r;
     float dxr;
-    float4 xf[ACT == KQ_ACT_NORM ? 8 : 1];  // this thread's 16-element chunk of x, then of w (NORM)
-    float4 xd[ACT == KQ_ACT_DEN ? 4 : 1];  // this thread's 16-element chunk (DEN)
+    float4 xf[NORMA ? 8 * CH : 1];  // chunk tid + 256 h of x, then of w (NORM), per h < CH
+    float4 xd[DENA ? 4 * CH : 1];   // chunk tid + 256 h (DEN)
     float4 xq4[ACT == KQ_ACT_QUANT ? 16 : 1];  // chunks tid + 256 r, r < 4 (QUANT)
-    float dd = 0.0f;
+    float dd[CH];
     if (ACT == KQ_ACT_XQ) {
         const int4 *src = (const int4 *)A.xq.qs;
         x0 = src[min(tid, n16 - 1)];
@@ -657,17 +671,23 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         bsr = ((const int4 *)A.xq.bsums)[min(tid, nbs - 1)];
         s16r = ((const int4 *)A.xq.sums16)[min(tid, ns16 - 1)];
         dxr = A.xq.d[min(tid, nb - 1)];
-    } else if (ACT == KQ_ACT_NORM) {
-        const int c = min(tid, n16 - 1);
+    } else if (NORMA) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) xf[i] = ((const float4 *)A.act_x)[4 * c + i];
+        for (int h = 0; h < CH; h++) {
+            const int c = min(tid + 256 * h, n16 - 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++) xf[4 + i] = ((const float4 *)A.act_w)[4 * c + i];
-    } else if (ACT == KQ_ACT_DEN) {
-        const int c = min(tid, n16 - 1);
+            for (int i = 0; i < 4; i++) xf[8 * h + i] = ((const float4 *)A.act_x)[4 * c + i];
 #pragma unroll
-        for (int i = 0; i < 4; i++) xd[i] = ((const float4 *)A.act_x)[4 * c + i];
-        dd = A.act_den[(16 * c) / A.act_group];
+            for (int i = 0; i < 4; i++) xf[8 * h + 4 + i] = ((const float4 *)A.act_w)[4 * c + i];
+        }
+    } else if (DENA) {
+#pragma unroll
+        for (int h = 0; h < CH; h++) {
+            const int c = min(tid + 256 * h, n16 - 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) xd[4 * h + i] = ((const float4 *)A.act_x)[4 * c + i];
+            dd[h] = A.act_den[(16 * c) / A.act_group];
+        }
     } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -693,7 +713,7 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
     KqEpi E0 = kq_epi_load<SWIGLU>(T0, lane);
     KqTile T1 = kq_tile_info<SWIGLU, KOFF>(A, tile + step, tr);
     KqEpi E1;
-    if (ACT != KQ_ACT_NORM) {
+    if (!NORMA) {
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
         E1 = kq_epi_load<SWIGLU>(T1, lane);
     }
@@ -708,23 +728,27 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         if (tid < nbs) ((int4 *)s_bs)[tid] = bsr;
         if (tid < ns16) ((int4 *)s_s16)[tid] = s16r;
         if (tid < nb) s_dx[tid] = dxr;
-    } else if (ACT == KQ_ACT_NORM) {
+    } else if (NORMA) {
         // rms_norm_into (src/model.rs:5429-5437): x staged as f32 in the
         // quant buffer, sum of squares in the reference's AVX2 order, then
         // (x * scale) * w per element and Q8_K of the result
-        // x and w (this thread's 16-element chunk, loaded ahead of the first
+        // x and w (this thread's 16-element chunks, loaded ahead of the first
         // tile's weights) stay in registers; x is also staged transposed
         // (element 32c + L at L*ld + c) for the sum of squares
         float *s_xt = (float *)s_xq;
         const int ld = (K >> 5) + 4;
-        if (tid < n16) {
-            const int c = tid >> 1, l0 = 16 * (tid & 1);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                s_xt[(l0 + 4 * i + 0) * ld + c] = xf[i].x;
-                s_xt[(l0 + 4 * i + 1) * ld + c] = xf[i].y;
-                s_xt[(l0 + 4 * i + 2) * ld + c] = xf[i].z;
-                s_xt[(l0 + 4 * i + 3) * ld + c] = xf[i].w;
+        for (int h = 0; h < CH; h++) {
+            const int ci = tid + 256 * h;
+            if (ci < n16) {
+                const int c = ci >> 1, l0 = 16 * (ci & 1);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    s_xt[(l0 + 4 * i + 0) * ld + c] = xf[8 * h + i].x;
+                    s_xt[(l0 + 4 * i + 1) * ld + c] = xf[8 * h + i].y;
+                    s_xt[(l0 + 4 * i + 2) * ld + c] = xf[8 * h + i].z;
+                    s_xt[(l0 + 4 * i + 3) * ld + c] = xf[8 * h + i].w;
+                }
             }
         }
         kq_load_tile<FMT, SWIGLU, KQ_U>(A, T1, G, L1);
@@ -732,18 +756,21 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
         __syncthreads();
         const float ss = kq_sumsq_t(s_xt, ld, K, s_red);
         const float scale = 1.0f / sqrtf(ss / (float)K + A.act_eps);
-        float v[16];
+        float v[CH][16];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 xv = xf[i];
-            const float4 wv = xf[4 + i];
-            v[4 * i + 0] = xv.x * scale * wv.x;
-            v[4 * i + 1] = xv.y * scale * wv.y;
-            v[4 * i + 2] = xv.z * scale * wv.z;
-            v[4 * i + 3] = xv.w * scale * wv.w;
-        }
+        for (int h = 0; h < CH; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 xv = xf[8 * h + i];
+                const float4 wv = xf[8 * h + 4 + i];
+                v[h][4 * i + 0] = xv.x * scale * wv.x;
+                v[h][4 * i + 1] = xv.y * scale * wv.y;
+                v[h][4 * i + 2] = xv.z * scale * wv.z;
+                v[h][4 * i + 3] = xv.w * scale * wv.w;
+            }
         __syncthreads();  // every read of the f32 staging precedes the quant stores over it
-        kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
+#pragma unroll
+        for (int h = 0; h < CH; h++) kq_quant_chunk(v[h], tid + 256 * h, tid + 256 * h < n16, s_xq, s_dx, s_bs, s_s16);
     } else if (ACT == KQ_ACT_QUANT) {
         // the standalone quantize_q8k_kernel's values, chunk by chunk
 #pragma unroll
@@ -761,22 +788,26 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
     } else {
         // attention normalisation (out *= 1/den where den > 0, as the
         // reference's final scale) and Q8_K
-        float v[16];
-        const float inv = dd > 0.0f ? 1.0f / dd : 1.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 a = xd[i];
-            v[4 * i + 0] = dd > 0.0f ? a.x * inv : a.x;
-            v[4 * i + 1] = dd > 0.0f ? a.y * inv : a.y;
-            v[4 * i + 2] = dd > 0.0f ? a.z * inv : a.z;
-            v[4 * i + 3] = dd > 0.0f ? a.w * inv : a.w;
+        for (int h = 0; h < CH; h++) {
+            float v[16];
+            const float d = dd[h];
+            const float inv = d > 0.0f ? 1.0f / d : 1.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 a = xd[4 * h + i];
+                v[4 * i + 0] = d > 0.0f ? a.x * inv : a.x;
+                v[4 * i + 1] = d > 0.0f ? a.y * inv : a.y;
+                v[4 * i + 2] = d > 0.0f ? a.z * inv : a.z;
+                v[4 * i + 3] = d > 0.0f ? a.w * inv : a.w;
+            }
+            kq_quant_chunk(v, tid + 256 * h, tid + 256 * h < n16, s_xq, s_dx, s_bs, s_s16);
         }
-        kq_quant_chunk(v, tid, tid < n16, s_xq, s_dx, s_bs, s_s16);
     }
     __syncthreads();
     if (ACT != KQ_ACT_XQ && A.act_store && blk == 0) {
         // the same vector for a later launch that consumes it as is
-        if (tid < n16) ((int4 *)A.xq.qs)[tid] = ((const int4 *)s_xq)[(tid >> 4) * (KQ_XQ_STRIDE / 4) + (tid & 15)];
+        for (int c = tid; c < n16; c += 256) ((int4 *)A.xq.qs)[c] = ((const int4 *)s_xq)[(c >> 4) * (KQ_XQ_STRIDE / 4) + (c & 15)];
         if (tid < nbs) ((int4 *)A.xq.bsums)[tid] = ((const int4 *)s_bs)[tid];
         if (tid < ns16) ((int4 *)A.xq.sums16)[tid] = ((const int4 *)s_s16)[tid];
         if (tid < nb) A.xq.d[tid] = s_dx[tid];
@@ -819,7 +850,7 @@ __device__ __forceinline__ void kq_run(const GemvArgs &A, int blk, int nblk, KqS
 
 template <int FMT, bool SWIGLU, int KQ_U, int ACT, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
-    __shared__ KqShared sh;
+    __shared__ KqSharedFor<ACT> sh;
     kq_run<FMT, SWIGLU, KQ_U, ACT, 0, SPLIT>(A, blockIdx.x, gridDim.x, sh);
 }
 
@@ -829,7 +860,7 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvArgs A) {
 // Every tile is computed exactly as in the one-group kernel.
 template <int FA, int UA, int FB, int UB, int ACT>
 __global__ __launch_bounds__(256) void gemv_kq2_kernel(GemvArgs A, GemvArgs B, int grid_a) {
-    __shared__ KqShared sh;
+    __shared__ KqSharedFor<ACT> sh;
     if ((int)blockIdx.x < grid_a)
         kq_run<FA, false, UA, ACT, 0>(A, blockIdx.x, grid_a, sh);
     else

@@ -497,6 +497,11 @@ template <int FMT, bool SW, int U>
 static int launch_kq(const GemvArgs &A, int act, hipStream_t s) {
     if (act == KQ_ACT_NORM) return launch_kq_act<FMT, SW, U, KQ_ACT_NORM>(A, s);
     if (act == KQ_ACT_DEN) return launch_kq_act<FMT, SW, U, KQ_ACT_DEN>(A, s);
+    if (act == KQ_ACT_NORM2) return launch_kq_act<FMT, SW, U, KQ_ACT_NORM2>(A, s);
+    if (act == KQ_ACT_DEN2) {
+        if constexpr (SW || U > 2) return 0;  // (wo: one row of fewer than 32 blocks in two units)
+        else return launch_kq_act<FMT, SW, U, KQ_ACT_DEN2>(A, s);
+    }
     if (act == KQ_ACT_QUANT) return launch_kq_act<FMT, SW, U, KQ_ACT_QUANT>(A, s);
     return launch_kq_act<FMT, SW, U, KQ_ACT_XQ>(A, s);
 }
@@ -616,10 +621,19 @@ static int kq_prologue_act(const ActSpec &a, int K) {
     if (a.mode == ACT_XQ) return KQ_ACT_XQ;
     if (off || K % 256 != 0) return -1;
     if (a.mode == ACT_QUANT && K <= KQ_ACT_QUANT_KMAX && ((uintptr_t)a.x & 15) == 0) return KQ_ACT_QUANT;
-    if (K > KQ_ACT_KMAX) return -1;
-    if (a.mode == ACT_RMSNORM && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.norm_w & 15) == 0) return KQ_ACT_NORM;
-    if (a.mode == ACT_DEN && a.group > 0 && a.group % 16 == 0 && ((uintptr_t)a.x & 15) == 0) return KQ_ACT_DEN;
+    if (K > KQ_ACT_KMAX2) return -1;
+    const bool wide = K > KQ_ACT_KMAX;  // two 16-element chunks per thread
+    if (a.mode == ACT_RMSNORM && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.norm_w & 15) == 0)
+        return wide ? KQ_ACT_NORM2 : KQ_ACT_NORM;
+    if (a.mode == ACT_DEN && a.group > 0 && a.group % 16 == 0 && ((uintptr_t)a.x & 15) == 0)
+        return wide ? KQ_ACT_DEN2 : KQ_ACT_DEN;
     return -1;
+}
+// The prologues the Q8_0 integer kernel builds: those of K-quant up to
+// K = 4096 (NORM stages K + 128 floats in its staging of KQ_XQ_WORDS).
+static int q8_prologue_act(const ActSpec &a, int K) {
+    const int k = kq_prologue_act(a, K);
+    return (k == KQ_ACT_NORM2 || k == KQ_ACT_DEN2) ? -1 : k;
 }
 
 // The launch arguments for y_i = W_i x over matrices of one category: the
@@ -651,7 +665,9 @@ static int gemv_cat_args(const MatSpec *ms, int n, int K, int epi, const ActSpec
         r = kq_tile_rows(K, it, epi == EPI_SWIGLU);
         if (kq_split(K, epi)) it = 1, r = 1;  // one row per workgroup tile
     }
-    const int kact = (cat == CAT_KQ || cat == CAT_Q8I) ? kq_prologue_act(act, K) : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
+    const int kact = cat == CAT_KQ ? kq_prologue_act(act, K)
+                     : cat == CAT_Q8I ? q8_prologue_act(act, K)
+                                      : (act.mode == ACT_XQ ? KQ_ACT_XQ : -1);
     if (kact < 0) return 0;
     memset(&A, 0, sizeof(A));
     A.K = K;
@@ -803,7 +819,7 @@ static int gemv_multi_act(const MatSpec *ms, int n, int K, int epi, const ActSpe
     // standalone activation kernel
     bool prologue = kq_prologue_act(act, K) > 0;
     for (int i = 0; i < n && prologue; i++) prologue = cat_of(ms[i].w.fmt, K) == CAT_KQ;
-    if (kq_prologue_act(act, K) > 0 && !prologue) {
+    if (q8_prologue_act(act, K) > 0 && !prologue) {
         // Q8_0 matrices build the same activation in their prologue (one
         // launch group: all Q8_0)
         prologue = true;
@@ -882,7 +898,9 @@ static int gemv_swiglu_act(const DevW &gate, const DevW &up, int K, const ActSpe
         (gc == CAT_Q8I || K / 256 <= 32)) {
         MatSpec ms[2] = {{gate, hidden, nullptr}, {up, hidden, nullptr}};
         ActSpec use = act;
-        if (kq_prologue_act(act, K) < 0 && !act_materialize(act, K, &use, s)) return 0;
+        if ((gc == CAT_Q8I ? q8_prologue_act(act, K) : kq_prologue_act(act, K)) < 0 &&
+            !act_materialize(act, K, &use, s))
+            return 0;
         return gemv_cat(ms, 2, K, EPI_SWIGLU, use, s);
     }
     MatSpec ms[2] = {{gate, tmp_g, nullptr}, {up, tmp_u, nullptr}};
