@@ -530,41 +530,60 @@ __device__ __forceinline__ bool scores8_tile(const AttnExactArgs &A, int tile, i
                 q[4 * r + 3] = f.w;
             }
         }
+        // two positions per step (tt and tt + 32), so two independent
+        // accumulation chains interleave; the form is chosen once per head
+        auto run = [&](auto x4c) {
+            constexpr bool X4 = decltype(x4c)::value;
 #pragma unroll
-        for (int it = 0; it < EX_TILE / 8; it++) {
-            const int tt = 8 * it + sub;
-            const float *kr = s_k + tt * RS + l * LS;
-            float k[M];
+            for (int it = 0; it < EX_TILE / 16; it++) {
+                float y[2];
+                float k[2][M];
 #pragma unroll
-            for (int r = 0; r < M / 4; r++) {
-                const float4 f = *(const float4 *)(kr + 4 * r);
-                k[4 * r] = f.x;
-                k[4 * r + 1] = f.y;
-                k[4 * r + 2] = f.z;
-                k[4 * r + 3] = f.w;
+                for (int p = 0; p < 2; p++) {
+                    const float *kr = s_k + (8 * it + 32 * p + sub) * RS + l * LS;
+#pragma unroll
+                    for (int r = 0; r < M / 4; r++) {
+                        const float4 f = *(const float4 *)(kr + 4 * r);
+                        k[p][4 * r] = f.x;
+                        k[p][4 * r + 1] = f.y;
+                        k[p][4 * r + 2] = f.z;
+                        k[p][4 * r + 3] = f.w;
+                    }
+                }
+                if (X4) {
+                    y[0] = 0.0f;
+                    y[1] = 0.0f;
+#pragma unroll
+                    for (int mm = 0; mm < M; mm++) {
+                        y[0] = fmaf(q[mm], k[0][mm], y[0]);
+                        y[1] = fmaf(q[mm], k[1][mm], y[1]);
+                    }
+                } else {
+#pragma unroll
+                    for (int p = 0; p < 2; p++) {
+                        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int c = 0; c < M / 4; c++)
+#pragma unroll
+                            for (int j = 0; j < 4; j++) a[j] = fmaf(q[4 * c + j], k[p][4 * c + j], a[j]);
+                        y[p] = (a[0] + a[1]) + (a[2] + a[3]);
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    // hsum_avx of the 8 lanes, needed in lane l = 0 only: lane i
+                    // takes lane i + N of its row (DPP row_shl), so lanes 0 and 8
+                    // of every row get (y0 + y4) + (y1 + y5) and (y2 + y6) +
+                    // (y3 + y7) and their sum, as the xor-4/1/2 butterfly gives
+                    const float a = y[p] + row_shl<4>(y[p]);
+                    const float b = a + row_shl<1>(a);
+                    const float d = b + row_shl<2>(b);
+                    if (l == 0) s_sc[g * EX_TILE + 8 * it + 32 * p + sub] = d * A.scale;
+                }
             }
-            float y;
-            if (x4) {
-                y = 0.0f;
-#pragma unroll
-                for (int mm = 0; mm < M; mm++) y = fmaf(q[mm], k[mm], y);
-            } else {
-                float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int c = 0; c < M / 4; c++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) a[j] = fmaf(q[4 * c + j], k[4 * c + j], a[j]);
-                y = (a[0] + a[1]) + (a[2] + a[3]);
-            }
-            // hsum_avx of the 8 lanes, needed in lane l = 0 only: lane i
-            // takes lane i + N of its row (DPP row_shl), so lanes 0 and 8 of
-            // every row get (y0 + y4) + (y1 + y5) and (y2 + y6) + (y3 + y7)
-            // and their sum, as the xor-4/1/2 butterfly gives there
-            const float a = y + row_shl<4>(y);
-            const float b = a + row_shl<1>(a);
-            const float d = b + row_shl<2>(b);
-            if (l == 0) s_sc[g * EX_TILE + tt] = d * A.scale;
-        }
+        };
+        if (x4) run(std::true_type{});
+        else run(std::false_type{});
     }
     __syncthreads();
     // coalesced score rows + tile maxima (max is exact in any order)
