@@ -450,6 +450,23 @@ __device__ __forceinline__ bool scores8_tile(const AttnExactArgs &A, int tile, i
     // never used), and issued again below if the range starts elsewhere.
     const bool spec = A.window == 0;
     if (spec) load_k(A.start_t, EX_TILE);
+    // q of the kv head's query heads, both elements of each RoPE pair, loaded
+    // before the range (the device step state) arrives: only the cos/sin row
+    // waits for the position
+    const RopeArgs &RA = A.rope;
+    const int half = HD / 2;
+    constexpr int QI = (CH_MAXG * HD + 255) / 256;  // elements per thread
+    const float *qsrc = (A.fuse_rope ? RA.q : A.q) + (size_t)h * kvm * HD;
+    float qv0[QI], qv1[QI];
+#pragma unroll
+    for (int u = 0; u < QI; u++) {
+        const int i = min(tid + 256 * u, kvm * HD - 1);
+        const int g = i / HD, e = i - g * HD;
+        const int p = RA.neox ? (e < half ? e : e - half) : e >> 1;
+        const int i0 = RA.neox ? p : 2 * p, i1 = RA.neox ? p + half : 2 * p + 1;
+        qv0[u] = qsrc[g * HD + i0];
+        qv1[u] = qsrc[g * HD + i1];
+    }
     int s0, e0;
     exact_range(A, s0, e0);
     const int ctx = e0 - s0 + 1;
@@ -457,18 +474,26 @@ __device__ __forceinline__ bool scores8_tile(const AttnExactArgs &A, int tile, i
     const int nt = min(EX_TILE, ctx - t_base);
     if (!spec || s0 != A.start_t) load_k(s0, nt);
     // fused RoPE: the current position e0 and its cos/sin row
-    const RopeArgs &RA = A.rope;
     const bool fuse = A.fuse_rope != 0 && e0 < RA.max_pos;
-    const int half = HD / 2;
     const float *ct = RA.cos_t + (size_t)e0 * half, *stb = RA.sin_t + (size_t)e0 * half;
     {
-        // q of the kv head's query heads (rotated here when RoPE is fused),
-        // element e of head g at lane slice e % 8, position e / 8
-        const float *qsrc = (fuse ? RA.q : A.q) + (size_t)h * kvm * HD;
-        for (int i = tid; i < kvm * HD; i += 256) {
-            const int g = i / HD, e = i - g * HD;
-            const float v = fuse ? rope_elem(qsrc + (size_t)g * HD, e, half, RA.neox != 0, ct, stb) : qsrc[i];
-            s_q[g * RS + (e & 7) * LS + (e >> 3)] = v;
+        // (rotated here when RoPE is fused, as rope_elem / rope_kv_kernel:
+        // r0 = v0*c - v1*s, r1 = v0*s + v1*c), element e of head g at lane
+        // slice e % 8, position e / 8
+#pragma unroll
+        for (int u = 0; u < QI; u++) {
+            const int i = tid + 256 * u;
+            if (i < kvm * HD) {
+                const int g = i / HD, e = i - g * HD;
+                const int p = RA.neox ? (e < half ? e : e - half) : e >> 1;
+                const bool first = RA.neox ? e < half : (e & 1) == 0;
+                float v = first ? qv0[u] : qv1[u];
+                if (fuse) {
+                    const float c = ct[p], sn = stb[p];
+                    v = first ? qv0[u] * c - qv1[u] * sn : qv0[u] * sn + qv1[u] * c;
+                }
+                s_q[g * RS + (e & 7) * LS + (e >> 3)] = v;
+            }
         }
     }
     {
