@@ -1053,8 +1053,9 @@ __device__ __forceinline__ void c4_group_ballots(uint32_t w, uint32_t &lo, uint3
 }
 
 // One tile (four 16-step chunks) of a consumer group in one of three forms:
-// FAST 16 DPP FMAs per chunk; AFF the grouped form o = fma(a, v, o*m) on
-// every step, (a, m) from the coefficient and the row's new-max bit; FLAGS
+// FAST 16 DPP FMAs per chunk; AFF per chunk the fast run unless a row holds
+// a new maximum in it, then the grouped form o = fma(a, v, o*m) on every
+// step, (a, m) from the coefficient and the row's new-max bit; FLAGS
 // (scale_add heads) per chunk the fast run unless the chunk holds a new
 // maximum, then each step in its own form.  Chunk k computes from register
 // set k & 1 while chunk k + 1 (or chunk 0 of the group's next tile) loads
@@ -1084,9 +1085,16 @@ __device__ __forceinline__ void c4_tile(const Chain4Lds &L, int i, int row, int 
         if (MODE == C4_FAST) {
             cons_fma16_dpp(a[c], v[c], o);
         } else if (MODE == C4_AFF) {
-            float a16, m16;
-            aff_pair16(a[c], bits, lane, a16, m16);
-            cons_affine16_dpp(a16, m16, v[c], o);
+            // the grouped form only on chunks where a row holds a new
+            // maximum: elsewhere (a, m) = (e, 1) and the forms agree
+            const uint32_t half = (k & 1) ? ghi : glo;
+            if (half & (0x55u << (8 * t + (k >> 1)))) {
+                float a16, m16;
+                aff_pair16(a[c], bits, lane, a16, m16);
+                cons_affine16_dpp(a16, m16, v[c], o);
+            } else {
+                cons_fma16_dpp(a[c], v[c], o);
+            }
         } else {
             const uint32_t half = (k & 1) ? ghi : glo;
             if (half & (0x55u << (8 * t + (k >> 1)))) c4_steps16_slow<X4>(a[c], v[c], o, bits);
@@ -1117,8 +1125,8 @@ __device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, in
         for (int t = 0; t < C4_PER; t++)
             c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
     } else if (X4 || DEN) {
-        // grouped form: a tile holding a new maximum for any of the four rows
-        // runs o = fma(a, v, o*m) on every step
+        // grouped form: the 16-step chunks of a tile holding a new maximum
+        // for any of the four rows run o = fma(a, v, o*m) on every step
 #pragma unroll
         for (int t = 0; t < C4_PER; t++) {
             if ((any >> (8 * t)) & 0xFFu)
