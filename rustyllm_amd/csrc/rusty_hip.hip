@@ -437,8 +437,11 @@ static int grid_cap() { return g.n_cu * 8; }
 
 // Persistent grid: as many workgroups as fit on the device at once (queried
 // once per kernel instantiation), never more than the tiles need.
+// Kinds of persistent GEMV launch, for the per-CU workgroup cap of launches
+// that build their activation in a prologue.
+enum GridKind { GK_PLAIN = 0, GK_PRO = 1, GK_PRO_SWIGLU = 2, GK_PRO_SPLIT = 3, GK_PRO_KQ2 = 4 };
 template <class Kern>
-static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, bool prologue = false) {
+static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, int kind = GK_PLAIN) {
     // RUSTY_HIP_WG_PER_CU caps the resident workgroups per CU (sweeps)
     static std::map<const void *, int> occ;
     auto it = occ.find((const void *)kernel);
@@ -451,18 +454,24 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, bool prol
     } else {
         per_cu = it->second;
     }
-    // Launches that build their activation in a prologue run two resident
-    // workgroups per CU: each wave then takes more tiles through its two-deep
-    // load pipeline, which amortises the prologue (8B decode: 290 -> 298
-    // tok/s); the others keep the occupancy limit, which streams faster on
-    // its own (Q4_K 14336x4096: 11.0 against 12.6 us).
+    // Launches that build their activation in a prologue run at most three
+    // resident workgroups per CU: each wave then takes more tiles through its
+    // two-deep load pipeline, which amortises the prologue (8B decode: 2 per
+    // CU 342.5, 3 per CU 350.5, 4 per CU 340.7 tok/s); the others keep the
+    // occupancy limit, which streams faster on its own (Q4_K 14336x4096: 11.0
+    // against 12.6 us).
+    // RUSTY_HIP_WG_CAPS="a,b,c,d" sets the prologue caps per kind (plain,
+    // SwiGLU, row-split, two-format)
     static int cap = -1;
+    static int pcap[5] = {0, 3, 3, 3, 3};
     if (cap < 0) {
         const char *e = getenv("RUSTY_HIP_WG_PER_CU");
         cap = e ? atoi(e) : 0;
+        const char *c = getenv("RUSTY_HIP_WG_CAPS");
+        if (c) sscanf(c, "%d,%d,%d,%d", &pcap[1], &pcap[2], &pcap[3], &pcap[4]);
     }
     if (cap > 0) per_cu = std::min(per_cu, cap);
-    else if (prologue) per_cu = std::min(per_cu, 2);
+    else if (kind != GK_PLAIN && pcap[kind] > 0) per_cu = std::min(per_cu, pcap[kind]);
     int need = (n_tiles + waves_per_wg - 1) / waves_per_wg;
     int grid = std::min(need, per_cu * g.n_cu);
     return grid < 1 ? 1 : grid;
@@ -471,7 +480,7 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, bool prol
 template <int FMT, bool SW, int U, int ACT>
 static int launch_kq_act(const GemvArgs &A, hipStream_t s) {
     auto kern = gemv_kq_kernel<FMT, SW, U, ACT>;
-    int grid = persistent_grid(kern, A.n_tiles, 4, ACT != KQ_ACT_XQ);
+    int grid = persistent_grid(kern, A.n_tiles, 4, ACT == KQ_ACT_XQ ? GK_PLAIN : SW ? GK_PRO_SWIGLU : GK_PRO);
     ProfScope ps(SW ? "gemv_kquant_swiglu" : "gemv_kquant", s);
     rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
@@ -480,7 +489,7 @@ static int launch_kq_act(const GemvArgs &A, hipStream_t s) {
 template <int FMT, int ACT>
 static int launch_kq_split_act(const GemvArgs &A, hipStream_t s) {
     auto kern = gemv_kq_kernel<FMT, false, 1, ACT, true>;
-    int grid = persistent_grid(kern, A.n_tiles * 4, 4, ACT != KQ_ACT_XQ);  // four waves per tile
+    int grid = persistent_grid(kern, A.n_tiles * 4, 4, ACT == KQ_ACT_XQ ? GK_PLAIN : GK_PRO_SPLIT);  // four waves per tile
     ProfScope ps("gemv_kquant", s);
     rh_launch(kern, dim3(grid), dim3(256), 0, s, A);
     RH_LAUNCH_OK();
@@ -777,7 +786,7 @@ template <int UA, int UB>
 static int launch_kq2(const GemvArgs &A, const GemvArgs &B, int bytes_a, int bytes_b, hipStream_t s) {
     auto kern = gemv_kq2_kernel<F_Q4_K, UA, F_Q6_K, UB, KQ_ACT_NORM>;
     const int need_a = (A.n_tiles + 3) / 4, need_b = (B.n_tiles + 3) / 4;
-    const int total = persistent_grid(kern, A.n_tiles + B.n_tiles, 4, true);
+    const int total = persistent_grid(kern, A.n_tiles + B.n_tiles, 4, GK_PRO_KQ2);
     int grid_a = (int)((double)total * bytes_a / ((double)bytes_a + bytes_b) + 0.5);
     grid_a = std::max(1, std::min(grid_a, std::min(need_a, total - 1)));
     const int grid_b = std::max(1, std::min(total - grid_a, need_b));
