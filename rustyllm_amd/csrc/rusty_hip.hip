@@ -455,7 +455,7 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, int kind 
         per_cu = it->second;
     }
     // Launches that build their activation in a prologue run at most three
-    // resident workgroups per CU: each wave then takes more tiles through its
+    // resident workgroups per CU (two for the two-format q/k/v launch): each wave then takes more tiles through its
     // two-deep load pipeline, which amortises the prologue (8B decode: 2 per
     // CU 342.5, 3 per CU 350.5, 4 per CU 340.7 tok/s); the others keep the
     // occupancy limit, which streams faster on its own (Q4_K 14336x4096: 11.0
@@ -463,7 +463,7 @@ static int persistent_grid(Kern kernel, int n_tiles, int waves_per_wg, int kind 
     // RUSTY_HIP_WG_CAPS="a,b,c,d" sets the prologue caps per kind (plain,
     // SwiGLU, row-split, two-format)
     static int cap = -1;
-    static int pcap[5] = {0, 3, 3, 3, 3};
+    static int pcap[5] = {0, 3, 3, 3, 2};  // q/k/v: 351.6 at 2 against 349.7 at 3
     if (cap < 0) {
         const char *e = getenv("RUSTY_HIP_WG_PER_CU");
         cap = e ? atoi(e) : 0;
