@@ -265,16 +265,20 @@ int rusty_hip_resident_configure_moe(uint32_t n_layers, uint32_t dim, uint32_t n
 int rusty_hip_resident_set_moe_layer(uint32_t l, const RustyMoeLayerDesc *desc);
 
 /* No reference counterpart: rusty_hip_attention for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Same arguments, checks, numerics and
- * attention mode as rusty_hip_attention, but query, keys, values, sinks and
- * out are DEVICE pointers, and the call makes no allocation: its scratch (the
- * exact order's scores, coefficients and masks, or the split-K partials) is
- * one fixed 16 MiB device array per GPU, held until the process ends.
- * Returns 0, with a message on stderr, when a call needs more than that
- * (exact order: about 8.2 bytes per query head per attended position, so
- * heads x positions up to ~2 M, e.g. 40 heads over 49152 positions).  Calls
- * that overlap on one GPU share the array and race.  Synchronous. */
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, checks, numerics and attention mode as
+ * rusty_hip_attention, but query, keys, values, sinks and out are DEVICE
+ * pointers, and the call makes no allocation: its scratch (the exact order's
+ * scores, coefficients and masks, or the split-K partials) is one fixed
+ * 16 MiB device array per GPU, held until the process ends.  Returns 0, with
+ * a message on stderr, when a call needs more than that (exact order: about
+ * 8.2 bytes per query head per attended position, so heads x positions up to
+ * ~2 M, e.g. 40 heads over 49152 positions).  Ordering: the call first waits
+ * for all work already submitted to the device (so inputs written on any of
+ * the caller's streams are complete), then runs on the library's own stream
+ * and returns once out is written.  It is synchronous and therefore cannot be
+ * recorded into a caller's HIP graph.  Calls that overlap on one GPU share
+ * the scratch array and race. */
 int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const float *keys, uintptr_t keys_len,
                                 const float *values, uintptr_t values_len, const float *sinks, uintptr_t sinks_len,
                                 float *out, uintptr_t out_len, uintptr_t heads, uintptr_t kv_mul, uintptr_t head_dim,
@@ -371,6 +375,11 @@ int rusty_hip_debug_greedy(const float *logits, uintptr_t n, const int32_t *rece
                            int32_t *token);
 int rusty_hip_debug_f16(const uint16_t *h, uintptr_t n, float *out);
 int rusty_hip_debug_expf(const float *x, uintptr_t n, float *out);
+/* Marks the resident decoder's next streamed attention launch as timed out
+ * (what a bounded wait that ran out records): its waits return at once, it
+ * ends normally with invalid values, and the decode call that ran it returns
+ * 0.  Test hook for that failure path; 0 when no streamed launch exists. */
+int rusty_hip_debug_stream_mark(void);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,24 @@ struct GgufValue {
         default: return false;
         }
     }
+    // one element of MetaValue::as_u32_array (src/gguf.rs:188-207): negative
+    // entries and 64-bit values above u32::MAX are dropped, not wrapped
+    bool as_u32_elem(uint32_t *out) const {
+        switch (type) {
+        case GV_U8: case GV_U16: case GV_U32:
+            *out = (uint32_t)u;
+            return true;
+        case GV_I8: case GV_I16: case GV_I32: case GV_I64:
+            if ((int64_t)u < 0 || (int64_t)u > (int64_t)0xFFFFFFFFll) return false;
+            *out = (uint32_t)u;
+            return true;
+        case GV_U64:
+            if (u > 0xFFFFFFFFull) return false;
+            *out = (uint32_t)u;
+            return true;
+        default: return false;
+        }
+    }
     bool as_f32(float *out) const {
         if (type != GV_F32 && type != GV_F64) return false;
         *out = (float)f;
@@ -191,6 +209,22 @@ class GgufFile {
         if (pos > size || n > size - pos) return fail("truncated GGUF header");
         return true;
     }
+    size_t remaining() const { return pos > size ? 0 : size - pos; }
+    // Fewest bytes one encoded value of a metadata type can take; 0 for an
+    // unknown type.  A count is accepted only if that many values could fit
+    // in the bytes left, so a corrupt count cannot make the parser reserve
+    // memory the file could never fill.
+    static size_t min_value_bytes(uint32_t t) {
+        switch (t) {
+        case GV_U8: case GV_I8: case GV_BOOL: return 1;
+        case GV_U16: case GV_I16: return 2;
+        case GV_U32: case GV_I32: case GV_F32: return 4;
+        case GV_U64: case GV_I64: case GV_F64: return 8;
+        case GV_STR: return 8;   // the length prefix
+        case GV_ARR: return 12;  // element type + count
+        default: return 0;
+        }
+    }
     template <class T>
     bool rd(T *v) {
         if (!need(sizeof(T))) return false;
@@ -223,7 +257,9 @@ class GgufFile {
             uint32_t et;
             uint64_t n;
             if (depth > 8 || !rd(&et) || !rd(&n)) return fail("bad GGUF array");
-            if (n > size) return fail("bad GGUF array length");
+            const size_t mb = min_value_bytes(et);
+            if (mb == 0) return fail("Unknown GGUF metadata value type");
+            if (n > remaining() / mb) return fail("bad GGUF array length");
             v->arr.resize((size_t)n);
             for (uint64_t i = 0; i < n; i++)
                 if (!rd_value(et, &v->arr[(size_t)i], depth + 1)) return false;
@@ -237,7 +273,9 @@ class GgufFile {
         pos = 4;
         uint64_t n_tensors, n_kv;
         if (!rd(&version) || !rd(&n_tensors) || !rd(&n_kv)) return false;
-        if (n_tensors > size || n_kv > size) return fail("bad GGUF counts");
+        // a key/value pair takes at least 8 + 4 + 1 bytes, a tensor info
+        // 8 (name length) + 4 (rank) + 4 (type) + 8 (offset)
+        if (n_kv > remaining() / 13) return fail("bad GGUF counts");
         for (uint64_t i = 0; i < n_kv; i++) {
             std::string key;
             uint32_t t;
@@ -245,6 +283,7 @@ class GgufFile {
             if (!rd_str(&key) || !rd(&t) || !rd_value(t, &v, 0)) return false;
             meta[key] = std::move(v);
         }
+        if (n_tensors > remaining() / 24) return fail("bad GGUF counts");
         tensors.resize((size_t)n_tensors);
         for (uint64_t i = 0; i < n_tensors; i++) {
             GgufTensor &T = tensors[(size_t)i];
@@ -283,9 +322,7 @@ static GgufConfig gguf_config(const GgufFile &G) {
         if (hc->type == GV_ARR)
             for (const GgufValue &e : hc->arr) {
                 uint32_t v;
-                bool neg = (e.type == GV_I8 || e.type == GV_I16 || e.type == GV_I32 || e.type == GV_I64) &&
-                           (int64_t)e.u < 0;
-                if (!neg && e.as_u32(&v) && (e.type != GV_U64 || e.u <= 0xFFFFFFFFull)) c.n_heads = std::max(c.n_heads, v);
+                if (e.as_u32_elem(&v)) c.n_heads = std::max(c.n_heads, v);
             }
     c.n_kv = G.get_u32(p + "attention.head_count_kv", c.n_heads);
     const uint32_t rope_dim = G.get_u32(p + "rope.dimension_count", 0);
@@ -294,7 +331,11 @@ static GgufConfig gguf_config(const GgufFile &G) {
     c.value_dim = G.get_u32(p + "attention.value_length", c.head_dim);
     c.vocab = G.get_u32(p + "vocab_size", 0);
     if (const GgufValue *tk = G.get("tokenizer.ggml.tokens"))
-        if (tk->type == GV_ARR) c.vocab = std::max(c.vocab, (uint32_t)tk->arr.size());
+        if (tk->type == GV_ARR) {  // as_string_array: string entries only
+            uint32_t n = 0;
+            for (const GgufValue &e : tk->arr) n += e.type == GV_STR ? 1u : 0u;
+            c.vocab = std::max(c.vocab, n);
+        }
     if (const GgufValue *ff = G.get(p + "feed_forward_length")) {
         uint32_t v;
         if (ff->as_u32(&v)) {

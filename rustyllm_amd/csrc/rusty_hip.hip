@@ -1652,6 +1652,9 @@ int rusty_hip_attention_noalloc(const float *query, uintptr_t query_len, const f
                 (unsigned)RH_NOALLOC_SCRATCH_BYTES);
         return 0;
     }
+    // the inputs may come from any stream of the caller's: all work already
+    // submitted to the device completes first
+    RH_CHECK(hipDeviceSynchronize());
     if (!attn_call_launch(C, scr, g.s)) return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
@@ -1957,6 +1960,7 @@ struct Resident {
     float *ex = nullptr;  // exact-attention scratch
     int ex_cap = 0;
     uint32_t *sync = nullptr;  // streamed exact attention: epoch, ticket, timeouts, flags [n_kv][ex_cap/64]
+    size_t sync_words = 0;
     float *am_v = nullptr;
     int32_t *am_i = nullptr;
     uint32_t *ticket = nullptr;
@@ -2038,6 +2042,24 @@ static void r_invalidate_graphs() {
     R.graphs.clear();
 }
 void r_invalidate_graphs_extern() { r_invalidate_graphs(); }
+
+// Whether every streamed attention launch since the last check finished its
+// bounded waits.  A wait that ran out marked its launch in sync[2] and the
+// launch ended with wrong values; the call that ran it must then report
+// failure (return 0, like the Metal decoder's incomplete command buffer,
+// metal_backend.m:1254-1257).  The whole flag block is cleared so the next
+// launch starts from epoch 0 with no stale flags; the captured graphs read
+// the epoch at run time and stay valid.  The stream must be idle.
+static int r_stream_ok() {
+    if (!R.sync) return 1;
+    uint32_t mark = 0;
+    RH_CHECK(hipMemcpy(&mark, R.sync + 2, 4, hipMemcpyDeviceToHost));
+    if (mark == 0) return 1;
+    if (debug_on()) fprintf(stderr, "[rusty_hip] streamed attention: a bounded wait ran out; results invalid\n");
+    RH_CHECK(hipMemset(R.sync, 0, R.sync_words * 4));
+    RH_CHECK(hipDeviceSynchronize());
+    return 0;
+}
 
 static int dt_to_fmt(uint32_t dt) {
     switch (dt) {
@@ -2927,6 +2949,7 @@ static int r_setup(uint32_t n_layers, uint32_t dim, uint32_t n_heads, uint32_t n
     const size_t sync_words = 3 + (size_t)n_kv_heads * (R.ex_cap / 64);
     if (!r_alloc((void **)&R.sync, sync_words * 4)) return 0;
     RH_CHECK(hipMemset(R.sync, 0, sync_words * 4));
+    R.sync_words = sync_words;
     R.am_blocks = std::min<int>(256, (int)((vocab + 255) / 256));
     if (!r_alloc((void **)&R.am_v, R.am_blocks * 4) || !r_alloc((void **)&R.am_i, R.am_blocks * 4) ||
         !r_alloc((void **)&R.ticket, 64) || !r_alloc((void **)&R.st, sizeof(StepState)) ||
@@ -3135,7 +3158,7 @@ int rusty_hip_resident_decode(const float *x_embed, uint32_t pos, uint32_t start
     if (want_logits) RH_CHECK(hipMemcpyAsync(logits_out, R.logits, (size_t)R.vocab * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
-    return 1;
+    return r_stream_ok();
 }
 
 int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32_t start_pos, uint32_t n_gen,
@@ -3177,7 +3200,7 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
     if (logits_out) RH_CHECK(hipMemcpyAsync(logits_out, R.logits, (size_t)R.vocab * 4, hipMemcpyDeviceToHost, g.s));
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
-    return 1;
+    return r_stream_ok();
 }
 
 int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos) {
@@ -3228,6 +3251,22 @@ int rusty_hip_resident_time_decode(uint32_t n_tokens, float penalty, double *ms)
     (void)hipEventDestroy(b);
     *ms = t;
     prof_drain();
+    return r_stream_ok();
+}
+
+// Test hook for the streamed attention's timeout path: marks the next
+// streamed launch (the epoch it will read) as timed out, as a bounded wait
+// that ran out would, so every wait of that launch returns at once and the
+// launch ends normally with invalid results.  0 when no streamed launch is
+// configured.
+int rusty_hip_debug_stream_mark(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!R.ready || !R.sync) return 0;
+    RH_CHECK(hipStreamSynchronize(g.s));
+    uint32_t ep = 0;
+    RH_CHECK(hipMemcpy(&ep, R.sync, 4, hipMemcpyDeviceToHost));
+    const uint32_t mark = ep + 1;
+    RH_CHECK(hipMemcpy(R.sync + 2, &mark, 4, hipMemcpyHostToDevice));
     return 1;
 }
 
@@ -3495,7 +3534,7 @@ int rusty_hip_bench_attention(uint32_t heads, uint32_t kv_mul, uint32_t head_dim
 // ---- GGUF on-disk path (src/gguf.rs, src/model.rs:3573-3860, :5180-5420) -------------
 
 // Model facts of a GGUF file as the reference's loaders see them.
-int rusty_hip_gguf_summary(const char *path, RustyGgufSummary *out) {
+static int gguf_summary_impl(const char *path, RustyGgufSummary *out) {
     if (!path || !out) return 0;
     GgufFile G;
     if (!G.open_path(path)) {
@@ -3543,6 +3582,17 @@ int rusty_hip_gguf_summary(const char *path, RustyGgufSummary *out) {
     out->fused_qkv = G.find("blk.0.attn_qkv.weight") ? 1 : 0;
     out->qkv_bias = (G.find("blk.0.attn_q.bias") || G.find("blk.0.attn_qkv.bias")) ? 1 : 0;
     return 1;
+}
+
+// GGUF summary: a parse or allocation failure (std::bad_alloc included) returns 0
+// instead of leaving through the C ABI.
+int rusty_hip_gguf_summary(const char *path, RustyGgufSummary *out) {
+    try {
+        return gguf_summary_impl(path, out);
+    } catch (...) {
+        if (debug_on()) fprintf(stderr, "[rusty_hip] gguf_summary_impl: exception\n");
+        return 0;
+    }
 }
 
 }  // extern "C"
@@ -3627,7 +3677,7 @@ static std::vector<float> rope_table(const GgufConfig &c, bool yarn, float *conc
 
 extern "C" {
 
-int rusty_hip_resident_load_gguf(const char *path, uint32_t max_len) {
+static int resident_load_gguf_impl(const char *path, uint32_t max_len) {
     if (!path || max_len == 0) return 0;
     GgufFile G;
     if (!G.open_path(path)) {
@@ -3799,6 +3849,17 @@ int rusty_hip_resident_load_gguf(const char *path, uint32_t max_len) {
         return 0;
     if (!rusty_hip_resident_set_embedding(emb.p, (uintptr_t)emb.len, emb.type)) return 0;
     return 1;
+}
+
+// GGUF resident load: a parse or allocation failure (std::bad_alloc included) returns 0
+// instead of leaving through the C ABI.
+int rusty_hip_resident_load_gguf(const char *path, uint32_t max_len) {
+    try {
+        return resident_load_gguf_impl(path, max_len);
+    } catch (...) {
+        if (debug_on()) fprintf(stderr, "[rusty_hip] resident_load_gguf_impl: exception\n");
+        return 0;
+    }
 }
 
 }  // extern "C"

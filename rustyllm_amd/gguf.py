@@ -205,7 +205,9 @@ def config_from_gguf(g: GGUFFile) -> dict:
     head_dim = g.get_u32(f"{p}.attention.key_length", default_hd)
     value_dim = g.get_u32(f"{p}.attention.value_length", head_dim)
     tok = g.metadata.get("tokenizer.ggml.tokens")
-    vocab = max(g.get_u32(f"{p}.vocab_size", 0), len(tok.value) if tok is not None and tok.vtype == ARRAY else 0)
+    # as_string_array (src/gguf.rs:161-176): only the string entries count
+    n_tok = sum(1 for v in tok.value if v.vtype == STRING) if tok is not None and tok.vtype == ARRAY else 0
+    vocab = max(g.get_u32(f"{p}.vocab_size", 0), n_tok)
     ff = g.metadata.get(f"{p}.feed_forward_length")
     hidden = 0
     if ff is not None:

@@ -34,7 +34,7 @@ SYMBOLS = [
     "rusty_hip_moe_ffn", "rusty_hip_resident_configure_moe", "rusty_hip_resident_set_moe_layer",
     "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
     "rusty_hip_bench_attention", "rusty_hip_attention_noalloc", "rusty_hip_gguf_summary",
-    "rusty_hip_resident_load_gguf", "rusty_hip_resident_enable_bf16",
+    "rusty_hip_resident_load_gguf", "rusty_hip_resident_enable_bf16", "rusty_hip_debug_stream_mark",
 ]
 
 
@@ -91,6 +91,7 @@ _sig("rusty_hip_debug_silu_mul", _i, _p, _p, _u, _p)
 _sig("rusty_hip_debug_rope", _i, _p, _p, _u32, _u32, _u32, _u32, _p, _u32)
 _sig("rusty_hip_debug_greedy", _i, _p, _u, _p, _u32, _f, _p)
 _sig("rusty_hip_debug_f16", _i, _p, _u, _p)
+_sig("rusty_hip_debug_stream_mark", _i)
 _sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f,
      _f)
 _sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
@@ -628,3 +629,9 @@ def debug_f16(h):
     out = np.zeros(h.size, np.float32)
     assert lib.rusty_hip_debug_f16(_ptr(h), h.size, _ptr(out)) == 1
     return out
+
+
+def debug_stream_mark() -> bool:
+    """Marks the resident decoder's next streamed attention launch as timed
+    out (the failure path's test hook)."""
+    return lib.rusty_hip_debug_stream_mark() == 1

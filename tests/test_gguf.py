@@ -221,3 +221,54 @@ def test_native_parser_gptoss_and_hand_file(tmp_path):
     assert hip.gguf_summary(str(bad)) is None
     bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 5))  # truncated metadata
     assert hip.gguf_summary(str(bad)) is None
+
+
+def test_head_count_arrays_of_every_integer_type_and_corrupt_counts(tmp_path):
+    """Config::from_gguf takes n_heads as the max over MetaValue::as_u32_array
+    of a per-layer head_count array, which keeps non-negative signed entries
+    (I8/I16 included) and drops negative ones and 64-bit values above
+    u32::MAX (src/gguf.rs:188-207).  The vocabulary counts only the string
+    entries of tokenizer.ggml.tokens (as_string_array, :161-176): an array of
+    arrays counts none.  Both parsers agree.  Then counts that no file of this
+    size could hold (metadata pairs, an array's length, tensor infos) are
+    refused at once, with no allocation."""
+    from rustyllm_amd import hip
+    fmt = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 10: "Q", 11: "q"}
+    cases = [(1, [-1, 40, 12], 40), (3, [-300, 36, 7], 36), (5, [-5, 24], 24), (11, [2 ** 33, -2, 30], 30),
+             (10, [2 ** 33, 28], 28), (0, [200, 3], 200), (2, [1000, 9], 1000), (4, [4000000000, 1], 4000000000)]
+    for et, vals, want in cases:
+        arr = struct.pack("<IIQ", 9, et, len(vals)) + b"".join(struct.pack("<" + fmt[et], v) for v in vals)
+        md = [_s("general.architecture") + struct.pack("<I", 8) + _s("llama"),
+              _s("llama.embedding_length") + struct.pack("<II", 4, 4096),
+              _s("llama.attention.head_count") + arr,
+              _s("tokenizer.ggml.tokens") + struct.pack("<IIQ", 9, 8, 3) + _s("a") + _s("bb") + _s("ccc")]
+        p = tmp_path / f"hc{et}.gguf"
+        p.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, len(md)) + b"".join(md) + b"\0" * 64)
+        g = gguf.GGUFFile(str(p))
+        c = gguf.config_from_gguf(g)
+        g.close()
+        assert c["n_heads"] == want and c["vocab"] == 3, (et, c["n_heads"])
+        s = hip.gguf_summary(str(p))
+        assert s is not None and s.n_heads == want and s.vocab == 3, (et, s.n_heads)
+        assert s.head_dim == c["head_dim"] == 4096 // want
+    # a token array whose entries are arrays (not strings) counts zero
+    md2 = [_s("tokenizer.ggml.tokens") + struct.pack("<IIQ", 9, 9, 2) + struct.pack("<IQ", 8, 1) + _s("x")
+           + struct.pack("<IQ", 8, 1) + _s("y"), _s("llama.vocab_size") + struct.pack("<II", 4, 1)]
+    p2 = tmp_path / "nested_tokens.gguf"
+    p2.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, len(md2)) + b"".join(md2) + b"\0" * 64)
+    g2 = gguf.GGUFFile(str(p2))
+    assert gguf.config_from_gguf(g2)["vocab"] == 1
+    g2.close()
+    assert hip.gguf_summary(str(p2)).vocab == 1
+    # counts far beyond what the file holds
+    bad = tmp_path / "huge.gguf"
+    bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 2 ** 60) + b"\0" * 256)
+    assert hip.gguf_summary(str(bad)) is None
+    bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 2 ** 50, 0) + b"\0" * 256)
+    assert hip.gguf_summary(str(bad)) is None
+    bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + _s("k") + struct.pack("<IIQ", 9, 8, 2 ** 40)
+                    + b"\0" * 256)
+    assert hip.gguf_summary(str(bad)) is None
+    bad.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + _s("k") + struct.pack("<IIQ", 9, 10, 33)
+                    + b"\0" * 256)  # 33 u64 entries need 264 bytes, 256 are left
+    assert hip.gguf_summary(str(bad)) is None

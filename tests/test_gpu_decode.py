@@ -149,3 +149,50 @@ def test_weight_cache_clear_leaves_resident_working(hip, exact):
     hip.weight_cache_clear()
     g2, _ = res.generate(toks[:4], 8, penalty=1.1, start_pos=20)
     assert list(g_toks) == list(g2)
+
+
+def test_streamed_attention_timeout_fails_loudly(hip, exact):
+    """A streamed attention launch whose bounded wait runs out ends with
+    invalid values; the call that ran it must return 0, as the Metal decoder
+    does for a command buffer that did not complete
+    (metal_backend.m:1254-1257).  The condition is forced from the host
+    (rusty_hip_debug_stream_mark marks the next launch as timed out, so its
+    waits return at once and every kernel exits normally).  A re-run of the
+    failed step, and every step after it, is bit-exact again."""
+    model, res, orc = _pair("tiny-q4km", 128, seed=17)
+    emb, emb_t = model["token_embd"]
+    dim = model["config"]["dim"]
+    toks = synth.token_ids(9, 40, model["config"]["vocab"])
+
+    def embed(t):
+        return O.dequant_row(emb_t, emb[int(t) * O.row_bytes(emb_t, dim):], dim)
+
+    # the failure path is the streamed launch's: this configuration takes it
+    hip.profile_enable(True)
+    try:
+        res.decode(embed(toks[0]), 0, 0, True)
+        names = hip.profile_results()
+    finally:
+        hip.profile_enable(False)
+    assert "attn_exact_stream" in names, sorted(names)
+    for pos, t in enumerate(toks):
+        if pos in (6, 23):
+            assert hip.debug_stream_mark()
+            with pytest.raises(RuntimeError):
+                res.decode(embed(t), pos, 0, True)
+        g = res.decode(embed(t), pos, 0, True)
+        r = orc.forward(int(t), pos)
+        assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (pos, np.max(np.abs(g - r)))
+    # the device-token path (generate) and the timed loop report it too
+    prompt = synth.token_ids(10, 12, model["config"]["vocab"])
+    o_toks, o_logits = orc.generate(prompt, 16, penalty=1.1)
+    assert hip.debug_stream_mark()
+    with pytest.raises(RuntimeError):
+        res.generate(prompt, 16, penalty=1.1)
+    g_toks, g_logits = res.generate(prompt, 16, penalty=1.1)
+    assert list(g_toks) == list(o_toks)
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))
+    assert hip.debug_stream_mark()
+    with pytest.raises(RuntimeError):
+        res.time_decode(4, penalty=1.1)
+    assert res.time_decode(4, penalty=1.1) > 0.0

@@ -75,3 +75,32 @@ def test_noalloc_rejects_oversize_and_bad_args(hip):
     lib = hip.lib
     assert lib.rusty_hip_attention_noalloc(None, 4, tk.data_ptr(), 4, tk.data_ptr(), 4, None, 0, out.data_ptr(), 4,
                                            1, 1, 64, 64, 64, 64, 1, 0, 0, 0.125, 0) == 0
+
+
+def test_noalloc_allocates_no_device_memory(hip, mode):
+    """The property the entry point exists for: after one warm-up call, calls
+    of every case leave the device's free memory exactly where it was."""
+    import torch
+    dev = torch.device("cuda:0")
+    bufs = []
+    for i, (heads, n_kv, hd, slots, st, en, sk) in enumerate(CASES):
+        q, k, v, s = _inputs(heads, n_kv, hd, slots, 200 + i, sk)
+        t = [torch.from_numpy(a).to(dev) for a in (q, k, v)]
+        t.append(torch.from_numpy(s).to(dev) if sk else None)
+        t.append(torch.zeros(heads * hd, dtype=torch.float32, device=dev))
+        bufs.append(t)
+    torch.cuda.synchronize()
+
+    def run_all():
+        for (heads, n_kv, hd, slots, st, en, sk), (tq, tk, tv, ts, out) in zip(CASES, bufs):
+            scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+            assert hip.attention_noalloc_dev(tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                                             ts.data_ptr() if sk else 0, out.data_ptr(), heads, heads // n_kv, hd,
+                                             hd, n_kv * hd, n_kv * hd, slots, st, en, scale)
+
+    run_all()  # warm-up: library initialisation and kernel loading happen here
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        run_all()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
