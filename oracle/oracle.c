@@ -657,9 +657,96 @@ int64_t orc_row_bytes(int dtype, int64_t cols) {
     }
 }
 
+/* dot_mxfp4_f32_scalar for 8 rows at once: each row's running sum takes
+ * exactly the steps of the one-row function above, in its order
+ * (sum += (LUT[n] * scale) * x, element by element); AVX2 lane r is row r.
+ * The rows only share the loop, which gives the CPU eight independent add
+ * chains instead of one (the checker's speed; no value changes).  Per block
+ * each row's 32 values LUT[n] * scale are built in registers (element 2i is
+ * the low nibble of byte i, 2i+1 the high one; the table's second half is
+ * the first with the sign bit set, -0.0 included, so LUT[n] =
+ * LUT[n & 7] | (n & 8) << 28 exactly), then an 8 x 8 transpose per quarter
+ * turns them into one vector per element index.  (Shuffles, not gathers:
+ * AVX2 gathers are slow on the EPYC hosts of the GPU boxes.) */
+__attribute__((target("avx2,fma")))
+static inline void transpose8_ps(__m256 *r) {
+    __m256 t0 = _mm256_unpacklo_ps(r[0], r[1]), t1 = _mm256_unpackhi_ps(r[0], r[1]);
+    __m256 t2 = _mm256_unpacklo_ps(r[2], r[3]), t3 = _mm256_unpackhi_ps(r[2], r[3]);
+    __m256 t4 = _mm256_unpacklo_ps(r[4], r[5]), t5 = _mm256_unpackhi_ps(r[4], r[5]);
+    __m256 t6 = _mm256_unpacklo_ps(r[6], r[7]), t7 = _mm256_unpackhi_ps(r[6], r[7]);
+    __m256 u0 = _mm256_shuffle_ps(t0, t2, 0x44), u1 = _mm256_shuffle_ps(t0, t2, 0xEE);
+    __m256 u2 = _mm256_shuffle_ps(t1, t3, 0x44), u3 = _mm256_shuffle_ps(t1, t3, 0xEE);
+    __m256 u4 = _mm256_shuffle_ps(t4, t6, 0x44), u5 = _mm256_shuffle_ps(t4, t6, 0xEE);
+    __m256 u6 = _mm256_shuffle_ps(t5, t7, 0x44), u7 = _mm256_shuffle_ps(t5, t7, 0xEE);
+    r[0] = _mm256_permute2f128_ps(u0, u4, 0x20);
+    r[1] = _mm256_permute2f128_ps(u1, u5, 0x20);
+    r[2] = _mm256_permute2f128_ps(u2, u6, 0x20);
+    r[3] = _mm256_permute2f128_ps(u3, u7, 0x20);
+    r[4] = _mm256_permute2f128_ps(u0, u4, 0x31);
+    r[5] = _mm256_permute2f128_ps(u1, u5, 0x31);
+    r[6] = _mm256_permute2f128_ps(u2, u6, 0x31);
+    r[7] = _mm256_permute2f128_ps(u3, u7, 0x31);
+}
+
+/* orc_mxfp4_scale for every byte, filled by orc_matvec before its threads
+ * start (the same function's values, so nothing changes but the lookup) */
+static float g_mxfp4_scale[256];
+static int g_mxfp4_scale_ready = 0;
+static void mxfp4_scale_table_init(void) {
+    if (g_mxfp4_scale_ready) return;
+    for (int e = 0; e < 256; e++) g_mxfp4_scale[e] = orc_mxfp4_scale((uint8_t)e);
+    g_mxfp4_scale_ready = 1;
+}
+
+__attribute__((target("avx2,fma")))
+static void dot_mxfp4_f32_scalar_rows8(const uint8_t *w, int64_t rb, const float *x, int64_t n, float *out) {
+    const int64_t nb = n / 32;
+    const __m256 lut = _mm256_loadu_ps(MXFP4_LUT);
+    const __m256i sign = _mm256_set1_epi32((int)0x80000000u);
+    const __m128i m4 = _mm_set1_epi8(0x0F);
+    __m256 sum = _mm256_setzero_ps();
+    for (int64_t b = 0; b < nb; b++) {
+        __m256 v[4][8];  /* [quarter][row]: elements 8q..8q+7 of row r */
+        for (int r = 0; r < 8; r++) {
+            const uint8_t *blk = w + r * rb + b * 17;
+            const __m256 sc = _mm256_set1_ps(g_mxfp4_scale[blk[16]]);
+            __m128i bytes;
+            memcpy(&bytes, blk, 16);
+            const __m128i lo = _mm_and_si128(bytes, m4), hi = _mm_and_si128(_mm_srli_epi16(bytes, 4), m4);
+            const __m128i e0 = _mm_unpacklo_epi8(lo, hi), e1 = _mm_unpackhi_epi8(lo, hi); /* elements 0..15, 16..31 */
+            const __m128i parts[4] = {e0, _mm_srli_si128(e0, 8), e1, _mm_srli_si128(e1, 8)};
+            for (int q = 0; q < 4; q++) {
+                const __m256i idx = _mm256_cvtepu8_epi32(parts[q]);
+                const __m256 val = _mm256_or_ps(_mm256_permutevar8x32_ps(lut, idx),
+                                                _mm256_castsi256_ps(_mm256_and_si256(_mm256_slli_epi32(idx, 28), sign)));
+                v[q][r] = _mm256_mul_ps(val, sc);
+            }
+        }
+        const float *xb = x + b * 32;
+        for (int q = 0; q < 4; q++) {
+            transpose8_ps(v[q]);
+            for (int jj = 0; jj < 8; jj++)
+                sum = _mm256_add_ps(sum, _mm256_mul_ps(v[q][jj], _mm256_set1_ps(xb[q * 8 + jj])));
+        }
+    }
+    _mm256_storeu_ps(out, sum);
+}
+
 void orc_matvec(int dtype, const uint8_t *w, const float *x, int64_t rows, int64_t cols, float *out, int threads) {
     if (threads <= 0) threads = g_threads;
     int64_t rb = orc_row_bytes(dtype, cols);
+    if (dtype == ORC_MXFP4) {
+        /* scheduling only: groups of 8 rows, each row's value as the
+         * one-row kernel's (a row's value does not depend on the split) */
+        mxfp4_scale_table_init();
+        if (threads > rows) threads = (int)rows;
+        int serial = threads <= 1 || rows < (int64_t)threads * 8;
+        int64_t groups = rows / 8;
+#pragma omp parallel for schedule(dynamic, 8) num_threads(threads) if (!serial)
+        for (int64_t gi = 0; gi < groups; gi++) dot_mxfp4_f32_scalar_rows8(w + gi * 8 * rb, rb, x, cols, out + gi * 8);
+        for (int64_t r = groups * 8; r < rows; r++) out[r] = orc_dot_mxfp4_f32_scalar(w + r * rb, x, cols);
+        return;
+    }
     int use_xq = (dtype == ORC_Q8_0 || dtype == ORC_Q4_K || dtype == ORC_Q6_K) && cols >= 256 && cols % 256 == 0;
     int8_t *qs = NULL;
     float *dx = NULL;
@@ -997,10 +1084,16 @@ void orc_attention_over_kv_heads_bf16(const float *q, const uint16_t *keys, cons
 }
 
 /* per-head sink attention loop, model.rs:6812-6833 (output zeroed first) */
+/* The gpt-oss per-head sink loop (model.rs:6812-6833).  The reference runs
+ * the heads one after another; each writes only its own output band, so the
+ * checker runs them on its threads with the same values. */
 void orc_attention_sink_heads(const float *q, const float *keys, const float *values, const float *sinks,
                               int64_t ks, int64_t vs, int64_t slots, int64_t hd, int64_t vd, int64_t n_heads,
                               int64_t kv_mul, int64_t start_t, int64_t end_t, float scale, float *out) {
     memset(out, 0, (size_t)(n_heads * vd) * 4);
+    int nt = g_threads < (int)n_heads ? g_threads : (int)n_heads;
+    int64_t work = (end_t >= start_t ? end_t - start_t + 1 : 0) * n_heads;
+#pragma omp parallel for schedule(static) num_threads(nt > 0 ? nt : 1) if (n_heads > 1 && nt > 1 && work >= 4096)
     for (int64_t h = 0; h < n_heads; h++) {
         int64_t kvh = h / kv_mul;
         orc_online_attention_with_sink(q + h * hd, keys + kvh * hd, values + kvh * vd, ks, vs, slots, hd, vd,
@@ -1427,6 +1520,144 @@ int64_t orc_model_generate(orc_model *m, const uint32_t *prompt, int64_t n_promp
     if (last_logits && n_gen == 0) memcpy(last_logits, logits, (size_t)vocab * 4);
     free(logits);
     return produced;
+}
+
+/* ------------------------------------------------------------------------ */
+/* gpt-oss decode model: forward_gpt_oss_into, model.rs:6733-6908 (and, with
+ * want_logits = 0, forward_prefill_gpt_oss = forward_hidden_gpt_oss_impl
+ * without the final norm, model.rs:10286-10295: the same layer loop, no
+ * head), with the reference's KVCache::with_sliding_window(max_len, window)
+ * (model.rs:1363-1385): a window > 0 makes every layer's cache a ring of
+ * storage_len_for(max_len, window) = min(window, max_len) slots, position p
+ * at slot p % storage (slot_for_pos, :1458-1464), and every layer's attention
+ * scans that ring with slot_count = storage (:6793-6810); even layers start
+ * at attention_start_pos(pos, window), odd layers at 0.                      */
+struct orc_gptoss {
+    orc_gptoss_config c;
+    orc_gptoss_layer *layers;
+    const float *output_norm;
+    const uint8_t *output_w, *embd;
+    uint32_t output_type, embd_type;
+    float *inv_freq;
+    int64_t storage;
+    float **k, **v;
+    float *x, *xn, *xn2, *q, *kk, *vv, *attn, *proj, *router, *gate, *up, *moe;
+};
+
+orc_gptoss *orc_gptoss_create(const orc_gptoss_config *cfg) {
+    orc_gptoss *m = (orc_gptoss *)calloc(1, sizeof(orc_gptoss));
+    m->c = *cfg;
+    int64_t max_len = cfg->max_len > 0 ? cfg->max_len : 1;
+    m->storage = cfg->sliding_window > 0 ? (cfg->sliding_window < max_len ? cfg->sliding_window : max_len) : max_len;
+    int64_t kdim = (int64_t)cfg->n_kv_heads * cfg->head_dim, vdim = (int64_t)cfg->n_kv_heads * cfg->value_dim;
+    m->layers = (orc_gptoss_layer *)calloc((size_t)cfg->n_layers, sizeof(orc_gptoss_layer));
+    m->k = (float **)calloc((size_t)cfg->n_layers, sizeof(float *));
+    m->v = (float **)calloc((size_t)cfg->n_layers, sizeof(float *));
+    for (int l = 0; l < cfg->n_layers; l++) {
+        m->k[l] = (float *)calloc((size_t)(m->storage * kdim), 4);
+        m->v[l] = (float *)calloc((size_t)(m->storage * vdim), 4);
+    }
+    int64_t dim = cfg->dim, hid = cfg->hidden_dim;
+    m->x = (float *)calloc((size_t)dim, 4);
+    m->xn = (float *)calloc((size_t)dim, 4);
+    m->xn2 = (float *)calloc((size_t)dim, 4);
+    m->q = (float *)calloc((size_t)cfg->n_heads * cfg->head_dim, 4);
+    m->kk = (float *)calloc((size_t)kdim, 4);
+    m->vv = (float *)calloc((size_t)vdim, 4);
+    m->attn = (float *)calloc((size_t)cfg->n_heads * cfg->value_dim, 4);
+    m->proj = (float *)calloc((size_t)dim, 4);
+    m->router = (float *)calloc((size_t)cfg->n_experts, 4);
+    m->gate = (float *)calloc((size_t)hid, 4);
+    m->up = (float *)calloc((size_t)hid, 4);
+    m->moe = (float *)calloc((size_t)dim, 4);
+    m->inv_freq = (float *)calloc((size_t)cfg->head_dim, 4);
+    return m;
+}
+
+void orc_gptoss_free(orc_gptoss *m) {
+    if (!m) return;
+    for (int l = 0; l < m->c.n_layers; l++) {
+        free(m->k[l]);
+        free(m->v[l]);
+    }
+    free(m->k); free(m->v); free(m->layers);
+    free(m->x); free(m->xn); free(m->xn2); free(m->q); free(m->kk); free(m->vv); free(m->attn);
+    free(m->proj); free(m->router); free(m->gate); free(m->up); free(m->moe); free(m->inv_freq);
+    free(m);
+}
+
+int orc_gptoss_set_layer(orc_gptoss *m, int32_t l, const orc_gptoss_layer *layer) {
+    if (l < 0 || l >= m->c.n_layers) return 0;
+    m->layers[l] = *layer;
+    return 1;
+}
+
+int orc_gptoss_set_output(orc_gptoss *m, const float *output_norm, const uint8_t *output_w, uint32_t output_type,
+                          const uint8_t *embd, uint32_t embd_type, const float *inv_freq) {
+    m->output_norm = output_norm;
+    m->output_w = output_w;
+    m->output_type = output_type;
+    m->embd = embd;
+    m->embd_type = embd_type;
+    memcpy(m->inv_freq, inv_freq, (size_t)(m->c.head_dim / 2) * 4);
+    return 1;
+}
+
+int64_t orc_gptoss_storage(const orc_gptoss *m) { return m->storage; }
+float *orc_gptoss_kv(orc_gptoss *m, int32_t layer, int32_t which) { return which ? m->v[layer] : m->k[layer]; }
+
+void orc_gptoss_forward(orc_gptoss *m, uint32_t token, int64_t pos, float *logits, int want_logits) {
+    const orc_gptoss_config *c = &m->c;
+    const int64_t dim = c->dim, hd = c->head_dim, vd = c->value_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+    const int64_t hid = c->hidden_dim, kdim = nkv * hd, vdim = nkv * vd, kv_mul = nh / nkv;
+    const int th = g_threads;
+    orc_dequant_row((int)m->embd_type, m->embd + (int64_t)token * orc_row_bytes((int)m->embd_type, dim), m->x, dim);
+    const int64_t slot = c->sliding_window > 0 ? pos % m->storage : pos;
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int l = 0; l < c->n_layers; l++) {
+        const orc_gptoss_layer *L = &m->layers[l];
+        orc_rms_norm(m->x, L->attn_norm, c->eps, dim, m->xn);
+        orc_matvec((int)L->wq_type, L->wq, m->xn, nh * hd, dim, m->q, th);
+        orc_matvec((int)L->wk_type, L->wk, m->xn, kdim, dim, m->kk, th);
+        orc_matvec((int)L->wv_type, L->wv, m->xn, vdim, dim, m->vv, th);
+        for (int64_t i = 0; i < nh * hd; i++) m->q[i] += L->bq[i];
+        for (int64_t i = 0; i < kdim; i++) m->kk[i] += L->bk[i];
+        for (int64_t i = 0; i < vdim; i++) m->vv[i] += L->bv[i];
+        orc_rope_gpt_oss(m->q, m->kk, pos, hd, nh, nkv, c->concentration, m->inv_freq);
+        memcpy(m->k[l] + slot * kdim, m->kk, (size_t)kdim * 4);
+        memcpy(m->v[l] + slot * vdim, m->vv, (size_t)vdim * 4);
+        const int64_t start = l % 2 == 0 ? orc_attention_start_pos(pos, c->sliding_window) : 0;
+        orc_attention_sink_heads(m->q, m->k[l], m->v[l], L->sinks, kdim, vdim, m->storage, hd, vd, nh, kv_mul, start,
+                                 pos, scale, m->attn);
+        orc_matvec((int)L->wo_type, L->wo, m->attn, dim, nh * vd, m->proj, th);
+        for (int64_t i = 0; i < dim; i++) m->x[i] += m->proj[i] + L->bo[i];
+        orc_rms_norm(m->x, L->post_attn_norm, c->eps, dim, m->xn2);
+        /* router: gate_inp + bias, top-k in total order, softmax over the
+         * chosen (model.rs:6846-6857) */
+        orc_matvec((int)L->router_type, L->router, m->xn2, c->n_experts, dim, m->router, th);
+        for (int64_t i = 0; i < c->n_experts; i++) m->router[i] += L->router_bias[i];
+        int32_t sel[64];
+        float val[64], prob[64];
+        orc_select_top_logits(m->router, c->n_experts, c->top_k, sel, val);
+        orc_softmax_selected(val, c->top_k, prob);
+        const int64_t rg = orc_row_bytes((int)L->exps_type, dim) * hid;
+        const int64_t rd = orc_row_bytes((int)L->exps_type, hid) * dim;
+        memset(m->moe, 0, (size_t)dim * 4);
+        for (int64_t s = 0; s < c->top_k; s++) {
+            const int64_t e = sel[s];
+            const float *gb = L->gate_exps_bias + e * hid, *ub = L->up_exps_bias + e * hid;
+            const float *db = L->down_exps_bias + e * dim;
+            orc_matvec((int)L->exps_type, L->gate_exps + e * rg, m->xn2, hid, dim, m->gate, th);
+            orc_matvec((int)L->exps_type, L->up_exps + e * rg, m->xn2, hid, dim, m->up, th);
+            for (int64_t i = 0; i < hid; i++) m->gate[i] = orc_swiglu_gpt_oss(m->gate[i] + gb[i], m->up[i] + ub[i]);
+            orc_matvec((int)L->exps_type, L->down_exps + e * rd, m->gate, dim, hid, m->proj, th);
+            for (int64_t i = 0; i < dim; i++) m->moe[i] += (m->proj[i] + db[i]) * prob[s];
+        }
+        for (int64_t i = 0; i < dim; i++) m->x[i] += m->moe[i];
+    }
+    if (!want_logits) return;
+    orc_rms_norm(m->x, m->output_norm, c->eps, dim, m->xn);
+    orc_matvec((int)m->output_type, m->output_w, m->xn, c->vocab, dim, logits, th);
 }
 
 /* ------------------------------------------------------------------------ */

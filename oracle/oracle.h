@@ -158,6 +158,36 @@ void orc_attention_over_kv_heads_bf16(const float *q, const uint16_t *keys, cons
 int64_t orc_model_generate(orc_model *m, const uint32_t *prompt, int64_t n_prompt, int64_t start_pos,
                            int64_t n_gen, float penalty, uint32_t *out_tokens, float *last_logits);
 
+/* ---- gpt-oss decode model (forward_gpt_oss_into, model.rs:6733-6908) ---- */
+typedef struct {
+    int32_t n_layers, dim, n_heads, n_kv_heads, head_dim, value_dim, hidden_dim, n_experts, top_k, vocab;
+    int32_t max_len;          /* positions; the ring holds min(window, max_len) of them */
+    int32_t sliding_window;   /* even layers attend the last `window` positions */
+    float eps, concentration; /* RMSNorm eps; YaRN concentration of the RoPE table */
+} orc_gptoss_config;
+
+typedef struct {
+    const uint8_t *wq, *wk, *wv, *wo;
+    uint32_t wq_type, wk_type, wv_type, wo_type;
+    const float *bq, *bk, *bv, *bo, *sinks, *attn_norm, *post_attn_norm;
+    const uint8_t *router;
+    uint32_t router_type;
+    const float *router_bias;
+    const uint8_t *gate_exps, *up_exps, *down_exps; /* expert-major [n_experts][rows] */
+    uint32_t exps_type;
+    const float *gate_exps_bias, *up_exps_bias, *down_exps_bias; /* [n_experts][hidden|dim] */
+} orc_gptoss_layer;
+
+typedef struct orc_gptoss orc_gptoss;
+orc_gptoss *orc_gptoss_create(const orc_gptoss_config *cfg);
+void orc_gptoss_free(orc_gptoss *m);
+int orc_gptoss_set_layer(orc_gptoss *m, int32_t l, const orc_gptoss_layer *layer);
+int orc_gptoss_set_output(orc_gptoss *m, const float *output_norm, const uint8_t *output_w, uint32_t output_type,
+                          const uint8_t *embd, uint32_t embd_type, const float *inv_freq);
+int64_t orc_gptoss_storage(const orc_gptoss *m);
+float *orc_gptoss_kv(orc_gptoss *m, int32_t layer, int32_t which);
+void orc_gptoss_forward(orc_gptoss *m, uint32_t token, int64_t pos, float *logits, int want_logits);
+
 /* ---- reference test fixtures (src/simd.rs tests) ------------------------- */
 void orc_make_q4k_weights(int64_t rows, int64_t cols, uint8_t seed, uint8_t *out);
 void orc_make_q4k_weights_dmin(int64_t rows, int64_t cols, uint8_t seed, uint8_t *out);

@@ -97,6 +97,13 @@ _sig("orc_model_forward", None, _p, C.c_uint32, _i64, _p, C.c_int)
 _sig("orc_model_forward_from", None, _p, C.c_uint32, _i64, _i64, _p, C.c_int)
 _sig("orc_model_kv", C.POINTER(C.c_float), _p, C.c_int32, C.c_int32)
 _sig("orc_model_generate", _i64, _p, _p, _i64, _i64, _i64, _f, _p, _p)
+_sig("orc_gptoss_create", _p, _p)
+_sig("orc_gptoss_free", None, _p)
+_sig("orc_gptoss_set_layer", C.c_int, _p, C.c_int32, _p)
+_sig("orc_gptoss_set_output", C.c_int, _p, _p, _p, C.c_uint32, _p, C.c_uint32, _p)
+_sig("orc_gptoss_storage", _i64, _p)
+_sig("orc_gptoss_kv", C.POINTER(C.c_float), _p, C.c_int32, C.c_int32)
+_sig("orc_gptoss_forward", None, _p, C.c_uint32, _i64, _p, C.c_int)
 _sig("orc_make_q4k_weights", None, _i64, _i64, C.c_uint8, _p)
 _sig("orc_make_q4k_weights_dmin", None, _i64, _i64, C.c_uint8, _p)
 _sig("orc_make_q6k_weights", None, _i64, _i64, C.c_uint8, _p)
@@ -305,9 +312,10 @@ def moe_block(x, router, router_t, router_bias, experts, experts_t, hidden, bias
     return moe, idx, probs
 
 
-class OracleGptOss:
-    """forward_gpt_oss_into (model.rs:6733-6908) composed from the C
-    restatements, with the KV cache on the host.  The cache is the
+class OracleGptOssComposed:
+    """forward_gpt_oss_into (model.rs:6733-6908) composed in Python from the
+    C restatements of its parts, with the KV cache on the host; it checks the
+    C layer loop (OracleGptOss) step for step on small models.  The cache is the
     reference's KVCache::with_sliding_window(max_len, window)
     (model.rs:1363-1385): with a window it is a ring of
     storage_len_for(max_len, window) = min(window, max_len) slots and
@@ -380,6 +388,113 @@ class OracleGptOss:
             logits = self.forward(tok, pos)
             pos += 1
         return np.array(toks, np.uint32), last
+
+
+class OrcGptOssConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_layers", "dim", "n_heads", "n_kv_heads", "head_dim", "value_dim",
+                                          "hidden_dim", "n_experts", "top_k", "vocab", "max_len", "sliding_window")] + \
+               [("eps", C.c_float), ("concentration", C.c_float)]
+
+
+class OrcGptOssLayer(C.Structure):
+    _fields_ = [("wq", _p), ("wk", _p), ("wv", _p), ("wo", _p), ("wq_type", C.c_uint32), ("wk_type", C.c_uint32),
+                ("wv_type", C.c_uint32), ("wo_type", C.c_uint32)] + \
+               [(n, _p) for n in ("bq", "bk", "bv", "bo", "sinks", "attn_norm", "post_attn_norm", "router")] + \
+               [("router_type", C.c_uint32), ("router_bias", _p), ("gate_exps", _p), ("up_exps", _p),
+                ("down_exps", _p), ("exps_type", C.c_uint32), ("gate_exps_bias", _p), ("up_exps_bias", _p),
+                ("down_exps_bias", _p)]
+
+
+class OracleGptOss:
+    """forward_gpt_oss_into (model.rs:6733-6908) as one C layer loop
+    (orc_gptoss_forward), with the reference's window-sized ring KV cache
+    (KVCache::with_sliding_window, model.rs:1363-1385): storage =
+    min(window, max_len) slots, position p at slot p % storage, every layer's
+    attention over that ring, the odd (full) layers from position 0.
+    forward(..., want_logits=False) is forward_prefill_gpt_oss (no head).
+    kc[l] / vc[l] are numpy views of the C cache (writes reach the oracle).
+    Test infrastructure only."""
+
+    def __init__(self, model, max_len: int, threads: int = 0):
+        self.m = model
+        c = self.c = model["config"]
+        self.max_len = max(1, max_len)
+        w = c.get("window", 0)
+        self.ring = w > 0
+        cfg = OrcGptOssConfig(c["n_layers"], c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["value_dim"],
+                              c["hidden_dim"], c["n_experts"], c["top_k"], c["vocab"], self.max_len, w, c["eps"],
+                              model["concentration"])
+        if threads:
+            lib.orc_set_threads(threads)
+        self.h = lib.orc_gptoss_create(C.byref(cfg))
+        self.storage = int(lib.orc_gptoss_storage(self.h))
+        self._keep = []
+
+        def hold(a, dt=np.float32):
+            a = np.ascontiguousarray(a, dt)
+            self._keep.append(a)
+            return ptr(a)
+
+        for l, L in enumerate(model["layers"]):
+            d = OrcGptOssLayer()
+            for nm in ("wq", "wk", "wv", "wo"):
+                setattr(d, nm, hold(L[nm][0], np.uint8))
+                setattr(d, nm + "_type", L[nm][1])
+            for nm in ("bq", "bk", "bv", "bo", "sinks", "attn_norm", "post_attn_norm", "router_bias",
+                       "gate_exps_bias", "up_exps_bias", "down_exps_bias"):
+                setattr(d, nm, hold(L[nm]))
+            d.router, d.router_type = hold(L["router"], np.uint8), Q8_0
+            for nm in ("gate_exps", "up_exps", "down_exps"):
+                setattr(d, nm, hold(L[nm], np.uint8))
+            d.exps_type = MXFP4
+            lib.orc_gptoss_set_layer(self.h, l, C.byref(d))
+        out_w, out_t = model["output"]
+        emb, emb_t = model["token_embd"]
+        lib.orc_gptoss_set_output(self.h, hold(model["output_norm"]), hold(out_w, np.uint8), out_t,
+                                  hold(emb, np.uint8), emb_t, hold(model["inv_freq"]))
+        kd = c["n_kv_heads"] * c["head_dim"]
+        vdim = c["n_kv_heads"] * c["value_dim"]
+        self.kc = [np.ctypeslib.as_array(lib.orc_gptoss_kv(self.h, l, 0), shape=(self.storage * kd,))
+                   for l in range(c["n_layers"])]
+        self.vc = [np.ctypeslib.as_array(lib.orc_gptoss_kv(self.h, l, 1), shape=(self.storage * vdim,))
+                   for l in range(c["n_layers"])]
+
+    def slot(self, pos: int) -> int:
+        return pos % self.storage if self.ring else pos
+
+    def forward(self, token: int, pos: int, want_logits: bool = True) -> np.ndarray:
+        logits = np.zeros(self.c["vocab"], np.float32)
+        lib.orc_gptoss_forward(self.h, int(token), int(pos), ptr(logits), 1 if want_logits else 0)
+        return logits
+
+    def generate(self, prompt, n_gen, penalty=1.1, start_pos=0):
+        """The decode loop of the reference runtime (forward_prefill_gpt_oss
+        per prompt token but the last, runtime.rs:3760-3790; greedy + repeat
+        penalty over the last <= 64 tokens, runtime.rs:493-521)."""
+        recent = [int(t) for t in prompt[-64:]]
+        pos = start_pos
+        logits = None
+        for i, t in enumerate(prompt):
+            logits = self.forward(int(t), pos, want_logits=i + 1 == len(prompt))
+            pos += 1
+        toks = []
+        last = logits
+        for g in range(n_gen):
+            last = logits
+            tok, _ = greedy(logits, recent, penalty)
+            toks.append(tok)
+            recent = (recent + [tok])[-64:]
+            if g + 1 == n_gen:
+                break
+            logits = self.forward(tok, pos)
+            pos += 1
+        return np.array(toks, np.uint32), last
+
+    def __del__(self):
+        try:
+            lib.orc_gptoss_free(self.h)
+        except Exception:
+            pass
 
 
 # ---- reference fixtures ------------------------------------------------------

@@ -17,6 +17,17 @@ bit: logits, K/V of the new positions and tokens.
 - config 5, gpt-oss-20B past two ring lengths: the 128-slot window ring
   scanned cyclically by the full layers, sinks, MXFP4 experts, 201088-row
   Q8_0 head on f32 activations, then a 24-token greedy stream.
+
+The prompt legs of configs 3 and 5 go through the batched prefill and are
+checked against the oracle's sequential forward over the same prompt (the
+reference prefills token by token: forward_prefill_batch against sequential
+decode, src/model.rs:2877-2955; forward_prefill_gpt_oss per token,
+src/runtime.rs:3760-3790):
+- config 3: the 512-token prompt through the MFMA products at the 8B shape,
+  KV of every layer and the next logits bit-exact;
+- config 5: the 1024-token prompt at the 20B shape in two chunks (ring
+  layers through the linear view), ring KV of every layer and the next
+  logits bit-exact, then 64 greedy tokens.
 """
 import numpy as np
 import pytest
@@ -56,8 +67,21 @@ def _decode_steps(res, orc_forward, model, toks, pos0):
         assert np.array_equal(g.view(np.uint32), r.view(np.uint32)), (pos0 + i, np.max(np.abs(g - r)))
 
 
+_MODELS = {}
+
+
+def _model(name, seed, gptoss=False):
+    """One synthetic model per (name, seed) for the whole module: the 8B and
+    20B shapes take tens of seconds to generate."""
+    key = (name, seed)
+    if key not in _MODELS:
+        _MODELS.clear()  # hold one large model at a time
+        _MODELS[key] = synth.make_gptoss(name, seed=seed) if gptoss else synth.make_model(name, seed=seed)
+    return _MODELS[key]
+
+
 def _standard_case(hip, name, ctx, n_steps, n_gen, seed):
-    model = synth.make_model(name, seed=seed)
+    model = _model(name, seed)
     cfg = model["config"]
     storage = ctx + n_steps + n_gen + 8
     res = hip.Resident(model, storage)
@@ -86,20 +110,46 @@ def test_config3_llama3_8b_ctx4096(hip, exact):
     _standard_case(hip, "llama3-8b-q4km", 4096, 4, 64, seed=1234)
 
 
+def test_config3_llama3_8b_prompt_prefill_512(hip, exact):
+    """BASELINE config 3's 512-token random prompt through the batched (MFMA)
+    prefill at the 8B shape: every layer's K/V of the 511 prefilled
+    positions and the next logits (the last prompt token's decode step)
+    bit-identical to the oracle's token-by-token forward."""
+    model = _model("llama3-8b-q4km", 1234)
+    cfg = model["config"]
+    n = 512
+    storage = n + 16
+    prompt = synth.token_ids(512, n, cfg["vocab"])
+    res = hip.Resident(model, storage)
+    _, g_logits = res.generate(prompt, 0)
+    orc = O.OracleModel(model, storage, threads=16)
+    for p, t in enumerate(prompt):
+        o_logits = orc.forward(int(t), p, want_logits=p + 1 == n)
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32)), np.max(np.abs(g_logits - o_logits))
+    wk = cfg["n_kv_heads"] * cfg["head_dim"]
+    wv = cfg["n_kv_heads"] * cfg["value_dim"]
+    for layer in range(cfg["n_layers"]):
+        ok, ov = orc.kv(layer, storage)
+        assert np.array_equal(res.kv_read(layer, 0, 0, n).view(np.uint32), ok[: n * wk].view(np.uint32)), layer
+        assert np.array_equal(res.kv_read(layer, 1, 0, n).view(np.uint32), ov[: n * wv].view(np.uint32)), layer
+    del res, orc
+    hip.weight_cache_clear()
+
+
 def test_config4_qwen14b_ctx8192(hip, exact):
     _standard_case(hip, "qwen2.5-14b-q4km", 8192, 3, 4, seed=14)
 
 
 def test_config4_qwen14b_ctx32768(hip, exact):
-    _standard_case(hip, "qwen2.5-14b-q4km", 32768, 1, 0, seed=15)
+    _standard_case(hip, "qwen2.5-14b-q4km", 32768, 1, 8, seed=15)
 
 
 def test_config5_gptoss20b_past_two_windows(hip, exact):
-    model = synth.make_gptoss("gpt-oss-20b", seed=20)
+    model = _model("gpt-oss-20b", 20, gptoss=True)
     cfg = model["config"]
     max_len = 1024 + 256
     res = hip.ResidentGptOss(model, max_len)
-    orc = O.OracleGptOss(model, max_len)
+    orc = O.OracleGptOss(model, max_len, threads=16)
     S = orc.storage
     assert S == 128 == res.slots
     _fill_kv(res, lambda l: (orc.kc[l], orc.vc[l]), cfg, S, 77)
@@ -109,11 +159,57 @@ def test_config5_gptoss20b_past_two_windows(hip, exact):
     for layer in (0, 1, cfg["n_layers"] - 1):
         assert np.array_equal(res.kv_read(layer, 0, 0, S), orc.kc[layer])
         assert np.array_equal(res.kv_read(layer, 1, 0, S), orc.vc[layer])
-    # then 24 greedy tokens on the device against the oracle's decode loop
-    # (the oracle composes this model's layers in Python, ~1.2 s per token)
+    # then 64 greedy tokens on the device against the oracle's decode loop
     pos = pos0 + len(toks)
     prompt = synth.token_ids(21, 2, cfg["vocab"])
-    g_toks, g_logits = res.generate(prompt, 24, penalty=1.1, start_pos=pos)
-    o_toks, o_logits = orc.generate(prompt, 24, penalty=1.1, start_pos=pos)
+    g_toks, g_logits = res.generate(prompt, 64, penalty=1.1, start_pos=pos)
+    o_toks, o_logits = orc.generate(prompt, 64, penalty=1.1, start_pos=pos)
     assert list(g_toks) == list(o_toks)
     assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32))
+    del res, orc
+    hip.weight_cache_clear()
+
+
+def test_config5_gptoss20b_prompt_prefill_1024(hip, exact):
+    """BASELINE config 5's 1024-token prompt at the gpt-oss-20B shape through
+    the batched prefill (two chunks: 512 + 511 tokens, then the last token's
+    decode step), against the reference's token-by-token prefill: the ring
+    K/V of every layer and the next logits bit-identical, then the prompt
+    again with 64 greedy tokens after it, identical to the oracle's decode
+    loop continued from the same state."""
+    model = _model("gpt-oss-20b", 20, gptoss=True)
+    cfg = model["config"]
+    n, n_gen = 1024, 64
+    max_len = n + n_gen + 8
+    prompt = synth.token_ids(1024, n, cfg["vocab"])
+    res = hip.ResidentGptOss(model, max_len)
+    S = res.slots
+    _, g_logits = res.generate(prompt, 0)
+    orc = O.OracleGptOss(model, max_len, threads=16)
+    assert orc.storage == S == cfg["window"]
+    for p, t in enumerate(prompt):
+        o_logits = orc.forward(int(t), p, want_logits=p + 1 == n)
+        if p % 256 == 255:
+            print(f"[config5 prefill] oracle at position {p + 1}/{n}", flush=True)
+    assert np.array_equal(g_logits.view(np.uint32), o_logits.view(np.uint32)), np.max(np.abs(g_logits - o_logits))
+    for layer in range(cfg["n_layers"]):
+        assert np.array_equal(res.kv_read(layer, 0, 0, S).view(np.uint32), orc.kc[layer].view(np.uint32)), layer
+        assert np.array_equal(res.kv_read(layer, 1, 0, S).view(np.uint32), orc.vc[layer].view(np.uint32)), layer
+    # the decode loop after the prompt (runtime.rs:3266-3342): the device
+    # prefills the prompt again and generates; the oracle continues from its
+    # state with the prompt's last 64 tokens as the penalty window
+    g_toks, g_last = res.generate(prompt, n_gen, penalty=1.1)
+    recent = [int(t) for t in prompt[-64:]]
+    logits, pos, o_toks = o_logits, n, []
+    for i in range(n_gen):
+        o_last = logits
+        tok, _ = O.greedy(logits, recent, 1.1)
+        o_toks.append(tok)
+        recent = (recent + [tok])[-64:]
+        if i + 1 < n_gen:
+            logits = orc.forward(tok, pos)
+            pos += 1
+    assert list(g_toks) == o_toks
+    assert np.array_equal(g_last.view(np.uint32), o_last.view(np.uint32))
+    del res, orc
+    hip.weight_cache_clear()

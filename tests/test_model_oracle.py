@@ -69,6 +69,31 @@ def test_gptoss_forward_vs_f64_with_ring():
     assert np.max(np.abs(lin[W + 1:] - ref[W + 1:])) > 1e-2 * scale
 
 
+def test_gptoss_c_layer_loop_equals_composed():
+    """The C layer loop (orc_gptoss_forward) against the same forward composed
+    step by step in Python from the C parts (router, experts, sinks, ring):
+    logits, prefill steps without the head, and every layer's ring KV
+    bit-identical past three ring lengths.  The composed form is the one the
+    float64 checks above pin; this carries that pin over to the C loop."""
+    model = synth.make_gptoss("tiny-gptoss", seed=9)
+    c = model["config"]
+    n = 3 * c["window"] + 7
+    toks = [int(t) for t in synth.token_ids(23, n, c["vocab"])]
+    a = O.OracleGptOss(model, 64, threads=4)
+    b = O.OracleGptOssComposed(model, 64)
+    for p, t in enumerate(toks):
+        la = a.forward(t, p, want_logits=p % 5 != 3)
+        lb = b.forward(t, p)
+        if p % 5 != 3:
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), p
+    for l in range(c["n_layers"]):
+        assert np.array_equal(a.kc[l].view(np.uint32), b.kc[l].view(np.uint32)), l
+        assert np.array_equal(a.vc[l].view(np.uint32), b.vc[l].view(np.uint32)), l
+    ta, la = a.generate(toks[:9], 6, penalty=1.1, start_pos=n)
+    tb, lb = b.generate(toks[:9], 6, penalty=1.1, start_pos=n)
+    assert list(ta) == list(tb) and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
 def test_gptoss_short_cache_is_linear():
     """max_len below the window: storage_len_for gives max_len slots and no
     position ever wraps."""

@@ -229,6 +229,25 @@ def test_f32_dots_vs_f64(t, cols):
     assert abs(got - ref) <= 1e-5 * norm
 
 
+@pytest.mark.parametrize("rows,threads", [(37, 1), (37, 4), (8, 1), (130, 8)])
+def test_mxfp4_matvec_rows_equal_scalar_dot(rows, threads):
+    """orc_matvec runs MXFP4 rows eight at a time (independent add chains
+    for the CPU); every row must still be dot_mxfp4_f32_scalar's value
+    (simd.rs:5886-5902), bit for bit, including the tail rows and every
+    scale byte class (normal, subnormal e = 0, infinite e = 255)."""
+    rng = np.random.default_rng(rows * 7 + threads)
+    cols = 2880
+    w = _random_blocks(39, rows * cols // 32, rng)
+    w.reshape(-1, 17)[::97, 16] = 0
+    w.reshape(-1, 17)[::131, 16] = 255
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = O.matvec(39, w, x, rows, cols, threads=threads)
+    rb = cols // 32 * 17
+    for r in range(rows):
+        ref = O.lib.orc_dot_mxfp4_f32_scalar(O.ptr(w[r * rb:]), O.ptr(x), cols)
+        assert np.float32(ref).view(np.uint32) == y[r].view(np.uint32), r
+
+
 def test_matvec_dispatch_by_shape():
     """dot_row (simd.rs:962-1060): Q8_0 uses the Q8_K int kernel only when
     cols % 256 == 0, the f32 kernel otherwise."""
