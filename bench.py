@@ -258,7 +258,8 @@ def bench_gptoss(args):
     model = synth.make_gptoss(args.config, seed=args.seed)
     cfg = model["config"]
     log(f"model {args.config} generated in {time.time() - t0:.1f}s")
-    storage = args.ctx + args.warmup + args.steps + args.profile_tokens + 8
+    cpu_slots = 0 if args.no_cpu else 512
+    storage = args.ctx + args.warmup + args.steps + args.profile_tokens + 8 + cpu_slots
     res = hip.ResidentGptOss(model, max(storage, args.prefill_tokens + 1))
     prefill = None
     if args.prefill_tokens:
@@ -292,6 +293,25 @@ def bench_gptoss(args):
     kv = sum(min(pos, cfg["window"]) if l % 2 == 0 else pos for l in range(cfg["n_layers"])) * 2 * kd * 4
     token_bytes = cfg["n_layers"] * per_layer + model["output"][0].nbytes + kv
     eff = token_bytes * tok_s / 1e9
+    # dominant kernel family: the routed experts' MXFP4 products (per layer one
+    # gate/up launch over the k experts' 2 x hidden rows and one down launch
+    # over their dim rows); algorithmic bytes = the k experts' blocks + x + y
+    roofline = None
+    tot, cnt = prof.get("gemv_mxfp4", (0.0, 0))
+    if cnt:
+        exp_bytes = k * (L0["gate_exps"].nbytes + L0["up_exps"].nbytes + L0["down_exps"].nbytes) // ne
+        act_bytes = k * (2 * (dim * 4 + hid * 4) + (hid * 4 + dim * 4))
+        bytes_per_launch = (exp_bytes + act_bytes) / 2.0
+        avg_ms = tot / cnt
+        gbs = bytes_per_launch / (avg_ms * 1e-3) / 1e9
+        roofline = {
+            "kernel": "gemv_mxfp4 (top-%d of %d experts, gate+up %dx%d and down %dx%d MXFP4 rows, reference "
+                      "serial row sums)" % (k, ne, 2 * hid, dim, dim, hid),
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": int(bytes_per_launch),
+            "avg_launch_us": round(avg_ms * 1e3, 3), "launches": cnt,
+        }
+    cpu = None if args.no_cpu else cpu_baseline_gptoss(model, res, args, log)
     line = {
         "metric": "decode tok/s gpt-oss-20B-shape MXFP4 MoE bs1 ctx%d" % args.ctx,
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -300,15 +320,49 @@ def bench_gptoss(args):
         "config": {"workload": f"{args.config} greedy decode bs1, KV filled to ctx {args.ctx}", "ctx": args.ctx,
                    "layers": cfg["n_layers"], "d_model": dim, "experts": [ne, k], "window": cfg["window"],
                    "seed": args.seed},
-        "roofline": None,
+        "roofline": roofline,
         "token_bytes": token_bytes,
         "effective_GBps": round(eff, 1),
         "effective_frac": round(eff / HBM_PEAK_GBS, 4),
         "profile_ms_per_token": {kk: round(v[0] / args.profile_tokens, 4) for kk, v in fam},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
         "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_gptoss(model, res, args, log):
+    """The CPU oracle's gpt-oss decode step (orc_gptoss_forward: the C
+    restatement of forward_gpt_oss_into with the reference's ring cache)
+    continues from the GPU's ring KV at the same position, bounded sample.
+    The restatement runs the per-head sink attention on its threads, where the
+    reference runs the heads one after another, so it is if anything faster
+    than the reference."""
+    from oracle import oracle as O
+
+    cfg = model["config"]
+    cores = host_cores()
+    t0 = time.time()
+    pos0 = args.ctx + args.warmup + args.steps + args.profile_tokens - 1
+    orc = O.OracleGptOss(model, res.storage_len, threads=cores)
+    S = orc.storage
+    for layer in range(cfg["n_layers"]):
+        orc.kc[layer][:] = res.kv_read(layer, 0, 0, S)
+        orc.vc[layer][:] = res.kv_read(layer, 1, 0, S)
+    log(f"cpu baseline: ring KV copied in {time.time() - t0:.1f}s, {cores} threads")
+    tok, n, pos = 1, 0, pos0
+    t_start = time.time()
+    while pos < res.storage_len and (n < 2 or time.time() - t_start < args.cpu_seconds):
+        logits = orc.forward(tok, pos)
+        tok, _ = O.greedy(logits, [], 1.0)
+        pos += 1
+        n += 1
+    dt = time.time() - t_start
+    v = n / dt
+    log(f"cpu baseline: {n} tokens in {dt:.1f}s -> {v:.2f} tok/s")
+    return {"value": round(v, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} greedy decode tokens of the same gpt-oss-20B-shape model at positions "
+                      f"{pos0}..{pos0 + n} (C restatement of the reference x86 path, {cores} threads)"}
 
 
 def measure_prefill_gptoss(hip, res, toks, log):

@@ -209,12 +209,15 @@ __device__ __forceinline__ void stream_wait_prefix(const AttnExactArgs &A, int h
     const int lane = threadIdx.x & 63;
     for (int it = 0; it < STREAM_SPIN_MAX; it++) {
         const int t = ready + lane;
-        const uint32_t v = t < ntiles ? __hip_atomic_load(stream_flag(A, h, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                      : A.ep + 1;
+        // the timeout mark and the flags in flight together (unconditional
+        // loads, clamped index): one round trip per poll
+        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t fv = __hip_atomic_load(stream_flag(A, h, min(t, ntiles - 1)), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t v = t < ntiles ? fv : A.ep + 1;
         const unsigned long long ok = __ballot(v == A.ep + 1);
         ready += ~ok == 0ull ? 64 : (int)__builtin_ctzll(~ok);  // the published run from `ready` on
         if (tile < ready) return;
-        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane(bad) == A.ep + 1) {
             ready = ntiles;
             return;
@@ -227,9 +230,9 @@ __device__ __forceinline__ void stream_wait_prefix(const AttnExactArgs &A, int h
 __device__ __forceinline__ void stream_wait(const AttnExactArgs &A, int h, int tile) {
     const uint32_t *f = stream_flag(A, h, tile);
     for (int it = 0; it < STREAM_SPIN_MAX; it++) {
+        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane(v) == A.ep + 1) return;
-        const uint32_t bad = __hip_atomic_load(A.sync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane(bad) == A.ep + 1) return;
         __builtin_amdgcn_s_sleep(2);
     }

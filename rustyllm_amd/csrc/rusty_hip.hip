@@ -563,7 +563,16 @@ template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
     if constexpr (FMT == F_MXFP4) {
         ProfScope ps("gemv_mxfp4", s);
-        if (A.n_tiles > g.n_cu) {
+        // RUSTY_HIP_MX_SERIAL_PER_CU: tiles per CU up to which the
+        // producer/adder workgroups serve a launch (two per CU fit in LDS,
+        // but measured slower on the gpt-oss expert launches: 279 against
+        // 285 tok/s)
+        static int serial_per_cu = -1;
+        if (serial_per_cu < 0) {
+            const char *e = getenv("RUSTY_HIP_MX_SERIAL_PER_CU");
+            serial_per_cu = e ? atoi(e) : 1;
+        }
+        if (A.n_tiles > serial_per_cu * g.n_cu) {
             // more tiles than CUs: one wave per tile computes its own terms,
             // several tiles per SIMD
             rh_launch(gemv_mxfp4_fused_kernel, dim3(A.n_tiles), dim3(64), 0, s, A);
@@ -1040,12 +1049,20 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     // The streamed launch: the scores workgroups (as many per kv head, J, as
     // the CUs the chain workgroups leave, each scoring every J-th tile), then
     // the chain workgroups.  A scores workgroup takes about 4.5 us per tile
-    // and the recurrence about 0.27 us, so with J >= 17 (or one tile each)
-    // the scores stay ahead of it; otherwise separate launches.
+    // and the recurrence about 0.3 us, so with J >= 12 (or one tile each)
+    // the scores keep up with it; otherwise separate launches.
     const int nc = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
     const int J = std::max(1, std::min(ntl, (g.n_cu - nc) / A.n_kv));
+    // J >= 12 also takes the Qwen2.5-14B shape (144 chain workgroups, J =
+    // 14): at ctx 32768 its scores then run about level with the recurrence,
+    // 171 us per layer against 193 for the separate launches
+    static int jmin = -1;
+    if (jmin < 0) {
+        const char *e = getenv("RUSTY_HIP_STREAM_JMIN");
+        jmin = e ? std::max(1, atoi(e)) : 12;
+    }
     if (sync && s8 && c4 && A.n_tok == 0 && !A.lin && stream_enabled() && nc + 32 <= g.n_cu &&
-        (J >= 17 || J >= ntl)) {
+        (J >= jmin || J >= ntl)) {
         A.sync = sync;
         const int blocks = J * A.n_kv + nc;
         ProfScope ps("attn_exact_stream", s);
