@@ -335,9 +335,9 @@ def cpu_baseline_gptoss(model, res, args, log):
     """The CPU oracle's gpt-oss decode step (orc_gptoss_forward: the C
     restatement of forward_gpt_oss_into with the reference's ring cache)
     continues from the GPU's ring KV at the same position, bounded sample.
-    The restatement runs the per-head sink attention on its threads, where the
-    reference runs the heads one after another, so it is if anything faster
-    than the reference."""
+    It runs on the reference's own schedule (orc_set_fast_schedule(0): MXFP4
+    rows one dot_mxfp4_f32_scalar call each in the 64-row worker split, the
+    sink loop's heads one after another), not the checker's faster one."""
     from oracle import oracle as O
 
     cfg = model["config"]
@@ -352,11 +352,15 @@ def cpu_baseline_gptoss(model, res, args, log):
     log(f"cpu baseline: ring KV copied in {time.time() - t0:.1f}s, {cores} threads")
     tok, n, pos = 1, 0, pos0
     t_start = time.time()
-    while pos < res.storage_len and (n < 2 or time.time() - t_start < args.cpu_seconds):
-        logits = orc.forward(tok, pos)
-        tok, _ = O.greedy(logits, [], 1.0)
-        pos += 1
-        n += 1
+    O.lib.orc_set_fast_schedule(0)
+    try:
+        while pos < res.storage_len and (n < 2 or time.time() - t_start < args.cpu_seconds):
+            logits = orc.forward(tok, pos)
+            tok, _ = O.greedy(logits, [], 1.0)
+            pos += 1
+            n += 1
+    finally:
+        O.lib.orc_set_fast_schedule(1)
     dt = time.time() - t_start
     v = n / dt
     log(f"cpu baseline: {n} tokens in {dt:.1f}s -> {v:.2f} tok/s")

@@ -645,6 +645,12 @@ void orc_q8_0_block_ints(const uint8_t *w, const int8_t *qs, int64_t n, int32_t 
  * simd.rs:1130-1212); a row's value does not depend on the split.            */
 static int g_threads = 1;
 void orc_set_threads(int threads) { g_threads = threads > 0 ? threads : 1; }
+/* 1 (default): the checker's schedule (MXFP4 rows eight at a time, the sink
+ * loop's heads on the threads); 0: the reference's own schedule (one row per
+ * dot_mxfp4_f32_scalar call in the 64-row worker split, heads one after
+ * another), for timing the CPU baseline.  Values are the same either way. */
+static int g_fast_schedule = 1;
+void orc_set_fast_schedule(int on) { g_fast_schedule = on ? 1 : 0; }
 
 int64_t orc_row_bytes(int dtype, int64_t cols) {
     switch (dtype) {
@@ -735,7 +741,7 @@ static void dot_mxfp4_f32_scalar_rows8(const uint8_t *w, int64_t rb, const float
 void orc_matvec(int dtype, const uint8_t *w, const float *x, int64_t rows, int64_t cols, float *out, int threads) {
     if (threads <= 0) threads = g_threads;
     int64_t rb = orc_row_bytes(dtype, cols);
-    if (dtype == ORC_MXFP4) {
+    if (dtype == ORC_MXFP4 && g_fast_schedule) {
         /* scheduling only: groups of 8 rows, each row's value as the
          * one-row kernel's (a row's value does not depend on the split) */
         mxfp4_scale_table_init();
@@ -1093,7 +1099,8 @@ void orc_attention_sink_heads(const float *q, const float *keys, const float *va
     memset(out, 0, (size_t)(n_heads * vd) * 4);
     int nt = g_threads < (int)n_heads ? g_threads : (int)n_heads;
     int64_t work = (end_t >= start_t ? end_t - start_t + 1 : 0) * n_heads;
-#pragma omp parallel for schedule(static) num_threads(nt > 0 ? nt : 1) if (n_heads > 1 && nt > 1 && work >= 4096)
+#pragma omp parallel for schedule(static) num_threads(nt > 0 ? nt : 1) \
+    if (g_fast_schedule && n_heads > 1 && nt > 1 && work >= 4096)
     for (int64_t h = 0; h < n_heads; h++) {
         int64_t kvh = h / kv_mul;
         orc_online_attention_with_sink(q + h * hd, keys + kvh * hd, values + kvh * vd, ks, vs, slots, hd, vd,

@@ -65,6 +65,7 @@ void orc_q8_0_block_ints(const uint8_t *w, const int8_t *qs, int64_t n, int32_t 
 int64_t orc_row_bytes(int dtype, int64_t cols);
 void orc_matvec(int dtype, const uint8_t *w, const float *x, int64_t rows, int64_t cols, float *out, int threads);
 void orc_set_threads(int threads);
+void orc_set_fast_schedule(int on);
 
 /* ---- attention ---------------------------------------------------------- */
 void orc_online_attention(const float *q, const float *keys, const float *values,

@@ -63,6 +63,7 @@ _sig("orc_q8_0_block_ints", None, _p, _p, _i64, _p)
 _sig("orc_row_bytes", _i64, C.c_int, _i64)
 _sig("orc_matvec", None, C.c_int, _p, _p, _i64, _i64, _p, C.c_int)
 _sig("orc_set_threads", None, C.c_int)
+_sig("orc_set_fast_schedule", None, C.c_int)
 _sig("orc_online_attention", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)
 _sig("orc_online_attention_with_sink", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _f, _p)
 _sig("orc_online_attention_grouped", None, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _p)

@@ -94,6 +94,24 @@ def test_gptoss_c_layer_loop_equals_composed():
     assert list(ta) == list(tb) and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
 
 
+def test_gptoss_reference_schedule_same_values():
+    """The CPU baseline times the oracle on the reference's own schedule (one
+    MXFP4 row per scalar dot, sink heads one after another); the checker's
+    faster schedule must give the same bits."""
+    model = synth.make_gptoss("tiny-gptoss", seed=3)
+    toks = [int(t) for t in synth.token_ids(5, 30, model["config"]["vocab"])]
+    a = O.OracleGptOss(model, 64, threads=4)
+    la = [a.forward(t, p) for p, t in enumerate(toks)]
+    O.lib.orc_set_fast_schedule(0)
+    try:
+        b = O.OracleGptOss(model, 64, threads=4)
+        lb = [b.forward(t, p) for p, t in enumerate(toks)]
+    finally:
+        O.lib.orc_set_fast_schedule(1)
+    for x, y in zip(la, lb):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
 def test_gptoss_short_cache_is_linear():
     """max_len below the window: storage_len_for gives max_len slots and no
     position ever wraps."""
