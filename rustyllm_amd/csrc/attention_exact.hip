@@ -631,6 +631,163 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
     scores8_tile<HD>(A, blockIdx.x, blockIdx.y);
 }
 
+// A for many query tokens at once (prefill without a window or ring view:
+// every token's range starts at start_t, so all tokens share the tile
+// boundaries).  One workgroup per (tile, kv head, block of MQ_PAIRS / kv_mul
+// consecutive tokens): the K tile is staged once, lane-sliced as in
+// scores8_tile, and each wave holds 16 of its positions in registers
+// (positions 16w + 8p + sub, p = 0, 1) while it walks the block's
+// (token, head) pairs, whose q slices are read from LDS.  Per pair and
+// position the lane arithmetic is scores8_tile's (dot_f32x4 / dot_bf16 one
+// accumulator, dot_f32_avx2 four, then the row_shl hsum and the scale), so
+// every token's scores and tile maxima equal its single-token launch's.
+// Tokens whose range ends before the tile write nothing.
+#define MQ_PAIRS 32
+__host__ __device__ inline int mq_tokens(int kvm) { return kvm >= MQ_PAIRS ? 1 : MQ_PAIRS / kvm; }
+template <int HD>
+__global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs A) {
+    constexpr int M = HD / 8, LS = M + 4, RS = 8 * LS;
+    __shared__ __align__(16) float s_k[EX_TILE * RS];
+    __shared__ __align__(16) float s_q[MQ_PAIRS * RS];
+    __shared__ float s_sc[MQ_PAIRS * EX_TILE];
+    const int kvm = A.kv_mul, qb = mq_tokens(kvm);
+    const int tile = blockIdx.x, h = blockIdx.y, z0 = blockIdx.z * qb;
+    const int nz = min(qb, A.n_tok - z0), npair = nz * kvm;
+    const int t_base = tile * EX_TILE;
+    // the block's last token has the longest range
+    const int ctx_last = A.pos0 + z0 + nz - 1 - A.start_t + 1;
+    if (nz <= 0 || ctx_last <= t_base) return;
+    const int rows = min(EX_TILE, ctx_last - t_base);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    {
+        // K rows t_base.. (clamped to the rows any token of the block reads)
+        constexpr int H4 = HD / 4, RSTEP = 256 / H4, NKR = EX_TILE / RSTEP;
+        const int r0 = tid / H4, c4 = tid - r0 * H4;
+        const float *kh = A.k + (size_t)h * HD;
+        const uint16_t *kh16 = (const uint16_t *)A.k + (size_t)h * HD;
+        // every load (the K tile's rows, then the pairs' q rows: float4
+        // column c of pair pr, clamped to the last pair) issued before any
+        // LDS store, in straight-line code
+        float4 kreg[NKR];
+        size_t kr[NKR];
+#pragma unroll
+        for (int i = 0; i < NKR; i++)
+            kr[i] = (size_t)((A.start_t + t_base + min(r0 + i * RSTEP, rows - 1)) % A.slot_count) * A.key_stride +
+                    4 * c4;
+        if (A.kv_bf16) {
+#pragma unroll
+            for (int i = 0; i < NKR; i++) kreg[i] = bf16x4_load(kh16 + kr[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NKR; i++) kreg[i] = *(const float4 *)(kh + kr[i]);
+        }
+        constexpr int NQ4 = MQ_PAIRS * H4 / 256;
+        float4 qreg[NQ4];
+#pragma unroll
+        for (int u = 0; u < NQ4; u++) {
+            const int idx = tid + 256 * u, pr = min(idx / H4, npair - 1), c = idx - (idx / H4) * H4;
+            const int zz = pr / kvm, g = pr - zz * kvm;
+            qreg[u] = *(const float4 *)(A.q + (int64_t)(z0 + zz) * A.q_tok + (size_t)(h * kvm + g) * HD + 4 * c);
+        }
+        // q of every (token, head) pair, lane-sliced like a K row
+#pragma unroll
+        for (int u = 0; u < NQ4; u++) {
+            const int idx = tid + 256 * u, pr = idx / H4, e = 4 * (idx - pr * H4);
+            if (pr < npair) {
+                float *d = s_q + pr * RS + (e >> 3);
+                d[((e + 0) & 7) * LS] = qreg[u].x;
+                d[((e + 1) & 7) * LS] = qreg[u].y;
+                d[((e + 2) & 7) * LS] = qreg[u].z;
+                d[((e + 3) & 7) * LS] = qreg[u].w;
+            }
+        }
+        const int lbase = (4 * c4) & 7, m = (4 * c4) >> 3;
+#pragma unroll
+        for (int i = 0; i < NKR; i++) {
+            float *d = s_k + (r0 + i * RSTEP) * RS + m;
+            d[(lbase + 0) * LS] = kreg[i].x;
+            d[(lbase + 1) * LS] = kreg[i].y;
+            d[(lbase + 2) * LS] = kreg[i].z;
+            d[(lbase + 3) * LS] = kreg[i].w;
+        }
+    }
+    __syncthreads();
+    const int l = lane & 7, sub = lane >> 3;
+    float k[2][M];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const float *kr = s_k + (16 * wave + 8 * p + sub) * RS + l * LS;
+#pragma unroll
+        for (int r = 0; r < M / 4; r++) {
+            const float4 f = *(const float4 *)(kr + 4 * r);
+            k[p][4 * r] = f.x;
+            k[p][4 * r + 1] = f.y;
+            k[p][4 * r + 2] = f.z;
+            k[p][4 * r + 3] = f.w;
+        }
+    }
+    for (int pr = 0; pr < npair; pr++) {
+        const int g = pr % kvm;
+        const bool x4 = A.kv_bf16 || (A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4);
+        float q[M];
+        {
+            const float *qr = s_q + pr * RS + l * LS;
+#pragma unroll
+            for (int r = 0; r < M / 4; r++) {
+                const float4 f = *(const float4 *)(qr + 4 * r);
+                q[4 * r] = f.x;
+                q[4 * r + 1] = f.y;
+                q[4 * r + 2] = f.z;
+                q[4 * r + 3] = f.w;
+            }
+        }
+        float y[2];
+        if (x4) {
+            y[0] = 0.0f;
+            y[1] = 0.0f;
+#pragma unroll
+            for (int mm = 0; mm < M; mm++) {
+                y[0] = fmaf(q[mm], k[0][mm], y[0]);
+                y[1] = fmaf(q[mm], k[1][mm], y[1]);
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int c = 0; c < M / 4; c++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) a[j] = fmaf(q[4 * c + j], k[p][4 * c + j], a[j]);
+                y[p] = (a[0] + a[1]) + (a[2] + a[3]);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const float a = y[p] + row_shl<4>(y[p]);
+            const float b = a + row_shl<1>(a);
+            const float d = b + row_shl<2>(b);
+            if (l == 0) s_sc[pr * EX_TILE + 16 * wave + 8 * p + sub] = d * A.scale;
+        }
+    }
+    __syncthreads();
+    // coalesced score rows and tile maxima of the tokens whose range reaches
+    // the tile, each into its own scratch block
+    const int ntl = A.cap / EX_TILE;
+    for (int pr = wave; pr < npair; pr += 4) {
+        const int zz = pr / kvm, g = pr - zz * kvm, z = z0 + zz;
+        const int ctx = A.pos0 + z - A.start_t + 1;
+        if (ctx <= t_base) continue;
+        const int nt = min(EX_TILE, ctx - t_base);
+        const int head = h * kvm + g;
+        const int64_t sc = (int64_t)z * A.tok_scratch;
+        const float v = lane < nt ? s_sc[pr * EX_TILE + lane] : -INFINITY;
+        if (lane < nt) A.scores[sc + (size_t)head * A.cap + t_base + lane] = v;
+        const float mx = wave_max(v);
+        if (lane == 0) A.tmax[sc + (size_t)head * ntl + tile] = mx;
+    }
+}
+
 // B: one wave per (tile of 64 positions, query head), four tiles per workgroup.  The running max before
 // each step is max(initial, maxima of the earlier tiles, prefix max inside the
 // tile), so every step's branch and expf argument are known without a serial
@@ -1354,6 +1511,84 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_stream_kernel(AttnEx
 // coefficients and new-max words from global memory, and many
 // waves per SIMD hide the latency.  The update forms are the chain4
 // consumer's, step for step.
+// One chain of attn_exact_chain_tok_kernel: V from the transposed copy
+// (MODE 1), from f32 cache rows (MODE 2) or bf16 ones (MODE 3), or v = 1 for
+// the denominator (MODE 0).  Chunk k + 1's coefficient word, new-max bits and V values are
+// loaded before chunk k's steps (two register sets, clamped indices, every
+// load unconditional and straight-line), so a wave waits for one load round
+// trip per launch rather than one per 16 steps.
+template <int MODE>
+__device__ __forceinline__ float chain_tok_run(const AttnExactArgs &A, int s0, int ctx, const float *ef,
+                                               const uint32_t *mk, const float *vtr, int dim, bool x4, int lane,
+                                               int dcol, float o) {
+    constexpr bool DEN = MODE == 0;
+    const int nk = (ctx + 15) / 16;
+    auto load = [&](int k, float &e16, uint32_t &bits, float *v) {
+        k = min(k, nk - 1);
+        e16 = ef[16 * k + dcol];
+        bits = (mk[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+        if constexpr (MODE == 0) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = 1.0f;
+        } else if constexpr (MODE == 1) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                // four consecutive slots of the lane's dim: 64 floats per slot group
+                const float4 f = *(const float4 *)(vtr + (size_t)(4 * k + q) * 64);
+                v[4 * q] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
+            }
+        } else {
+            const int n = min(16, ctx - 16 * k);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int slot = (s0 + 16 * k + min(j, n - 1)) % A.slot_count;
+                const size_t vr = (size_t)kv_row(A, slot) * A.value_stride + dim;
+                v[j] = MODE == 3 ? bf16_to_f32(((const uint16_t *)A.v)[vr]) : A.v[vr];
+            }
+        }
+    };
+    auto step = [&](int k, float e16, uint32_t bits, const float *v) {
+        const int n = min(16, ctx - 16 * k);
+        if (n == 16) {
+            const uint32_t f = bits ? 1u : 0u;
+            const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
+                                 __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
+            if (any == 0u) {
+                cons_fma16_dpp(e16, v, o);
+            } else if (x4 || DEN) {
+                float a16, m16;
+                aff_pair16(e16, bits, lane, a16, m16);
+                cons_affine16_dpp(a16, m16, v, o);
+            } else {
+                c4_steps16_slow<false>(e16, v, o, bits);
+            }
+        } else {
+            // the last, partial chunk: step by step in its own form
+            for (int j = 0; j < n; j++) {
+                const float e = ef[16 * k + j];
+                const float vj = v[j];
+                const float on = fmaf(e, vj, o);
+                const float ox = (x4 || DEN) ? fmaf(vj, 1.0f, o * e) : fmaf(o, e, vj);
+                o = ((bits >> j) & 1u) ? ox : on;
+            }
+        }
+    };
+    float ea, eb, va[16], vb[16];
+    uint32_t ba, bb;
+    load(0, ea, ba, va);
+    for (int k = 0; k < nk; k += 2) {
+        load(k + 1, eb, bb, vb);
+        step(k, ea, ba, va);
+        if (k + 1 >= nk) break;
+        load(k + 2, ea, ba, va);
+        step(k + 1, eb, bb, vb);
+    }
+    return o;
+}
+
 __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
     int s0, e0;
@@ -1377,56 +1612,10 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
                     s0 + (ctx + EX_TILE - 1) / EX_TILE * EX_TILE <= A.vt_stride;
     const float *vtr = vt ? A.vt + vt4_off(dim, s0, A.vt_stride) : nullptr;
     float o = (den && A.sinks) ? 1.0f : 0.0f;
-    for (int k = 0; 16 * k < ctx; k++) {
-        const int n = min(16, ctx - 16 * k);
-        const float e16 = ef[16 * k + dcol];
-        const uint32_t bits = (mk[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-        float v[16];
-        if (den) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) v[j] = 1.0f;
-        } else if (vt) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                // four consecutive slots of the lane's dim: 64 floats per slot group
-                const float4 f = *(const float4 *)(vtr + (size_t)(4 * k + q) * 64);
-                v[4 * q] = f.x;
-                v[4 * q + 1] = f.y;
-                v[4 * q + 2] = f.z;
-                v[4 * q + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int slot = (s0 + 16 * k + min(j, n - 1)) % A.slot_count;
-                const size_t vr = (size_t)kv_row(A, slot) * A.value_stride + dim;
-                v[j] = A.kv_bf16 ? bf16_to_f32(((const uint16_t *)A.v)[vr]) : A.v[vr];
-            }
-        }
-        if (n == 16) {
-            const uint32_t f = bits ? 1u : 0u;
-            const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
-                                 __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
-            if (any == 0u) {
-                cons_fma16_dpp(e16, v, o);
-            } else if (x4 || den) {
-                float a16, m16;
-                aff_pair16(e16, bits, lane, a16, m16);
-                cons_affine16_dpp(a16, m16, v, o);
-            } else {
-                c4_steps16_slow<false>(e16, v, o, bits);
-            }
-        } else {
-            // the last, partial chunk: step by step in its own form
-            for (int j = 0; j < n; j++) {
-                const float e = ef[16 * k + j];
-                const float vj = v[j];
-                const float on = fmaf(e, vj, o);
-                const float ox = (x4 || den) ? fmaf(vj, 1.0f, o * e) : fmaf(o, e, vj);
-                o = ((bits >> j) & 1u) ? ox : on;
-            }
-        }
-    }
+    if (den) o = chain_tok_run<0>(A, s0, ctx, ef, mk, nullptr, dim, x4, lane, dcol, o);
+    else if (vt) o = chain_tok_run<1>(A, s0, ctx, ef, mk, vtr, dim, x4, lane, dcol, o);
+    else if (A.kv_bf16) o = chain_tok_run<3>(A, s0, ctx, ef, mk, nullptr, dim, x4, lane, dcol, o);
+    else o = chain_tok_run<2>(A, s0, ctx, ef, mk, nullptr, dim, x4, lane, dcol, o);
     if (g < kvm) {
         if (den) {
             if (dcol == 0) A.den[h * kvm + g] = o;

@@ -43,15 +43,18 @@ __device__ __forceinline__ void rmsnorm_row(const float *x, const float *w, floa
     extern __shared__ float s_x[];
     __shared__ float red[40];
     {
-        // all loads first (n <= 16384: at most 16 float4 per thread)
+        // loads eight float4 per thread at a time, all issued before their
+        // stores (clamped unconditional loads: conditionally loaded array
+        // elements were kept in scratch)
         const int n4 = n >> 2, tid = threadIdx.x;
-        float4 t[16];
+        for (int k0 = 0; 256 * k0 < n4; k0 += 8) {
+            float4 t[8];
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (tid + 256 * k < n4) t[k] = ((const float4 *)x)[tid + 256 * k];
+            for (int k = 0; k < 8; k++) t[k] = ((const float4 *)x)[min(tid + 256 * (k0 + k), n4 - 1)];
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (tid + 256 * k < n4) ((float4 *)s_x)[tid + 256 * k] = t[k];
+            for (int k = 0; k < 8; k++)
+                if (tid + 256 * (k0 + k) < n4) ((float4 *)s_x)[tid + 256 * (k0 + k)] = t[k];
+        }
         for (int i = 4 * n4 + tid; i < n; i += 256) s_x[i] = x[i];
     }
     __syncthreads();

@@ -1079,7 +1079,16 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     }
     {
         ProfScope ps("attn_exact_scores", s);
-        if (s8 && A.hd == 128) {
+        // many query tokens sharing the tile boundaries (no window, no ring
+        // view): one K tile staging per block of tokens
+        const bool mq = s8 && A.n_tok > 0 && !A.lin && A.window == 0 && !A.fuse_rope && A.q_tok % 4 == 0 &&
+                        ((uintptr_t)A.q & 15) == 0;
+        const unsigned nzb = (unsigned)((A.n_tok + mq_tokens(A.kv_mul) - 1) / mq_tokens(A.kv_mul));
+        if (mq && A.hd == 128) {
+            rh_launch(attn_exact_scores_mq_kernel<128>, dim3(ntl, A.n_kv, nzb), dim3(256), 0, s, A);
+        } else if (mq) {
+            rh_launch(attn_exact_scores_mq_kernel<64>, dim3(ntl, A.n_kv, nzb), dim3(256), 0, s, A);
+        } else if (s8 && A.hd == 128) {
             rh_launch(attn_exact_scores8_kernel<128>, dim3(ntl, A.n_kv, nz), dim3(256), 0, s, A);
         } else if (s8) {
             rh_launch(attn_exact_scores8_kernel<64>, dim3(ntl, A.n_kv, nz), dim3(256), 0, s, A);
