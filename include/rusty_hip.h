@@ -204,6 +204,29 @@ int rusty_hip_resident_generate(const int32_t *prompt, uint32_t n_prompt, uint32
  * K/V value is bit-identical to decoding the tokens in turn with the
  * reference-order attention. */
 int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_t start_pos);
+/* Chooses the expert product of the batched gpt-oss prefill (no counterpart
+ * in the reference, which prefills gpt-oss token by token): 0 (the default,
+ * or environment RUSTY_HIP_EXPERT_MFMA=1 for 1) keeps every expert row the
+ * reference's serial dot_mxfp4_f32_scalar sum, bit for bit; 1 runs the
+ * products on the matrix cores (f32 MFMA over the exact f32 weights
+ * lut * 2^(e-127) and the f32 activations), whose sums differ from the serial
+ * ones in rounding only (within 1e-4 of sum |w x| per product).  Returns the
+ * previous setting. */
+int rusty_hip_set_expert_mfma(int on);
+/* The batched expert product on DEVICE buffers (no counterpart in the
+ * reference; the product the gpt-oss prefill runs per layer, for tests and
+ * callers that route tokens themselves): for every pair p < n_pairs with
+ * expert e = sel[p] (0 <= e < n_exp; other values select nothing),
+ * y[p * ldy + r] = sum over c of row r of expert e's MXFP4 matrix times
+ * x[(x_per_pair ? p : p / top_k) * ldx + c], r < rows, c < cols.  Expert e's
+ * row r starts at w + e * exp_stride + r * row_stride (row_stride a multiple
+ * of 16 holding cols / 32 blocks of 17 bytes).  mfma = 0: the serial sums
+ * (bit-exact with dot_mxfp4_f32_scalar, src/simd.rs:5886-5902); 1: the
+ * matrix cores.  n_pairs <= 1024 * top_k.  Waits for all device work first
+ * and returns once y is written; returns 0 on bad arguments. */
+int rusty_hip_mxfp4_experts(const uint8_t *w, int64_t row_stride, int64_t exp_stride, uint32_t n_exp, uint32_t rows,
+                            uint32_t cols, const float *x, int64_t ldx, int x_per_pair, uint32_t top_k,
+                            const int32_t *sel, uint32_t n_pairs, float *y, int64_t ldy, int mfma);
 /* Copies slots [slot0, slot0+n_slots) of layer l's K (which = 0) or V
  * (which = 1) cache to / from host memory. */
 int rusty_hip_resident_kv_read(uint32_t l, uint32_t which, uint32_t slot0, uint32_t n_slots, float *host_out);

@@ -176,6 +176,7 @@ struct MxExpArgs {
     int64_t ldx, ldy;
     int32_t x_pair;
     const int32_t *sel;  // [n_pairs]
+    int32_t n_exp;       // the matrix-core kernel's expert count
 };
 
 __global__ __launch_bounds__(256) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
@@ -294,6 +295,181 @@ __global__ __launch_bounds__(256) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
 #pragma unroll
         for (int i = 0; i < MXE_G; i++)
             if (q0 + i < n && live) A.y[mat][(int64_t)s_list[q0 + i] * A.ldy + row] = sum[i];
+    }
+}
+
+// ---- opt-in expert product on the matrix cores ------------------------------
+// The reference sums each MXFP4 row serially (dot_mxfp4_f32_scalar); the
+// matrix cores sum in their own order, so this path is not bit-exact and is
+// off unless rusty_hip_set_expert_mfma(1) selects it.  Its inputs keep the
+// reference's precision: the weights lut[n] * 2^(e-127) are exact in f32 and
+// the activations are the f32 rows; only the order of the f32 additions of
+// the K products differs (v_mfma_f32_32x32x2_f32).
+//
+// moe_expert_lists_kernel: for every expert, the pairs routed to it in pair
+// order (lists[e * cap ..]), their count, and tile0[e] = the number of
+// 32-pair tiles of the experts before e (tile0[n_exp] = all tiles).  One
+// workgroup; wave w lists experts w, w + 4, ...
+#define MXM_PAIRS 32
+#define MXM_ROWS 128
+__global__ __launch_bounds__(256) void moe_expert_lists_kernel(const int32_t *sel, int n_pairs, int n_exp, int cap,
+                                                               int32_t *lists, int32_t *counts, int32_t *tile0) {
+    __shared__ int32_t s_cnt[64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int e = wave; e < n_exp; e += 4) {
+        int cnt = 0;
+        for (int base = 0; base < n_pairs; base += 64) {
+            const int p = base + lane;
+            const bool hit = p < n_pairs && sel[p] == e;
+            const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
+            const int at = cnt + __builtin_popcountll(m & ((1ull << lane) - 1ull));
+            if (hit && at < cap) lists[(size_t)e * cap + at] = p;
+            cnt += __builtin_popcountll(m);
+        }
+        cnt = min(cnt, cap);
+        if (lane == 0) {
+            counts[e] = cnt;
+            s_cnt[e] = cnt;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int t = 0;
+        for (int e = 0; e < n_exp; e++) {
+            tile0[e] = t;
+            t += (s_cnt[e] + MXM_PAIRS - 1) / MXM_PAIRS;
+        }
+        tile0[n_exp] = t;
+    }
+}
+
+// y[mat] row p = expert rows times pair p's activation for one (128-row tile,
+// 32-pair tile of one expert, matrix): grid (ceil(rows / 128), an upper bound
+// of the pair tiles, n_mats); workgroups past tile0[n_exp] return.  Wave w
+// owns rows row0 + 32 w + (lane % 32); per 32-element block, 16 MFMAs
+// 32x32x2: MFMA i takes element 16 h + i (h = lane / 32) of the block from
+// both operands, A = the pair's activation (m = pair), B = the weight (n =
+// row), so lane h decodes bytes 8h..8h+7 of its row's block (element 2b + 1
+// is the high nibble of byte b).  The weights arrive in 16-block chunks of
+// 272 bytes per row by coalesced direct loads into a double-buffered LDS
+// chunk; each lane then reads its row's chunk into registers (17 reads, an
+// odd number of 16-byte units per row: conflict-free); the activations come
+// from global memory one block ahead.
+__global__ __launch_bounds__(256) void gemm_mxfp4_experts_mfma_kernel(MxExpArgs A, const int32_t *lists,
+                                                                      const int32_t *counts, const int32_t *tile0,
+                                                                      int cap) {
+    __shared__ __align__(16) uint4 s_b[2][MXM_ROWS * 17];
+    __shared__ int32_t s_pair[MXM_PAIRS];
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int mat = blockIdx.z, gt = blockIdx.y;
+    const int n_exp = A.n_exp;
+    if (gt >= tile0[n_exp]) return;  // uniform
+    int e = 0;
+    while (e + 1 < n_exp && tile0[e + 1] <= gt) e++;
+    const int p0 = (gt - tile0[e]) * MXM_PAIRS;
+    const int np = min(MXM_PAIRS, counts[e] - p0);
+    if (tid < MXM_PAIRS) s_pair[tid] = lists[(size_t)e * cap + p0 + min(tid, np - 1)];
+    const int m = lane & 31, h = lane >> 5;
+    const int row0 = blockIdx.x * MXM_ROWS, row = row0 + 32 * wave + m;
+    const uint8_t *w = A.w[mat] + (int64_t)e * A.exp_stride;
+    const int64_t stride = A.row_stride;
+    const int nb = A.K >> 5, nch = (nb + MXF_C - 1) / MXF_C;
+    // piece f = 256 i + tid of a chunk: row f / 17, bytes 16 (f % 17); the
+    // 2176 pieces are 34 whole wave instructions, so a wave's instruction is
+    // either all inside the chunk or skipped
+    auto issue_chunk = [&](int c, int buf) {
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            if (256 * i + 64 * wave >= MXM_ROWS * 17) continue;  // uniform
+            const int f = 256 * i + tid, r = f / 17, pc = f - 17 * r;
+            const int rr = min(row0 + r, A.rows - 1);
+            const int64_t o = min((int64_t)(MXF_C * 17 * c + 16 * pc), stride - 16);
+            dma16(w + (int64_t)rr * stride + o, &s_b[buf][256 * i + 64 * wave]);
+        }
+    };
+    issue_chunk(0, 0);
+    __syncthreads();  // s_pair
+    const int pair = s_pair[m];
+    const float *xr = A.x + (A.x_pair ? (int64_t)pair : (int64_t)(pair / A.k)) * A.ldx + 16 * h;
+    float4 xa[4], xb[4];
+    auto load_x = [&](int b, float4 (&xv)[4]) {
+        const float4 *p = (const float4 *)(xr + 32 * (int64_t)min(b, nb - 1));
+#pragma unroll
+        for (int q = 0; q < 4; q++) xv[q] = p[q];
+    };
+    load_x(0, xa);
+    v16f acc = {};
+    for (int c = 0; c < nch; c++) {
+        RH_WAIT_VM(0);
+        __syncthreads();  // chunk c landed from every wave; every read of chunk c - 1 done
+        uint32_t wr[68];
+        {
+            const uint4 *rp = &s_b[c & 1][(32 * wave + m) * 17];
+#pragma unroll
+            for (int q = 0; q < 17; q++) {
+                const uint4 v = rp[q];
+                wr[4 * q] = v.x;
+                wr[4 * q + 1] = v.y;
+                wr[4 * q + 2] = v.z;
+                wr[4 * q + 3] = v.w;
+            }
+        }
+        // block j of the chunk with its activations in cur; the next block's
+        // go to nxt (clamped past the end), then, late in the chunk, the next
+        // chunk's weights are issued: a load issued after them would wait for
+        // them too (loads retire in order), and only the next chunk's first
+        // activations are
+        auto block = [&](int j, const float4 (&cur)[4], float4 (&nxt)[4]) {
+            const int b = MXF_C * c + j;
+            if (b >= nb) return;  // uniform
+            load_x(b + 1, nxt);
+            if (j == MXF_C - 2 && c + 1 < nch) issue_chunk(c + 1, (c + 1) & 1);
+            // bytes 17 j + 8 h .. + 7 and the scale byte 17 j + 16
+            const int o0 = 17 * j, o1 = 17 * j + 8, os = 17 * j + 16;
+            const uint32_t a0 = __builtin_amdgcn_alignbyte(wr[o0 / 4 + 1], wr[o0 / 4], o0 % 4);
+            const uint32_t a1 = __builtin_amdgcn_alignbyte(wr[o0 / 4 + 2], wr[o0 / 4 + 1], o0 % 4);
+            const uint32_t c0 = __builtin_amdgcn_alignbyte(wr[o1 / 4 + 1], wr[o1 / 4], o1 % 4);
+            const uint32_t c1 = __builtin_amdgcn_alignbyte(wr[o1 / 4 + 2], wr[o1 / 4 + 1], o1 % 4);
+            const uint32_t d0 = h ? c0 : a0, d1 = h ? c1 : a1;
+            const uint32_t ex = (wr[os / 4] >> (8 * (os % 4))) & 0xFFu;
+            const float sc = mxfp4_scale(ex);
+            float wv[16];
+            if (__builtin_amdgcn_ballot_w64(ex == 0u || ex == 255u) == 0) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const fp4x2_f32 lo = fp4x2_scaled(d0, sc, u), hi = fp4x2_scaled(d1, sc, u);
+                    wv[2 * u] = lo.x;
+                    wv[2 * u + 1] = lo.y;
+                    wv[8 + 2 * u] = hi.x;
+                    wv[9 + 2 * u] = hi.y;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t b0 = (d0 >> (8 * u)) & 0xFFu, b1 = (d1 >> (8 * u)) & 0xFFu;
+                    wv[2 * u] = mxfp4_nibble(b0 & 0xFu) * sc;
+                    wv[2 * u + 1] = mxfp4_nibble(b0 >> 4) * sc;
+                    wv[8 + 2 * u] = mxfp4_nibble(b1 & 0xFu) * sc;
+                    wv[9 + 2 * u] = mxfp4_nibble(b1 >> 4) * sc;
+                }
+            }
+            const float xs[16] = {cur[0].x, cur[0].y, cur[0].z, cur[0].w, cur[1].x, cur[1].y, cur[1].z, cur[1].w,
+                                  cur[2].x, cur[2].y, cur[2].z, cur[2].w, cur[3].x, cur[3].y, cur[3].z, cur[3].w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[i], wv[i], acc, 0, 0, 0);
+        };
+#pragma unroll
+        for (int j = 0; j < MXF_C; j += 2) {
+            block(j, xa, xb);
+            block(j + 1, xb, xa);
+        }
+    }
+    if (row >= A.rows) return;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int mi = 8 * (i >> 2) + 4 * h + (i & 3);
+        if (mi < np) A.y[mat][(int64_t)s_pair[mi] * A.ldy + row] = acc[i];
     }
 }
 

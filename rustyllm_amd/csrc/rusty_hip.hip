@@ -2009,6 +2009,9 @@ struct Resident {
     float *pxn = nullptr, *plk = nullptr, *plv = nullptr, *plog = nullptr, *pprob = nullptr, *pgate = nullptr,
           *pup = nullptr, *pproj = nullptr;
     int32_t *psel = nullptr;
+    // the matrix-core expert product's per-expert pair lists, counts and
+    // tile offsets (rusty_hip_set_expert_mfma)
+    int32_t *plists = nullptr, *pcounts = nullptr, *ptile0 = nullptr;
     std::map<std::pair<int, uint32_t>, hipGraphExec_t> graphs;  // by (mode, penalty bits)
     std::vector<void *> allocs;
     std::vector<std::pair<const void *, DevW>> wown;  // weight copies owned by the decoder
@@ -2643,8 +2646,53 @@ static int r_prefill_moe_alloc() {
         !r_alloc((void **)&R.plog, C * 64 * 4) || !r_alloc((void **)&R.psel, C * k * 4) ||
         !r_alloc((void **)&R.pprob, C * k * 4) || !r_alloc((void **)&R.pgate, C * k * hid * 4) ||
         !r_alloc((void **)&R.pup, C * k * hid * 4) || !r_alloc((void **)&R.pproj, C * k * R.dim * 4) ||
-        !r_alloc((void **)&R.pxn, C * R.dim * 4))
+        !r_alloc((void **)&R.pxn, C * R.dim * 4) || !r_alloc((void **)&R.plists, (size_t)64 * MXE_MAX_PAIRS * 4) ||
+        !r_alloc((void **)&R.pcounts, 64 * 4) || !r_alloc((void **)&R.ptile0, 65 * 4))
         return 0;
+    return 1;
+}
+
+// The expert product of the batched gpt-oss prefill: the reference's serial
+// row sums (gemv_mxfp4_experts_kernel, bit-exact; the default) or, when
+// rusty_hip_set_expert_mfma(1) chose it, the matrix cores (the pair lists
+// first, then gemm_mxfp4_experts_mfma_kernel).  lists/counts/tile0: the list
+// buffers; with lists_ready the lists of this sel are already built.
+static int g_expert_mfma = -1;
+static bool expert_mfma_on() {
+    if (g_expert_mfma < 0) {
+        const char *e = getenv("RUSTY_HIP_EXPERT_MFMA");
+        g_expert_mfma = (e && e[0] == '1') ? 1 : 0;
+    }
+    return g_expert_mfma == 1;
+}
+static int experts_enqueue(MxExpArgs A, int n_mats, bool mfma, int32_t *lists, int32_t *counts, int32_t *tile0,
+                           bool lists_ready, const char *name, hipStream_t s) {
+    if (A.n_exp < 1 || A.n_exp > 64 || A.K % 32 != 0 || A.n_pairs <= 0 || A.rows <= 0 || n_mats < 1 || n_mats > 2)
+        return 0;
+    if (!mfma) {
+        if (A.n_pairs > MXE_MAX_PAIRS * A.k) return 0;
+        ProfScope ps(name, s);
+        rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((A.rows + 63) / 64), (unsigned)A.n_exp, (unsigned)n_mats),
+                  dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+        return 1;
+    }
+    // the activation rows are read as 16-byte pieces
+    if (A.ldx % 4 != 0 || ((uintptr_t)A.x & 15) != 0 || A.row_stride % 16 != 0) return 0;
+    if (!lists_ready) {
+        ProfScope ps("moe_expert_lists", s);
+        rh_launch(moe_expert_lists_kernel, dim3(1), dim3(256), 0, s, A.sel, A.n_pairs, A.n_exp, MXE_MAX_PAIRS, lists,
+                  counts, tile0);
+        RH_LAUNCH_OK();
+    }
+    // at most ceil(n_pairs / 32) + n_exp pair tiles in all
+    const unsigned tiles = (unsigned)((A.n_pairs + MXM_PAIRS - 1) / MXM_PAIRS + A.n_exp);
+    ProfScope ps(name, s);
+    rh_launch(gemm_mxfp4_experts_mfma_kernel, dim3((unsigned)((A.rows + MXM_ROWS - 1) / MXM_ROWS), tiles,
+                                                   (unsigned)n_mats),
+              dim3(256), 0, s, A, (const int32_t *)lists, (const int32_t *)counts, (const int32_t *)tile0,
+              (int)MXE_MAX_PAIRS);
+    RH_LAUNCH_OK();
     return 1;
 }
 
@@ -2816,6 +2864,7 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
         // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2) (src/model.rs:6846-6898)
         if (!r_norm_batch_moe(Ly.ffn_norm, T, bd, s)) return 0;
         const int k = M.k, hid = M.hidden, np = T * k;
+        const bool mfma = expert_mfma_on();
         if (!q80_batch_enqueue(M.router, M.n_exp, dim, T, R.pxn, &bd, M.router_bias, R.plog, 64, EPI_STORE,
                                "pf_router", s))
             return 0;
@@ -2843,11 +2892,9 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
             A.ldy = hid;
             A.x_pair = 0;
             A.sel = R.psel;
+            A.n_exp = M.n_exp;
             if (M.up.stride != M.gate.stride) return 0;
-            ProfScope ps("pf_mxfp4_gate_up", s);
-            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((hid + 63) / 64), (unsigned)M.n_exp, 2), dim3(256), 0,
-                      s, A);
-            RH_LAUNCH_OK();
+            if (!experts_enqueue(A, 2, mfma, R.plists, R.pcounts, R.ptile0, false, "pf_mxfp4_gate_up", s)) return 0;
         }
         {
             ProfScope ps("moe_swiglu_batch", s);
@@ -2871,10 +2918,8 @@ static int r_prefill_chunk_moe(const int32_t *tok, int T, int pos0, hipStream_t 
             A.ldy = dim;
             A.x_pair = 1;
             A.sel = R.psel;
-            ProfScope ps("pf_mxfp4_down", s);
-            rh_launch(gemv_mxfp4_experts_kernel, dim3((unsigned)((dim + 63) / 64), (unsigned)M.n_exp, 1), dim3(256), 0,
-                      s, A);
-            RH_LAUNCH_OK();
+            A.n_exp = M.n_exp;
+            if (!experts_enqueue(A, 1, mfma, R.plists, R.pcounts, R.ptile0, true, "pf_mxfp4_down", s)) return 0;
         }
         {
             ProfScope ps("moe_combine_batch", s);
@@ -3239,6 +3284,53 @@ int rusty_hip_resident_prefill(const int32_t *tokens, uint32_t n_tokens, uint32_
     if (!r_ensure_tokens(n_tokens + 1)) return 0;
     RH_CHECK(hipMemcpy(R.tokens, tokens, (size_t)n_tokens * 4, hipMemcpyHostToDevice));
     if (!r_prefill_tokens((int)n_tokens, (int)start_pos)) return 0;
+    RH_CHECK(hipStreamSynchronize(g.s));
+    prof_drain();
+    return 1;
+}
+
+int rusty_hip_set_expert_mfma(int on) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    const int prev = expert_mfma_on() ? 1 : 0;
+    g_expert_mfma = on ? 1 : 0;
+    return prev;
+}
+
+int rusty_hip_mxfp4_experts(const uint8_t *w, int64_t row_stride, int64_t exp_stride, uint32_t n_exp, uint32_t rows,
+                            uint32_t cols, const float *x, int64_t ldx, int x_per_pair, uint32_t top_k,
+                            const int32_t *sel, uint32_t n_pairs, float *y, int64_t ldy, int mfma) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!init_locked() || !w || !x || !sel || !y || n_exp < 1 || n_exp > 64 || rows < 1 || cols < 32 ||
+        cols % 32 != 0 || top_k < 1 || top_k > 8 || n_pairs < 1 || n_pairs > (uint32_t)MXE_MAX_PAIRS * top_k ||
+        row_stride < (int64_t)cols / 32 * 17 || row_stride % 16 != 0 || exp_stride < (int64_t)rows * row_stride ||
+        ldy < (int64_t)rows || ldx < (int64_t)cols)
+        return 0;
+    static int32_t *lists[64] = {};  // per device: pair lists, counts, tile offsets
+    int32_t *&L = lists[g.dev];
+    if (mfma && !L && hipMalloc((void **)&L, ((size_t)64 * MXE_MAX_PAIRS + 64 + 65) * 4) != hipSuccess) {
+        L = nullptr;
+        return 0;
+    }
+    MxExpArgs A;
+    memset(&A, 0, sizeof(A));
+    A.w[0] = w;
+    A.y[0] = y;
+    A.row_stride = row_stride;
+    A.exp_stride = exp_stride;
+    A.rows = (int32_t)rows;
+    A.K = (int32_t)cols;
+    A.n_pairs = (int32_t)n_pairs;
+    A.k = (int32_t)top_k;
+    A.x = x;
+    A.ldx = ldx;
+    A.ldy = ldy;
+    A.x_pair = x_per_pair ? 1 : 0;
+    A.sel = sel;
+    A.n_exp = (int32_t)n_exp;
+    RH_CHECK(hipDeviceSynchronize());  // the caller's writes of w, x and sel are complete
+    int32_t *lp = L, *cp = L ? L + (size_t)64 * MXE_MAX_PAIRS : nullptr, *tp = cp ? cp + 64 : nullptr;
+    if (!experts_enqueue(A, 1, mfma != 0, lp, cp, tp, false, mfma ? "mxfp4_experts_mfma" : "mxfp4_experts", g.s))
+        return 0;
     RH_CHECK(hipStreamSynchronize(g.s));
     prof_drain();
     return 1;

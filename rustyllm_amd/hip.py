@@ -35,6 +35,7 @@ SYMBOLS = [
     "rusty_hip_kquant_matvec_batch", "rusty_hip_resident_prefill", "rusty_hip_bench_matvec",
     "rusty_hip_bench_attention", "rusty_hip_attention_noalloc", "rusty_hip_gguf_summary",
     "rusty_hip_resident_load_gguf", "rusty_hip_resident_enable_bf16", "rusty_hip_debug_stream_mark",
+    "rusty_hip_set_expert_mfma", "rusty_hip_mxfp4_experts",
 ]
 
 
@@ -92,6 +93,8 @@ _sig("rusty_hip_debug_rope", _i, _p, _p, _u32, _u32, _u32, _u32, _p, _u32)
 _sig("rusty_hip_debug_greedy", _i, _p, _u, _p, _u32, _f, _p)
 _sig("rusty_hip_debug_f16", _i, _p, _u, _p)
 _sig("rusty_hip_debug_stream_mark", _i)
+_sig("rusty_hip_set_expert_mfma", _i, _i)
+_sig("rusty_hip_mxfp4_experts", _i, _p, _i64, _i64, _u32, _u32, _u32, _p, _i64, _i, _u32, _p, _u32, _p, _i64, _i)
 _sig("rusty_hip_resident_configure_moe", _i, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f,
      _f)
 _sig("rusty_hip_resident_set_moe_layer", _i, _u32, _p)
@@ -635,3 +638,18 @@ def debug_stream_mark() -> bool:
     """Marks the resident decoder's next streamed attention launch as timed
     out (the failure path's test hook)."""
     return lib.rusty_hip_debug_stream_mark() == 1
+
+
+def set_expert_mfma(on: bool) -> bool:
+    """rusty_hip_set_expert_mfma: the gpt-oss prefill's expert product on the
+    matrix cores (True) or as the reference's serial sums (False, the
+    default).  Returns the previous setting."""
+    return lib.rusty_hip_set_expert_mfma(1 if on else 0) == 1
+
+
+def mxfp4_experts_dev(w_ptr, row_stride, exp_stride, n_exp, rows, cols, x_ptr, ldx, x_per_pair, top_k, sel_ptr,
+                      n_pairs, y_ptr, ldy, mfma) -> bool:
+    """rusty_hip_mxfp4_experts on device buffers given by address."""
+    return lib.rusty_hip_mxfp4_experts(w_ptr, row_stride, exp_stride, n_exp, rows, cols, x_ptr, ldx,
+                                       1 if x_per_pair else 0, top_k, sel_ptr, n_pairs, y_ptr, ldy,
+                                       1 if mfma else 0) == 1
