@@ -213,3 +213,64 @@ def test_config5_gptoss20b_prompt_prefill_1024(hip, exact):
     assert np.array_equal(g_last.view(np.uint32), o_last.view(np.uint32))
     del res, orc
     hip.weight_cache_clear()
+
+
+def test_config5_gptoss20b_expert_mfma_stream(hip, exact):
+    """The opt-in matrix-core expert product (rusty_hip_set_expert_mfma) at
+    the gpt-oss-20B shape: config 5's 1024-token prompt prefilled with it, then
+    64 greedy tokens, against the same run with the reference's serial sums
+    (the stream the test above pins to the oracle).  After a 16-token prompt
+    the first layer's K (computed before any expert product) is identical and
+    the second layer's (through f32 paths from the first layer's products)
+    within a relative 1e-5; the difference in later layers, in the logits
+    after longer prompts, and how many greedy tokens agree are printed: the
+    int8 (Q8_K) activation of wo and the top-k routing turn rounding-level
+    differences into whole quantization steps and expert flips, so the
+    difference grows through the layers."""
+    model = _model("gpt-oss-20b", 20, gptoss=True)
+    cfg = model["config"]
+    n, n_gen = 1024, 64
+    prompt = synth.token_ids(1024, n, cfg["vocab"])
+    res = hip.ResidentGptOss(model, n + n_gen + 8)
+    prev = hip.set_expert_mfma(False)
+    growth, layers = [], []
+    try:
+        # where the difference enters: the K/V of every layer after a 16-token
+        # prompt (layer 0's come before any expert product, layer 1's from the
+        # first layer's products through f32 paths only); then how it grows
+        # with the prompt's length
+        kv = []
+        for on in (False, True):
+            hip.set_expert_mfma(on)
+            assert res.prefill(prompt[:16], 0)
+            kv.append([res.kv_read(layer, 0, 0, 16) for layer in range(cfg["n_layers"])])
+        for layer in range(cfg["n_layers"]):
+            a, b = kv[0][layer], kv[1][layer]
+            layers.append(float(np.max(np.abs(b - a)) / np.max(np.abs(a))))
+        for m in (16, 128, 512):
+            hip.set_expert_mfma(False)
+            _, a = res.generate(prompt[:m], 0)
+            hip.set_expert_mfma(True)
+            _, b = res.generate(prompt[:m], 0)
+            growth.append((m, float(np.max(np.abs(b - a)) / np.max(np.abs(a)))))
+        hip.set_expert_mfma(False)
+        _, e_logits = res.generate(prompt, 0)
+        e_toks, _ = res.generate(prompt, n_gen, penalty=1.1)
+        hip.set_expert_mfma(True)
+        _, m_logits = res.generate(prompt, 0)
+        m_toks, _ = res.generate(prompt, n_gen, penalty=1.1)
+    finally:
+        hip.set_expert_mfma(prev)
+    rel = float(np.max(np.abs(m_logits - e_logits)) / np.max(np.abs(e_logits)))
+    print("[config5 expert mfma] relative K difference by layer after 16 tokens: " +
+          ", ".join(f"{r:.2g}" for r in layers), flush=True)
+    print("[config5 expert mfma] relative logit difference by prompt length: " +
+          ", ".join(f"{m}: {r:.3g}" for m, r in growth + [(n, rel)]), flush=True)
+    e_toks, m_toks = list(e_toks), list(m_toks)
+    same = sum(int(a == b) for a, b in zip(e_toks, m_toks))
+    prefix = next((i for i, (a, b) in enumerate(zip(e_toks, m_toks)) if a != b), len(e_toks))
+    print(f"[config5 expert mfma] logits after the prompt: max relative difference {rel:.3g}; greedy tokens "
+          f"equal {same}/{n_gen}, identical prefix {prefix}", flush=True)
+    assert layers[0] == 0.0 and layers[1] <= 1e-5, layers
+    del res
+    hip.weight_cache_clear()
