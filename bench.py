@@ -241,6 +241,7 @@ def main():
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 
 
 def bench_gptoss(args):
@@ -266,6 +267,9 @@ def bench_gptoss(args):
         # BASELINE configs[4]'s prompt: batched prefill of prefill_tokens ids
         prompt_pf = synth.token_ids(args.seed + 2, args.prefill_tokens, cfg["vocab"]).astype(np.int32)
         prefill = measure_prefill_gptoss(hip, res, prompt_pf, log)
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill}), flush=True)
+        return
     kd = cfg["n_kv_heads"] * cfg["head_dim"]
     # the cache is the reference's ring of min(window, max_len) slots: random
     # rows in every slot stand for the last positions before ctx - 1
@@ -385,10 +389,29 @@ def measure_prefill_gptoss(hip, res, toks, log):
     res.prefill(toks, 0)
     prof = hip.profile_results()
     hip.profile_enable(False)
-    log(f"prefill {n} tokens: {sec * 1e3:.1f} ms -> {n / sec:.1f} tok/s")
+    mfma = hip.set_expert_mfma(False)  # read the setting back
+    hip.set_expert_mfma(mfma)
+    log(f"prefill {n} tokens ({'matrix-core' if mfma else 'serial'} expert product): {sec * 1e3:.1f} ms -> "
+        f"{n / sec:.1f} tok/s")
     fam = sorted(((k, v) for k, v in prof.items() if v[1] > 0), key=lambda kv: -kv[1][0])
     log("prefill profile: " + ", ".join(f"{k}={v[0]:.2f}ms/{v[1]}" for k, v in fam[:12]))
+    # the expert gate/up products: 2 x (tokens x top_k pairs) x (2 x hidden
+    # rows) x d_model f32 operations per layer, over all of the prefill's
+    # launches (one per layer and chunk)
+    cfg = res.cfg
+    ops = 2.0 * n * cfg["top_k"] * 2 * cfg["hidden_dim"] * cfg["dim"] * cfg["n_layers"]
+    tot, cnt = prof.get("pf_mxfp4_gate_up", (0.0, 0))
+    tflops = ops / (tot * 1e-3) / 1e12 if cnt else 0.0
+    roofline = {"kernel": "pf_mxfp4_gate_up (%s: %d pairs x %d rows x %d, f32)"
+                % ("gemm_mxfp4_experts_mfma_kernel, f32 MFMA" if mfma else
+                   "gemv_mxfp4_experts_kernel, serial reference-order sums", n * cfg["top_k"],
+                   2 * cfg["hidden_dim"], cfg["dim"]),
+                "bound": "mfma" if mfma else "valu", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+                "ops_per_launch": ops / cnt if cnt else None,
+                "avg_launch_us": round(tot / cnt * 1e3, 1) if cnt else None, "launches": cnt}
     return {"tokens": n, "tok_s": round(n / sec, 1), "ms": round(sec * 1e3, 2),
+            "experts": "mfma" if mfma else "serial", "roofline": roofline,
             "profile_ms": {k: round(v[0], 3) for k, v in fam}}
 
 
