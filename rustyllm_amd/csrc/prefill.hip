@@ -35,21 +35,36 @@ __global__ __launch_bounds__(256) void quantize_q8k_batch_kernel(const float *x,
 
 // rms_norm_slice_into (src/model.rs:9889-9897, the same arithmetic as
 // rms_norm_into): each token row of x [T][n] normalized with w, then Q8_K.
-// Every workgroup of a row computes the row's sum in the reference's order.
-// grid (n/256, T), dynamic LDS n floats.
+// One workgroup per token: the row's sum of squares once, in the reference's
+// order, then wave w quantizes blocks w, w + 4, ... (four elements per lane;
+// the block maximum is exact in any order, so the values are
+// q8k_batch_store's).  n a multiple of 256.  grid (T), dynamic LDS n floats.
 __global__ __launch_bounds__(256) void rmsnorm_q8k_batch_kernel(const float *x, const float *w, float eps, int n,
                                                                 int8_t *qs, float *dx, int ldx) {
     extern __shared__ float s_x[];
     __shared__ float red[40];
-    const int t = blockIdx.y;
+    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *xr = x + (int64_t)t * n;
     for (int i = threadIdx.x; i < (n >> 2); i += 256) ((float4 *)s_x)[i] = ((const float4 *)xr)[i];
     __syncthreads();
     const float ss = sumsq_avx2_order(s_x, n, red);
     const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-    const int e = blockIdx.x * 256 + threadIdx.x;
-    const float o = s_x[e] * scale * w[e];
-    q8k_batch_store(o, blockIdx.x, t, n, qs, dx, ldx, red);
+    for (int b = wave; b < (n >> 8); b += 4) {
+        const int e = 256 * b + 4 * lane;
+        const float4 xv = *(const float4 *)(s_x + e), wv = *(const float4 *)(w + e);
+        const float o[4] = {xv.x * scale * wv.x, xv.y * scale * wv.y, xv.z * scale * wv.z, xv.w * scale * wv.w};
+        const float amax = wave_max(fmaxf(fmaxf(fabsf(o[0]), fabsf(o[1])), fmaxf(fabsf(o[2]), fabsf(o[3]))));
+        const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int q = (int)__builtin_rintf(o[i] * id);
+            q = max(-128, min(127, q));
+            packed |= (uint32_t)(q & 0xFF) << (8 * i);
+        }
+        *(uint32_t *)(qs + (int64_t)t * n + e) = packed;
+        if (lane == 0) dx[(int64_t)b * ldx + t] = amax * (1.0f / 127.0f);
+    }
 }
 
 // silu_mul_into over the batch (src/model.rs:10071-10075): h = silu(g) * u

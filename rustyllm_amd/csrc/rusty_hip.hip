@@ -2509,7 +2509,7 @@ static int r_prefill_alloc() {
 
 static int r_rmsnorm_batch(const float *norm_w, int T, const BatchXq &b, hipStream_t s) {
     ProfScope ps("rmsnorm_q8k_batch", s);
-    rh_launch(rmsnorm_q8k_batch_kernel, dim3(R.dim / 256, (unsigned)T), dim3(256), R.dim * 4, s, (const float *)R.px,
+    rh_launch(rmsnorm_q8k_batch_kernel, dim3((unsigned)T), dim3(256), R.dim * 4, s, (const float *)R.px,
               norm_w, R.eps, (int)R.dim, b.qs, b.dx, b.ldx);
     RH_LAUNCH_OK();
     return 1;
