@@ -133,6 +133,14 @@ struct AttnExactArgs {
     // launch reads at its start.  null: separate launches.
     uint32_t *sync;
     uint32_t ep;
+    // Streamed launch only, optional: the next GEMV's weight rows (pf_rows
+    // rows at pf_stride bytes), which its persistent grid (a multiple of 8
+    // workgroups) takes in groups of pf_group_rows rows round robin over the
+    // workgroups; the scores workgroups, once their tiles are scored, load
+    // the groups their XCD will compute into that XCD's L2.  null: none.
+    const uint8_t *pf;
+    int64_t pf_stride;
+    int32_t pf_rows, pf_group_rows;
 };
 
 // Element e of a head vector x after RoPE with the row's cos/sin, exactly as
@@ -1489,6 +1497,24 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_stream_kernel(AttnEx
             __syncthreads();  // also: the tile's LDS is free for the next
             if (threadIdx.x == 0)
                 __hip_atomic_store(stream_flag(A, h, tile), A.ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (A.pf) {
+            // workgroup i of a launch runs on XCD i % 8, in this launch and in
+            // the GEMV's, so the row groups g with g % 8 == this XCD are the
+            // ones its workgroups will compute there: one load per 128-byte
+            // line of them, spread over this XCD's scores workgroups, while the
+            // recurrences still run
+            const int x = (int)blockIdx.x & 7, nx = (ns - x + 7) >> 3, ib = (int)blockIdx.x >> 3;
+            const int ngr = (A.pf_rows + A.pf_group_rows - 1) / A.pf_group_rows;
+            const int64_t gbytes = (int64_t)A.pf_group_rows * A.pf_stride;
+            uint32_t acc = 0;
+            for (int gi = x + 8 * ib; gi < ngr; gi += 8 * nx) {
+                const uint8_t *base = A.pf + gi * gbytes;
+                const int64_t nbytes = min(gbytes, (int64_t)(A.pf_rows - gi * A.pf_group_rows) * A.pf_stride);
+                for (int64_t off = 128 * (int64_t)threadIdx.x; off < nbytes; off += 128 * 256)
+                    acc ^= *(const uint32_t *)(base + off);
+            }
+            asm volatile("" ::"v"(acc));  // the loads stay; their values are not used
         }
     }
     if (threadIdx.x == 0) {

@@ -2137,6 +2137,34 @@ __global__ void kv_transpose16_kernel(const uint16_t *v, int w, int slot0, int n
 
 // One token through the layer stack (and head / greedy by mode) on stream s.
 static int r_enqueue_moe(int mode, float penalty, hipStream_t s);
+// The wo rows the next launch computes, for the streamed attention's
+// scores workgroups to load into each XCD's L2 (AttnExactArgs.pf): only for
+// the launch shape that maps row groups to XCDs simply, a K-quant wo with one
+// row per wave tile (K <= 4096) and the attention-normalisation prologue,
+// whose persistent grid is a multiple of 8 workgroups taking four rows (one
+// per wave) at a time.  RUSTY_HIP_WO_PREFETCH=0 turns it off.
+static void wo_prefetch(const DevW &w, int K, const float *attn, int vd, AttnExactArgs &E) {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("RUSTY_HIP_WO_PREFETCH");
+        on = (e && e[0] == '0') ? 0 : 1;
+    }
+    E.pf = nullptr;
+    ActSpec a;
+    memset(&a, 0, sizeof(a));
+    a.mode = ACT_DEN;
+    a.x = (float *)attn;
+    a.group = vd;
+    if (!on || kq_prologue_act(a, K) != KQ_ACT_DEN || K > 4096 || (w.fmt != 12 && w.fmt != 14)) return;
+    const int grid = w.fmt == 12 ? persistent_grid(gemv_kq_kernel<12, false, 1, KQ_ACT_DEN>, w.rows, 4, GK_PRO)
+                                 : persistent_grid(gemv_kq_kernel<14, false, 1, KQ_ACT_DEN>, w.rows, 4, GK_PRO);
+    if (grid % 8 != 0) return;
+    E.pf = w.p;
+    E.pf_stride = w.stride;
+    E.pf_rows = w.rows;
+    E.pf_group_rows = 4;
+}
+
 static int r_enqueue(int mode, float penalty, hipStream_t s) {
     if (R.moe) return r_enqueue_moe(mode, penalty, s);
     const int dim = R.dim, qd = R.n_heads * R.hd, kd = R.n_kv * R.hd, vdim = R.n_kv * R.vd;
@@ -2232,6 +2260,7 @@ static int r_enqueue(int mode, float penalty, hipStream_t s) {
             E.fuse_rope = 1;
             E.kv_bf16 = R.kv_bf16 ? 1 : 0;
             E.start_t = R.st_host ? R.st_host->start_t : 0;  // the range's start as of this enqueue (a hint)
+            wo_prefetch(Ly.w[3], attn_cols, R.attn, R.vd, E);
             const float *den = nullptr;
             if (!attn_exact_launch(E, R.ex, XQ{}, s, false, &den, R.sync)) return 0;
             act_o.mode = ACT_DEN;
