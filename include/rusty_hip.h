@@ -222,7 +222,7 @@ int rusty_hip_set_expert_mfma(int on);
  * row r starts at w + e * exp_stride + r * row_stride (row_stride a multiple
  * of 16 holding cols / 32 blocks of 17 bytes).  mfma = 0: the serial sums
  * (bit-exact with dot_mxfp4_f32_scalar, src/simd.rs:5886-5902); 1: the
- * matrix cores.  n_pairs <= 1024 * top_k.  Waits for all device work first
+ * matrix cores.  n_pairs <= 1024.  Waits for all device work first
  * and returns once y is written; returns 0 on bad arguments. */
 int rusty_hip_mxfp4_experts(const uint8_t *w, int64_t row_stride, int64_t exp_stride, uint32_t n_exp, uint32_t rows,
                             uint32_t cols, const float *x, int64_t ldx, int x_per_pair, uint32_t top_k,

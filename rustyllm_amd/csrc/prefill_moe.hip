@@ -205,9 +205,13 @@ __global__ __launch_bounds__(256) void gemv_mxfp4_experts_kernel(MxExpArgs A) {
         const int p = base + lane;
         const bool hit = p < pb && A.sel[p] == e;
         const unsigned long long m = __builtin_amdgcn_ballot_w64(hit);
-        if (hit) s_list[off + __builtin_popcountll(m & ((1ull << lane) - 1ull))] = p;
+        const int at = off + __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        if (hit && at < MXE_MAX_PAIRS) s_list[at] = p;
         off += __builtin_popcountll(m);
     }
+    // the callers route every token to an expert at most once, so n <= T <=
+    // MXE_MAX_PAIRS; the bound only keeps the list inside its array
+    n = min(n, MXE_MAX_PAIRS);
     if (n == 0) return;  // uniform over the workgroup
     __syncthreads();
     const uint8_t *w = A.w[mat] + (int64_t)e * A.exp_stride;

@@ -3329,12 +3329,14 @@ int rusty_hip_mxfp4_experts(const uint8_t *w, int64_t row_stride, int64_t exp_st
                             uint32_t cols, const float *x, int64_t ldx, int x_per_pair, uint32_t top_k,
                             const int32_t *sel, uint32_t n_pairs, float *y, int64_t ldy, int mfma) {
     std::lock_guard<std::mutex> lk(g.mu);
+    // n_pairs <= 1024: an expert's pair list holds at most that many
     if (!init_locked() || !w || !x || !sel || !y || n_exp < 1 || n_exp > 64 || rows < 1 || cols < 32 ||
-        cols % 32 != 0 || top_k < 1 || top_k > 8 || n_pairs < 1 || n_pairs > (uint32_t)MXE_MAX_PAIRS * top_k ||
+        cols % 32 != 0 || top_k < 1 || top_k > 8 || n_pairs < 1 || n_pairs > (uint32_t)MXE_MAX_PAIRS ||
         row_stride < (int64_t)cols / 32 * 17 || row_stride % 16 != 0 || exp_stride < (int64_t)rows * row_stride ||
         ldy < (int64_t)rows || ldx < (int64_t)cols)
         return 0;
     static int32_t *lists[64] = {};  // per device: pair lists, counts, tile offsets
+    if (g.dev < 0 || g.dev >= 64) return 0;
     int32_t *&L = lists[g.dev];
     if (mfma && !L && hipMalloc((void **)&L, ((size_t)64 * MXE_MAX_PAIRS + 64 + 65) * 4) != hipSuccess) {
         L = nullptr;

@@ -49,8 +49,8 @@ def _routing(T, k, n_exp, seed, unused=()):
 @pytest.mark.parametrize("x_per_pair,shape", [
     (False, (6, 300, 2880, 70, 3)),     # ragged row tile, an empty expert, several pair tiles
     (True, (6, 300, 2880, 70, 3)),
-    (False, (32, 2880, 2880, 512, 4)),  # a gpt-oss-20B gate/up launch of one 512-token chunk
-    (True, (32, 2880, 2880, 512, 4)),   # ... and its down launch
+    (False, (32, 2880, 2880, 256, 4)),  # a gpt-oss-20B gate/up launch (1024 pairs)
+    (True, (32, 2880, 2880, 256, 4)),   # ... and its down launch
 ])
 def test_expert_product_mfma_within_tolerance(hip, x_per_pair, shape):
     import torch
