@@ -654,10 +654,15 @@ __global__ __launch_bounds__(256) void attn_exact_scores8_kernel(AttnExactArgs A
 __host__ __device__ inline int mq_tokens(int kvm) { return kvm >= MQ_PAIRS ? 1 : MQ_PAIRS / kvm; }
 template <int HD>
 __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs A) {
-    constexpr int M = HD / 8, LS = M + 4, RS = 8 * LS;
-    __shared__ __align__(16) float s_k[EX_TILE * RS];
+    // q slices padded (LS: a pair's eight slices in distinct banks, read once
+    // per pair); K slices unpadded (LSK, read once per wave), and the staged
+    // scores over the K tile once every wave holds its K in registers: 52 KB
+    // at HD 128, three workgroups per CU
+    constexpr int M = HD / 8, LS = M + 4, RS = 8 * LS, LSK = M, RSK = 8 * LSK;
+    static_assert(MQ_PAIRS * EX_TILE <= EX_TILE * RSK, "the score staging fits in the K tile");
+    __shared__ __align__(16) float s_k[EX_TILE * RSK];
     __shared__ __align__(16) float s_q[MQ_PAIRS * RS];
-    __shared__ float s_sc[MQ_PAIRS * EX_TILE];
+    float *s_sc = s_k;
     const int kvm = A.kv_mul, qb = mq_tokens(kvm);
     const int tile = blockIdx.x, h = blockIdx.y, z0 = blockIdx.z * qb;
     const int nz = min(qb, A.n_tok - z0), npair = nz * kvm;
@@ -713,11 +718,11 @@ __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs
         const int lbase = (4 * c4) & 7, m = (4 * c4) >> 3;
 #pragma unroll
         for (int i = 0; i < NKR; i++) {
-            float *d = s_k + (r0 + i * RSTEP) * RS + m;
-            d[(lbase + 0) * LS] = kreg[i].x;
-            d[(lbase + 1) * LS] = kreg[i].y;
-            d[(lbase + 2) * LS] = kreg[i].z;
-            d[(lbase + 3) * LS] = kreg[i].w;
+            float *d = s_k + (r0 + i * RSTEP) * RSK + m;
+            d[(lbase + 0) * LSK] = kreg[i].x;
+            d[(lbase + 1) * LSK] = kreg[i].y;
+            d[(lbase + 2) * LSK] = kreg[i].z;
+            d[(lbase + 3) * LSK] = kreg[i].w;
         }
     }
     __syncthreads();
@@ -725,7 +730,7 @@ __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs
     float k[2][M];
 #pragma unroll
     for (int p = 0; p < 2; p++) {
-        const float *kr = s_k + (16 * wave + 8 * p + sub) * RS + l * LS;
+        const float *kr = s_k + (16 * wave + 8 * p + sub) * RSK + l * LSK;
 #pragma unroll
         for (int r = 0; r < M / 4; r++) {
             const float4 f = *(const float4 *)(kr + 4 * r);
@@ -735,22 +740,24 @@ __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs
             k[p][4 * r + 3] = f.w;
         }
     }
-    for (int pr = 0; pr < npair; pr++) {
-        const int g = pr % kvm;
-        const bool x4 = A.kv_bf16 || (A.sinks == nullptr && (kvm == 4 || kvm == 6) && g < 4);
-        float q[M];
-        {
-            const float *qr = s_q + pr * RS + l * LS;
+    __syncthreads();  // every wave holds its K: the tile's LDS now takes the scores
+    // pair pr's q slice; pairs two at a time, so four independent chains
+    // (two pairs x two positions) interleave, and both pairs' reads go out
+    // together
+    auto read_q = [&](int pr, float (&q)[M]) {
+        const float *qr = s_q + pr * RS + l * LS;
 #pragma unroll
-            for (int r = 0; r < M / 4; r++) {
-                const float4 f = *(const float4 *)(qr + 4 * r);
-                q[4 * r] = f.x;
-                q[4 * r + 1] = f.y;
-                q[4 * r + 2] = f.z;
-                q[4 * r + 3] = f.w;
-            }
+        for (int r = 0; r < M / 4; r++) {
+            const float4 f = *(const float4 *)(qr + 4 * r);
+            q[4 * r] = f.x;
+            q[4 * r + 1] = f.y;
+            q[4 * r + 2] = f.z;
+            q[4 * r + 3] = f.w;
         }
-        float y[2];
+    };
+    // one pair's two positions in scores8_tile's lane arithmetic (x4: one
+    // accumulator; dot_f32_avx2: four, then (a0 + a1) + (a2 + a3))
+    auto dots = [&](bool x4, const float (&q)[M], float (&y)[2]) {
         if (x4) {
             y[0] = 0.0f;
             y[1] = 0.0f;
@@ -770,6 +777,8 @@ __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs
                 y[p] = (a[0] + a[1]) + (a[2] + a[3]);
             }
         }
+    };
+    auto store = [&](int pr, const float (&y)[2]) {
 #pragma unroll
         for (int p = 0; p < 2; p++) {
             const float a = y[p] + row_shl<4>(y[p]);
@@ -777,6 +786,39 @@ __global__ __launch_bounds__(256) void attn_exact_scores_mq_kernel(AttnExactArgs
             const float d = b + row_shl<2>(b);
             if (l == 0) s_sc[pr * EX_TILE + 16 * wave + 8 * p + sub] = d * A.scale;
         }
+    };
+    // the x4 form: every head of a bf16 cache, heads 0..3 of a kv_mul 4/6
+    // group without sinks (as scores8_tile)
+    const bool bf = A.kv_bf16 != 0, gx = A.sinks == nullptr && (kvm == 4 || kvm == 6);
+    int g = 0;  // head of pair pr within its group
+    for (int pr = 0; pr < npair; pr += 2) {
+        const int pr1 = min(pr + 1, npair - 1), g1 = g + 1 == kvm ? 0 : g + 1;
+        float qa[M], qb[M], ya[2], yb[2];
+        read_q(pr, qa);
+        read_q(pr1, qb);
+        const bool xa = bf || (gx && g < 4), xb = bf || (gx && g1 < 4);
+        if (xa == xb) {
+            // the same form: the two pairs' chains interleaved
+            if (xa) {
+                ya[0] = ya[1] = yb[0] = yb[1] = 0.0f;
+#pragma unroll
+                for (int mm = 0; mm < M; mm++) {
+                    ya[0] = fmaf(qa[mm], k[0][mm], ya[0]);
+                    ya[1] = fmaf(qa[mm], k[1][mm], ya[1]);
+                    yb[0] = fmaf(qb[mm], k[0][mm], yb[0]);
+                    yb[1] = fmaf(qb[mm], k[1][mm], yb[1]);
+                }
+            } else {
+                dots(false, qa, ya);
+                dots(false, qb, yb);
+            }
+        } else {
+            dots(xa, qa, ya);
+            dots(xb, qb, yb);
+        }
+        store(pr, ya);
+        if (pr + 1 < npair) store(pr + 1, yb);
+        g = g1 + 1 == kvm ? 0 : g1 + 1;
     }
     __syncthreads();
     // coalesced score rows and tile maxima of the tokens whose range reaches
