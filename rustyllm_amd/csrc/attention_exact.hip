@@ -1251,6 +1251,23 @@ __device__ __forceinline__ void c4_steps16_slow(float e16, const float *v, float
     chain_steps16_flags<false, X4>(e, v, o, bits);
 }
 
+// The last, partial chunk of a range: steps 0..n-1 (n < 16), each in its
+// own form as chain_steps16_flags (xd: the grouped/denominator form on a new
+// maximum), e of step j from lane j of the row.
+__device__ __forceinline__ void steps16_partial(float e16, const float *v, float &o, uint32_t bits, int n,
+                                                bool xd) {
+    float e[16];
+    bcast16_all(e16, e);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        if (j < n) {
+            const float on = fmaf(e[j], v[j], o);
+            const float ox = xd ? fmaf(v[j], 1.0f, o * e[j]) : fmaf(o, e[j], v[j]);
+            o = ((bits >> j) & 1u) ? ox : on;
+        }
+    }
+}
+
 // New-max summary of a group for the wave's four rows.  w: lane l < 8*C4_PER
 // holds new-max word l & 1 of row (l >> 1) & 3 in tile l >> 3 of the group
 // (0 in the other lanes); bit l of lo (hi) is set when that word has a new
@@ -1634,14 +1651,7 @@ __device__ __forceinline__ float chain_tok_run(const AttnExactArgs &A, int s0, i
                 c4_steps16_slow<false>(e16, v, o, bits);
             }
         } else {
-            // the last, partial chunk: step by step in its own form
-            for (int j = 0; j < n; j++) {
-                const float e = ef[16 * k + j];
-                const float vj = v[j];
-                const float on = fmaf(e, vj, o);
-                const float ox = (x4 || DEN) ? fmaf(vj, 1.0f, o * e) : fmaf(o, e, vj);
-                o = ((bits >> j) & 1u) ? ox : on;
-            }
+            steps16_partial(e16, v, o, bits, n, x4 || DEN);  // the last, partial chunk
         }
     };
     float ea, eb, va[16], vb[16];
@@ -1689,6 +1699,178 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok_kernel(AttnExactArgs
             if (dcol == 0) A.den[h * kvm + g] = o;
         } else {
             A.out[(size_t)(h * kvm + g) * A.vd + slice * 16 + dcol] = o;
+        }
+    }
+}
+
+// Eight steps of four independent chains o_t += e_t(step) * v(step) with
+// each e_t's step j from lane j of its 16-lane row (DPP row_newbcast), the
+// chains interleaved so that the four FMAs of a step issue back to back.
+#define FMA8X4_STEP(J, V)                                                                             \
+    "v_fmac_f32_dpp %0, %4, " V " row_newbcast:" J " row_mask:0xf bank_mask:0xf\n\t"                  \
+    "v_fmac_f32_dpp %1, %5, " V " row_newbcast:" J " row_mask:0xf bank_mask:0xf\n\t"                  \
+    "v_fmac_f32_dpp %2, %6, " V " row_newbcast:" J " row_mask:0xf bank_mask:0xf\n\t"                  \
+    "v_fmac_f32_dpp %3, %7, " V " row_newbcast:" J " row_mask:0xf bank_mask:0xf\n\t"
+__device__ __forceinline__ void cons_fma8x4_dpp_lo(const float (&e)[4], const float *v, float (&o)[4]) {
+    asm("s_nop 1\n\t" FMA8X4_STEP("0", "%8") FMA8X4_STEP("1", "%9") FMA8X4_STEP("2", "%10") FMA8X4_STEP("3", "%11")
+            FMA8X4_STEP("4", "%12") FMA8X4_STEP("5", "%13") FMA8X4_STEP("6", "%14") FMA8X4_STEP("7", "%15")
+        : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3])
+        : "v"(e[0]), "v"(e[1]), "v"(e[2]), "v"(e[3]), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]),
+          "v"(v[5]), "v"(v[6]), "v"(v[7]));
+}
+__device__ __forceinline__ void cons_fma8x4_dpp_hi(const float (&e)[4], const float *v, float (&o)[4]) {
+    asm("s_nop 1\n\t" FMA8X4_STEP("8", "%8") FMA8X4_STEP("9", "%9") FMA8X4_STEP("10", "%10")
+            FMA8X4_STEP("11", "%11") FMA8X4_STEP("12", "%12") FMA8X4_STEP("13", "%13") FMA8X4_STEP("14", "%14")
+                FMA8X4_STEP("15", "%15")
+        : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3])
+        : "v"(e[0]), "v"(e[1]), "v"(e[2]), "v"(e[3]), "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]),
+          "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
+}
+#undef FMA8X4_STEP
+
+// A raw buffer resource over p: no stride, the largest record count (the
+// callers keep every offset in range themselves), 32-bit data format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// C for four consecutive query tokens at once (prefill with a shared range
+// start: no window, a linear cache and its tiled transposed V copy): each
+// wave is attn_exact_chain_tok_kernel's task for tokens 4 Z .. 4 Z + 3 (grid
+// z = Z), four chains per lane.  A chunk of V (four 16-byte loads per lane)
+// serves the four tokens, each with its own coefficient word and new-max
+// bits; chunk k + 1's loads are issued before chunk k's steps.  Chunks that
+// every token runs whole without a new maximum take the interleaved DPP
+// chains; others run each token's chain in its own form, exactly as the
+// one-token kernel, so every token's output and denominator are its values.
+__global__ __launch_bounds__(256) void attn_exact_chain_tok4_kernel(AttnExactArgs A) {
+    constexpr int NT = 4;
+    const int z0 = (int)blockIdx.z * NT, nt = min(NT, A.n_tok - z0);
+    const int s0 = A.start_t;
+    const int ctx0 = A.pos0 + z0 - s0 + 1;  // the first token's range; token i's is ctx0 + i
+    const int kvm = A.kv_mul, ngrp = (kvm + 3) / 4, nsl = A.vd / 16;
+    const int n_chain = A.n_kv * ngrp * nsl, n_task = n_chain + A.n_kv * ngrp;
+    const int task = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (nt <= 0 || ctx0 <= 0 || task >= n_task) return;
+    const bool den = task >= n_chain;
+    const int r = den ? task - n_chain : task;
+    const int h = r % A.n_kv, rr = r / A.n_kv;
+    const int g0 = 4 * (den ? rr : rr / nsl), slice = den ? 0 : rr % nsl;
+    const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
+    const int g = g0 + row, gr = min(g, kvm - 1);
+    const bool x4 = A.sinks == nullptr && (kvm == 4 || kvm == 6) && g0 == 0;
+    // Every load is a buffer load: a wave-uniform resource and byte offset
+    // (scalar registers) plus a lane's 32-bit byte offset, so that a chunk's
+    // loads need no vector address registers and the next chunk's loads never
+    // wait on this one's.  Token i's scratch is i * tok_scratch floats past
+    // the first token's (tokens past the launch's end repeat its last).
+    const __amdgpu_buffer_rsrc_t re = buf_rsrc(A.e + (int64_t)z0 * A.tok_scratch);
+    const __amdgpu_buffer_rsrc_t rm = buf_rsrc(A.newmask + (int64_t)z0 * A.tok_scratch);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(A.vt + vt4_off(h * A.vd + slice * 16, s0, A.vt_stride));
+    int ctx[NT], tofs[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+        ctx[i] = ctx0 + min(i, nt - 1);
+        tofs[i] = min(i, nt - 1) * (int)A.tok_scratch * 4;
+    }
+    const int off_e = ((int)e_index(A, h, gr, 0) + dcol) * 4;
+    const int off_m = (h * kvm + gr) * (A.cap / 32) * 4, off_v = dcol * 16;
+    const int nk = (ctx[NT - 1] + 15) / 16;  // chunks of the longest range
+    float o[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) o[i] = (den && A.sinks) ? 1.0f : 0.0f;
+    auto load = [&](auto dc, int k, float (&e16)[NT], uint32_t (&bits)[NT], float *v) {
+        constexpr bool DEN = decltype(dc)::value;
+        k = min(k, nk - 1);
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const int ki = min(k, (ctx[i] + 15) / 16 - 1);  // a chunk past a token's range is not used
+            e16[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, off_e, tofs[i] + 64 * ki, 0));
+            // the word; step takes chunk k's half
+            bits[i] = __builtin_amdgcn_raw_buffer_load_b32(rm, off_m, tofs[i] + 4 * (ki >> 1), 0);
+        }
+        if constexpr (DEN) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = 1.0f;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                // four consecutive slots of the lane's dim: 64 floats per slot group
+                const auto f = __builtin_amdgcn_raw_buffer_load_b128(rv, off_v, (4 * k + q) * 256, 0);
+                v[4 * q] = __uint_as_float(f[0]);
+                v[4 * q + 1] = __uint_as_float(f[1]);
+                v[4 * q + 2] = __uint_as_float(f[2]);
+                v[4 * q + 3] = __uint_as_float(f[3]);
+            }
+        }
+    };
+    // one token's 16-or-fewer steps of chunk k in its own form (the one-token
+    // kernel's step)
+    auto step1 = [&](int k, int i, float e16, uint32_t bits, const float *v) {
+        const int n = min(16, ctx[i] - 16 * k);
+        if (n <= 0) return;
+        if (n == 16) {
+            const uint32_t f = bits ? 1u : 0u;
+            const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
+                                 __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
+            if (any == 0u) {
+                cons_fma16_dpp(e16, v, o[i]);
+            } else if (x4 || den) {
+                float a16, m16;
+                aff_pair16(e16, bits, lane, a16, m16);
+                cons_affine16_dpp(a16, m16, v, o[i]);
+            } else {
+                c4_steps16_slow<false>(e16, v, o[i], bits);
+            }
+        } else {
+            steps16_partial(e16, v, o[i], bits, n, x4 || den);
+        }
+    };
+    auto step = [&](int k, const float (&e16)[NT], const uint32_t (&words)[NT], const float *v) {
+        uint32_t bits[NT], f = 0u;
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            bits[i] = (words[i] >> (16 * (k & 1))) & 0xFFFFu;  // chunk k of a token whose range holds it
+            f |= bits[i];
+        }
+        f = f ? 1u : 0u;
+        const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
+                             __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
+        if (any == 0u && 16 * k + 16 <= ctx[0]) {
+            // every token runs the whole chunk, none with a new maximum
+            cons_fma8x4_dpp_lo(e16, v, o);
+            cons_fma8x4_dpp_hi(e16, v, o);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NT; i++) step1(k, i, e16[i], bits[i], v);
+        }
+    };
+    // the pipeline in two copies, the denominators' (v = 1, no V loads) and
+    // the outputs', so that each copy's load waits count only its own loads
+    auto run = [&](auto dc) {
+        float ea[NT], eb[NT], va[16], vb[16];
+        uint32_t ba[NT], bb[NT];
+        load(dc, 0, ea, ba, va);
+        for (int k = 0; k < nk; k += 2) {
+            load(dc, k + 1, eb, bb, vb);
+            step(k, ea, ba, va);
+            if (k + 1 >= nk) break;
+            load(dc, k + 2, ea, ba, va);
+            step(k + 1, eb, bb, vb);
+        }
+    };
+    if (den) run(std::true_type{});
+    else run(std::false_type{});
+    if (g < kvm) {
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            if (i >= nt) break;
+            const int64_t zo = (int64_t)(z0 + i);
+            if (den) {
+                if (dcol == 0) A.den[zo * A.tok_scratch + h * kvm + g] = o[i];
+            } else {
+                A.out[zo * A.o_tok + (size_t)(h * kvm + g) * A.vd + slice * 16 + dcol] = o[i];
+            }
         }
     }
 }

@@ -1009,6 +1009,17 @@ static bool stream_enabled() {
     return on == 1;
 }
 
+// RUSTY_HIP_CHAIN_TOK4=0: the multi-token recurrence one token per wave
+// throughout (the four-token kernel off)
+static bool chain_tok4_enabled() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("RUSTY_HIP_CHAIN_TOK4");
+        on = (e && e[0] == '0') ? 0 : 1;
+    }
+    return on == 1;
+}
+
 // sync: the resident decoder's flag block for the streamed launch (null:
 // separate scores, coefficient and chain launches).
 static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipStream_t s, bool finish = true,
@@ -1107,9 +1118,23 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
     {
         ProfScope ps("attn_exact_chain", s);
         if (c4 && A.n_tok > 0) {
-            // many query tokens: one independent wave per task, no LDS ring
+            // many query tokens: one independent wave per task, no LDS ring;
+            // four tokens per wave where they share the range start and the
+            // transposed V copy covers the last token's range
             const int tasks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
-            rh_launch(attn_exact_chain_tok_kernel, dim3((tasks + 3) / 4, 1, nz), dim3(256), 0, s, A);
+            const int64_t ctx_last = (int64_t)A.pos0 + A.n_tok - A.start_t;
+            const bool tok4 = chain_tok4_enabled() && A.vt != nullptr && A.window == 0 && !A.lin &&
+                              (A.start_t & 3) == 0 && A.pos0 >= A.start_t &&
+                              A.pos0 + A.n_tok - 1 < A.slot_count &&
+                              A.start_t + (ctx_last + EX_TILE - 1) / EX_TILE * EX_TILE <= A.vt_stride &&
+                              (int64_t)A.n_heads * A.cap < (1ll << 28) &&
+                              A.tok_scratch < (1ll << 27);  // byte offsets within 31 bits
+            if (tok4) {
+                rh_launch(attn_exact_chain_tok4_kernel, dim3((tasks + 3) / 4, 1, (A.n_tok + 3) / 4), dim3(256), 0,
+                          s, A);
+            } else {
+                rh_launch(attn_exact_chain_tok_kernel, dim3((tasks + 3) / 4, 1, nz), dim3(256), 0, s, A);
+            }
         } else if (c4) {
             const int blocks = A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
             rh_launch(attn_exact_chain4_kernel, dim3(blocks, 1, nz), dim3(64 * C4_WAVES), 0, s, A);
