@@ -1745,7 +1745,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p) {
 // one-token kernel, so every token's output and denominator are its values.
 __global__ __launch_bounds__(256) void attn_exact_chain_tok4_kernel(AttnExactArgs A) {
     constexpr int NT = 4;
-    const int z0 = (int)blockIdx.z * NT, nt = min(NT, A.n_tok - z0);
+    // the longest ranges (the last tokens) are dispatched first
+    const int z0 = (int)(gridDim.z - 1 - blockIdx.z) * NT, nt = min(NT, A.n_tok - z0);
     const int s0 = A.start_t;
     const int ctx0 = A.pos0 + z0 - s0 + 1;  // the first token's range; token i's is ctx0 + i
     const int kvm = A.kv_mul, ngrp = (kvm + 3) / 4, nsl = A.vd / 16;
@@ -1833,10 +1834,9 @@ __global__ __launch_bounds__(256) void attn_exact_chain_tok4_kernel(AttnExactArg
             bits[i] = (words[i] >> (16 * (k & 1))) & 0xFFFFu;  // chunk k of a token whose range holds it
             f |= bits[i];
         }
-        f = f ? 1u : 0u;
-        const uint32_t any = __builtin_amdgcn_readlane(f, 0) | __builtin_amdgcn_readlane(f, 16) |
-                             __builtin_amdgcn_readlane(f, 32) | __builtin_amdgcn_readlane(f, 48);
-        if (any == 0u && 16 * k + 16 <= ctx[0]) {
+        // (a row's lanes hold the same words)
+        const bool any = __builtin_amdgcn_ballot_w64(f != 0u) != 0u;
+        if (!any && 16 * k + 16 <= ctx[0]) {
             // every token runs the whole chunk, none with a new maximum
             cons_fma8x4_dpp_lo(e16, v, o);
             cons_fma8x4_dpp_hi(e16, v, o);
