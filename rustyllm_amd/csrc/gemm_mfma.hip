@@ -12,10 +12,12 @@
 // m = 8*(i/4) + 4*(l/32) + i%4, n = l%32, with K8 = 16 (x32) or 8 (x16).
 // Here m = token and n = weight row: a lane owns one weight row, so its
 // scales and minimums are per-lane values, and 16 tokens.
-//   Q4_K: one x32 MFMA per 32-element sub-block on the raw nibbles (C_j =
-//         sum q x exactly), isum += sc_j * C_j; imin = sum_j m_j * bsums_j =
-//         sum_e m_j(e) * x_e is one more MFMA per sub-block with m_j as the
-//         B operand; value = dx * (d*isum - dmin*imin).
+//   Q4_K: two x32 MFMAs per 32-element sub-block on the nibbles times the
+//         two base-8 digits of the sub-block scale, accumulated over the
+//         block, so isum = sum_j sc_j * C_j (C_j = sum q x) exactly; imin =
+//         sum_j m_j * bsums_j = sum_e m_j(e) * x_e is one more MFMA per
+//         sub-block with m_j as the B operand; value = dx * (d*isum -
+//         dmin*imin).
 //   Q6_K: one x16 MFMA per 16-element scale group on q - 32 as signed
 //         bytes, isum += sc_g * C_g; value = (dx*d) * isum.
 // Rows and tokens past the ends read clamped (in-bounds) data and are not
@@ -93,15 +95,37 @@ __device__ __forceinline__ void gemm_w_load(GemmW<F_Q6_K> &W, const uint8_t *blk
 
 // Integer sums of block b for the wave's 32 rows x 32*NT tokens: isum (and
 // for Q4_K imin) per C element, from the activation tile xs.
+typedef unsigned short rh_u16x2 __attribute__((ext_vector_type(2)));
+
+// Each byte of the four dwords of x (nibbles, < 16) times s (< 8): one packed
+// 16-bit multiply per dword, exact because no byte product (< 128) carries
+// into the next byte.
+__device__ __forceinline__ rh_v4i bytes_times(const rh_v4i &x, int s) {
+    const rh_u16x2 m = {(unsigned short)s, (unsigned short)s};
+    rh_v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int xi = x[i];  // a plain int (a bit-cast of the element expression itself reads element 0)
+        r[i] = __builtin_bit_cast(int, __builtin_bit_cast(rh_u16x2, xi) * m);
+    }
+    return r;
+}
+
+// Q4_K: the sub-block scale (6 bits) enters the B operand as two digits, sc
+// = 8 * (sc >> 3) + (sc & 7), each digit times a nibble fitting a signed
+// byte, so that the MFMAs accumulate the whole block: isum = 8 * hi + lo =
+// sum_j sc_j * C_j exactly (the same integer as one MFMA per sub-block scaled
+// afterwards, with no per-sub-block multiply-add on the vector ALU).
 template <int NT>
 __device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q4_K> &W, const int8_t *xs, int lane,
                                                 int (&isum)[NT][16], rh_v16i (&imin)[NT]) {
     const int half = lane >> 5, n = lane & 31;
+    rh_v16i ahi[NT], alo[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
         imin[tt] = rh_v16i{};
-#pragma unroll
-        for (int i = 0; i < 16; i++) isum[tt][i] = 0;
+        ahi[tt] = rh_v16i{};
+        alo[tt] = rh_v16i{};
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -113,6 +137,8 @@ __device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q4_K> &W, const in
                             (int)(qs.w & 0x0F0F0F0Fu)};
         const rh_v4i bhi = {(int)((qs.x >> 4) & 0x0F0F0F0Fu), (int)((qs.y >> 4) & 0x0F0F0F0Fu),
                             (int)((qs.z >> 4) & 0x0F0F0F0Fu), (int)((qs.w >> 4) & 0x0F0F0F0Fu)};
+        const rh_v4i l8 = bytes_times(blo, sc0 >> 3), l1 = bytes_times(blo, sc0 & 7);
+        const rh_v4i h8 = bytes_times(bhi, sc1 >> 3), h1 = bytes_times(bhi, sc1 & 7);
         const int mb0 = bcast_byte(m0), mb1 = bcast_byte(m1);
         const rh_v4i bm0 = {mb0, mb0, mb0, mb0}, bm1 = {mb1, mb1, mb1, mb1};
 #pragma unroll
@@ -120,17 +146,18 @@ __device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q4_K> &W, const in
             const int8_t *xr = xs + (32 * tt + n) * GEMM_XS + 64 * q + 16 * half;
             const rh_v4i a0 = *(const rh_v4i *)xr;
             const rh_v4i a1 = *(const rh_v4i *)(xr + 32);
-            const rh_v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, blo, rh_v16i{}, 0, 0, 0);
-            const rh_v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bhi, rh_v16i{}, 0, 0, 0);
+            ahi[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, l8, ahi[tt], 0, 0, 0);
+            alo[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, l1, alo[tt], 0, 0, 0);
             imin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bm0, imin[tt], 0, 0, 0);
+            ahi[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, h8, ahi[tt], 0, 0, 0);
+            alo[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, h1, alo[tt], 0, 0, 0);
             imin[tt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bm1, imin[tt], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                isum[tt][i] = __mul24(sc0, c0[i]) + isum[tt][i];
-                isum[tt][i] = __mul24(sc1, c1[i]) + isum[tt][i];
-            }
         }
     }
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) isum[tt][i] = (ahi[tt][i] << 3) + alo[tt][i];
 }
 
 template <int NT>
@@ -281,6 +308,130 @@ __global__ __launch_bounds__(256) void gemm_kq_mfma_kernel(GemmArgs A) {
             else
                 *yp = v;
         }
+}
+
+// The same products with the blocks of K split over the workgroup's four
+// waves, for launches with too few (row tile, token tile) pairs to fill the
+// chip (the q/k/v/o projections, the long-K down projection): one workgroup
+// per 32 weight rows x 32 tokens, wave w computing blocks w, w+4, w+8, ...
+// Each wave stages its own block's activations in its own LDS tile, computes
+// the block's per-output value exactly as gemm_kq_mfma_kernel does, and
+// leaves the 16 values of each lane in LDS; after a barrier, wave w adds the
+// round's values of C elements 4w..4w+3 to its accumulators in block order
+// (a barrier before the next round's values are written keeps them until
+// every wave has read these).  Every output is therefore the same sum of
+// the same per-block values in the same order: bit-identical to the
+// one-wave-per-row-tile kernel.
+template <int FMT>
+__global__ __launch_bounds__(256) void gemm_kq_mfma_ks_kernel(GemmArgs A) {
+    __shared__ __align__(16) int8_t s_xs[4][32 * GEMM_XS];  // per wave: 32 token rows of one block
+    __shared__ float s_v[4][16][64];                        // [wave][C element][lane]
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, n = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = blockIdx.x * 32, t0 = blockIdx.y * 32;
+    const int row = min(r0 + n, A.rows - 1);
+    const uint8_t *wr = A.w + (int64_t)row * A.row_stride;
+    const int nb = A.K >> 8, rounds = (nb + 3) >> 2;
+    constexpr int BB = FMT == F_Q4_K ? 144 : 210;
+    // activation pieces of the wave's block: lane -> (token, 16-byte part),
+    // 16 lanes per token row, 4 rows per load
+    const int8_t *xsrc[8];
+    int xdst[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int p = lane + 64 * j, tok = p >> 4, part = p & 15;
+        xsrc[j] = A.xq + (int64_t)min(t0 + tok, A.T - 1) * A.K + 16 * part;
+        xdst[j] = tok * GEMM_XS + 16 * part;
+    }
+    int8_t *xs = s_xs[wave];
+    int b = min(wave, nb - 1);
+    GemmW<FMT> W;
+    gemm_w_load(W, wr + (int64_t)b * BB, half);
+    {
+        uint4 st[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) st[j] = *(const uint4 *)(xsrc[j] + 256 * b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) *(uint4 *)(xs + xdst[j]) = st[j];
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int it = 0; it < rounds; it++) {
+        b = 4 * it + wave;
+        const bool have = b < nb;
+        const int bn = min(b + 4, nb - 1);  // the wave's next block (clamped; unused past the end)
+        GemmW<FMT> Wn;
+        gemm_w_load(Wn, wr + (int64_t)bn * BB, half);
+        float v[16] = {};
+        if (have) {
+            float4 dv[4];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++)
+                dv[g4] = *(const float4 *)(A.dx + (int64_t)b * A.ldx + t0 + 4 * half + 8 * g4);
+            int isum[1][16];
+            rh_v16i imin[1];
+            gemm_block_ints<1>(W, xs, lane, isum, imin);
+            float d, dmin = 0.0f;
+            if constexpr (FMT == F_Q4_K) {
+                d = h2f(W.hdr.x & 0xFFFF);
+                dmin = h2f(W.hdr.x >> 16);
+            } else {
+                d = h2f(W.d & 0xFFFF);
+            }
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const float dxs[4] = {dv[g4].x, dv[g4].y, dv[g4].z, dv[g4].w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int i = 4 * g4 + r;
+                    if constexpr (FMT == F_Q4_K) {
+                        const float t1 = d * (float)isum[0][i];
+                        const float t2 = dmin * (float)imin[0][i];
+                        v[i] = dxs[r] * (t1 - t2);
+                    } else {
+                        v[i] = (dxs[r] * d) * (float)isum[0][i];
+                    }
+                }
+            }
+        }
+        // the next block's activations, in flight over the barrier (issued
+        // after this block's products, so that they hold no registers there)
+        rh_v4i st[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) st[j] = *(const rh_v4i *)(xsrc[j] + 256 * bn);
+        __syncthreads();  // every wave has read the previous round's values
+        if (have) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) s_v[wave][i][lane] = v[i];
+        }
+        // (this wave's own tile: its LDS reads above complete before these
+        // writes, in program order)
+#pragma unroll
+        for (int j = 0; j < 8; j++) *(rh_v4i *)(xs + xdst[j]) = st[j];
+        __syncthreads();
+        // the round's blocks in order, for this wave's four C elements
+#pragma unroll
+        for (int w2 = 0; w2 < 4; w2++) {
+            if (4 * it + w2 >= nb) break;
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] += s_v[w2][4 * wave + e][lane];
+        }
+        W = Wn;
+    }
+    if (r0 + n >= A.rows) return;
+    const float bias = A.bias ? A.bias[r0 + n] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = 4 * wave + e;
+        const int t = t0 + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (t >= A.T) continue;
+        float *yp = A.y + (int64_t)t * A.ldy + r0 + n;
+        float v = acc[e];
+        if (A.bias) v = v + bias;
+        if (A.epi == EPI_ADD)
+            *yp += v;
+        else
+            *yp = v;
+    }
 }
 
 }  // namespace rh

@@ -1203,12 +1203,34 @@ static int gemm_kq_enqueue(const DevW &W, const BatchXq &b, int T, float *y, int
     A.y = y;
     A.bias = bias;
     // 32 tokens per workgroup: a 64-token tile needs twice the registers
-    // (one wave per SIMD) and measured slower at every size tried
+    // (two waves per SIMD) and measured slower (the smaller grids lose more
+    // than the 14336-row products gain).
+    // RUSTY_HIP_GEMM_KSPLIT: 0 never, 2 always, else (default) the K-split
+    // kernel for Q6_K (whose row-tile kernel holds 256 registers, one wave
+    // per SIMD) and for Q4_K when the row-tile grid would hold fewer
+    // workgroups than CUs (the 1024-row k projection of an 8B-class model;
+    // the 4096-row ones measured faster on the row-tile kernel)
+    static int ksm = -1;
+    if (ksm < 0) {
+        const char *e = getenv("RUSTY_HIP_GEMM_KSPLIT");
+        ksm = e ? atoi(e) : 1;
+    }
     const int64_t row_tiles = (W.rows + 127) / 128;
     const int tok = 32;
-    const dim3 grid((unsigned)row_tiles, (unsigned)((T + tok - 1) / tok));
-    const uint32_t lds = 2u * tok * GEMM_XS;
+    const int64_t tok_tiles = (T + tok - 1) / tok;
+    const bool ks = ksm == 2 || (ksm == 1 && (W.fmt == 14 || row_tiles * tok_tiles < (int64_t)g.n_cu));
     ProfScope ps(prof_name ? prof_name : (W.fmt == 12 ? "gemm_q4k_mfma" : "gemm_q6k_mfma"), s);
+    if (ks) {
+        const dim3 grid((unsigned)((W.rows + 31) / 32), (unsigned)tok_tiles);
+        if (W.fmt == 12)
+            rh_launch(gemm_kq_mfma_ks_kernel<F_Q4_K>, grid, dim3(256), 0, s, A);
+        else
+            rh_launch(gemm_kq_mfma_ks_kernel<F_Q6_K>, grid, dim3(256), 0, s, A);
+        RH_LAUNCH_OK();
+        return 1;
+    }
+    const dim3 grid((unsigned)row_tiles, (unsigned)tok_tiles);
+    const uint32_t lds = 2u * tok * GEMM_XS;
     if (W.fmt == 12)
         rh_launch(gemm_kq_mfma_kernel<F_Q4_K, 1>, grid, dim3(256), lds, s, A);
     else
