@@ -20,7 +20,8 @@ def _batch_ref(t, w, xs, rows, cols):
 
 
 @pytest.mark.parametrize("t,rows,cols,T", [
-    (12, 4096, 4096, 70),    # ragged token tile
+    (12, 4096, 4096, 70),    # ragged token tile (K split over a workgroup's waves)
+    (12, 4096, 1024, 250),   # a grid of 256 row tiles: one row tile per wave, ragged tokens
     (12, 33, 512, 1),        # one token, partial row tile
     (12, 1000, 256, 64),     # one block per row, exact token tile
     (14, 1024, 14336, 5),    # Q6_K down-projection width
@@ -36,10 +37,12 @@ def test_kquant_batch_bit_exact(hip, t, rows, cols, T):
 
 
 @pytest.mark.parametrize("t", [12, 14])
-def test_kquant_batch_random_blocks(hip, t):
+@pytest.mark.parametrize("rows,cols,T", [(96, 1024, 40), (4096, 256, 256)])
+def test_kquant_batch_random_blocks(hip, t, rows, cols, T):
     """Uniformly random block bytes: every scale, minimum and quant value the
-    formats allow, so the integer sums reach their extremes."""
-    rows, cols, T = 96, 1024, 40
+    formats allow, so the integer sums reach their extremes (Q4_K's largest
+    scale digit times the largest nibble included).  The second shape is a
+    Q4_K grid large enough for one row tile per wave."""
     rng = np.random.default_rng(t)
     w = _blocks(t, rows * cols // 256, rng)
     xs = (rng.standard_normal((T, cols)) * rng.uniform(0.1, 10, (T, 1))).astype(np.float32)
