@@ -1408,37 +1408,55 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
 // blocks are funnel-shifted out of the registers.  A row-per-lane global load
 // would touch 64 cache lines per instruction.
 #define MXF_C 16  // blocks per chunk
+__device__ __forceinline__ float swiglu_gpt_oss_ref(float g, float u);
+
+// SWI = false: tile t is 64 rows of one matrix, lane = row.  SWI = true (the
+// routed experts' gate/up with gpt-oss's SwiGLU as the epilogue): matrices
+// 0..n/2-1 are the gates and n/2.. the ups of the same experts; tile t is 32
+// rows of gate matrix g (lanes 0..31) and the same 32 rows of up matrix g +
+// n/2 (lanes 32..63), each lane's row summed exactly as without SWI, its
+// bias added, then lane l < 32 stores swiglu_gpt_oss(gate, up of lane l + 32)
+// at the gate's row, as moe_swiglu_kernel would from the two stored rows.
+template <bool SWI>
 __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
     __shared__ __align__(16) uint4 s_b[64 * 17];
     const int K = A.K, nb = K >> 5, lane = threadIdx.x;
     const int tile = blockIdx.x;
+    const int n_sel = SWI ? A.n_mats / 2 : A.n_mats;  // matrices the tiles are counted over
     int mi = 0;
 #pragma unroll
     for (int t = 1; t < GEMV_MAX_MATS; t++)
-        if (t < A.n_mats && tile >= A.m[t].tile_begin) mi = t;
+        if (t < n_sel && tile >= A.m[t].tile_begin) mi = t;
     const GemvMat M = mat_sel(A, mi);
+    const GemvMat MU = SWI ? mat_sel(A, mi + n_sel) : M;  // SWI: the up matrix of the same expert
     const float *xs = M.x ? M.x : A.x;
-    const uint8_t *w = M.w;
-    const float *bias = M.bias;
+    const uint8_t *w = M.w, *wu = MU.w;
+    const float *bias = M.bias, *bias_u = MU.bias;
     if (M.sel) {
         const int64_t e = *M.sel;
         w += e * M.sel_w;
+        wu += e * MU.sel_w;
         if (bias) bias += e * M.sel_b;
+        if (bias_u) bias_u += e * MU.sel_b;
     }
-    const int row0 = (tile - M.tile_begin) * 64, row = row0 + lane;
+    constexpr int TR = SWI ? 32 : 64;  // rows of one matrix per tile
+    const bool up_lane = SWI && lane >= 32;
+    const int row0 = (tile - M.tile_begin) * TR, row = row0 + (SWI ? (lane & 31) : lane);
     const bool live = row < M.rows;
-    const int64_t stride = M.row_stride;  // a multiple of 16 that holds nb * 17 bytes
+    const int64_t stride = M.row_stride;  // a multiple of 16 that holds nb * 17 bytes (the same for the ups)
     const int nch = (nb + MXF_C - 1) / MXF_C;
     // the 17 pieces this lane moves per chunk: piece f = 64 i + lane of the
-    // tile is row f / 17, bytes 16 (f % 17) of the chunk; rows past the
-    // matrix read its last row and bytes past the row's end its last piece
+    // tile is tile row f / 17, bytes 16 (f % 17) of the chunk (SWI: tile rows
+    // 32.. are the up matrix's); rows past the matrix read its last row and
+    // bytes past the row's end its last piece
     auto issue_chunk = [&](int c) {
         int r = lane / 17, p = lane - 17 * (lane / 17);
 #pragma unroll
         for (int i = 0; i < 17; i++) {
-            const int rr = min(row0 + r, M.rows - 1);
+            const bool ru = SWI && r >= 32;
+            const int rr = min(row0 + (SWI ? (r & 31) : r), M.rows - 1);
             const int64_t off = min((int64_t)(MXF_C * 17 * c + 16 * p), stride - 16);
-            dma16(w + (int64_t)rr * stride + off, &s_b[64 * i]);
+            dma16((ru ? wu : w) + (int64_t)rr * stride + off, &s_b[64 * i]);
             r += 3;  // 64 = 3 * 17 + 13
             p += 13;
             if (p >= 17) {
@@ -1518,7 +1536,13 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
             }
         }
     }
-    if (live) {
+    if constexpr (SWI) {
+        const float *bl = up_lane ? bias_u : bias;
+        float out = sum;
+        if (bl && live) out += bl[row];
+        const float u = __shfl_down(out, 32);  // lane l < 32: the up row's value from lane l + 32
+        if (!up_lane && live) M.y[row] = swiglu_gpt_oss_ref(out, u);
+    } else if (live) {
         float out = sum;
         if (bias) out += bias[row];
         if (A.epi == EPI_ADD)

@@ -559,23 +559,25 @@ static int launch_q8p_any(const GemvArgs &A, int act, bool sw, hipStream_t s) {
     default: return launch_q8p_w<7>(A, act, sw, s);
     }
 }
+// RUSTY_HIP_MX_SERIAL_PER_CU: tiles per CU up to which the producer/adder
+// workgroups serve an MXFP4 launch (two per CU fit in LDS, but measured
+// slower on the gpt-oss expert launches: 279 against 285 tok/s)
+static int mx_serial_per_cu() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("RUSTY_HIP_MX_SERIAL_PER_CU");
+        v = e ? atoi(e) : 1;
+    }
+    return v;
+}
 template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
     if constexpr (FMT == F_MXFP4) {
         ProfScope ps("gemv_mxfp4", s);
-        // RUSTY_HIP_MX_SERIAL_PER_CU: tiles per CU up to which the
-        // producer/adder workgroups serve a launch (two per CU fit in LDS,
-        // but measured slower on the gpt-oss expert launches: 279 against
-        // 285 tok/s)
-        static int serial_per_cu = -1;
-        if (serial_per_cu < 0) {
-            const char *e = getenv("RUSTY_HIP_MX_SERIAL_PER_CU");
-            serial_per_cu = e ? atoi(e) : 1;
-        }
-        if (A.n_tiles > serial_per_cu * g.n_cu) {
+        if (A.n_tiles > mx_serial_per_cu() * g.n_cu) {
             // more tiles than CUs: one wave per tile computes its own terms,
             // several tiles per SIMD
-            rh_launch(gemv_mxfp4_fused_kernel, dim3(A.n_tiles), dim3(64), 0, s, A);
+            rh_launch(gemv_mxfp4_fused_kernel<false>, dim3(A.n_tiles), dim3(64), 0, s, A);
         } else {
             // one workgroup per tile: the serial row sums are spread over a
             // summing wave and MXP term-producing waves
@@ -1372,6 +1374,36 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
         return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
     };
     const int rpt_in = M.gate.fmt == 8 ? 8 : 64, rpt_down = M.down.fmt == 8 ? 8 : 64;
+    // MXFP4 gate/up with as many 32-row tiles as the one-wave kernel takes:
+    // SwiGLU (and the biases) in its epilogue, no moe_swiglu launch
+    static int swi_fuse = -1;
+    if (swi_fuse < 0) {
+        const char *e = getenv("RUSTY_HIP_MOE_SWIGLU_FUSE");
+        swi_fuse = (e && e[0] == '0') ? 0 : 1;
+    }
+    const int swi_tiles = k * ((hidden + 31) / 32);
+    if (swi_fuse && M.gate.fmt == F_MXFP4 && 2 * k <= GEMV_MAX_MATS && M.up.stride == M.gate.stride &&
+        swi_tiles > mx_serial_per_cu() * g.n_cu) {
+        GemvArgs A;
+        memset(&A, 0, sizeof(A));
+        A.K = dim;
+        A.epi = EPI_STORE;
+        A.x = xn;
+        A.n_mats = 2 * k;
+        for (int r = 0; r < k; r++) {
+            A.m[r] = expert_mat(M.gate, hidden, r, gate + (size_t)r * hidden, nullptr);
+            A.m[r].bias = M.gb;
+            A.m[r].sel_b = M.gb_stride;
+            A.m[r].tile_begin = r * ((hidden + 31) / 32);
+            A.m[k + r] = expert_mat(M.up, hidden, r, up + (size_t)r * hidden, nullptr);
+            A.m[k + r].bias = M.ub;
+            A.m[k + r].sel_b = M.ub_stride;
+        }
+        A.n_tiles = swi_tiles;
+        ProfScope ps("gemv_mxfp4", s);
+        rh_launch(gemv_mxfp4_fused_kernel<true>, dim3(A.n_tiles), dim3(64), 0, s, A);
+        RH_LAUNCH_OK();
+    } else {
     {
         GemvArgs A;
         memset(&A, 0, sizeof(A));
@@ -1390,6 +1422,7 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
         rh_launch(moe_swiglu_kernel, dim3((hidden + 255) / 256, k), dim3(256), 0, s, gate, (const float *)up, hidden, k,
                   (const int32_t *)sel, M.gb, M.gb_stride, M.ub, M.ub_stride);
         RH_LAUNCH_OK();
+    }
     }
     {
         GemvArgs A;
