@@ -78,6 +78,15 @@ struct GemvArgs {
     float act_eps;
     int32_t act_group;
     int32_t act_store;  // prologue modes: workgroup 0 also writes the Q8_K vector it built to xq
+    // MoE expert launches (MXFP4 one-wave kernel): the router's topk_n logits
+    // are ranked in every workgroup (moe_topk_row's selection) and slot r =
+    // GemvMat::sel - topk_sel takes the rank-r expert instead of reading
+    // *sel; workgroup 0 also stores every slot's expert and weight to
+    // topk_sel / topk_prob for the later launches.  null: *sel as given.
+    const float *topk_logits;
+    int32_t topk_n, topk_k;
+    int32_t *topk_sel;
+    float *topk_prob;
 };
 // byte offset of a kernel's second GemvArgs argument in its argument segment
 constexpr int KARG_SECOND = (int)((sizeof(GemvArgs) + alignof(GemvArgs) - 1) / alignof(GemvArgs) * alignof(GemvArgs));
@@ -1409,6 +1418,7 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
 // would touch 64 cache lines per instruction.
 #define MXF_C 16  // blocks per chunk
 __device__ __forceinline__ float swiglu_gpt_oss_ref(float g, float u);
+__device__ __forceinline__ int moe_topk_wave(const float *logits, int n, int k, int slot, int32_t *sel, float *prob);
 
 // SWI = false: tile t is 64 rows of one matrix, lane = row.  SWI = true (the
 // routed experts' gate/up with gpt-oss's SwiGLU as the epilogue): matrices
@@ -1433,7 +1443,10 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
     const uint8_t *w = M.w, *wu = MU.w;
     const float *bias = M.bias, *bias_u = MU.bias;
     if (M.sel) {
-        const int64_t e = *M.sel;
+        const int64_t e = A.topk_logits
+                              ? moe_topk_wave(A.topk_logits, A.topk_n, A.topk_k, (int)(M.sel - A.topk_sel),
+                                              blockIdx.x == 0 ? A.topk_sel : nullptr, A.topk_prob)
+                              : *M.sel;
         w += e * M.sel_w;
         wu += e * MU.sel_w;
         if (bias) bias += e * M.sel_b;

@@ -54,6 +54,47 @@ __device__ __forceinline__ void moe_topk_row(const float *logits, int n, int k, 
     }
 }
 
+// moe_topk_row's selection inside a one-wave workgroup (no LDS, no
+// workgroup barrier): returns the expert of slot `slot` (wave-uniform); with
+// sel non-null lane 0 also stores every slot's expert and softmax weight,
+// computed as moe_topk_row computes them.
+__device__ __forceinline__ int moe_topk_wave(const float *logits, int n, int k, int slot, int32_t *sel, float *prob) {
+    const int lane = threadIdx.x & 63;
+    const float v = lane < n ? logits[lane] : 0.0f;
+    const int32_t key = total_key(v);
+    int rank = 0;
+    for (int j = 0; j < n; j++) {
+        const int32_t kj = __shfl(key, j, 64);
+        rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
+    }
+    const unsigned long long ms = __builtin_amdgcn_ballot_w64(lane < n && rank == slot);
+    const int e_slot = ms ? (int)__builtin_ctzll(ms) : 0;
+    if (sel) {
+        float vr[8];
+        int ir[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const unsigned long long m = __builtin_amdgcn_ballot_w64(lane < n && rank == r);
+            ir[r] = m ? (int)__builtin_ctzll(m) : 0;
+            vr[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), ir[r]));
+        }
+        if (lane == 0) {
+            float mx = -INFINITY;
+            for (int r = 0; r < k; r++) mx = fmaxf(mx, vr[r]);  // f32::max keeps the non-NaN operand
+            float e[8], sum = 0.0f;
+            for (int r = 0; r < k; r++) {
+                e[r] = expf_glibc(vr[r] - mx);
+                sum += e[r];
+            }
+            for (int r = 0; r < k; r++) {
+                sel[r] = ir[r];
+                prob[r] = sum > 0.0f ? e[r] / sum : e[r];
+            }
+        }
+    }
+    return e_slot;
+}
+
 __global__ __launch_bounds__(64) void moe_topk_kernel(const float *logits, int n, int k, int32_t *sel, float *prob) {
     moe_topk_row(logits, n, k, sel, prob);
 }

@@ -1346,7 +1346,18 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
         a.xq = a.mode == ACT_QUANT ? g.xq : (dim % 256 == 0 ? xq : XQ{});
         if (!gemv_multi_act(&mr, 1, dim, EPI_STORE, a, s)) return 0;
     }
-    {
+    // MXFP4 gate/up with as many 32-row tiles as the one-wave kernel takes:
+    // SwiGLU (and the biases) in its epilogue, no moe_swiglu launch, and the
+    // top-k selection in every workgroup, no moe_topk launch
+    static int swi_fuse = -1;
+    if (swi_fuse < 0) {
+        const char *e = getenv("RUSTY_HIP_MOE_SWIGLU_FUSE");
+        swi_fuse = (e && e[0] == '0') ? 0 : 1;
+    }
+    const int swi_tiles = k * ((hidden + 31) / 32);
+    const bool swi = swi_fuse && M.gate.fmt == F_MXFP4 && 2 * k <= GEMV_MAX_MATS && M.up.stride == M.gate.stride &&
+                     swi_tiles > mx_serial_per_cu() * g.n_cu;
+    if (!swi) {
         ProfScope ps("moe_topk", s);
         rh_launch(moe_topk_kernel, dim3(1), dim3(64), 0, s, (const float *)logits, M.n_exp, k, sel, prob);
         RH_LAUNCH_OK();
@@ -1374,16 +1385,7 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
         return A.m[0].fmt == 8 ? launch_f32x<F_Q8_0>(A, s) : launch_f32x<F_MXFP4>(A, s);
     };
     const int rpt_in = M.gate.fmt == 8 ? 8 : 64, rpt_down = M.down.fmt == 8 ? 8 : 64;
-    // MXFP4 gate/up with as many 32-row tiles as the one-wave kernel takes:
-    // SwiGLU (and the biases) in its epilogue, no moe_swiglu launch
-    static int swi_fuse = -1;
-    if (swi_fuse < 0) {
-        const char *e = getenv("RUSTY_HIP_MOE_SWIGLU_FUSE");
-        swi_fuse = (e && e[0] == '0') ? 0 : 1;
-    }
-    const int swi_tiles = k * ((hidden + 31) / 32);
-    if (swi_fuse && M.gate.fmt == F_MXFP4 && 2 * k <= GEMV_MAX_MATS && M.up.stride == M.gate.stride &&
-        swi_tiles > mx_serial_per_cu() * g.n_cu) {
+    if (swi) {
         GemvArgs A;
         memset(&A, 0, sizeof(A));
         A.K = dim;
@@ -1400,6 +1402,11 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
             A.m[k + r].sel_b = M.ub_stride;
         }
         A.n_tiles = swi_tiles;
+        A.topk_logits = logits;
+        A.topk_n = M.n_exp;
+        A.topk_k = k;
+        A.topk_sel = sel;
+        A.topk_prob = prob;
         ProfScope ps("gemv_mxfp4", s);
         rh_launch(gemv_mxfp4_fused_kernel<true>, dim3(A.n_tiles), dim3(64), 0, s, A);
         RH_LAUNCH_OK();
