@@ -87,6 +87,12 @@ struct GemvArgs {
     int32_t topk_n, topk_k;
     int32_t *topk_sel;
     float *topk_prob;
+    // Q8_0 f32-activation kernel, NORM instance: the staged activation is
+    // replaced by its RMSNorm with norm_w (rms_norm_into's sum order and expression), and
+    // workgroup 0 also stores the normalised vector to norm_out.
+    const float *norm_w;
+    float norm_eps;
+    float *norm_out;
 };
 // byte offset of a kernel's second GemvArgs argument in its argument segment
 constexpr int KARG_SECOND = (int)((sizeof(GemvArgs) + alignof(GemvArgs) - 1) / alignof(GemvArgs) * alignof(GemvArgs));
@@ -1145,6 +1151,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_q8_0_pipe_kernel(GemvArgs A) 
 // loads in flight while this one is summed; each lane then reads its
 // block's scale (2 bytes) and its four quants (bytes 8i + j) from LDS.
 #define Q8F_C 32  // blocks per chunk
+template <bool NORM>
 __global__ __launch_bounds__(64) void gemv_q8_0_f32x_kernel(GemvArgs A) {
     extern __shared__ float s_x[];  // [K]
     __shared__ __align__(16) uint4 s_w[2][9 * 64];
@@ -1176,7 +1183,39 @@ __global__ __launch_bounds__(64) void gemv_q8_0_f32x_kernel(GemvArgs A) {
         }
     };
     issue_chunk(0, 0);
-    for (int i = 4 * lane; i < K; i += 256) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
+    if constexpr (NORM) {
+        // rms_norm_into (src/model.rs:5429-5437) over the staged x, as
+        // rmsnorm_row computes it; the weights (K <= 3072: twelve float4 per
+        // lane) are loaded with x, before the sum of squares
+        __shared__ float red[40];
+        const int k4 = K >> 2;
+        float4 wv[12], xv[12];
+#pragma unroll
+        for (int k = 0; k < 12; k++) {
+            const int i4 = min(lane + 64 * k, k4 - 1);
+            xv[k] = ((const float4 *)xs)[i4];
+            wv[k] = ((const float4 *)A.norm_w)[i4];
+        }
+#pragma unroll
+        for (int k = 0; k < 12; k++)
+            if (lane + 64 * k < k4) ((float4 *)s_x)[lane + 64 * k] = xv[k];
+        __syncthreads();
+        const float ss = sumsq_avx2_order(s_x, K, red);
+        const float scale = 1.0f / sqrtf(ss / (float)K + A.norm_eps);
+#pragma unroll
+        for (int k = 0; k < 12; k++) {
+            const int i4 = lane + 64 * k;
+            if (i4 < k4) {
+                const float4 x4 = xv[k], w4 = wv[k];
+                const float4 o = make_float4(x4.x * scale * w4.x, x4.y * scale * w4.y, x4.z * scale * w4.z,
+                                             x4.w * scale * w4.w);
+                ((float4 *)s_x)[i4] = o;
+                if (blockIdx.x == 0) ((float4 *)A.norm_out)[i4] = o;
+            }
+        }
+    } else {
+        for (int i = 4 * lane; i < K; i += 256) *(float4 *)(s_x + i) = *(const float4 *)(xs + i);
+    }
     const int j = lane & 7, rr = lane >> 3;
     const int row = row0 + rr;
     const bool ok = row < M.rows;

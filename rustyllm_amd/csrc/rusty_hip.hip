@@ -589,7 +589,7 @@ static int launch_f32x(const GemvArgs &A, hipStream_t s) {
         static_assert(FMT == F_Q8_0, "f32-activation formats: Q8_0 and MXFP4");
         // one workgroup per 8-row tile
         ProfScope ps("gemv_f32x", s);
-        rh_launch(gemv_q8_0_f32x_kernel, dim3(A.n_tiles), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
+        rh_launch(gemv_q8_0_f32x_kernel<false>, dim3(A.n_tiles), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
         RH_LAUNCH_OK();
         return 1;
     }
@@ -1321,8 +1321,12 @@ struct MoeDev {
 // xq: the Q8_K form of xn for the router's integer path when dim is a whole
 // number of 256-blocks; an empty XQ quantizes xn here into a buffer this call
 // may allocate (so not under graph capture).
-static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float *moe_out, float *x_add, float *buf,
-                           hipStream_t s, int32_t **sel_out = nullptr, float **prob_out = nullptr) {
+// norm_w: xn is first built as RMSNorm(norm_x) with norm_w (rms_norm_into),
+// by the router launch's prologue where the router takes the Q8_0
+// f32-activation kernel, else by a standalone RMSNorm launch.
+static int moe_ffn_enqueue(const MoeDev &M, float *xn, const XQ &xq, float *moe_out, float *x_add, float *buf,
+                           hipStream_t s, int32_t **sel_out = nullptr, float **prob_out = nullptr,
+                           const float *norm_x = nullptr, const float *norm_w = nullptr, float norm_eps = 0.0f) {
     const int k = M.k, dim = M.dim, hidden = M.hidden;
     if (k < 1 || k > 8 || M.n_exp > 64 || k > M.n_exp) return 0;
     if (cat_of(M.gate.fmt, dim) != CAT_F32 || M.up.fmt != M.gate.fmt || cat_of(M.down.fmt, hidden) != CAT_F32)
@@ -1336,7 +1340,34 @@ static int moe_ffn_enqueue(const MoeDev &M, const float *xn, const XQ &xq, float
     gate = (float *)(((uintptr_t)gate + 15) & ~(uintptr_t)15);
     up = gate + (size_t)k * hidden;
     proj = up + (size_t)k * hidden;
-    {
+    static int norm_fuse = -1;
+    if (norm_fuse < 0) {
+        const char *e = getenv("RUSTY_HIP_MOE_NORM_FUSE");
+        norm_fuse = (e && e[0] == '0') ? 0 : 1;
+    }
+    if (norm_w && norm_fuse && M.router.fmt == F_Q8_0 && cat_of(M.router.fmt, dim) == CAT_F32 && dim % 4 == 0 &&
+        dim <= 3072 && ((uintptr_t)norm_x & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)xn & 15) == 0) {
+        GemvArgs A;
+        memset(&A, 0, sizeof(A));
+        A.K = dim;
+        A.epi = EPI_STORE;
+        A.x = norm_x;
+        A.n_mats = 1;
+        A.m[0].w = M.router.p;
+        A.m[0].row_stride = M.router.stride;
+        A.m[0].rows = M.router.rows;
+        A.m[0].fmt = M.router.fmt;
+        A.m[0].y = logits;
+        A.m[0].bias = M.router_bias;
+        A.n_tiles = (M.router.rows + 7) / 8;
+        A.norm_w = norm_w;
+        A.norm_eps = norm_eps;
+        A.norm_out = xn;
+        ProfScope ps("gemv_f32x", s);
+        rh_launch(gemv_q8_0_f32x_kernel<true>, dim3(A.n_tiles), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
+        RH_LAUNCH_OK();
+    } else {
+        if (norm_w && !launch_rmsnorm(norm_x, norm_w, norm_eps, dim, xn, nullptr, s)) return 0;
         MatSpec mr = {M.router, logits, M.router_bias};
         ActSpec a;
         memset(&a, 0, sizeof(a));
@@ -2496,9 +2527,8 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
         MatSpec mo = {Ly.w[3], R.x, Ly.bo};
         if (!gemv_multi_act(&mo, 1, attn_cols, EPI_ADD, act_o, s)) return 0;
         // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2)
-        ActSpec use;
-        if (!act_materialize(r_act_norm(Ly.ffn_norm), dim, &use, s)) return 0;
-        if (!moe_ffn_enqueue(Ly.moe, R.xn, use.xq, nullptr, R.x, R.moebuf, s)) return 0;
+        if (!moe_ffn_enqueue(Ly.moe, R.xn, XQ{}, nullptr, R.x, R.moebuf, s, nullptr, nullptr, R.x, Ly.ffn_norm, R.eps))
+            return 0;
     }
     if (mode & (MODE_LOGITS | MODE_GREEDY)) {
         MatSpec mh = {R.out_w, R.logits, nullptr};
