@@ -44,12 +44,11 @@ struct GemmArgs {
     const float *bias;  // [rows] or null
 };
 
-// Q6_K bytes q (0..63, four per dword) as signed q - 32: flip bit 5, then copy
-// it into bits 6 and 7.
-__device__ __forceinline__ uint32_t q6_signed4(uint32_t q) {
-    const uint32_t b = q ^ 0x20202020u, s = b & 0x20202020u;
-    return b | (s << 1) | (s << 2);
-}
+// Q6_K bytes q (0..63, four per dword) as signed q - 32: (q + 0x60) ^ 0x80
+// per byte, where q + 0x60 <= 0x9F never carries into the next byte (one add
+// and one xor per dword; a copy of bit 5 into bits 6 and 7 compiled to a
+// quarter-rate multiply by 6).
+__device__ __forceinline__ uint32_t q6_signed4(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
 // Byte m (< 256) in all four bytes of a dword (one v_perm_b32).
 __device__ __forceinline__ int bcast_byte(int m) { return (int)__builtin_amdgcn_perm(0u, (uint32_t)m, 0u); }
@@ -190,7 +189,12 @@ __device__ __forceinline__ void gemm_block_ints(const GemmW<F_Q6_K> &W, const in
                     const long a = *(const long *)(xs + (32 * tt + n) * GEMM_XS + e0);
                     const rh_v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, bq, rh_v16i{}, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 16; i++) isum[tt][i] = __mul24(sc, c[i]) + isum[tt][i];
+                    for (int i = 0; i < 16; i++) {
+                        isum[tt][i] = __mul24(sc, c[i]) + isum[tt][i];
+                        // opaque to the optimiser: keeps one 24-bit multiply-add per
+                        // update instead of products paired into three-input adds
+                        asm("" : "+v"(isum[tt][i]));
+                    }
                 }
             }
         }
