@@ -1367,7 +1367,10 @@ static int moe_ffn_enqueue(const MoeDev &M, float *xn, const XQ &xq, float *moe_
         rh_launch(gemv_q8_0_f32x_kernel<true>, dim3(A.n_tiles), dim3(64), (uint32_t)(A.K * sizeof(float)), s, A);
         RH_LAUNCH_OK();
     } else {
-        if (norm_w && !launch_rmsnorm(norm_x, norm_w, norm_eps, dim, xn, nullptr, s)) return 0;
+        // the norm also writes the Q8_K form into the caller's buffer when the
+        // router takes the integer path (no allocation: this may be captured)
+        if (norm_w && !launch_rmsnorm(norm_x, norm_w, norm_eps, dim, xn, (dim % 256 == 0 && xq.qs) ? &xq : nullptr, s))
+            return 0;
         MatSpec mr = {M.router, logits, M.router_bias};
         ActSpec a;
         memset(&a, 0, sizeof(a));
@@ -2527,7 +2530,8 @@ static int r_enqueue_moe(int mode, float penalty, hipStream_t s) {
         MatSpec mo = {Ly.w[3], R.x, Ly.bo};
         if (!gemv_multi_act(&mo, 1, attn_cols, EPI_ADD, act_o, s)) return 0;
         // xn2 = rms_norm(x, post_attn_norm); x += moe(xn2)
-        if (!moe_ffn_enqueue(Ly.moe, R.xn, XQ{}, nullptr, R.x, R.moebuf, s, nullptr, nullptr, R.x, Ly.ffn_norm, R.eps))
+        if (!moe_ffn_enqueue(Ly.moe, R.xn, dim % 256 == 0 ? R.xq_dim : XQ{}, nullptr, R.x, R.moebuf, s, nullptr, nullptr,
+                             R.x, Ly.ffn_norm, R.eps))
             return 0;
     }
     if (mode & (MODE_LOGITS | MODE_GREEDY)) {
