@@ -1057,9 +1057,19 @@ static_assert(C4_NT >= C4_P + C4_PER, "ring too small");
 template <int IPT, int LEAD, class Issue>
 __device__ __forceinline__ void c4_producer_loop(int ntiles, Issue &issue) {
     const int ngroups = (ntiles + C4_PER - 1) / C4_PER;
-    for (int i = 0; i < min(C4_P, ntiles); i++) issue(i);
-    if (LEAD) c4_wait_tiles_after<IPT>(min(C4_P, ntiles) - 1 - min(C4_PER - 1, ntiles - 1));
-    tile_barrier();
+    if (LEAD) {
+        // the coefficient waves need only group 0 before the first barrier:
+        // its tiles are issued and awaited first, the rest of the initial
+        // window after that barrier (a streamed launch's issue waits for each
+        // tile's flag, so the first barrier no longer waits for C4_P flags)
+        for (int i = 0; i < min(C4_PER, ntiles); i++) issue(i);
+        c4_wait_tiles_after<IPT>(0);
+        tile_barrier();
+        for (int i = C4_PER; i < min(C4_P, ntiles); i++) issue(i);
+    } else {
+        for (int i = 0; i < min(C4_P, ntiles); i++) issue(i);
+        tile_barrier();
+    }
     for (int j = 0; j < ngroups; j++) {
         const int last = min(C4_PER * (j + LEAD) + C4_PER - 1, ntiles - 1);
         const int issued = min(C4_P + C4_PER * j, ntiles);
