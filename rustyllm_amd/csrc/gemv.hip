@@ -1386,10 +1386,12 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
     if (wave == 0) {
         lds_barrier();  // group 0 produced
         float sum = 0.0f;
-        for (int j = 0; j < npad; j++) {
+        // group j: the next block's eight reads are in flight while this
+        // block's 32 adds run.  Every block of a full group is added without
+        // a condition, so the reads stay ahead of the adds (a conditional add
+        // would draw its reads into its branch, next to their use)
+        auto group = [&](int j, bool full) {
             const int b0 = P * j;
-            // the next block's eight reads are in flight while this block's
-            // 32 adds run
             float4 v[2][8];
 #pragma unroll
             for (int k = 0; k < 8; k++) v[0][k] = *(const float4 *)(&s_t[b0 % SLOTS][lane * 4] + 256 * k);
@@ -1400,7 +1402,7 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
                     for (int k = 0; k < 8; k++)
                         v[(i + 1) & 1][k] = *(const float4 *)(&s_t[(b0 + i + 1) % SLOTS][lane * 4] + 256 * k);
                 }
-                if (b0 + i < nb) {
+                if (full || b0 + i < nb) {
 #pragma unroll
                     for (int k = 0; k < 8; k++) {
                         sum += v[i & 1][k].x;
@@ -1409,9 +1411,17 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
                         sum += v[i & 1][k].w;
                     }
                 }
+                // the next block's reads stay here, one block ahead (issued
+                // all at once, a group's 32 reads overrun the LDS counter)
+                __builtin_amdgcn_sched_barrier(0);
             }
             lds_barrier();
-        }
+        };
+        int j = 0;
+        for (; j + 1 < ngroups; j++) group(j, true);
+        group(j, false);
+        // the producers' padding groups: barriers only
+        for (j++; j < npad; j++) lds_barrier();
         if (live) {
             float out = sum;
             if (bias) out += bias[row];
@@ -1456,6 +1466,37 @@ __global__ __launch_bounds__(64 * (P + 1)) void gemv_mxfp4_serial_kernel(
 // blocks are funnel-shifted out of the registers.  A row-per-lane global load
 // would touch 64 cache lines per instruction.
 #define MXF_C 16  // blocks per chunk
+// sum += t[i] for i = 0..3 in order, and n[i] = x[4 G + i] * p[i] issued
+// between the adds, so each add's operand sum is two instructions old.  x[e]
+// of the block is in row lane e % 16 of xh (the pair's half e / 16), taken by
+// a DPP row broadcast.  One asm statement, so the compiler keeps the
+// interleaving; the leading s_nop gives a DPP read of xh two wait states
+// after any VALU write of it before the statement.
+#define MX_AM4_DPP(R0, R1, R2, R3)                                                            \
+    asm("s_nop 0\n\t"                                                                          \
+        "v_add_f32 %0, %0, %5\n\t"                                                             \
+        "v_mul_f32_dpp %1, %9, %10 row_newbcast:" #R0 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_add_f32 %0, %0, %6\n\t"                                                             \
+        "v_mul_f32_dpp %2, %9, %11 row_newbcast:" #R1 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_add_f32 %0, %0, %7\n\t"                                                             \
+        "v_mul_f32_dpp %3, %9, %12 row_newbcast:" #R2 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_add_f32 %0, %0, %8\n\t"                                                             \
+        "v_mul_f32_dpp %4, %9, %13 row_newbcast:" #R3 " row_mask:0xf bank_mask:0xf"           \
+        : "+v"(sum), "=&v"(n[0]), "=&v"(n[1]), "=&v"(n[2]), "=&v"(n[3])                         \
+        : "v"(t[0]), "v"(t[1]), "v"(t[2]), "v"(t[3]), "v"(xh), "v"(p[0]), "v"(p[1]), "v"(p[2]), \
+          "v"(p[3]))
+template <int G>
+__device__ __forceinline__ void mx_add4_mul4_dpp(float &sum, const float *t, float xh, const float *p, float *n) {
+    if constexpr ((G & 3) == 0)
+        MX_AM4_DPP(0, 1, 2, 3);
+    else if constexpr ((G & 3) == 1)
+        MX_AM4_DPP(4, 5, 6, 7);
+    else if constexpr ((G & 3) == 2)
+        MX_AM4_DPP(8, 9, 10, 11);
+    else
+        MX_AM4_DPP(12, 13, 14, 15);
+}
+#undef MX_AM4_DPP
 __device__ __forceinline__ float swiglu_gpt_oss_ref(float g, float u);
 __device__ __forceinline__ int moe_topk_wave(const float *logits, int n, int k, int slot, int32_t *sel, float *prob);
 
@@ -1469,6 +1510,9 @@ __device__ __forceinline__ int moe_topk_wave(const float *logits, int n, int k, 
 template <bool SWI>
 __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
     __shared__ __align__(16) uint4 s_b[64 * 17];
+    // x, K floats rounded up to 256, each 32-element block stored as 16
+    // pairs (x[i], x[i + 16]): lane l reads its pair for element row l % 16
+    extern __shared__ __align__(16) float s_x[];
     const int K = A.K, nb = K >> 5, lane = threadIdx.x;
     const int tile = blockIdx.x;
     const int n_sel = SWI ? A.n_mats / 2 : A.n_mats;  // matrices the tiles are counted over
@@ -1479,6 +1523,34 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
     const GemvMat M = mat_sel(A, mi);
     const GemvMat MU = SWI ? mat_sel(A, mi + n_sel) : M;  // SWI: the up matrix of the same expert
     const float *xs = M.x ? M.x : A.x;
+    // x into LDS (loads in flight during the expert selection, stores after
+    // it): every block then takes its x with one LDS read of a fixed latency,
+    // where scalar loads would wait behind the weight stream.  Ordinary loads
+    // and stores, not direct loads: LDS filled by direct loads makes the
+    // compiler wait for every outstanding direct load before each read of it.
+    constexpr int XQ = 12;  // 16-byte pieces per lane and batch (K <= 3072 in one)
+    const int k4 = K / 4;
+    float4 xv[XQ];
+    auto x_load = [&](int base) {
+#pragma unroll
+        for (int i = 0; i < XQ; i++) xv[i] = ((const float4 *)xs)[min(base + 64 * i + lane, k4 - 1)];
+    };
+    // piece q holds x[4 q .. 4 q + 3]: one half (4 q & 16) of block 4 q / 32,
+    // element rows r .. r + 3 (r = 4 q & 15), stored at 32 b + 2 r + h
+    auto x_store = [&](int base) {
+#pragma unroll
+        for (int i = 0; i < XQ; i++) {
+            const int q = base + 64 * i + lane;
+            if (q < k4) {
+                float *d = &s_x[(4 * q & ~31) + 2 * (4 * q & 15) + ((4 * q >> 4) & 1)];
+                d[0] = xv[i].x;
+                d[2] = xv[i].y;
+                d[4] = xv[i].z;
+                d[6] = xv[i].w;
+            }
+        }
+    };
+    x_load(0);
     const uint8_t *w = M.w, *wu = MU.w;
     const float *bias = M.bias, *bias_u = MU.bias;
     if (M.sel) {
@@ -1490,6 +1562,11 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
         wu += e * MU.sel_w;
         if (bias) bias += e * M.sel_b;
         if (bias_u) bias_u += e * MU.sel_b;
+    }
+    x_store(0);
+    for (int base = 64 * XQ; base < k4; base += 64 * XQ) {
+        x_load(base);
+        x_store(base);
     }
     constexpr int TR = SWI ? 32 : 64;  // rows of one matrix per tile
     const bool up_lane = SWI && lane >= 32;
@@ -1520,36 +1597,43 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
     struct XBlk {
         float v[32];
     };
+    // block b's x as 32 uniform values (broadcast LDS reads), for the terms
+    // computed outside the pipelined adds
     auto load_x = [&](int b, XBlk &xr) {
-        const const_f32_ptr p = (const_f32_ptr)xs + min(b, nb - 1) * 32;
+        const float *p = &s_x[min(b, nb - 1) * 32];
 #pragma unroll
-        for (int i = 0; i < 32; i++) xr.v[i] = p[i];
+        for (int i = 0; i < 32; i++) xr.v[i] = p[2 * (i & 15) + (i >> 4)];
     };
-    // one block's 32 terms added to sum in element order; fast: every lane's
-    // scale is normal, so the hardware conversion applies (lut * scale exact)
-    auto add_block = [&](float sum, const uint32_t (&wd)[4], uint32_t e, const XBlk &xr) {
+    // block b's x pair of this lane: (x[32 b + l % 16], x[32 b + 16 + l % 16])
+    auto load_xp = [&](int b) { return *(const float2 *)&s_x[min(b, nb - 1) * 32 + 2 * (lane & 15)]; };
+    // one block's 32 terms (lut[n] * scale) * x in element order.  fast: the
+    // hardware conversion gives lut * scale exactly when the lane's scale is
+    // normal; table: any scale byte (0 is the subnormal 2^-127, 255 infinite)
+    auto terms_fast = [&](const uint32_t (&wd)[4], uint32_t e, const XBlk &xr, float (&t)[32]) {
         const float sc = mxfp4_scale(e);
-        if (__builtin_amdgcn_ballot_w64(e == 0u || e == 255u) == 0) {
 #pragma unroll
-            for (int k = 0; k < 4; k++)
+        for (int k = 0; k < 4; k++)
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const fp4x2_f32 p = fp4x2_scaled(wd[k], sc, u);
-                    sum += p.x * xr.v[8 * k + 2 * u];
-                    sum += p.y * xr.v[8 * k + 2 * u + 1];
-                }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const uint32_t byte = (wd[k] >> (8 * u)) & 0xFFu;
-                    sum += mxfp4_nibble(byte & 0xFu) * sc * xr.v[8 * k + 2 * u];
-                    sum += mxfp4_nibble(byte >> 4) * sc * xr.v[8 * k + 2 * u + 1];
-                }
-        }
-        return sum;
+            for (int u = 0; u < 4; u++) {
+                const fp4x2_f32 p = fp4x2_scaled(wd[k], sc, u);
+                t[8 * k + 2 * u] = p.x * xr.v[8 * k + 2 * u];
+                t[8 * k + 2 * u + 1] = p.y * xr.v[8 * k + 2 * u + 1];
+            }
     };
+    auto terms_table = [&](const uint32_t (&wd)[4], uint32_t e, const XBlk &xr, float (&t)[32]) {
+        const float sc = mxfp4_scale(e);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                // lut[n] itself from the conversion at scale 1, then the
+                // reference's (lut * scale) * x
+                const fp4x2_f32 q = fp4x2_scaled(wd[k], 1.0f, u);
+                t[8 * k + 2 * u] = q.x * sc * xr.v[8 * k + 2 * u];
+                t[8 * k + 2 * u + 1] = q.y * sc * xr.v[8 * k + 2 * u + 1];
+            }
+    };
+    auto rare_scale = [](uint32_t e) { return __builtin_amdgcn_ballot_w64(e == 0u || e == 255u) != 0; };
     // block j of this lane's chunk: bytes 17 j .. 17 j + 16 of the 68 dwords
     auto block_of = [&](const uint32_t (&dw)[68], int j, uint32_t (&wd)[4], uint32_t &e) {
         const int d = (17 * j) >> 2, o = (17 * j) & 3;
@@ -1557,13 +1641,19 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
         for (int k = 0; k < 4; k++) wd[k] = o ? __builtin_amdgcn_alignbyte(dw[d + k + 1], dw[d + k], o) : dw[d + k];
         e = (dw[d + 4] >> (8 * o)) & 0xFFu;
     };
+    // The running sum is a chain of dependent adds; the terms are not.  Block
+    // j's 32 adds alternate with the multiplies of block j + 1's terms, whose
+    // x enters each multiply through a DPP row broadcast of the lane's x pair
+    // (mx_add4_mul4_dpp), so each add finds its predecessor's result ready.
+    // T[j & 1] holds block j's terms, XP[b & 1] block b's x pair, read a
+    // block before the block whose adds it joins.
     float sum = 0.0f;
-    XBlk xr[2];
-    load_x(0, xr[0]);
+    float2 XP[2];
+    XP[1] = load_xp(1);
     issue_chunk(0);
     for (int c = 0; c < nch; c++) {
-        // chunk c: from LDS into registers, then chunk c + 1 into the freed
-        // LDS while this one is summed
+        // chunk c (and, before the first, x): from LDS into registers, then
+        // chunk c + 1 into the freed LDS while this one is summed
         RH_WAIT_VM(0);
         uint32_t dw[68];
         const uint4 *src = &s_b[17 * lane];
@@ -1578,13 +1668,57 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
         RH_WAIT_LGKM0();
         if (c + 1 < nch) issue_chunk(c + 1);  // uniform
         const int b0 = MXF_C * c;
+        XP[0] = load_xp(b0 + 2);
+        float T[2][32];
+        {
+            XBlk xr;
+            load_x(b0, xr);
+            uint32_t wd[4], e;
+            block_of(dw, 0, wd, e);
+            if (rare_scale(e))
+                terms_table(wd, e, xr, T[0]);
+            else
+                terms_fast(wd, e, xr, T[0]);
+        }
 #pragma unroll
         for (int j = 0; j < MXF_C; j++) {
             if (b0 + j < nb) {  // uniform; false only in a last, partial chunk
-                load_x(b0 + j + 1, xr[(j + 1) & 1]);
-                uint32_t wd[4], e;
-                block_of(dw, j, wd, e);
-                sum = add_block(sum, wd, e, xr[j & 1]);
+                const float(&t)[32] = T[j & 1];
+                if (j + 1 < MXF_C) {
+                    // block j + 1's terms between block j's adds (past the
+                    // row's end: values that are never added)
+                    float(&tn)[32] = T[(j + 1) & 1];
+                    const float2 xp = XP[(j + 1) & 1];
+                    uint32_t wd[4], e;
+                    block_of(dw, j + 1, wd, e);
+                    const float sc = mxfp4_scale(e);
+                    float pr[32];
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const fp4x2_f32 q = fp4x2_scaled(wd[k], sc, u);
+                            pr[8 * k + 2 * u] = q.x;
+                            pr[8 * k + 2 * u + 1] = q.y;
+                        }
+                    mx_add4_mul4_dpp<0>(sum, &t[0], xp.x, &pr[0], &tn[0]);
+                    mx_add4_mul4_dpp<1>(sum, &t[4], xp.x, &pr[4], &tn[4]);
+                    mx_add4_mul4_dpp<2>(sum, &t[8], xp.x, &pr[8], &tn[8]);
+                    mx_add4_mul4_dpp<3>(sum, &t[12], xp.x, &pr[12], &tn[12]);
+                    mx_add4_mul4_dpp<4>(sum, &t[16], xp.y, &pr[16], &tn[16]);
+                    mx_add4_mul4_dpp<5>(sum, &t[20], xp.y, &pr[20], &tn[20]);
+                    mx_add4_mul4_dpp<6>(sum, &t[24], xp.y, &pr[24], &tn[24]);
+                    mx_add4_mul4_dpp<7>(sum, &t[28], xp.y, &pr[28], &tn[28]);
+                    if (rare_scale(e)) {
+                        XBlk xr;
+                        load_x(b0 + j + 1, xr);
+                        terms_table(wd, e, xr, tn);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 32; i++) sum += t[i];
+                }
+                if (j + 1 < MXF_C) XP[(j + 1) & 1] = load_xp(b0 + j + 3);  // block j + 1's pair is no longer needed
             }
         }
     }

@@ -62,9 +62,11 @@ __device__ __forceinline__ int moe_topk_wave(const float *logits, int n, int k, 
     const int lane = threadIdx.x & 63;
     const float v = lane < n ? logits[lane] : 0.0f;
     const int32_t key = total_key(v);
+    // rank = the number of lanes ahead of this one in (key descending, index
+    // ascending) order; each key is broadcast by a scalar read of its lane
     int rank = 0;
     for (int j = 0; j < n; j++) {
-        const int32_t kj = __shfl(key, j, 64);
+        const int32_t kj = __builtin_amdgcn_readlane(key, j);
         rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
     }
     const unsigned long long ms = __builtin_amdgcn_ballot_w64(lane < n && rank == slot);

@@ -562,6 +562,10 @@ static int launch_q8p_any(const GemvArgs &A, int act, bool sw, hipStream_t s) {
 // RUSTY_HIP_MX_SERIAL_PER_CU: tiles per CU up to which the producer/adder
 // workgroups serve an MXFP4 launch (two per CU fit in LDS, but measured
 // slower on the gpt-oss expert launches: 279 against 285 tok/s)
+// LDS bytes of the fused MXFP4 kernel's x (K floats rounded up to 256), and
+// the largest K it serves: with its 17 KB chunk, at most 64 KB per workgroup
+static size_t mx_fused_x_bytes(int K) { return (size_t)(K + 255) / 256 * 1024; }
+static bool mx_fused_fits(int K) { return 17408 + mx_fused_x_bytes(K) <= 65536; }
 static int mx_serial_per_cu() {
     static int v = -1;
     if (v < 0) {
@@ -574,10 +578,10 @@ template <int FMT>
 static int launch_f32x(const GemvArgs &A, hipStream_t s) {
     if constexpr (FMT == F_MXFP4) {
         ProfScope ps("gemv_mxfp4", s);
-        if (A.n_tiles > mx_serial_per_cu() * g.n_cu) {
+        if (A.n_tiles > mx_serial_per_cu() * g.n_cu && mx_fused_fits(A.K)) {
             // more tiles than CUs: one wave per tile computes its own terms,
             // several tiles per SIMD
-            rh_launch(gemv_mxfp4_fused_kernel<false>, dim3(A.n_tiles), dim3(64), 0, s, A);
+            rh_launch(gemv_mxfp4_fused_kernel<false>, dim3(A.n_tiles), dim3(64), mx_fused_x_bytes(A.K), s, A);
         } else {
             // one workgroup per tile: the serial row sums are spread over a
             // summing wave and MXP term-producing waves
@@ -1390,7 +1394,7 @@ static int moe_ffn_enqueue(const MoeDev &M, float *xn, const XQ &xq, float *moe_
     }
     const int swi_tiles = k * ((hidden + 31) / 32);
     const bool swi = swi_fuse && M.gate.fmt == F_MXFP4 && 2 * k <= GEMV_MAX_MATS && M.up.stride == M.gate.stride &&
-                     swi_tiles > mx_serial_per_cu() * g.n_cu;
+                     swi_tiles > mx_serial_per_cu() * g.n_cu && mx_fused_fits(dim);
     if (!swi) {
         ProfScope ps("moe_topk", s);
         rh_launch(moe_topk_kernel, dim3(1), dim3(64), 0, s, (const float *)logits, M.n_exp, k, sel, prob);
@@ -1442,7 +1446,7 @@ static int moe_ffn_enqueue(const MoeDev &M, float *xn, const XQ &xq, float *moe_
         A.topk_sel = sel;
         A.topk_prob = prob;
         ProfScope ps("gemv_mxfp4", s);
-        rh_launch(gemv_mxfp4_fused_kernel<true>, dim3(A.n_tiles), dim3(64), 0, s, A);
+        rh_launch(gemv_mxfp4_fused_kernel<true>, dim3(A.n_tiles), dim3(64), mx_fused_x_bytes(A.K), s, A);
         RH_LAUNCH_OK();
     } else {
     {
