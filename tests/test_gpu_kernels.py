@@ -128,7 +128,8 @@ def test_gemv_bit_exact(hip, t, rows, cols):
 
 @pytest.mark.parametrize("t,rows,cols", [(39, 2880, 2880), (39, 513, 4096), (39, 200, 14336), (39, 70, 96),
                                          (8, 4096, 2880),
-                                         (8, 201, 2880), (8, 9, 160)])
+                                         (8, 201, 2880), (8, 9, 160),
+                                         (8, 100, 5152)])  # six 32-block chunks through the three-chunk ring
 def test_gemv_f32_paths_bit_exact(hip, t, rows, cols):
     """f32-activation rows (MXFP4 always; Q8_0 when K % 256 != 0) in the
     reference's order: dot_mxfp4_f32_scalar's single running sum and
