@@ -1078,8 +1078,18 @@ static int attn_exact_launch(AttnExactArgs A, float *scratch, const XQ &xq, hipS
         const char *e = getenv("RUSTY_HIP_STREAM_JMIN");
         jmin = e ? std::max(1, atoi(e)) : 12;
     }
+    // A sliding window shorter than RUSTY_HIP_STREAM_MIN_WINDOW positions
+    // (default 256) takes the separate launches: at gpt-oss's 128 positions
+    // the streamed launch's start (scores published, polled, loaded) costs
+    // more than the two extra launches (24.5 against 18.8 us per layer)
+    static int min_window = -1;
+    if (min_window < 0) {
+        const char *e = getenv("RUSTY_HIP_STREAM_MIN_WINDOW");
+        min_window = e ? std::max(0, atoi(e)) : 256;
+    }
+    const bool short_window = A.window > 0 && A.window < min_window;
     if (sync && s8 && c4 && A.n_tok == 0 && !A.lin && stream_enabled() && nc + 32 <= g.n_cu &&
-        (J >= jmin || J >= ntl)) {
+        (J >= jmin || J >= ntl) && !short_window) {
         A.sync = sync;
         const int blocks = J * A.n_kv + nc;
         ProfScope ps("attn_exact_stream", s);
