@@ -1341,13 +1341,16 @@ __device__ __forceinline__ void c4_tile(const Chain4Lds &L, int i, int row, int 
     }
 }
 
-// One full group (C4_PER tiles) of a consumer wave, each tile in the form its
-// new-max summary calls for.
-template <bool X4, bool DEN, bool VT>
-__device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, int dcol, int lane, float &o) {
+// The first nt (1..C4_PER) tiles of a consumer group, all complete, each tile
+// in the form its new-max summary calls for (PART = false: all C4_PER, the
+// count a constant).
+template <bool X4, bool DEN, bool VT, bool PART>
+__device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, int dcol, int lane, float &o,
+                                         int nt_part) {
+    const int nt = PART ? nt_part : C4_PER;
     // the group's new-max words first, then chunk 0, so the summary is ready
     // while chunk 0 is still in flight
-    const uint32_t wraw = lane < 8 * C4_PER ? L.m[(i0 + (lane >> 3)) & (C4_NT - 1)][lane & 7] : 0u;
+    const uint32_t wraw = lane < 8 * nt ? L.m[(i0 + (lane >> 3)) & (C4_NT - 1)][lane & 7] : 0u;
     const int s0 = i0 & (C4_NT - 1);
     float a[2], v[2][16];
     c4_load16<DEN, VT>(&L.e[s0][row * EX_TILE], &L.v[s0][VT ? 4 * dcol : dcol], 0, lane, a[0], v[0]);
@@ -1360,23 +1363,26 @@ __device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, in
         // the first tiles): straight-line FMA runs
 #pragma unroll
         for (int t = 0; t < C4_PER; t++)
-            c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+            if (t < nt)
+                c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < nt, glo, ghi, t, a, v, o);
     } else if (X4 || DEN) {
         // grouped form: the 16-step chunks of a tile holding a new maximum
         // for any of the four rows run o = fma(a, v, o*m) on every step
 #pragma unroll
         for (int t = 0; t < C4_PER; t++) {
+            if (t >= nt) break;
             if ((any >> (8 * t)) & 0xFFu)
-                c4_tile<X4, DEN, VT, C4_AFF>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+                c4_tile<X4, DEN, VT, C4_AFF>(L, i0 + t, row, dcol, lane, t + 1 < nt, glo, ghi, t, a, v, o);
             else
-                c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+                c4_tile<X4, DEN, VT, C4_FAST>(L, i0 + t, row, dcol, lane, t + 1 < nt, glo, ghi, t, a, v, o);
         }
     } else {
         // scale_add heads: each 16-step chunk holding a new maximum runs
         // every step in its own form
 #pragma unroll
         for (int t = 0; t < C4_PER; t++)
-            c4_tile<X4, DEN, VT, C4_FLAGS>(L, i0 + t, row, dcol, lane, t + 1 < C4_PER, glo, ghi, t, a, v, o);
+            if (t < nt)
+                c4_tile<X4, DEN, VT, C4_FLAGS>(L, i0 + t, row, dcol, lane, t + 1 < nt, glo, ghi, t, a, v, o);
     }
 }
 
@@ -1384,7 +1390,10 @@ __device__ __forceinline__ void c4_group(const Chain4Lds &L, int i0, int row, in
 // its row's head), DEN = true the denominators, the same recurrence with
 // v = 1 (fma(e, 1, d) = d + e; on a new maximum fma(1, 1, d*e) = d*e + 1,
 // the x4 form), starting from 1 with sinks; no V is read.
-template <bool X4, bool DEN, bool VT>
+// PF: the complete tiles of a partial group in the chunked forms too (the
+// separate chain launch; in the streamed launch the second instance of the
+// group code would not fit the ten waves' registers)
+template <bool X4, bool DEN, bool VT, bool PF>
 __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float *dst) {
     const int lane = threadIdx.x & 63, row = lane >> 4, dcol = lane & 15;
     const int ntiles = (ctx + EX_TILE - 1) / EX_TILE;
@@ -1396,9 +1405,16 @@ __device__ void c4_consumer(const AttnExactArgs &A, Chain4Lds &L, int ctx, float
         const int i0 = C4_PER * j;
         const bool full = i0 + C4_PER <= ntiles && ctx >= (i0 + C4_PER) * EX_TILE;
         if (full) {
-            c4_group<X4, DEN, VT>(L, i0, row, dcol, lane, o);
+            c4_group<X4, DEN, VT, false>(L, i0, row, dcol, lane, o, C4_PER);
         } else {
-            for (int i = i0; i < min(i0 + C4_PER, ntiles); i++) {
+            // (PF) the complete tiles in the chunked forms, then the rest
+            // step by step
+            int nfull = 0;
+            if constexpr (PF) {
+                while (nfull < C4_PER && i0 + nfull < ntiles && ctx >= (i0 + nfull + 1) * EX_TILE) nfull++;
+                if (nfull > 0) c4_group<X4, DEN, VT, true>(L, i0, row, dcol, lane, o, nfull);
+            }
+            for (int i = i0 + nfull; i < min(i0 + C4_PER, ntiles); i++) {
                 const int sl = i & (C4_NT - 1);
                 const int ntok = min(EX_TILE, ctx - i * EX_TILE);
                 const float *vt = &L.v[sl][dcol];
@@ -1477,6 +1493,7 @@ __device__ __forceinline__ int c4_vwave_part(int wave) {
 __device__ __forceinline__ int chain4_blocks(const AttnExactArgs &A) {
     return A.n_kv * ((A.kv_mul + 3) / 4) * (A.vd / 16 + 1);
 }
+template <bool PF>
 __device__ __forceinline__ void chain4_block(const AttnExactArgs &A, int block) {
     __shared__ Chain4Lds L;
     int s0, e0;
@@ -1501,7 +1518,7 @@ __device__ __forceinline__ void chain4_block(const AttnExactArgs &A, int block) 
     } else if (wave == 9) {
         c4_sproducer(A, L, ctx, h, g0);
     } else if (den) {
-        if (wave == 0) c4_consumer<true, true, false>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
+        if (wave == 0) c4_consumer<true, true, false, PF>(A, L, ctx, (g < kvm && (lane & 15) == 0) ? A.den + h * kvm + g : nullptr);
         else c4_idle(ctx);
     } else if (wave == 0) {
         float *dst = g < kvm ? A.out + (size_t)(h * kvm + g) * A.vd + slice * 16 + (lane & 15) : nullptr;
@@ -1510,11 +1527,11 @@ __device__ __forceinline__ void chain4_block(const AttnExactArgs &A, int block) 
             if (x4) c4_consumer_vg<true>(A, L, s0, ctx, h, slice, dst);
             else c4_consumer_vg<false>(A, L, s0, ctx, h, slice, dst);
         } else if (vt_ok) {
-            if (x4) c4_consumer<true, false, true>(A, L, ctx, dst);
-            else c4_consumer<false, false, true>(A, L, ctx, dst);
+            if (x4) c4_consumer<true, false, true, PF>(A, L, ctx, dst);
+            else c4_consumer<false, false, true, PF>(A, L, ctx, dst);
         } else {
-            if (x4) c4_consumer<true, false, false>(A, L, ctx, dst);
-            else c4_consumer<false, false, false>(A, L, ctx, dst);
+            if (x4) c4_consumer<true, false, false, PF>(A, L, ctx, dst);
+            else c4_consumer<false, false, false, PF>(A, L, ctx, dst);
         }
     } else if (vg) {
         c4_idle(ctx);
@@ -1533,7 +1550,7 @@ __device__ __forceinline__ void chain4_block(const AttnExactArgs &A, int block) 
 
 __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_chain4_kernel(AttnExactArgs A0) {
     const AttnExactArgs A = tok_view(A0);
-    chain4_block(A, blockIdx.x);
+    chain4_block<true>(A, blockIdx.x);
 }
 
 // A, B and C of one decode step in one launch, sized so every workgroup is
@@ -1550,7 +1567,7 @@ __global__ __launch_bounds__(64 * C4_WAVES) void attn_exact_stream_kernel(AttnEx
     A.ep = __hip_atomic_load(A0.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int ns = (int)gridDim.x - chain4_blocks(A);
     if ((int)blockIdx.x >= ns) {
-        chain4_block(A, (int)blockIdx.x - ns);
+        chain4_block<false>(A, (int)blockIdx.x - ns);
         __syncthreads();
     } else {
         if (threadIdx.x >= 256) return;  // the scores work takes four waves
