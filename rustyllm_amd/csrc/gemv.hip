@@ -1633,7 +1633,8 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
                 t[8 * k + 2 * u + 1] = q.y * sc * xr.v[8 * k + 2 * u + 1];
             }
     };
-    auto rare_scale = [](uint32_t e) { return __builtin_amdgcn_ballot_w64(e == 0u || e == 255u) != 0; };
+    // e == 0 or e == 255 in one unsigned compare
+    auto rare_scale = [](uint32_t e) { return __builtin_amdgcn_ballot_w64(e - 1u > 253u) != 0; };
     // block j of this lane's chunk: bytes 17 j .. 17 j + 16 of the 68 dwords
     auto block_of = [&](const uint32_t (&dw)[68], int j, uint32_t (&wd)[4], uint32_t &e) {
         const int d = (17 * j) >> 2, o = (17 * j) & 3;
@@ -1691,7 +1692,9 @@ __global__ __launch_bounds__(64) void gemv_mxfp4_fused_kernel(GemvArgs A) {
                     const float2 xp = XP[(j + 1) & 1];
                     uint32_t wd[4], e;
                     block_of(dw, j + 1, wd, e);
-                    const float sc = mxfp4_scale(e);
+                    // 2^(e-127) for a normal scale byte; the others take the
+                    // table form below, whatever this gives them
+                    const float sc = __builtin_bit_cast(float, e << 23);
                     float pr[32];
 #pragma unroll
                     for (int k = 0; k < 4; k++)
